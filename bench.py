@@ -1,0 +1,299 @@
+"""Benchmark of the MoE layer forward on one MI355X (default: the Mixtral-8x7B shape, bf16).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config mixtral|tiny|deepseek|qwen3_fp8|qwen3_bwd]
+
+A step is one MoE layer forward over one batch of synthetic tokens, inputs resident in HBM:
+router top-k on the gate logits -> route (dispatch) -> grouped GEMM gate_up with the fused
+SwiGLU -> grouped GEMM down -> weighted combine.  (The gate GEMM producing the logits is not
+part of the path; the logits are an input.)  For ``qwen3_bwd`` a step is the grouped-GEMM
+backward (dlhs + tgmm for both expert GEMMs) under Zipf-skewed routing.
+
+Prints ONE JSON line (rank 0).  ``roofline`` is measured live for the dominant kernel with HIP
+events on the stream the kernels run on; ``cpu_baseline`` times the numpy oracle (the CPU
+restatement of the reference algorithm) on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_FP8_TFLOPS = 5000.0    # MI355X dense fp8 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+CONFIGS = {
+    "tiny": dict(T=256, D=128, E=8, K=2, I=256, dtype="f32", scoring="softmax", wstd=0.02),
+    "mixtral": dict(T=8192, D=4096, E=8, K=2, I=14336, dtype="bf16", scoring="softmax", wstd=0.02),
+    "deepseek": dict(T=4096, D=7168, E=256, K=8, I=2048, dtype="bf16", scoring="sigmoid_group", wstd=0.006,
+                     n_group=8, topk_group=4, scale=2.5, shared=1),
+    "qwen3_fp8": dict(T=16384, D=2048, E=128, K=8, I=768, dtype="fp8", scoring="softmax", wstd=0.02),
+    "qwen3_bwd": dict(T=16384, D=2048, E=128, K=8, I=768, dtype="bf16", scoring="softmax", wstd=0.02, zipf=1.2),
+}
+
+
+def _traffic(name: str):
+    p = ROOT / "profiles" / f"traffic_{name}.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("bytes_per_launch")
+        except Exception:
+            return None
+    return None
+
+
+class EventTimer:
+    """Accumulates HIP-event durations of one region inside the timed loop."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs = []
+
+    def start(self):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs.append([e, None])
+
+    def stop(self):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs[-1][1] = e
+
+    def mean_ms(self):
+        return float(np.mean([a.elapsed_time(b) for a, b in self.pairs])) if self.pairs else 0.0
+
+
+def _cpu_baseline_layer(x, logits, gate_up, down, cfg, budget_s=12.0):
+    """Oracle forward (float64) on the first Ts tokens; Ts doubles until the run takes >= budget/3."""
+    from oracle import moe_oracle as O
+
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        cores = len(os.sched_getaffinity(0))
+    gu = gate_up.astype(np.float64)
+    dn = down.astype(np.float64)
+    T = x.shape[0]
+    ts, best = 16, None
+    while True:
+        t0 = time.perf_counter()
+        if cfg["scoring"] == "softmax":
+            idx, w, _ = O.router_softmax(logits[:ts], cfg["K"])
+        else:
+            idx, w, _ = O.router_sigmoid_group(logits[:ts], cfg["K"], n_group=cfg.get("n_group", 1),
+                                               topk_group=cfg.get("topk_group", 1),
+                                               routed_scaling_factor=cfg.get("scale", 1.0))
+        O.moe_experts(x[:ts].astype(np.float64), idx, w, gu, dn)
+        dt = time.perf_counter() - t0
+        best = (ts, dt)
+        if dt >= budget_s / 3 or ts >= T:
+            break
+        ts = min(T, ts * 2)
+    ts, dt = best
+    return {"value": ts / dt, "unit": "tokens/s", "cores": int(cores), "kind": "port",
+            "sample": f"numpy float64 oracle (oracle/moe_oracle.py) of the full layer forward on the first {ts} "
+                      f"of {T} tokens of the same inputs, one run, {dt:.2f} s"}
+
+
+def _zipf_bias(E, s, rng, beta=0.55):
+    rank = rng.permutation(E) + 1
+    return (-beta * s * np.log(rank)).astype(np.float32)
+
+
+def run(cfg_name, steps, warmup, cpu_baseline=True):
+    import torch
+
+    from mintext_amd import _lib
+    from mintext_amd.kernels import grouped_matmul_swiglu, grouped_matmul_vjp, route, route_topk, tgmm, unroute
+    from mintext_amd.kernels.grouped_matmul import _gmm_dlhs
+
+    _lib.lib()
+    cfg = CONFIGS[cfg_name]
+    dev = torch.device("cuda:0")
+    T, D, E, K, I = cfg["T"], cfg["D"], cfg["E"], cfg["K"], cfg["I"]
+    M = T * K
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    cdt = torch.float32 if cfg["dtype"] == "f32" else torch.bfloat16
+    x = torch.randn(T, D, device=dev, generator=g).to(cdt)
+    wg = torch.randn(D, E, device=dev, generator=g) * cfg["wstd"]
+    logits = (x.float() @ wg).to(cdt)  # the gate GEMM output: an input of the path
+    if cfg.get("zipf"):
+        bias = torch.from_numpy(_zipf_bias(E, cfg["zipf"], np.random.default_rng(5))).to(dev)
+        logits = (logits.float() + bias).to(cdt)
+    gate_up = (torch.randn(E, D, 2 * I, device=dev, generator=g) * cfg["wstd"]).to(cdt)
+    down = (torch.randn(E, I, D, device=dev, generator=g) * cfg["wstd"]).to(cdt)
+    shared = None
+    if cfg.get("shared"):
+        shared = ((torch.randn(1, D, 2 * I * cfg["shared"], device=dev, generator=g) * cfg["wstd"]).to(cdt),
+                  (torch.randn(1, I * cfg["shared"], D, device=dev, generator=g) * cfg["wstd"]).to(cdt))
+    rkw = dict(scoring=cfg["scoring"], n_group=cfg.get("n_group", 1), topk_group=cfg.get("topk_group", 1),
+               routed_scaling_factor=cfg.get("scale", 1.0))
+
+    t_gu, t_dn, t_disp, t_comb = EventTimer(torch), EventTimer(torch), EventTimer(torch), EventTimer(torch)
+    flops_fwd = 2.0 * M * D * 2 * I + 2.0 * M * I * D
+    fp8 = cfg["dtype"] == "fp8"
+    if fp8:
+        from mintext_amd.kernels.fp8 import (grouped_matmul_fp8, grouped_matmul_fp8_swiglu, quantize_fp8_rows,
+                                             quantize_fp8_weights)
+        from mintext_amd.kernels.moe_dispatch import route_with_scales
+
+        guq, gus = quantize_fp8_weights(gate_up)
+        dnq, dns = quantize_fp8_weights(down)
+
+    def step(timed):
+        with torch.no_grad():
+            idx, w = route_topk(logits, K, **rkw)
+            if timed:
+                t_disp.start()
+            if fp8:
+                xq, xs = quantize_fp8_rows(x)
+                sq, ss, si, gs, _ = route_with_scales(xq, xs, idx, E)
+            else:
+                st, si, gs = route(x, idx, E)
+            if timed:
+                t_disp.stop()
+                t_gu.start()
+            if fp8:
+                yq, ys = grouped_matmul_fp8_swiglu(sq, ss, guq, gus, gs)
+            else:
+                y = grouped_matmul_swiglu(st, gate_up, gs)
+            if timed:
+                t_gu.stop()
+                t_dn.start()
+            o = grouped_matmul_fp8(yq, ys, dnq, dns, gs) if fp8 else grouped_matmul_vjp(y, down, gs)
+            if timed:
+                t_dn.stop()
+                t_comb.start()
+            out = unroute(o, si, w, K)
+            if timed:
+                t_comb.stop()
+            if shared is not None:
+                from mintext_amd.moe import shared_expert_forward
+
+                out = out + shared_expert_forward(x, shared[0], shared[1]).float()
+            return out
+
+    if cfg_name == "qwen3_bwd":
+        with torch.no_grad():
+            idx, w = route_topk(logits, K)
+            st, si, gs = route(x, idx, E)
+            h = grouped_matmul_vjp(st, gate_up, gs)
+            y = grouped_matmul_swiglu(st, gate_up, gs)
+        gy = torch.randn(M, D, device=dev, generator=g).to(cdt)
+        gh = torch.randn(M, 2 * I, device=dev, generator=g).to(cdt)
+        flops_fwd = 2 * (2.0 * M * D * 2 * I + 2.0 * M * I * D)
+        t_dl, t_tg = t_gu, t_dn
+
+        def step(timed):  # noqa: F811
+            with torch.no_grad():
+                if timed:
+                    t_dl.start()
+                a = _gmm_dlhs(gy, down, gs)      # d inter  [M, I]
+                b = _gmm_dlhs(gh, gate_up, gs)   # d x      [M, D]
+                if timed:
+                    t_dl.stop()
+                    t_tg.start()
+                c = tgmm(y, gy, gs)              # d down   [E, I, D]
+                d = tgmm(st, gh, gs)             # d gate_up [E, D, 2I]
+                if timed:
+                    t_tg.stop()
+                return a, b, c, d
+
+    for _ in range(warmup):
+        step(False)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        step(True)
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(end) / steps
+
+    gs_host = None
+    with torch.no_grad():
+        idx, w = route_topk(logits, K, **rkw)
+        gs_host = torch.bincount(idx.reshape(-1).long(), minlength=E).cpu().numpy()
+
+    gu_ms, dn_ms = t_gu.mean_ms(), t_dn.mean_ms()
+    peak = PEAK_FP8_TFLOPS if fp8 else PEAK_BF16_TFLOPS
+    if cfg_name == "qwen3_bwd":
+        kern_flops = 2 * (2.0 * M * I * D) + 0  # dlhs pair: [M,D]x[D..]: 2*M*D*I + 2*M*2I*D
+        kern_flops = 2.0 * M * D * I + 2.0 * M * 2 * I * D
+        achieved = kern_flops / (gu_ms * 1e-3) / 1e12
+        dominant = "gmm_dlhs (both expert GEMMs)"
+    else:
+        kern_flops = 2.0 * M * D * 2 * I
+        achieved = kern_flops / (gu_ms * 1e-3) / 1e12
+        dominant = "gmm_fp8_swiglu (gate_up + SwiGLU + requant)" if fp8 else "gmm_swiglu (gate_up + fused SwiGLU)"
+    tokens_per_s = T / (ms * 1e-3)
+    gemm_ms = gu_ms + dn_ms
+    disp_b = T * D * (1 if fp8 else 2) + M * D * (1 if fp8 else 2) + T * K * 4 + M * 4 + E * 4
+    comb_b = M * D * 2 + T * K * 4 + M * 4 + T * D * 4
+    res = {
+        "metric": "MoE layer fwd tokens/s + grouped-GEMM TFLOP/s (% of peak), 1x MI355X",
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"bf16": "bf16", "f32": "f32", "fp8": "fp8e4m3"}[cfg["dtype"]],
+        "data": "synthetic (seeded N(0,1) activations, N(0,%g) weights, random-init experts)" % cfg["wstd"],
+        "config": {"workload": f"{cfg_name} MoE layer forward" if cfg_name != "qwen3_bwd" else
+                   "qwen3 grouped-GEMM backward (dlhs+tgmm), Zipf(1.2) skew",
+                   "T": T, "d_model": D, "experts": E, "top_k": K, "d_ff": I, "routing": cfg["scoring"],
+                   "parallelism": "single GPU"},
+        "gemm": {"tflops": round(flops_fwd / (gemm_ms * 1e-3) / 1e12 if cfg_name != "qwen3_bwd" else
+                                 flops_fwd / ((gu_ms + dn_ms) * 1e-3) / 1e12, 1),
+                 "frac_of_peak": round((flops_fwd / (gemm_ms * 1e-3) / 1e12) / peak, 4),
+                 "gate_up_ms": round(gu_ms, 4), "down_ms": round(dn_ms, 4)},
+        "dispatch_combine": {"dispatch_ms": round(t_disp.mean_ms(), 4), "combine_ms": round(t_comb.mean_ms(), 4),
+                             "dispatch_GBs": round(disp_b / (t_disp.mean_ms() * 1e-3) / 1e9, 1) if t_disp.pairs else None,
+                             "combine_GBs": round(comb_b / (t_comb.mean_ms() * 1e-3) / 1e9, 1) if t_comb.pairs else None},
+        "roofline": {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 1), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": _traffic(cfg_name)},
+        "load": {"min": int(gs_host.min()), "max": int(gs_host.max()), "mean": float(gs_host.mean()),
+                 "empty": int((gs_host == 0).sum())},
+        "wall_s": round(wall, 3),
+    }
+    if cpu_baseline and cfg_name not in ("qwen3_bwd",):
+        res["cpu_baseline"] = _cpu_baseline_layer(x.float().cpu().numpy(), logits.float().cpu().numpy(),
+                                                  gate_up.float().cpu().numpy(), down.float().cpu().numpy(), cfg)
+    return res
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="mixtral", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    a = ap.parse_args(argv)
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (no expert parallelism or "
+              "collectives); run with --gpus 1", file=sys.stderr)
+        return 2
+    res = run(a.config, a.steps, a.warmup, cpu_baseline=not a.no_cpu_baseline)
+    print(json.dumps(res))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,174 @@
+/*
+ * mintext_moe.h -- C-ABI of the MI355X (gfx950) MoE hot path.
+ *
+ * Every entry point takes plain device pointers, element counts and a HIP stream
+ * (passed as void*), enqueues its kernels asynchronously on that stream and returns
+ * an MTX_* status code.  No entry point allocates device memory: scratch memory is
+ * passed in by the caller as a `workspace` whose size is given by the matching
+ * *_workspace_size() query.  All index arrays are int32, all scale arrays float32.
+ * Matrices are row-major and dense.
+ *
+ * Reference interfaces replaced (bzantium/mintext, file:line):
+ *   mtx_router_topk        <- MoERouter.__call__ / _group_topk_routing
+ *                             (mintext/modules/moe.py:41-103); softmax mode has no
+ *                             counterpart in the reference (Mixtral/Qwen3 router)
+ *   mtx_route              <- route (mintext/kernels/moe_dispatch.py:47-81)
+ *   mtx_gather_rows        <- _sort_with_vjp forward (moe_dispatch.py:21-24)
+ *   mtx_scatter_rows       <- _sort_with_vjp backward (moe_dispatch.py:33-38)
+ *   mtx_invert_permutation <- jnp.argsort(sort_indices) (moe_dispatch.py:102)
+ *   mtx_unroute            <- unroute (moe_dispatch.py:84-111); with topk_w == NULL it is
+ *                             the route VJP (sum over the K copies, moe_dispatch.py:33-38,67)
+ *   mtx_unroute_bwd        <- VJP of unroute (_sort_bwd gather + einsum transpose,
+ *                             moe_dispatch.py:33-38,102-111)
+ *   mtx_gmm                <- grouped_matmul / _gmm_ragged_dot / _gmm_vjp_fwd
+ *                             (mintext/kernels/grouped_matmul.py:58-76,128-148,242-277)
+ *   mtx_gmm_swiglu         <- ragged_dot + split + silu*up
+ *                             (grouped_matmul.py:143-147; mintext/modules/moe.py:189-196)
+ *   mtx_gmm_dlhs           <- _gmm_vjp_bwd dlhs (grouped_matmul.py:162-176)
+ *   mtx_tgmm               <- tgmm (grouped_matmul.py:197-235)
+ *   mtx_swiglu             <- split + silu*up (mintext/modules/moe.py:195-196)
+ *   mtx_swiglu_bwd         <- its autodiff VJP (taken by jax.grad through moe.py:195-196)
+ *   mtx_quant_fp8_rows     <- no counterpart (per-tensor analogue: _fp8_matmul,
+ *                             mintext/modules/linear.py:37-57); 1x128 activation groups
+ *   mtx_quant_fp8_weights  <- no counterpart; 128x128 weight blocks
+ *   mtx_gmm_fp8            <- no counterpart; blockwise-fp8 form of mtx_gmm
+ *   mtx_gmm_fp8_swiglu     <- no counterpart; blockwise-fp8 form of mtx_gmm_swiglu
+ */
+#ifndef MINTEXT_MOE_H
+#define MINTEXT_MOE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------------------- */
+#define MTX_OK               0
+#define MTX_ERR_ARG         -1   /* invalid shape, dtype or argument combination      */
+#define MTX_ERR_WORKSPACE   -2   /* workspace missing or smaller than required        */
+#define MTX_ERR_UNSUPPORTED -3   /* valid request that this build does not implement  */
+#define MTX_ERR_HIP         -4   /* a HIP runtime call failed (see mtx_last_hip_error) */
+
+/* ---- dtype codes ------------------------------------------------------------------ */
+#define MTX_F32      0
+#define MTX_BF16     1
+#define MTX_FP8E4M3  2   /* OCP float8_e4m3fn (max 448), as jnp.float8_e4m3fn      */
+
+/* ---- router scoring modes ---------------------------------------------------------- */
+#define MTX_SCORING_SOFTMAX       0  /* top-k on logits, softmax renormalised over top-k */
+#define MTX_SCORING_SIGMOID_GROUP 1  /* sigmoid + bias, group-limited top-k (DeepSeek-V3) */
+
+const char* mtx_status_string(int status);
+int         mtx_last_hip_error(void);
+/* Library version / capability word; bit 0 = gfx950 code object present. */
+int         mtx_version(void);
+
+/* ---- router top-k ------------------------------------------------------------------
+ * logits [T,E] (F32 or BF16) -> topk_idx [T,K] int32 (descending by selection value,
+ * ties to the lower expert index), topk_w [T,K] float32, scores [T,E] float32 (may be
+ * NULL; sigmoid scores in SIGMOID_GROUP mode, softmax probabilities in SOFTMAX mode).
+ * SOFTMAX: selection on the logits; w = exp(l-lmax)/sum_topk exp(l-lmax) when
+ *   norm_topk_prob, else the full-softmax probability; then * routed_scaling_factor.
+ * SIGMOID_GROUP: s = sigmoid(l); r = s + bias (bias may be NULL = zeros); group score =
+ *   sum of the top-2 r in each of n_group groups; keep topk_group groups; top-K of r in
+ *   the kept groups; w = s[idx]; if norm_topk_prob w /= (sum w + 1e-20); w *= scale.
+ * Limits: 1 <= K <= min(E, 64), E <= 1024, E % n_group == 0.                          */
+int mtx_router_topk(const void* logits, int logits_dtype, int64_t T, int64_t E, int64_t K,
+                    int scoring, const float* bias, int64_t n_group, int64_t topk_group,
+                    int norm_topk_prob, float routed_scaling_factor,
+                    int32_t* topk_idx, float* topk_w, float* scores, void* stream);
+
+/* ---- route (dispatch) ------------------------------------------------------------------
+ * tokens [N,D] (F32/BF16/FP8E4M3), topk_idx [N,K] -> sorted_tokens [N*K,D] (same dtype),
+ * sort_indices [N*K] (stable argsort of ravel(topk_idx): value = flat position n*K+k),
+ * group_sizes [E], and optionally inverse [N*K] (inverse[sort_indices[j]] = j; may be NULL).
+ * tokens / sorted_tokens may both be NULL to compute only the permutation.
+ * token_scales [N,D/128] f32 (may be NULL) are gathered alongside into sorted_scales.
+ * Expert ids outside [0,E) are sorted after every valid id and not counted.          */
+int64_t mtx_route_workspace_size(int64_t N, int64_t K, int64_t E);
+int mtx_route(const void* tokens, int dtype, const int32_t* topk_idx,
+              int64_t N, int64_t D, int64_t K, int64_t E,
+              void* sorted_tokens, int32_t* sort_indices, int32_t* group_sizes,
+              int32_t* inverse, const float* token_scales, float* sorted_scales,
+              void* workspace, int64_t workspace_bytes, void* stream);
+
+/* out[j,:] = src[index[j] / div, :]  for j < rows (gather; rows with index outside
+ * [0, src_rows*div) are zero-filled).  dtype F32/BF16/FP8E4M3.                         */
+int mtx_gather_rows(const void* src, int dtype, int64_t src_rows, int64_t D,
+                    const int32_t* index, int64_t rows, int64_t div, void* out, void* stream);
+
+/* out[index[j],:] = src[j,:]  for j < rows (inverse of a permutation gather).          */
+int mtx_scatter_rows(const void* src, int dtype, int64_t rows, int64_t D,
+                     const int32_t* index, void* out, void* stream);
+
+/* inverse[perm[j]] = j for j < M (entries of perm outside [0,M) are ignored).         */
+int mtx_invert_permutation(const int32_t* perm, int64_t M, int32_t* inverse, void* stream);
+
+/* ---- unroute (combine) -------------------------------------------------------------
+ * sorted_output [N*K,D] (F32/BF16), inverse [N*K] (from mtx_route or
+ * mtx_invert_permutation), topk_w [N,K] (F32/BF16, or NULL = all ones) -> out [N,D]
+ * (out_dtype F32/BF16): out[n,:] = sum_k w[n,k] * sorted_output[inverse[n*K+k], :],
+ * k ascending, f32 math.                                                              */
+int mtx_unroute(const void* sorted_output, int y_dtype, const int32_t* inverse,
+                const void* topk_w, int w_dtype, int64_t N, int64_t K, int64_t D,
+                void* out, int out_dtype, void* stream);
+/* VJP of mtx_unroute: d_sorted[inverse[n*K+k],:] = w[n,k] * dout[n,:]  (dtype y_dtype),
+ * d_w[n,k] = sum_d dout[n,d] * sorted_output[inverse[n*K+k],d]  (dtype w_dtype; may be NULL). */
+int mtx_unroute_bwd(const void* dout, int g_dtype, const void* sorted_output, int y_dtype,
+                    const int32_t* inverse, const void* topk_w, int w_dtype, int64_t N, int64_t K,
+                    int64_t D, void* d_sorted, void* d_w, void* stream);
+
+/* ---- grouped GEMM ----------------------------------------------------------------------
+ * Rows of x are grouped contiguously in group_sizes order (a device array that is never
+ * read on the host).  Rows past sum(group_sizes) produce zeros.  F32 (exact fp32 FMA) or
+ * BF16 (MFMA, f32 accumulate, one rounding).  Output dtype = input dtype.              */
+int64_t mtx_gmm_workspace_size(int64_t M, int64_t E);
+/* out[r,:] = x[r,:] @ w[g(r)]       x [M,Kin], w [E,Kin,Kout] -> out [M,Kout]          */
+int mtx_gmm(const void* x, const void* w, const int32_t* group_sizes, int dtype,
+            int64_t M, int64_t Kin, int64_t Kout, int64_t E, void* out,
+            void* workspace, int64_t workspace_bytes, void* stream);
+/* h = x @ w[g] (w [E,Kin,2I], gate = first I columns); out = silu(gate) * up  [M,I]   */
+int mtx_gmm_swiglu(const void* x, const void* w, const int32_t* group_sizes, int dtype,
+                   int64_t M, int64_t Kin, int64_t I, int64_t E, void* out,
+                   void* workspace, int64_t workspace_bytes, void* stream);
+/* dx[r,:] = g[r,:] @ w[g(r)]^T      g [M,Kout], w [E,Kin,Kout] -> dx [M,Kin]           */
+int mtx_gmm_dlhs(const void* g, const void* w, const int32_t* group_sizes, int dtype,
+                 int64_t M, int64_t Kin, int64_t Kout, int64_t E, void* dx,
+                 void* workspace, int64_t workspace_bytes, void* stream);
+/* dw[e] = x[rows_e]^T @ g[rows_e]   x [M,K], g [M,N] -> dw [E,K,N]; empty group -> 0  */
+int mtx_tgmm(const void* x, const void* g, const int32_t* group_sizes, int dtype,
+             int64_t M, int64_t K, int64_t N, int64_t E, void* dw,
+             void* workspace, int64_t workspace_bytes, void* stream);
+/* out[r,j] = silu(h[r,j]) * h[r,I+j]   h [M,2I] -> out [M,I] (F32/BF16)                */
+int mtx_swiglu(const void* h, int dtype, int64_t M, int64_t I, void* out, void* stream);
+/* VJP of mtx_swiglu: dh [M,2I] from h [M,2I] and dy [M,I]                              */
+int mtx_swiglu_bwd(const void* h, const void* dy, int dtype, int64_t M, int64_t I, void* dh, void* stream);
+
+/* ---- fp8 e4m3fn blockwise ----------------------------------------------------------------
+ * Activations: 1x128 groups along the row, scale = amax/448 (1 when amax == 0),
+ * q = RNE(x / scale).  Weights: 128x128 blocks over (Kout, Kin), stored k-contiguous
+ * w_q [E,Kout,Kin] with w_scale [E,Kout/128,Kin/128] (the per-expert nn.Linear layout).
+ * Kin, Kout (and I) must be multiples of 128.                                           */
+int mtx_quant_fp8_rows(const void* x, int dtype, int64_t M, int64_t D,
+                       uint8_t* xq, float* x_scale, void* stream);
+/* w [E,Kin,Kout] (F32/BF16, reference layout) -> w_q [E,Kout,Kin], w_scale [E,Kout/128,Kin/128] */
+int mtx_quant_fp8_weights(const void* w, int dtype, int64_t E, int64_t Kin, int64_t Kout,
+                          uint8_t* w_q, float* w_scale, void* stream);
+/* out [M,Kout] bf16 = sum_kb (xq*xs)(wq*ws) over 128-K blocks, f32 accumulate         */
+int mtx_gmm_fp8(const uint8_t* xq, const float* x_scale, const uint8_t* w_q,
+                const float* w_scale, const int32_t* group_sizes,
+                int64_t M, int64_t Kin, int64_t Kout, int64_t E, void* out,
+                void* workspace, int64_t workspace_bytes, void* stream);
+/* SwiGLU of the fp8 gate_up GEMM (w_q [E,2I,Kin]) fused with 1x128 re-quantisation:
+ * out_q [M,I] e4m3fn + out_scale [M,I/128]; out_bf16 [M,I] optional (may be NULL).    */
+int mtx_gmm_fp8_swiglu(const uint8_t* xq, const float* x_scale, const uint8_t* w_q,
+                       const float* w_scale, const int32_t* group_sizes,
+                       int64_t M, int64_t Kin, int64_t I, int64_t E,
+                       uint8_t* out_q, float* out_scale, void* out_bf16,
+                       void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MINTEXT_MOE_H */

@@ -1,0 +1,476 @@
+// Token dispatch (route) and combine (unroute) for the MoE layer on gfx950.
+//
+// route (bzantium/mintext mintext/kernels/moe_dispatch.py:47-81) is a stable argsort of
+// ravel(topk_indices) by expert id, a row gather x[p // K] in that order and a bincount.
+// Here the argsort is a stable counting sort, with no comparison sort and no atomics in
+// the ranking:
+//   1. route_count   : one workgroup per chunk of the flat index array builds an LDS
+//                      histogram over E+1 buckets (bucket E = ids outside [0,E)).
+//   2. route_scan    : one workgroup turns the [chunk][bucket] counts into exclusive
+//                      offsets (bucket-major, then chunk) and writes group_sizes.
+//   3. route_scatter : each chunk ranks its elements in flat order; within a wave the
+//                      rank is a ballot "multisplit" (log2(E+1) ballots build the mask of
+//                      lanes with an equal key, rank = popcount of the lower lanes), across
+//                      waves per-wave counts in LDS, across sub-tiles a running LDS base.
+//   4. gather_rows   : one wave per output row, 16-byte vector copies.
+// unroute (moe_dispatch.py:84-111) inverts the permutation (scatter of j to perm[j]) and
+// combines out[n] = sum_k w[n,k] * Y[inv[n*K+k]] in f32 with k ascending, one wave per token.
+#include "common.h"
+
+namespace mtx {
+
+int g_last_hip_error = 0;
+
+static constexpr int kRouteThreads = 256;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+
+struct RoutePlan {
+  int64_t M;
+  int nb;      // number of buckets = E + 1
+  int nchunks;
+  int64_t chunk;
+  int64_t ws_counts;  // bytes
+};
+
+static RoutePlan route_plan(int64_t N, int64_t K, int64_t E) {
+  RoutePlan p;
+  p.M = N * K;
+  p.nb = (int)E + 1;
+  int64_t nch = ceil_div(p.M, 1024);
+  if (nch < 1) nch = 1;
+  if (nch > 256) nch = 256;
+  p.nchunks = (int)nch;
+  p.chunk = round_up(ceil_div(p.M > 0 ? p.M : 1, nch), kRouteThreads);
+  p.ws_counts = round_up((int64_t)p.nchunks * p.nb * 4, 256);
+  return p;
+}
+
+__device__ __forceinline__ int route_key(const int32_t* idx, int64_t p, int E) {
+  const int v = idx[p];
+  return (v < 0 || v >= E) ? E : v;
+}
+
+__global__ __launch_bounds__(kRouteThreads) void route_count_kernel(
+    const int32_t* __restrict__ idx, int64_t M, int E, int nb, int64_t chunk,
+    int32_t* __restrict__ counts) {
+  extern __shared__ int hist[];
+  for (int b = threadIdx.x; b < nb; b += blockDim.x) hist[b] = 0;
+  __syncthreads();
+  const int64_t start = (int64_t)blockIdx.x * chunk;
+  const int64_t end = min(start + chunk, M);
+  for (int64_t p = start + threadIdx.x; p < end; p += blockDim.x)
+    atomicAdd(&hist[route_key(idx, p, E)], 1);
+  __syncthreads();
+  for (int b = threadIdx.x; b < nb; b += blockDim.x)
+    counts[(int64_t)blockIdx.x * nb + b] = hist[b];
+}
+
+// Single workgroup of 1024 threads; nb <= 1024.
+__global__ __launch_bounds__(1024) void route_scan_kernel(
+    int32_t* __restrict__ counts, int nchunks, int nb, int E, int32_t* __restrict__ group_sizes) {
+  __shared__ int wsum[16];
+  const int b = threadIdx.x;
+  int sum = 0;
+  if (b < nb)
+    for (int c = 0; c < nchunks; ++c) sum += counts[(int64_t)c * nb + b];
+  // block-wide exclusive scan of sum over b (wave scan + scan of wave totals)
+  const int lane = b & 63, w = b >> 6;
+  int incl = sum;
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  if (b == 0) {
+    int run = 0;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) { const int x = wsum[i]; wsum[i] = run; run += x; }
+  }
+  __syncthreads();
+  const int excl = incl - sum + wsum[w];
+  if (b < nb) {
+    int base = excl;
+    for (int c = 0; c < nchunks; ++c) {
+      const int64_t o = (int64_t)c * nb + b;
+      const int x = counts[o];
+      counts[o] = base;
+      base += x;
+    }
+    if (b < E) group_sizes[b] = sum;
+  }
+}
+
+__global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
+    const int32_t* __restrict__ idx, int64_t M, int E, int nb, int nbits, int64_t chunk,
+    const int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ inv) {
+  extern __shared__ int sh[];
+  int* run = sh;            // [nb]
+  int* wcnt = sh + nb;      // [4][nb]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int b = tid; b < nb; b += blockDim.x) run[b] = offsets[(int64_t)blockIdx.x * nb + b];
+  const int64_t start = (int64_t)blockIdx.x * chunk;
+  const int64_t end = min(start + chunk, M);
+  const unsigned long long lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
+  for (int64_t base = start; base < end; base += kRouteThreads) {
+    for (int b = tid; b < 4 * nb; b += blockDim.x) wcnt[b] = 0;
+    __syncthreads();
+    const int64_t p = base + tid;
+    const bool valid = p < end;
+    const int key = valid ? route_key(idx, p, E) : 0;
+    unsigned long long m = __ballot(valid);
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool on = (key >> bit) & 1;
+      const unsigned long long bb = __ballot(on);
+      m &= on ? bb : ~bb;
+    }
+    const int rank = __popcll(m & lt);
+    const int cnt = __popcll(m);
+    if (valid && rank == 0) wcnt[w * nb + key] = cnt;
+    __syncthreads();
+    if (valid) {
+      int pos = run[key] + rank;
+      for (int ww = 0; ww < w; ++ww) pos += wcnt[ww * nb + key];
+      perm[pos] = (int32_t)p;
+      if (inv) inv[p] = pos;
+    }
+    __syncthreads();
+    if (valid && rank == 0) atomicAdd(&run[key], cnt);
+    __syncthreads();
+  }
+}
+
+// out[j] = src[index[j] / div] for rows of `row_bytes` bytes; VT is the copy unit.
+template <typename VT>
+__global__ __launch_bounds__(256) void gather_rows_kernel(
+    const char* __restrict__ src, int64_t src_rows, int64_t row_bytes,
+    const int32_t* __restrict__ index, int64_t rows, int64_t div, char* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nvec = row_bytes / (int64_t)sizeof(VT);
+  const int64_t wave_id = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t j = wave_id; j < rows; j += nwaves) {
+    const int64_t p = index[j];
+    const int64_t r = (p >= 0) ? p / div : -1;
+    VT* o = (VT*)(out + j * row_bytes);
+    if (r < 0 || r >= src_rows) {
+      VT z;
+      memset(&z, 0, sizeof(VT));
+      for (int64_t c = lane; c < nvec; c += 64) o[c] = z;
+      continue;
+    }
+    const VT* s = (const VT*)(src + r * row_bytes);
+    int64_t c = lane;
+    for (; c + 192 < nvec; c += 256) {
+      const VT a0 = s[c], a1 = s[c + 64], a2 = s[c + 128], a3 = s[c + 192];
+      o[c] = a0; o[c + 64] = a1; o[c + 128] = a2; o[c + 192] = a3;
+    }
+    for (; c < nvec; c += 64) o[c] = s[c];
+  }
+}
+
+// out[index[j]] = src[j]
+template <typename VT>
+__global__ __launch_bounds__(256) void scatter_rows_kernel(
+    const char* __restrict__ src, int64_t rows, int64_t row_bytes,
+    const int32_t* __restrict__ index, char* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nvec = row_bytes / (int64_t)sizeof(VT);
+  const int64_t wave_id = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t j = wave_id; j < rows; j += nwaves) {
+    const int64_t d = index[j];
+    if (d < 0 || d >= rows) continue;
+    const VT* s = (const VT*)(src + j * row_bytes);
+    VT* o = (VT*)(out + d * row_bytes);
+    for (int64_t c = lane; c < nvec; c += 64) o[c] = s[c];
+  }
+}
+
+__global__ void invert_perm_kernel(const int32_t* __restrict__ perm, int64_t M, int32_t* __restrict__ inv) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j < M) {
+    const int64_t p = perm[j];
+    if (p >= 0 && p < M) inv[p] = (int32_t)j;
+  }
+}
+
+static int launch_gather(const void* src, int64_t src_rows, int64_t row_bytes, const int32_t* index,
+                         int64_t rows, int64_t div, void* out, hipStream_t st) {
+  if (rows == 0 || row_bytes == 0) return MTX_OK;
+  const int64_t waves = rows;
+  int64_t blocks = ceil_div(waves, 4);
+  if (blocks > 65536) blocks = 65536;
+  const bool a16 = (row_bytes % 16 == 0) && ((uintptr_t)src % 16 == 0) && ((uintptr_t)out % 16 == 0);
+  const bool a4 = (row_bytes % 4 == 0) && ((uintptr_t)src % 4 == 0) && ((uintptr_t)out % 4 == 0);
+  if (a16)
+    hipLaunchKernelGGL(gather_rows_kernel<u32x4>, dim3(blocks), dim3(256), 0, st, (const char*)src,
+                       src_rows, row_bytes, index, rows, div, (char*)out);
+  else if (a4)
+    hipLaunchKernelGGL(gather_rows_kernel<uint32_t>, dim3(blocks), dim3(256), 0, st, (const char*)src,
+                       src_rows, row_bytes, index, rows, div, (char*)out);
+  else
+    hipLaunchKernelGGL(gather_rows_kernel<uint8_t>, dim3(blocks), dim3(256), 0, st, (const char*)src,
+                       src_rows, row_bytes, index, rows, div, (char*)out);
+  return check_launch();
+}
+
+// ---- unroute -------------------------------------------------------------------------------
+template <typename T> __device__ __forceinline__ float ldf(const T* p, int64_t i);
+template <> __device__ __forceinline__ float ldf<float>(const float* p, int64_t i) { return p[i]; }
+template <> __device__ __forceinline__ float ldf<uint16_t>(const uint16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
+template <typename T> __device__ __forceinline__ void stf(T* p, int64_t i, float v);
+template <> __device__ __forceinline__ void stf<float>(float* p, int64_t i, float v) { p[i] = v; }
+template <> __device__ __forceinline__ void stf<uint16_t>(uint16_t* p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+
+// Load 8 consecutive elements as floats (aligned 16B / 32B vector loads).
+__device__ __forceinline__ void load8(const float* p, float* o) {
+  const float4 a = ((const float4*)p)[0], b = ((const float4*)p)[1];
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+__device__ __forceinline__ void load8(const uint16_t* p, float* o) {
+  const uint4 a = *(const uint4*)p;
+  const uint32_t u[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = __uint_as_float(u[i] << 16);
+    o[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void store8(float* p, const float* v) {
+  ((float4*)p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+  ((float4*)p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+__device__ __forceinline__ void store8(uint16_t* p, const float* v) {
+  *(uint4*)p = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                          pack_bf16x2(v[6], v[7]));
+}
+
+// One wave per token; VEC8 = D % 8 == 0 and aligned pointers.
+template <typename YT, typename WT, typename OT, bool VEC8>
+__global__ __launch_bounds__(256) void unroute_kernel(
+    const YT* __restrict__ Y, const int32_t* __restrict__ inv, const WT* __restrict__ w,
+    int64_t N, int K, int64_t D, OT* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  if (n >= N) return;
+  const int64_t M = N * (int64_t)K;
+  if (VEC8) {
+    for (int64_t d = (int64_t)lane * 8; d < D; d += 512) {
+      float acc[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+      for (int k = 0; k < K; ++k) {
+        const int64_t j = inv[n * K + k];
+        const float wk = w ? ldf<WT>(w, n * K + k) : 1.0f;
+        if (j < 0 || j >= M) continue;
+        float y[8];
+        load8(Y + j * D + d, y);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = fmaf(wk, y[i], acc[i]);
+      }
+      store8(out + n * D + d, acc);
+    }
+  } else {
+    for (int64_t d = lane; d < D; d += 64) {
+      float acc = 0.0f;
+      for (int k = 0; k < K; ++k) {
+        const int64_t j = inv[n * K + k];
+        const float wk = w ? ldf<WT>(w, n * K + k) : 1.0f;
+        if (j < 0 || j >= M) continue;
+        acc = fmaf(wk, ldf<YT>(Y, j * D + d), acc);
+      }
+      stf<OT>(out, n * D + d, acc);
+    }
+  }
+}
+
+template <typename YT, typename WT, typename OT>
+static void launch_unroute_t(const void* Y, const int32_t* inv, const void* w, int64_t N, int K,
+                             int64_t D, void* out, hipStream_t st) {
+  const int64_t blocks = ceil_div(N, 4);
+  const bool v8 = (D % 8 == 0) && ((uintptr_t)Y % 16 == 0) && ((uintptr_t)out % 16 == 0);
+  if (v8)
+    hipLaunchKernelGGL((unroute_kernel<YT, WT, OT, true>), dim3(blocks), dim3(256), 0, st,
+                       (const YT*)Y, inv, (const WT*)w, N, K, D, (OT*)out);
+  else
+    hipLaunchKernelGGL((unroute_kernel<YT, WT, OT, false>), dim3(blocks), dim3(256), 0, st,
+                       (const YT*)Y, inv, (const WT*)w, N, K, D, (OT*)out);
+}
+
+// unroute backward, one wave per token n (reference VJP of moe_dispatch.py:102-111):
+//   dY[inv[n*K+k], :] = w[n,k] * dout[n, :]
+//   dw[n,k]          = sum_d dout[n,d] * Y[inv[n*K+k], d]      (f32 math)
+template <typename GT, typename YT, typename WT>
+__global__ __launch_bounds__(256) void unroute_bwd_kernel(
+    const GT* __restrict__ dout, const YT* __restrict__ Y, const int32_t* __restrict__ inv,
+    const WT* __restrict__ w, int64_t N, int K, int64_t D, YT* __restrict__ dY, WT* __restrict__ dw) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  if (n >= N) return;
+  const int64_t M = N * (int64_t)K;
+  for (int k = 0; k < K; ++k) {
+    const int64_t j = inv[n * K + k];
+    if (j < 0 || j >= M) continue;
+    const float wk = ldf<WT>(w, n * K + k);
+    float dot = 0.0f;
+    for (int64_t d = lane; d < D; d += 64) {
+      const float g = ldf<GT>(dout, n * D + d);
+      dot = fmaf(g, ldf<YT>(Y, j * D + d), dot);
+      stf<YT>(dY, j * D + d, wk * g);
+    }
+    if (dw) {
+      for (int off = 32; off > 0; off >>= 1) dot += __shfl_xor(dot, off);
+      if (lane == 0) stf<WT>(dw, n * K + k, dot);
+    }
+  }
+}
+
+}  // namespace mtx
+
+using namespace mtx;
+
+extern "C" const char* mtx_status_string(int s) {
+  switch (s) {
+    case MTX_OK: return "ok";
+    case MTX_ERR_ARG: return "invalid argument (shape, dtype or combination)";
+    case MTX_ERR_WORKSPACE: return "workspace missing or too small";
+    case MTX_ERR_UNSUPPORTED: return "unsupported configuration";
+    case MTX_ERR_HIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+extern "C" int mtx_last_hip_error(void) { return g_last_hip_error; }
+extern "C" int mtx_version(void) { return 1; }
+
+extern "C" int64_t mtx_route_workspace_size(int64_t N, int64_t K, int64_t E) {
+  if (N < 0 || K < 1 || E < 1) return -1;
+  return route_plan(N, K, E).ws_counts;
+}
+
+extern "C" int mtx_route(const void* tokens, int dtype, const int32_t* topk_idx,
+                         int64_t N, int64_t D, int64_t K, int64_t E,
+                         void* sorted_tokens, int32_t* sort_indices, int32_t* group_sizes,
+                         int32_t* inverse, const float* token_scales, float* sorted_scales,
+                         void* workspace, int64_t workspace_bytes, void* stream) {
+  if (N < 0 || D < 0 || K < 1 || E < 1 || E > 1023) return MTX_ERR_ARG;
+  if (dtype_size(dtype) == 0) return MTX_ERR_ARG;
+  if ((tokens == nullptr) != (sorted_tokens == nullptr)) return MTX_ERR_ARG;
+  if ((token_scales == nullptr) != (sorted_scales == nullptr)) return MTX_ERR_ARG;
+  if (token_scales && D % 128 != 0) return MTX_ERR_ARG;
+  if (N * K > INT32_MAX) return MTX_ERR_ARG;
+  if (!sort_indices || !group_sizes) return MTX_ERR_ARG;
+  const RoutePlan p = route_plan(N, K, E);
+  if (!workspace || workspace_bytes < p.ws_counts) return MTX_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  int32_t* counts = (int32_t*)workspace;
+  const size_t hist_shm = (size_t)p.nb * sizeof(int);
+  hipLaunchKernelGGL(route_count_kernel, dim3(p.nchunks), dim3(kRouteThreads), hist_shm, st,
+                     topk_idx, p.M, (int)E, p.nb, p.chunk, counts);
+  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(1024), 0, st, counts, p.nchunks, p.nb, (int)E,
+                     group_sizes);
+  int nbits = 0;
+  while ((1 << nbits) < p.nb) ++nbits;
+  const size_t sc_shm = (size_t)5 * p.nb * sizeof(int);
+  if (p.M > 0)
+    hipLaunchKernelGGL(route_scatter_kernel, dim3(p.nchunks), dim3(kRouteThreads), sc_shm, st, topk_idx,
+                       p.M, (int)E, p.nb, nbits, p.chunk, counts, sort_indices, inverse);
+  int rc = check_launch();
+  if (rc != MTX_OK) return rc;
+  if (tokens) {
+    rc = launch_gather(tokens, N, D * dtype_size(dtype), sort_indices, p.M, K, sorted_tokens, st);
+    if (rc != MTX_OK) return rc;
+  }
+  if (token_scales) {
+    rc = launch_gather(token_scales, N, (D / 128) * 4, sort_indices, p.M, K, sorted_scales, st);
+    if (rc != MTX_OK) return rc;
+  }
+  return MTX_OK;
+}
+
+extern "C" int mtx_gather_rows(const void* src, int dtype, int64_t src_rows, int64_t D,
+                               const int32_t* index, int64_t rows, int64_t div, void* out, void* stream) {
+  if (src_rows < 0 || D < 0 || rows < 0 || div < 1 || dtype_size(dtype) == 0) return MTX_ERR_ARG;
+  if (rows > 0 && (!src || !index || !out)) return MTX_ERR_ARG;
+  return launch_gather(src, src_rows, D * dtype_size(dtype), index, rows, div, out, (hipStream_t)stream);
+}
+
+extern "C" int mtx_scatter_rows(const void* src, int dtype, int64_t rows, int64_t D,
+                                const int32_t* index, void* out, void* stream) {
+  if (rows < 0 || D < 0 || dtype_size(dtype) == 0) return MTX_ERR_ARG;
+  if (rows == 0 || D == 0) return MTX_OK;
+  if (!src || !index || !out) return MTX_ERR_ARG;
+  const int64_t rb = D * dtype_size(dtype);
+  int64_t blocks = ceil_div(rows, 4);
+  if (blocks > 65536) blocks = 65536;
+  hipStream_t st = (hipStream_t)stream;
+  const bool a16 = (rb % 16 == 0) && ((uintptr_t)src % 16 == 0) && ((uintptr_t)out % 16 == 0);
+  const bool a4 = (rb % 4 == 0) && ((uintptr_t)src % 4 == 0) && ((uintptr_t)out % 4 == 0);
+  if (a16)
+    hipLaunchKernelGGL(scatter_rows_kernel<u32x4>, dim3(blocks), dim3(256), 0, st, (const char*)src, rows, rb,
+                       index, (char*)out);
+  else if (a4)
+    hipLaunchKernelGGL(scatter_rows_kernel<uint32_t>, dim3(blocks), dim3(256), 0, st, (const char*)src, rows,
+                       rb, index, (char*)out);
+  else
+    hipLaunchKernelGGL(scatter_rows_kernel<uint8_t>, dim3(blocks), dim3(256), 0, st, (const char*)src, rows,
+                       rb, index, (char*)out);
+  return check_launch();
+}
+
+extern "C" int mtx_invert_permutation(const int32_t* perm, int64_t M, int32_t* inverse, void* stream) {
+  if (M < 0 || M > INT32_MAX) return MTX_ERR_ARG;
+  if (M == 0) return MTX_OK;
+  if (!perm || !inverse) return MTX_ERR_ARG;
+  hipLaunchKernelGGL(invert_perm_kernel, dim3(ceil_div(M, 256)), dim3(256), 0, (hipStream_t)stream, perm, M,
+                     inverse);
+  return check_launch();
+}
+
+extern "C" int mtx_unroute(const void* sorted_output, int y_dtype, const int32_t* inverse,
+                           const void* topk_w, int w_dtype, int64_t N, int64_t K, int64_t D,
+                           void* out, int out_dtype, void* stream) {
+  if (N < 0 || K < 1 || K > 1024 || D < 0) return MTX_ERR_ARG;
+  if ((y_dtype != MTX_F32 && y_dtype != MTX_BF16) || (w_dtype != MTX_F32 && w_dtype != MTX_BF16) ||
+      (out_dtype != MTX_F32 && out_dtype != MTX_BF16))
+    return MTX_ERR_ARG;
+  if (N == 0 || D == 0) return MTX_OK;
+  if (!sorted_output || !inverse || !out) return MTX_ERR_ARG;  // topk_w == NULL: unit weights
+  hipStream_t st = (hipStream_t)stream;
+  const int k = (int)K;
+#define MTX_UNR(YT, WT, OT) launch_unroute_t<YT, WT, OT>(sorted_output, inverse, topk_w, N, k, D, out, st)
+  if (y_dtype == MTX_BF16) {
+    if (w_dtype == MTX_F32) { if (out_dtype == MTX_F32) MTX_UNR(uint16_t, float, float); else MTX_UNR(uint16_t, float, uint16_t); }
+    else { if (out_dtype == MTX_F32) MTX_UNR(uint16_t, uint16_t, float); else MTX_UNR(uint16_t, uint16_t, uint16_t); }
+  } else {
+    if (w_dtype == MTX_F32) { if (out_dtype == MTX_F32) MTX_UNR(float, float, float); else MTX_UNR(float, float, uint16_t); }
+    else { if (out_dtype == MTX_F32) MTX_UNR(float, uint16_t, float); else MTX_UNR(float, uint16_t, uint16_t); }
+  }
+#undef MTX_UNR
+  return check_launch();
+}
+
+extern "C" int mtx_unroute_bwd(const void* dout, int g_dtype, const void* sorted_output, int y_dtype,
+                               const int32_t* inverse, const void* topk_w, int w_dtype, int64_t N, int64_t K,
+                               int64_t D, void* d_sorted, void* d_w, void* stream) {
+  if (N < 0 || K < 1 || D < 0) return MTX_ERR_ARG;
+  if ((g_dtype != MTX_F32 && g_dtype != MTX_BF16) || (y_dtype != MTX_F32 && y_dtype != MTX_BF16) ||
+      (w_dtype != MTX_F32 && w_dtype != MTX_BF16))
+    return MTX_ERR_ARG;
+  if (N == 0) return MTX_OK;
+  if (!dout || !sorted_output || !inverse || !topk_w || !d_sorted) return MTX_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t blocks = ceil_div(N, 4);
+  const int k = (int)K;
+#define MTX_UB(GT, YT, WT)                                                                                   \
+  hipLaunchKernelGGL((unroute_bwd_kernel<GT, YT, WT>), dim3(blocks), dim3(256), 0, st, (const GT*)dout,     \
+                     (const YT*)sorted_output, inverse, (const WT*)topk_w, N, k, D, (YT*)d_sorted, (WT*)d_w)
+  if (g_dtype == MTX_F32) {
+    if (y_dtype == MTX_F32) { if (w_dtype == MTX_F32) MTX_UB(float, float, float); else MTX_UB(float, float, uint16_t); }
+    else { if (w_dtype == MTX_F32) MTX_UB(float, uint16_t, float); else MTX_UB(float, uint16_t, uint16_t); }
+  } else {
+    if (y_dtype == MTX_F32) { if (w_dtype == MTX_F32) MTX_UB(uint16_t, float, float); else MTX_UB(uint16_t, float, uint16_t); }
+    else { if (w_dtype == MTX_F32) MTX_UB(uint16_t, uint16_t, float); else MTX_UB(uint16_t, uint16_t, uint16_t); }
+  }
+#undef MTX_UB
+  return check_launch();
+}

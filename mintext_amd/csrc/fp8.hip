@@ -1,0 +1,524 @@
+// Blockwise fp8 (OCP e4m3fn) grouped GEMM for the MoE layer on gfx950.
+//
+// The reference has no fp8 grouped GEMM (its only fp8 code is per-tensor scaling of a dense
+// Linear, bzantium/mintext mintext/modules/linear.py:37-57).  Format used here (DeepSeek-V3
+// style blockwise scaling):
+//   activations  x ~ xq * xs : xq [M,K] e4m3fn, xs [M,K/128] f32 (1x128 groups per row)
+//   weights      W ~ wq * ws : wq [E,N,K] e4m3fn (k-contiguous, the per-expert nn.Linear
+//                              layout), ws [E,N/128,K/128] f32 (128x128 blocks)
+//   scale = amax / 448 (1 when amax == 0), q = RNE(x / scale) saturating at +-448.
+//   out[r,n] = sum_kb xs[r,kb] * ws[e,n/128,kb] * sum_{k in kb} xq[r,k] * wq[e,n,k]
+// with f32 accumulation (MFMA v_mfma_f32_32x32x64_f8f6f4, scales applied per 128-K block in
+// f32 on the partial sums) and a bf16 output, or -- for the gate_up GEMM -- the SwiGLU and
+// a 1x128 re-quantisation of its output fused into the epilogue.
+#include "common.h"
+
+namespace mtx {
+
+struct MTileF8 {
+  int e, r0, r1, pad;
+};
+
+namespace f8 {
+
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(8))) int i32x8;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+constexpr int BK = 128;  // bytes of k per step == one scale block
+
+__device__ __forceinline__ int lds_off(int r, int c) { return r * 128 + ((c ^ (r & 7) ^ ((r >> 3) & 7)) << 4); }
+
+// ---- quantisers ------------------------------------------------------------------------------
+// One wave per (row, 128-group): 2 elements per lane.
+template <typename T>
+__global__ __launch_bounds__(256) void quant_rows_kernel(const T* __restrict__ x, int64_t M, int64_t D,
+                                                         uint8_t* __restrict__ xq, float* __restrict__ xs) {
+  const int lane = threadIdx.x & 63;
+  const int64_t ng = D / 128;
+  const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t t = wid; t < M * ng; t += nw) {
+    const int64_t r = t / ng, g = t % ng;
+    const int64_t base = r * D + g * 128 + lane * 2;
+    float a, b;
+    if constexpr (sizeof(T) == 4) {
+      a = ((const float*)x)[base];
+      b = ((const float*)x)[base + 1];
+    } else {
+      const uint32_t u = *(const uint32_t*)((const uint16_t*)x + base);
+      a = __uint_as_float(u << 16);
+      b = __uint_as_float(u & 0xffff0000u);
+    }
+    float m = fmaxf(fabsf(a), fabsf(b));
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    float s = m / 448.0f;
+    if (s == 0.0f) s = 1.0f;
+    const uint16_t q = (uint16_t)f32_to_e4m3(a / s) | ((uint16_t)f32_to_e4m3(b / s) << 8);
+    *(uint16_t*)(xq + base) = q;
+    if (lane == 0) xs[r * ng + g] = s;
+  }
+}
+
+// One workgroup per 128x128 (Kin x Kout) block of one expert; writes the transposed block.
+template <typename T>
+__global__ __launch_bounds__(256) void quant_weights_kernel(const T* __restrict__ w, int64_t Kin, int64_t Kout,
+                                                            uint8_t* __restrict__ wq, float* __restrict__ ws) {
+  __shared__ float tile[128][129];
+  __shared__ float wmax[4];
+  const int e = blockIdx.z;
+  const int64_t k0 = (int64_t)blockIdx.y * 128, n0 = (int64_t)blockIdx.x * 128;
+  const T* src = w + (int64_t)e * Kin * Kout;
+  float m = 0.0f;
+  for (int i = threadIdx.x; i < 128 * 128; i += 256) {
+    const int kr = i / 128, nc = i % 128;
+    float v;
+    if constexpr (sizeof(T) == 4) v = ((const float*)src)[(k0 + kr) * Kout + n0 + nc];
+    else v = bf16_to_f32(((const uint16_t*)src)[(k0 + kr) * Kout + n0 + nc]);
+    tile[kr][nc] = v;
+    m = fmaxf(m, fabsf(v));
+  }
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  float s = m / 448.0f;
+  if (s == 0.0f) s = 1.0f;
+  uint8_t* dst = wq + (int64_t)e * Kout * Kin;
+  for (int i = threadIdx.x; i < 128 * 128; i += 256) {
+    const int nr = i / 128, kc = i % 128;
+    dst[(n0 + nr) * Kin + k0 + kc] = f32_to_e4m3(tile[kc][nr] / s);
+  }
+  if (threadIdx.x == 0) ws[((int64_t)e * (Kout / 128) + blockIdx.x) * (Kin / 128) + blockIdx.y] = s;
+}
+
+// ---- tile scheduler (same contract as the bf16 path) ---------------------------------------------
+__global__ __launch_bounds__(1024) void build_tiles_f8_kernel(const int32_t* __restrict__ gs, int E, int M, int BM,
+                                                              int* __restrict__ count, MTileF8* __restrict__ tiles) {
+  __shared__ int wsum[16];
+  __shared__ int s_total[2];
+  const int e = threadIdx.x, lane = e & 63, w = e >> 6;
+  const int g = (e < E) ? max(gs[e], 0) : 0;
+  int incl = g;
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  if (e == 0) {
+    int run = 0;
+    for (int i = 0; i < 16; ++i) { const int x = wsum[i]; wsum[i] = run; run += x; }
+    s_total[0] = run;
+  }
+  __syncthreads();
+  const int start = incl - g + wsum[w];
+  const int r0 = min(start, M), r1 = min(start + g, M);
+  const int nt = (r1 - r0 + BM - 1) / BM;
+  __syncthreads();
+  incl = nt;
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  if (e == 0) {
+    int run = 0;
+    for (int i = 0; i < 16; ++i) { const int x = wsum[i]; wsum[i] = run; run += x; }
+    s_total[1] = run;
+  }
+  __syncthreads();
+  const int tstart = incl - nt + wsum[w];
+  for (int i = 0; i < nt; ++i) {
+    MTileF8 t;
+    t.e = e;
+    t.r0 = r0 + i * BM;
+    t.r1 = min(r0 + (i + 1) * BM, r1);
+    t.pad = 0;
+    tiles[tstart + i] = t;
+  }
+  const int used = min(s_total[0], M);
+  const int ntail = (M - used + BM - 1) / BM;
+  if (e < ntail) {
+    MTileF8 t;
+    t.e = -1;
+    t.r0 = used + e * BM;
+    t.r1 = min(used + (e + 1) * BM, M);
+    t.pad = 0;
+    tiles[s_total[1] + e] = t;
+  }
+  if (e == 0) count[0] = s_total[1] + ntail;
+}
+
+// ---- GEMM --------------------------------------------------------------------------------------
+struct Args {
+  const uint8_t* xq;
+  const float* xs;
+  const uint8_t* wq;
+  const float* ws;
+  uint16_t* out;      // bf16 [M, ldc] (plain) / optional bf16 SwiGLU output
+  uint8_t* outq;      // SwiGLU: e4m3 [M, I]
+  float* outs;        // SwiGLU: [M, I/128]
+  const int* count;
+  const MTileF8* tiles;
+  int M, K, N, I, ldc;
+};
+
+enum { EPI_STORE = 0, EPI_SWIGLU_Q = 1 };
+
+template <int ROWS, int NT>
+struct RowLoader {  // ROWS rows x 128 bytes, 16-byte chunks
+  static constexpr int CPT = ROWS * 8 / NT;
+  static_assert((ROWS * 8) % NT == 0, "split");
+  u32x4 r[CPT];
+  template <typename RowMap>
+  __device__ __forceinline__ void load(const uint8_t* __restrict__ src, int64_t ld, RowMap rowmap, int k0, int tid) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int q = tid + i * NT;
+      r[i] = *(const u32x4*)(src + (int64_t)rowmap(q >> 3) * ld + k0 + (q & 7) * 16);
+    }
+  }
+  __device__ __forceinline__ void store(char* lds, int tid) const {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int q = tid + i * NT;
+      *(u32x4*)(lds + lds_off(q >> 3, q & 7)) = r[i];
+    }
+  }
+};
+
+template <int BM, int BN, int WM, int WN, int EPI>
+__global__ __launch_bounds__(WM* WN * 64, 1) void gmm_fp8_kernel(Args p) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  static_assert(WTN <= 128 && (128 % WTN == 0 || WTN == 128), "wave N-range within one 128-col scale block");
+  static_assert(EPI != EPI_SWIGLU_Q || (TN % 2 == 0 && WN == 2 && BN == 256), "SwiGLU layout");
+  constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128, S_BYTES = BM * 4;
+  constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+  __shared__ __attribute__((aligned(16))) char lds[2 * STAGE];
+  __shared__ float red[BM][2];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  const int nn = (EPI == EPI_SWIGLU_Q) ? (p.I / (BN / 2)) : (p.N / BN);
+  const int cnt = p.count[0];
+  const int total = cnt * nn;
+  const int pid = blockIdx.x;
+  const int total8 = (total + 7) & ~7;
+  if (pid >= total8) return;
+  const int lid = (pid & 7) * (total8 >> 3) + (pid >> 3);
+  if (lid >= total) return;
+  constexpr int GM = 8;
+  const int grp = lid / (GM * nn);
+  const int first_m = grp * GM;
+  const int gsz = min(GM, cnt - first_m);
+  const int local = lid - grp * GM * nn;
+  const int mt = first_m + local % gsz;
+  const int n_tile = local / gsz;
+  const MTileF8 t = p.tiles[mt];
+  const int e = t.e, r0 = t.r0, r1 = t.r1;
+  const int col0 = n_tile * BN;
+  if (e < 0) {
+    if (EPI == EPI_SWIGLU_Q) {
+      const int c0 = n_tile * (BN / 2);
+      for (int i = tid; i < BM * (BN / 2); i += NT) {
+        const int r = r0 + i / (BN / 2);
+        if (r < r1) {
+          p.outq[(int64_t)r * p.I + c0 + i % (BN / 2)] = 0;
+          if (p.out) p.out[(int64_t)r * p.I + c0 + i % (BN / 2)] = 0;
+        }
+      }
+      for (int i = tid; i < BM; i += NT)
+        if (r0 + i < r1) p.outs[(int64_t)(r0 + i) * (p.I / 128) + c0 / 128] = 1.0f;
+    } else {
+      for (int i = tid; i < BM * BN; i += NT) {
+        const int r = r0 + i / BN;
+        if (r < r1) p.out[(int64_t)r * p.ldc + col0 + i % BN] = 0;
+      }
+    }
+    return;
+  }
+  const int I = p.I;
+  // weight row (output column n) of tile-local column c
+  auto b_row = [=](int c) -> int {
+    if (EPI == EPI_SWIGLU_Q) {
+      const int w_ = c / WTN, within = c % WTN;
+      const int half = within / (WTN / 2), off = within % (WTN / 2);
+      return half * I + n_tile * (BN / 2) + w_ * (WTN / 2) + off;
+    }
+    return col0 + c;
+  };
+  const int Mlast = p.M - 1;
+  auto a_row = [=](int rr) -> int {
+    const int g = r0 + rr;
+    return g < Mlast ? g : Mlast;
+  };
+  const int nkb = p.K / BK;
+  const uint8_t* wsrc = p.wq + (int64_t)e * p.N * p.K;
+  const float* wsc = p.ws + (int64_t)e * (p.N / 128) * nkb;
+
+  RowLoader<BM, NT> la;
+  RowLoader<BN, NT> lb;
+  float sreg = 0.0f;  // one A-scale per thread (tid < BM)
+  auto issue = [&](int kb) {
+    la.load(p.xq, p.K, a_row, kb * BK, tid);
+    lb.load(wsrc, p.K, b_row, kb * BK, tid);
+    if (tid < BM) sreg = p.xs[(int64_t)a_row(tid) * nkb + kb];
+  };
+  auto stash = [&](char* st) {
+    la.store(st, tid);
+    lb.store(st + A_BYTES, tid);
+    if (tid < BM) ((float*)(st + A_BYTES + B_BYTES))[tid] = sreg;
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  // per-j weight-scale block row (constant over k)
+  int sb_row[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) sb_row[j] = b_row(wn * WTN + j * 32) / 128;
+
+  issue(0);
+  stash(lds);
+  __syncthreads();
+  const int frow = lane & 31, fhalf = lane >> 5;
+  for (int kb = 0; kb < nkb; ++kb) {
+    const char* As = lds + (kb & 1) * STAGE;
+    const char* Bs = As + A_BYTES;
+    const float* Ss = (const float*)(As + A_BYTES + B_BYTES);
+    const bool more = kb + 1 < nkb;
+    if (more) issue(kb + 1);
+    float sbv[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) sbv[j] = wsc[(int64_t)sb_row[j] * nkb + kb];
+    f32x16 part[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) part[i][j][v] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      i32x8 a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = wm * WTM + i * 32 + frow;
+        const u32x4 lo = *(const u32x4*)(As + lds_off(r, kk * 4 + fhalf * 2));
+        const u32x4 hi = *(const u32x4*)(As + lds_off(r, kk * 4 + fhalf * 2 + 1));
+        a[i] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int r = wn * WTN + j * 32 + frow;
+        const u32x4 lo = *(const u32x4*)(Bs + lds_off(r, kk * 4 + fhalf * 2));
+        const u32x4 hi = *(const u32x4*)(Bs + lds_off(r, kk * 4 + fhalf * 2 + 1));
+        b[j] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          part[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[i], b[j], part[i][j], 0, 0, 0, 127, 0, 127);
+    }
+    // promote: acc += part * xs[row] * ws[col block]
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 sa = *(const f32x4*)(Ss + wm * WTM + i * 32 + 8 * q + 4 * fhalf);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) acc[i][j][4 * q + u] = fmaf(part[i][j][4 * q + u], sa[u] * sbv[j], acc[i][j][4 * q + u]);
+      }
+    }
+    if (more) stash(lds + ((kb + 1) & 1) * STAGE);
+    __syncthreads();
+  }
+
+  const int ccol = lane & 31, rhalf = fhalf * 4;
+  if (EPI == EPI_STORE) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = r0 + wm * WTM + i * 32 + 8 * (v >> 2) + rhalf + (v & 3);
+          if (row < r1) p.out[(int64_t)row * p.ldc + col0 + wn * WTN + j * 32 + ccol] = f32_to_bf16(acc[i][j][v]);
+        }
+    return;
+  }
+  // SwiGLU + 1x128 quantisation: this tile holds y columns [n_tile*128, n_tile*128+128);
+  // wave wn holds 64 of them (j < TN/2 gate blocks, paired with up blocks j + TN/2).
+  float y[TM][TN / 2][16];
+  float rmax[TM][16];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      float m = 0.0f;
+#pragma unroll
+      for (int j = 0; j < TN / 2; ++j) {
+        const float yy = silu_f32(acc[i][j][v]) * acc[i][j + TN / 2][v];
+        y[i][j][v] = yy;
+        m = fmaxf(m, fabsf(yy));
+      }
+      // reduce over the 32 lanes that share this row (lane bits 0..4)
+#pragma unroll
+      for (int off = 1; off < 32; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+      rmax[i][v] = m;
+    }
+  if (ccol == 0) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) red[wm * WTM + i * 32 + 8 * (v >> 2) + rhalf + (v & 3)][wn] = rmax[i][v];
+  }
+  __syncthreads();
+  const int ycol0 = n_tile * 128 + wn * 64;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int rl = wm * WTM + i * 32 + 8 * (v >> 2) + rhalf + (v & 3);
+      const int row = r0 + rl;
+      float s = fmaxf(red[rl][0], red[rl][1]) / 448.0f;
+      if (s == 0.0f) s = 1.0f;
+      if (row < r1) {
+#pragma unroll
+        for (int j = 0; j < TN / 2; ++j) {
+          const int col = ycol0 + j * 32 + ccol;
+          p.outq[(int64_t)row * p.I + col] = f32_to_e4m3(y[i][j][v] / s);
+          if (p.out) p.out[(int64_t)row * p.I + col] = f32_to_bf16(y[i][j][v]);
+        }
+        if (wn == 0 && ccol == 0) p.outs[(int64_t)row * (p.I / 128) + n_tile] = s;
+      }
+    }
+}
+
+}  // namespace f8
+
+static inline int64_t f8_ws_bytes(int64_t M, int64_t E, int64_t BM) {
+  return 256 + (ceil_div(M, BM) + E + 1) * (int64_t)sizeof(MTileF8);
+}
+
+template <int EPI>
+static int launch_fp8(const f8::Args& a, const int32_t* gs, int64_t E, int64_t nn, void* ws, hipStream_t st) {
+  constexpr int BM = 128, BN = 256;
+  int* count = (int*)ws;
+  MTileF8* tiles = (MTileF8*)((char*)ws + 256);
+  hipLaunchKernelGGL(f8::build_tiles_f8_kernel, dim3(1), dim3(1024), 0, st, gs, (int)E, a.M, BM, count, tiles);
+  f8::Args b = a;
+  b.count = count;
+  b.tiles = tiles;
+  const int64_t grid = round_up((ceil_div(a.M, BM) + E + 1) * nn, 8);
+  hipLaunchKernelGGL((f8::gmm_fp8_kernel<BM, BN, 2, 2, EPI>), dim3((unsigned)grid), dim3(256), 0, st, b);
+  return check_launch();
+}
+
+}  // namespace mtx
+
+using namespace mtx;
+
+extern "C" int mtx_quant_fp8_rows(const void* x, int dtype, int64_t M, int64_t D, uint8_t* xq, float* x_scale,
+                                  void* stream) {
+  if (M < 0 || D < 0 || D % 128 != 0 || (dtype != MTX_F32 && dtype != MTX_BF16)) return MTX_ERR_ARG;
+  if (M == 0 || D == 0) return MTX_OK;
+  if (!x || !xq || !x_scale) return MTX_ERR_ARG;
+  int64_t blocks = ceil_div(M * (D / 128), 4);
+  if (blocks > 65536) blocks = 65536;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == MTX_F32)
+    hipLaunchKernelGGL(f8::quant_rows_kernel<float>, dim3(blocks), dim3(256), 0, st, (const float*)x, M, D, xq,
+                       x_scale);
+  else
+    hipLaunchKernelGGL(f8::quant_rows_kernel<uint16_t>, dim3(blocks), dim3(256), 0, st, (const uint16_t*)x, M, D,
+                       xq, x_scale);
+  return check_launch();
+}
+
+extern "C" int mtx_quant_fp8_weights(const void* w, int dtype, int64_t E, int64_t Kin, int64_t Kout, uint8_t* w_q,
+                                     float* w_scale, void* stream) {
+  if (E < 0 || Kin < 0 || Kout < 0 || Kin % 128 || Kout % 128 || (dtype != MTX_F32 && dtype != MTX_BF16))
+    return MTX_ERR_ARG;
+  if (E == 0 || Kin == 0 || Kout == 0) return MTX_OK;
+  if (!w || !w_q || !w_scale) return MTX_ERR_ARG;
+  dim3 grid((unsigned)(Kout / 128), (unsigned)(Kin / 128), (unsigned)E);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == MTX_F32)
+    hipLaunchKernelGGL(f8::quant_weights_kernel<float>, grid, dim3(256), 0, st, (const float*)w, Kin, Kout, w_q,
+                       w_scale);
+  else
+    hipLaunchKernelGGL(f8::quant_weights_kernel<uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)w, Kin, Kout,
+                       w_q, w_scale);
+  return check_launch();
+}
+
+static int fp8_checks(const void* xq, const float* xs, const uint8_t* wq, const float* ws, const int32_t* gs,
+                      int64_t M, int64_t Kin, int64_t E, void* workspace, int64_t workspace_bytes) {
+  if (M < 0 || M > INT32_MAX / 2 || E < 1 || E > 1024 || Kin <= 0 || Kin % 128) return MTX_ERR_ARG;
+  if (!workspace || workspace_bytes < f8_ws_bytes(M, E, 64)) return MTX_ERR_WORKSPACE;
+  if (M > 0 && (!xq || !xs || !wq || !ws || !gs)) return MTX_ERR_ARG;
+  if (((uintptr_t)xq | (uintptr_t)wq) % 16) return MTX_ERR_ARG;
+  return MTX_OK;
+}
+
+extern "C" int mtx_gmm_fp8(const uint8_t* xq, const float* x_scale, const uint8_t* w_q, const float* w_scale,
+                           const int32_t* group_sizes, int64_t M, int64_t Kin, int64_t Kout, int64_t E, void* out,
+                           void* workspace, int64_t workspace_bytes, void* stream) {
+  int rc = fp8_checks(xq, x_scale, w_q, w_scale, group_sizes, M, Kin, E, workspace, workspace_bytes);
+  if (rc) return rc;
+  if (Kout <= 0 || Kout % 256) return (Kout % 128 == 0 && Kout > 0) ? MTX_ERR_UNSUPPORTED : MTX_ERR_ARG;
+  if (M == 0) return MTX_OK;
+  if (!out) return MTX_ERR_ARG;
+  f8::Args a{};
+  a.xq = xq;
+  a.xs = x_scale;
+  a.wq = w_q;
+  a.ws = w_scale;
+  a.out = (uint16_t*)out;
+  a.M = (int)M;
+  a.K = (int)Kin;
+  a.N = (int)Kout;
+  a.I = 0;
+  a.ldc = (int)Kout;
+  return launch_fp8<f8::EPI_STORE>(a, group_sizes, E, Kout / 256, workspace, (hipStream_t)stream);
+}
+
+extern "C" int mtx_gmm_fp8_swiglu(const uint8_t* xq, const float* x_scale, const uint8_t* w_q, const float* w_scale,
+                                  const int32_t* group_sizes, int64_t M, int64_t Kin, int64_t I, int64_t E,
+                                  uint8_t* out_q, float* out_scale, void* out_bf16, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  int rc = fp8_checks(xq, x_scale, w_q, w_scale, group_sizes, M, Kin, E, workspace, workspace_bytes);
+  if (rc) return rc;
+  if (I <= 0 || I % 128) return MTX_ERR_ARG;
+  if (M == 0) return MTX_OK;
+  if (!out_q || !out_scale) return MTX_ERR_ARG;
+  f8::Args a{};
+  a.xq = xq;
+  a.xs = x_scale;
+  a.wq = w_q;
+  a.ws = w_scale;
+  a.out = (uint16_t*)out_bf16;
+  a.outq = out_q;
+  a.outs = out_scale;
+  a.M = (int)M;
+  a.K = (int)Kin;
+  a.N = (int)(2 * I);
+  a.I = (int)I;
+  a.ldc = (int)I;
+  return launch_fp8<f8::EPI_SWIGLU_Q>(a, group_sizes, E, I / 128, workspace, (hipStream_t)stream);
+}

@@ -1,0 +1,832 @@
+// Ragged grouped GEMM for the MoE layer on gfx950.
+//
+// Semantics (bzantium/mintext mintext/kernels/grouped_matmul.py):
+//   gmm   : out[r] = x[r] @ W[g(r)], rows grouped contiguously by group_sizes
+//           (jax.lax.ragged_dot, grouped_matmul.py:58-76,143-147,242-277); rows past
+//           sum(group_sizes) are zero.
+//   dlhs  : dx[r] = g[r] @ W[g(r)]^T  (ragged_dot(grad, swapaxes(W,1,2)), :162-176)
+//   tgmm  : dW[e] = x[rows_e]^T @ g[rows_e], zeros for an empty group (:197-235)
+//   swiglu: silu(h[:, :I]) * h[:, I:]  (mintext/modules/moe.py:195-196), fused into the
+//           gate_up GEMM epilogue so h never reaches HBM.
+//
+// group_sizes stays on the device: a one-workgroup prologue (build_tiles_kernel) turns it
+// into a compact list of (expert, row_begin, row_end) M-tiles plus group offsets; the GEMM
+// grid is sized to the upper bound ceil(M/BM) + E + 1 tiles and surplus workgroups exit.
+//
+// bf16 path: CDNA4 MFMA v_mfma_f32_32x32x16_bf16 with f32 accumulation.  A workgroup owns
+// a BM x BN output tile, its waves a (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks.
+// Operand tiles are staged through LDS in a k-contiguous layout (one 128-byte row = 64
+// bf16 of the reduction dim per M/N index) with the 16-byte chunks XOR-swizzled so that
+// both the 16-byte fragment reads and the tile writes avoid bank conflicts; two LDS
+// buffers alternate so the global loads of step k+1 overlap the MFMAs of step k.  Operands
+// whose reduction dim is not contiguous in HBM (W in the forward pass, both operands of
+// tgmm) are loaded as 8x8 blocks and transposed in registers with v_perm_b32.
+// f32 path (and shapes the MFMA tiling does not cover): an LDS-tiled exact-fp32 FMA kernel.
+#include "common.h"
+#include <type_traits>
+
+namespace mtx {
+
+struct MTile {
+  int e, r0, r1, pad;
+};
+
+// ---- tile scheduler ---------------------------------------------------------------------------
+// Workspace layout (ints): [0] m-tile count, [16 .. 16+E] group offsets (E+1, clamped to M),
+// [32+E .. ) expert order by descending group size (E), then the MTile array (16B aligned).
+struct GmmWs {
+  int* count;
+  int* offsets;
+  int* order;
+  MTile* tiles;
+};
+static inline int64_t gmm_ws_tiles_off(int64_t E) { return round_up((int64_t)(48 + 2 * E + 1) * 4, 256); }
+static inline int64_t gmm_max_tiles(int64_t M, int64_t E, int64_t BM) { return ceil_div(M, BM) + E + 1; }
+static inline GmmWs gmm_ws(void* ws, int64_t E) {
+  GmmWs w;
+  int* b = (int*)ws;
+  w.count = b;
+  w.offsets = b + 16;
+  w.order = b + 32 + E + 1;
+  w.tiles = (MTile*)((char*)ws + gmm_ws_tiles_off(E));
+  return w;
+}
+
+// One workgroup of 1024 threads, E <= 1024.
+__global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __restrict__ gs, int E, int M, int BM,
+                                                           int* __restrict__ count, int* __restrict__ offsets,
+                                                           int* __restrict__ order, MTile* __restrict__ tiles) {
+  __shared__ int wsum[16];
+  __shared__ int s_gs[1024];
+  __shared__ int s_total[2];
+  const int e = threadIdx.x, lane = e & 63, w = e >> 6;
+  const int g = (e < E) ? max(gs[e], 0) : 0;
+  s_gs[e] = g;
+  // exclusive scan of g -> row offsets (64-bit safe: M < 2^31 is checked on the host)
+  int incl = g;
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  if (e == 0) {
+    int run = 0;
+    for (int i = 0; i < 16; ++i) { const int x = wsum[i]; wsum[i] = run; run += x; }
+    s_total[0] = run;
+  }
+  __syncthreads();
+  const int start = incl - g + wsum[w];
+  const int r0 = min(start, M), r1 = min(start + g, M);
+  const int nt = (r1 - r0 + BM - 1) / BM;
+  if (e < E) offsets[e] = r0;
+  if (e == 0) offsets[E] = min(s_total[0], M);
+  __syncthreads();
+  // exclusive scan of tile counts
+  incl = nt;
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  if (e == 0) {
+    int run = 0;
+    for (int i = 0; i < 16; ++i) { const int x = wsum[i]; wsum[i] = run; run += x; }
+    s_total[1] = run;
+  }
+  __syncthreads();
+  const int tstart = incl - nt + wsum[w];
+  for (int i = 0; i < nt; ++i) {
+    MTile t;
+    t.e = e;
+    t.r0 = r0 + i * BM;
+    t.r1 = min(r0 + (i + 1) * BM, r1);
+    t.pad = 0;
+    tiles[tstart + i] = t;
+  }
+  // zero tiles for rows past sum(group_sizes)
+  const int used = min(s_total[0], M);
+  const int ntail = (M - used + BM - 1) / BM;
+  if (e < ntail) {
+    MTile t;
+    t.e = -1;
+    t.r0 = used + e * BM;
+    t.r1 = min(used + (e + 1) * BM, M);
+    t.pad = 0;
+    tiles[s_total[1] + e] = t;
+  }
+  if (e == 0) count[0] = s_total[1] + ntail;
+  // expert order by descending group size (ties: lower id first), used by tgmm
+  if (e < E) {
+    int rank = 0;
+    for (int h = 0; h < E; ++h) {
+      const int o = s_gs[h];
+      rank += (o > g || (o == g && h < e)) ? 1 : 0;
+    }
+    order[rank] = e;
+  }
+}
+
+// ---- generic exact-fp32 path ------------------------------------------------------------------
+template <typename T> __device__ __forceinline__ float gld(const T* p, int64_t i);
+template <> __device__ __forceinline__ float gld<float>(const float* p, int64_t i) { return p[i]; }
+template <> __device__ __forceinline__ float gld<uint16_t>(const uint16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
+template <typename T> __device__ __forceinline__ void gst(T* p, int64_t i, float v);
+template <> __device__ __forceinline__ void gst<float>(float* p, int64_t i, float v) { p[i] = v; }
+template <> __device__ __forceinline__ void gst<uint16_t>(uint16_t* p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+
+// MODE 0: C[r,n] = sum_k A[r,k] W[e,k,n]   (W: [E][Kred][Nout])
+// MODE 1: C[r,n] = sum_k A[r,k] W[e,n,k]   (W: [E][Nout][Kred], the dlhs transpose)
+// MODE 2: as MODE 0 with Nout = 2I, fused SwiGLU: the 64-column tile holds 32 gate columns
+//         and the 32 matching up columns; C[r,j] = silu(gate) * up, C is [M][I].
+template <typename T, int MODE>
+__global__ __launch_bounds__(256) void gmm_generic_kernel(const T* __restrict__ A, const T* __restrict__ W,
+                                                          const MTile* __restrict__ tiles,
+                                                          const int* __restrict__ count, int64_t Kred,
+                                                          int64_t Nout, T* __restrict__ C) {
+  __shared__ float As[16][65];
+  __shared__ float Bs[16][65];
+  if ((int)blockIdx.x >= count[0]) return;
+  const MTile t = tiles[blockIdx.x];
+  const int64_t I = Nout / 2;
+  const int64_t n0 = (MODE == 2) ? (int64_t)blockIdx.y * 32 : (int64_t)blockIdx.y * 64;
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  if (t.e < 0) {
+    const int ncol = (MODE == 2) ? 32 : 64;
+    const int64_t ldc = (MODE == 2) ? I : Nout;
+    for (int i = threadIdx.x; i < 64 * ncol; i += 256) {
+      const int64_t r = t.r0 + i / ncol, n = n0 + i % ncol;
+      if (r < t.r1 && n < ldc) gst<T>(C, r * ldc + n, 0.0f);
+    }
+    return;
+  }
+  const T* We = W + (int64_t)t.e * Kred * Nout;
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+  for (int64_t k0 = 0; k0 < Kred; k0 += 16) {
+    for (int i = threadIdx.x; i < 16 * 64; i += 256) {
+      const int kk = i % 16, rr = i / 16;
+      const int64_t r = t.r0 + rr, k = k0 + kk;
+      As[kk][rr] = (r < t.r1 && k < Kred) ? gld<T>(A, r * Kred + k) : 0.0f;
+      const int nn = i % 64, kb = i / 64;
+      const int64_t k2 = k0 + kb;
+      float b = 0.0f;
+      if (MODE == 2) {
+        const int64_t j = n0 + (nn & 31);
+        const int64_t n = (nn < 32) ? j : I + j;
+        if (j < I && k2 < Kred) b = gld<T>(We, k2 * Nout + n);
+      } else {
+        const int64_t n = n0 + nn;
+        if (n < Nout && k2 < Kred) b = (MODE == 0) ? gld<T>(We, k2 * Nout + n) : gld<T>(We, n * Kred + k2);
+      }
+      Bs[kb][nn] = b;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+  if (MODE == 2) {
+    __shared__ float Cs[64][65];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) Cs[ty * 4 + i][tx * 4 + j] = acc[i][j];
+    __syncthreads();
+    for (int i = threadIdx.x; i < 64 * 32; i += 256) {
+      const int rr = i / 32, jj = i % 32;
+      const int64_t r = t.r0 + rr, j = n0 + jj;
+      if (r < t.r1 && j < I) gst<T>(C, r * I + j, silu_f32(Cs[rr][jj]) * Cs[rr][32 + jj]);
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t r = t.r0 + ty * 4 + i;
+    if (r >= t.r1) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t n = n0 + tx * 4 + j;
+      if (n < Nout) gst<T>(C, r * Nout + n, acc[i][j]);
+    }
+  }
+}
+
+// dW[e,k,n] = sum_{r in group e} X[r,k] G[r,n]; grid (E, ceil(K/64), ceil(N/64))
+template <typename T>
+__global__ __launch_bounds__(256) void tgmm_generic_kernel(const T* __restrict__ X, const T* __restrict__ G,
+                                                           const int* __restrict__ offsets, int64_t K,
+                                                           int64_t N, T* __restrict__ dW) {
+  __shared__ float Xs[16][65];
+  __shared__ float Gs[16][65];
+  const int e = blockIdx.x;
+  const int64_t k0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.z * 64;
+  const int64_t r0 = offsets[e], r1 = offsets[e + 1];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+  for (int64_t rb = r0; rb < r1; rb += 16) {
+    for (int i = threadIdx.x; i < 16 * 64; i += 256) {
+      const int c = i % 64, rr = i / 64;
+      const int64_t r = rb + rr;
+      Xs[rr][c] = (r < r1 && k0 + c < K) ? gld<T>(X, r * K + k0 + c) : 0.0f;
+      Gs[rr][c] = (r < r1 && n0 + c < N) ? gld<T>(G, r * N + n0 + c) : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = Xs[rr][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Gs[rr][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+  T* out = dW + (int64_t)e * K * N;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t k = k0 + ty * 4 + i;
+    if (k >= K) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t n = n0 + tx * 4 + j;
+      if (n < N) gst<T>(out, k * N + n, acc[i][j]);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_kernel(const T* __restrict__ h, int64_t M, int64_t I,
+                                                     T* __restrict__ out) {
+  const int64_t total = M * I;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / I, j = i % I;
+    const float g = gld<T>(h, r * 2 * I + j), u = gld<T>(h, r * 2 * I + I + j);
+    gst<T>(out, i, silu_f32(g) * u);
+  }
+}
+
+// dh[r, j] = dy * up * silu'(gate), dh[r, I+j] = dy * silu(gate); silu'(g) = s (1 + g (1 - s))
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_bwd_kernel(const T* __restrict__ h, const T* __restrict__ dy,
+                                                         int64_t M, int64_t I, T* __restrict__ dh) {
+  const int64_t total = M * I;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / I, j = i % I;
+    const float g = gld<T>(h, r * 2 * I + j), u = gld<T>(h, r * 2 * I + I + j), d = gld<T>(dy, i);
+    const float s = 1.0f / (1.0f + expf(-g));
+    gst<T>(dh, r * 2 * I + j, d * u * (s * (1.0f + g * (1.0f - s))));
+    gst<T>(dh, r * 2 * I + I + j, d * g * s);
+  }
+}
+
+// ---- bf16 MFMA path -------------------------------------------------------------------------
+namespace mf {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;  // native vector: SROA-friendly, unlike u32x4
+
+constexpr int BK = 64;  // reduction elements per step; one LDS row = 128 bytes = 8 chunks
+
+__device__ __forceinline__ int lds_off(int r, int c) { return r * 128 + ((c ^ (r & 7) ^ ((r >> 3) & 7)) << 4); }
+
+enum { FWD = 0, DLHS = 1, TGMM = 2 };
+enum { EPI_STORE = 0, EPI_SWIGLU = 1 };
+
+__device__ __forceinline__ uint32_t u4c(const u32x4& v, int d) { return v[d]; }
+
+// 8x8 bf16 transpose: in[i] = row i (8 consecutive columns), result j = column j (8 rows).
+// Column j of rows (2i, 2i+1) sits in dword j/2 of each row, low half for even j.
+template <int J>
+__device__ __forceinline__ u32x4 transpose_col(const u32x4 (&in)[8]) {
+  constexpr uint32_t sel = (J & 1) ? 0x07060302u : 0x05040100u;
+  return u32x4{__builtin_amdgcn_perm(u4c(in[1], J / 2), u4c(in[0], J / 2), sel),
+                    __builtin_amdgcn_perm(u4c(in[3], J / 2), u4c(in[2], J / 2), sel),
+                    __builtin_amdgcn_perm(u4c(in[5], J / 2), u4c(in[4], J / 2), sel),
+                    __builtin_amdgcn_perm(u4c(in[7], J / 2), u4c(in[6], J / 2), sel)};
+}
+
+// Transpose one 8x8 block and write its 8 columns as 16-byte chunks `kb` of LDS rows c0..c0+7.
+__device__ __forceinline__ void store_transposed(char* base, const u32x4 (&in)[8], int c0, int kb) {
+  *(u32x4*)(base + lds_off(c0 + 0, kb)) = transpose_col<0>(in);
+  *(u32x4*)(base + lds_off(c0 + 1, kb)) = transpose_col<1>(in);
+  *(u32x4*)(base + lds_off(c0 + 2, kb)) = transpose_col<2>(in);
+  *(u32x4*)(base + lds_off(c0 + 3, kb)) = transpose_col<3>(in);
+  *(u32x4*)(base + lds_off(c0 + 4, kb)) = transpose_col<4>(in);
+  *(u32x4*)(base + lds_off(c0 + 5, kb)) = transpose_col<5>(in);
+  *(u32x4*)(base + lds_off(c0 + 6, kb)) = transpose_col<6>(in);
+  *(u32x4*)(base + lds_off(c0 + 7, kb)) = transpose_col<7>(in);
+}
+
+struct Args {
+  const uint16_t* A;  // FWD: x [M][K]; DLHS: g [M][Kout]; TGMM: x [M][Kd]
+  const uint16_t* B;  // FWD: W [E][K][N]; DLHS: W [E][N=Kin][Kout]; TGMM: g [M][N]
+  uint16_t* C;
+  const int* count;
+  const int* offsets;
+  const int* order;
+  const MTile* tiles;
+  int M;       // rows of A (FWD/DLHS) or of x/g (TGMM)
+  int Kred;    // reduction length (FWD: Kin; DLHS: Kout); TGMM: unused
+  int N;       // output columns (FWD: Kout or 2I; DLHS: Kin; TGMM: N)
+  int Kd;      // TGMM: output rows per expert (K of x)
+  int ldc;     // output row stride (FWD: Kout or I)
+  int I;       // SwiGLU intermediate size
+  int E;
+};
+
+// ---- tile loaders ------------------------------------------------------------------------------
+// Direct (reduction dim contiguous in HBM): ROWS x 64 elements, CPT 16-byte chunks per thread.
+template <int ROWS, int NT>
+struct DirectLoader {
+  static constexpr int CPT = ROWS * 8 / NT;
+  static_assert((ROWS * 8) % NT == 0, "tile split");
+  u32x4 r[CPT];
+  // element (row, k) at src[row_index(row) * ld + k0 + k]; rows past row_max are clamped.
+  __device__ __forceinline__ void load(const uint16_t* __restrict__ src, int64_t ld, int row_base, int row_max,
+                                       int k0, int tid) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int q = tid + i * NT;
+      int gr = row_base + (q >> 3);
+      gr = gr < row_max ? gr : row_max;
+      r[i] = *(const u32x4*)(src + (int64_t)gr * ld + k0 + (q & 7) * 8);
+    }
+  }
+  __device__ __forceinline__ void store(char* lds, int tid) const {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int q = tid + i * NT;
+      *(u32x4*)(lds + lds_off(q >> 3, q & 7)) = r[i];
+    }
+  }
+};
+
+// Transposed (columns contiguous in HBM): 64 reduction rows x COLS columns as 8x8 blocks.
+template <int COLS, int NT>
+struct TransLoader {
+  static constexpr int BPT = (COLS + NT - 1) / NT;
+  u32x4 r[BPT][8];
+  // element (red, col) at src[(red0 + red) * ld + colmap(col)]; reductions >= red_end are 0.
+  template <typename ColMap>
+  __device__ __forceinline__ void load(const uint16_t* __restrict__ src, int64_t ld, int red0, int red_end,
+                                       ColMap colmap, int tid) {
+#pragma unroll
+    for (int b = 0; b < BPT; ++b) {
+      const int q = tid + b * NT;
+      const int cb = q % (COLS / 8), kb = q / (COLS / 8);
+      const bool qok = (COLS % NT == 0) || (q < COLS);
+      const int gc = colmap(cb * 8);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int red = red0 + kb * 8 + i;
+        r[b][i] = (qok && red < red_end) ? *(const u32x4*)(src + (int64_t)red * ld + gc) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  }
+  __device__ __forceinline__ void store(char* lds, int tid) const {
+#pragma unroll
+    for (int b = 0; b < BPT; ++b) {
+      const int q = tid + b * NT;
+      if ((COLS % NT != 0) && q >= COLS) continue;
+      store_transposed(lds, r[b], (q % (COLS / 8)) * 8, q / (COLS / 8));
+    }
+  }
+};
+
+template <int BM, int BN, int WM, int WN, int MODE, int EPI>
+__global__ __launch_bounds__(WM* WN * 64, 1) void gmm_mfma_kernel(Args p) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  static_assert(TM >= 1 && TN >= 1, "wave tile too small");
+  static_assert(EPI != EPI_SWIGLU || TN % 2 == 0, "SwiGLU pairs gate/up MFMA blocks");
+  constexpr int STAGE = (BM + BN) * 128;
+
+  __shared__ __attribute__((aligned(16))) char lds[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  // ---- which output tile --------------------------------------------------------------
+  int e, r0, r1, col0, row0 = 0;  // FWD/DLHS: rows [r0,r1) of A; TGMM: reduction rows
+  int n_tile;
+  if (MODE == TGMM) {
+    const int ktiles = p.Kd / BM, ntiles = p.N / BN;
+    const int per_e = ktiles * ntiles;
+    const int total = p.E * per_e;
+    const int pid = blockIdx.x;
+    const int total8 = (total + 7) & ~7;
+    if (pid >= total8) return;
+    const int lid = (pid & 7) * (total8 >> 3) + (pid >> 3);
+    if (lid >= total) return;
+    e = p.order[lid / per_e];
+    const int rem = lid % per_e;
+    row0 = (rem / ntiles) * BM;  // k offset within dW[e]
+    n_tile = rem % ntiles;
+    col0 = n_tile * BN;
+    r0 = p.offsets[e];
+    r1 = p.offsets[e + 1];
+  } else {
+    const int nn = (EPI == EPI_SWIGLU) ? (p.I / (BN / 2)) : (p.N / BN);
+    const int cnt = p.count[0];
+    const int total = cnt * nn;
+    const int pid = blockIdx.x;
+    const int total8 = (total + 7) & ~7;
+    if (pid >= total8) return;
+    const int lid = (pid & 7) * (total8 >> 3) + (pid >> 3);
+    if (lid >= total) return;
+    constexpr int GM = 8;
+    const int grp = lid / (GM * nn);
+    const int first_m = grp * GM;
+    const int gsz = min(GM, cnt - first_m);
+    const int local = lid - grp * GM * nn;
+    const int mt = first_m + local % gsz;
+    n_tile = local / gsz;
+    const MTile t = p.tiles[mt];
+    e = t.e;
+    r0 = t.r0;
+    r1 = t.r1;
+    col0 = n_tile * BN;
+    if (e < 0) {  // rows past sum(group_sizes): zeros
+      const int ncols = (EPI == EPI_SWIGLU) ? BN / 2 : BN;
+      const int c0 = (EPI == EPI_SWIGLU) ? n_tile * (BN / 2) : col0;
+      for (int i = tid; i < BM * ncols; i += NT) {
+        const int r = r0 + i / ncols;
+        if (r < r1) p.C[(int64_t)r * p.ldc + c0 + i % ncols] = 0;
+      }
+      return;
+    }
+  }
+
+  // Global column of B for tile-local column c (a multiple of 8).
+  const int I = p.I;
+  auto b_col = [=](int c) -> int {
+    if (EPI == EPI_SWIGLU) {
+      const int w_ = c / WTN, within = c % WTN;
+      const int half = within / (WTN / 2), off = within % (WTN / 2);
+      return half * I + n_tile * (BN / 2) + w_ * (WTN / 2) + off;
+    }
+    return col0 + c;
+  };
+  auto a_col = [=](int c) -> int { return row0 + c; };
+
+  const int nk = (MODE == TGMM) ? (r1 - r0 + BK - 1) / BK : p.Kred / BK;
+
+  using ALoad = typename std::conditional<MODE == TGMM, TransLoader<BM, NT>, DirectLoader<BM, NT>>::type;
+  using BLoad = typename std::conditional<MODE == DLHS, DirectLoader<BN, NT>, TransLoader<BN, NT>>::type;
+  ALoad la;
+  BLoad lb;
+  const uint16_t* Bsrc = (MODE == FWD)    ? p.B + (int64_t)e * p.Kred * p.N
+                         : (MODE == DLHS) ? p.B + (int64_t)e * p.N * p.Kred
+                                          : p.B;
+
+  auto issue_loads = [&](int kt) {
+    if constexpr (MODE == TGMM) {
+      la.load(p.A, p.Kd, r0 + kt * BK, r1, a_col, tid);
+      lb.load(Bsrc, p.N, r0 + kt * BK, r1, b_col, tid);
+    } else if constexpr (MODE == FWD) {
+      la.load(p.A, p.Kred, r0, p.M - 1, kt * BK, tid);
+      lb.load(Bsrc, p.N, kt * BK, p.Kred, b_col, tid);
+    } else {
+      la.load(p.A, p.Kred, r0, p.M - 1, kt * BK, tid);
+      lb.load(Bsrc, p.Kred, col0, p.N - 1, kt * BK, tid);
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  if (nk > 0) {
+    issue_loads(0);
+    la.store(lds, tid);
+    lb.store(lds + BM * 128, tid);
+    __syncthreads();
+  }
+  const int frow = lane & 31, fchunk = lane >> 5;
+  for (int kt = 0; kt < nk; ++kt) {
+    const char* As = lds + (kt & 1) * STAGE;
+    const char* Bs = As + BM * 128;
+    const bool more = kt + 1 < nk;
+    if (more) issue_loads(kt + 1);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      bf16x8 a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        a[i] = *(const bf16x8*)(As + lds_off(wm * WTM + i * 32 + frow, kk * 2 + fchunk));
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        b[j] = *(const bf16x8*)(Bs + lds_off(wn * WTN + j * 32 + frow, kk * 2 + fchunk));
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) {
+      char* An = lds + ((kt + 1) & 1) * STAGE;
+      la.store(An, tid);
+      lb.store(An + BM * 128, tid);
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: 32x32 block (i,j), lane l, acc v -> row 8*(v/4) + 4*(l/32) + v%4, col l%32
+  const int ccol = lane & 31, rhalf = (lane >> 5) * 4;
+  if (MODE == TGMM) {
+    uint16_t* out = p.C + (int64_t)e * p.Kd * p.N;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = row0 + wm * WTM + i * 32 + 8 * (v >> 2) + rhalf + (v & 3);
+          const int col = col0 + wn * WTN + j * 32 + ccol;
+          out[(int64_t)row * p.N + col] = f32_to_bf16(acc[i][j][v]);
+        }
+  } else if (EPI == EPI_SWIGLU) {
+    const int ycol0 = n_tile * (BN / 2) + wn * (WTN / 2);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN / 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = r0 + wm * WTM + i * 32 + 8 * (v >> 2) + rhalf + (v & 3);
+          if (row < r1) {
+            const float gt = acc[i][j][v], up = acc[i][j + TN / 2][v];
+            p.C[(int64_t)row * p.ldc + ycol0 + j * 32 + ccol] = f32_to_bf16(silu_f32(gt) * up);
+          }
+        }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = r0 + wm * WTM + i * 32 + 8 * (v >> 2) + rhalf + (v & 3);
+          if (row < r1) p.C[(int64_t)row * p.ldc + col0 + wn * WTN + j * 32 + ccol] = f32_to_bf16(acc[i][j][v]);
+        }
+  }
+}
+
+}  // namespace mf
+
+// ---- host-side dispatch ----------------------------------------------------------------------
+struct MfmaCfg {
+  int BM, BN;
+};
+
+static int launch_build_tiles(const int32_t* gs, int64_t E, int64_t M, int BM, const GmmWs& w, hipStream_t st) {
+  hipLaunchKernelGGL(build_tiles_kernel, dim3(1), dim3(1024), 0, st, gs, (int)E, (int)M, BM, w.count, w.offsets,
+                     w.order, w.tiles);
+  return check_launch();
+}
+
+template <int BM, int BN, int WM, int WN, int MODE, int EPI>
+static int launch_mfma(const mf::Args& a, int64_t grid, hipStream_t st) {
+  if (grid <= 0) return MTX_OK;
+  grid = round_up(grid, 8);  // the XCD remap inside the kernel assumes a multiple of 8
+  hipLaunchKernelGGL((mf::gmm_mfma_kernel<BM, BN, WM, WN, MODE, EPI>), dim3((unsigned)grid), dim3(WM * WN * 64), 0,
+                     st, a);
+  return check_launch();
+}
+
+static int common_checks(int64_t M, int64_t E, void* ws, int64_t ws_bytes, int64_t BM) {
+  if (M < 0 || M > INT32_MAX / 2 || E < 1 || E > 1024) return MTX_ERR_ARG;
+  const int64_t need = gmm_ws_tiles_off(E) + gmm_max_tiles(M, E, BM) * (int64_t)sizeof(MTile);
+  if (!ws || ws_bytes < need) return MTX_ERR_WORKSPACE;
+  return MTX_OK;
+}
+
+// Smallest m-tile any path uses is 64 rows, so the workspace bound uses BM = 64.
+static constexpr int kMinBM = 64;
+
+// FWD / DLHS / SWIGLU driver. mode: 0 fwd, 1 dlhs, 2 swiglu
+static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs, int dtype, int64_t M, int64_t Kred,
+                      int64_t Nout, int64_t I, int64_t E, void* out, void* ws, int64_t ws_bytes, hipStream_t st) {
+  if (dtype != MTX_F32 && dtype != MTX_BF16) return MTX_ERR_ARG;
+  int rc = common_checks(M, E, ws, ws_bytes, kMinBM);
+  if (rc != MTX_OK) return rc;
+  if (Kred < 0 || Nout < 0 || Kred > INT32_MAX / 2 || Nout > INT32_MAX / 2) return MTX_ERR_ARG;
+  if (M == 0 || Nout == 0) return MTX_OK;
+  if (!x || !w || !gs || !out) return MTX_ERR_ARG;
+  GmmWs wsp = gmm_ws(ws, E);
+  const int64_t out_cols = (mode == 2) ? I : Nout;
+  if (mode == 2 && Nout != 2 * I) return MTX_ERR_ARG;
+  // bf16 MFMA eligibility
+  const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)w % 16 == 0);
+  if (dtype == MTX_BF16 && aligned && Kred % mf::BK == 0 && Kred > 0) {
+    mf::Args a;
+    a.A = (const uint16_t*)x;
+    a.B = (const uint16_t*)w;
+    a.C = (uint16_t*)out;
+    a.count = wsp.count;
+    a.offsets = wsp.offsets;
+    a.order = wsp.order;
+    a.tiles = wsp.tiles;
+    a.M = (int)M;
+    a.Kred = (int)Kred;
+    a.N = (int)Nout;
+    a.Kd = 0;
+    a.ldc = (int)out_cols;
+    a.I = (int)I;
+    a.E = (int)E;
+    // tile shape: 256-row tiles when groups are large on average, else 128
+    const bool big_m = (M / E) >= 192;
+    if (mode == 2 && I % 128 == 0) {
+      if (big_m) {
+        rc = launch_build_tiles(gs, E, M, 256, wsp, st);
+        if (rc) return rc;
+        return launch_mfma<256, 256, 2, 2, mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 256) * (I / 128), st);
+      }
+      rc = launch_build_tiles(gs, E, M, 128, wsp, st);
+      if (rc) return rc;
+      return launch_mfma<128, 256, 1, 2, mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 128) * (I / 128), st);
+    }
+    if (mode != 2 && Nout % 256 == 0) {
+      if (big_m) {
+        rc = launch_build_tiles(gs, E, M, 256, wsp, st);
+        if (rc) return rc;
+        const int64_t grid = gmm_max_tiles(M, E, 256) * (Nout / 256);
+        return mode == 0 ? launch_mfma<256, 256, 2, 2, mf::FWD, mf::EPI_STORE>(a, grid, st)
+                         : launch_mfma<256, 256, 2, 2, mf::DLHS, mf::EPI_STORE>(a, grid, st);
+      }
+      rc = launch_build_tiles(gs, E, M, 128, wsp, st);
+      if (rc) return rc;
+      const int64_t grid = gmm_max_tiles(M, E, 128) * (Nout / 256);
+      return mode == 0 ? launch_mfma<128, 256, 1, 2, mf::FWD, mf::EPI_STORE>(a, grid, st)
+                       : launch_mfma<128, 256, 1, 2, mf::DLHS, mf::EPI_STORE>(a, grid, st);
+    }
+    if (mode != 2 && Nout % 128 == 0) {
+      rc = launch_build_tiles(gs, E, M, 128, wsp, st);
+      if (rc) return rc;
+      const int64_t grid = gmm_max_tiles(M, E, 128) * (Nout / 128);
+      return mode == 0 ? launch_mfma<128, 128, 2, 2, mf::FWD, mf::EPI_STORE>(a, grid, st)
+                       : launch_mfma<128, 128, 2, 2, mf::DLHS, mf::EPI_STORE>(a, grid, st);
+    }
+  }
+  // generic path (exact fp32 FMA; also bf16 shapes the MFMA tiling does not cover)
+  rc = launch_build_tiles(gs, E, M, kMinBM, wsp, st);
+  if (rc) return rc;
+  const int64_t ntile_max = gmm_max_tiles(M, E, kMinBM);
+  const int64_t gy = (mode == 2) ? ceil_div(I, 32) : ceil_div(Nout, 64);
+  dim3 grid((unsigned)ntile_max, (unsigned)gy);
+#define MTX_GEN(T, MD)                                                                                   \
+  hipLaunchKernelGGL((gmm_generic_kernel<T, MD>), grid, dim3(256), 0, st, (const T*)x, (const T*)w, wsp.tiles, \
+                     wsp.count, Kred, Nout, (T*)out)
+  if (dtype == MTX_F32) {
+    if (mode == 0) MTX_GEN(float, 0);
+    else if (mode == 1) MTX_GEN(float, 1);
+    else MTX_GEN(float, 2);
+  } else {
+    if (mode == 0) MTX_GEN(uint16_t, 0);
+    else if (mode == 1) MTX_GEN(uint16_t, 1);
+    else MTX_GEN(uint16_t, 2);
+  }
+#undef MTX_GEN
+  return check_launch();
+}
+
+static int launch_swiglu(const void* h, int dtype, int64_t M, int64_t I, void* out, hipStream_t st) {
+  int64_t blocks = ceil_div(M * I, 256);
+  if (blocks > 65536) blocks = 65536;
+  if (blocks == 0) return MTX_OK;
+  if (dtype == MTX_F32)
+    hipLaunchKernelGGL(swiglu_kernel<float>, dim3(blocks), dim3(256), 0, st, (const float*)h, M, I, (float*)out);
+  else
+    hipLaunchKernelGGL(swiglu_kernel<uint16_t>, dim3(blocks), dim3(256), 0, st, (const uint16_t*)h, M, I,
+                       (uint16_t*)out);
+  return check_launch();
+}
+
+}  // namespace mtx
+
+using namespace mtx;
+
+extern "C" int64_t mtx_gmm_workspace_size(int64_t M, int64_t E) {
+  if (M < 0 || E < 1) return -1;
+  return gmm_ws_tiles_off(E) + gmm_max_tiles(M, E, kMinBM) * (int64_t)sizeof(MTile);
+}
+
+extern "C" int mtx_gmm(const void* x, const void* w, const int32_t* group_sizes, int dtype, int64_t M, int64_t Kin,
+                       int64_t Kout, int64_t E, void* out, void* workspace, int64_t workspace_bytes, void* stream) {
+  return gmm_driver(0, x, w, group_sizes, dtype, M, Kin, Kout, 0, E, out, workspace, workspace_bytes,
+                    (hipStream_t)stream);
+}
+
+extern "C" int mtx_gmm_dlhs(const void* g, const void* w, const int32_t* group_sizes, int dtype, int64_t M,
+                            int64_t Kin, int64_t Kout, int64_t E, void* dx, void* workspace, int64_t workspace_bytes,
+                            void* stream) {
+  // reduction over Kout, output columns Kin
+  return gmm_driver(1, g, w, group_sizes, dtype, M, Kout, Kin, 0, E, dx, workspace, workspace_bytes,
+                    (hipStream_t)stream);
+}
+
+extern "C" int mtx_gmm_swiglu(const void* x, const void* w, const int32_t* group_sizes, int dtype, int64_t M,
+                              int64_t Kin, int64_t I, int64_t E, void* out, void* workspace, int64_t workspace_bytes,
+                              void* stream) {
+  if (I < 0) return MTX_ERR_ARG;
+  const int rc = gmm_driver(2, x, w, group_sizes, dtype, M, Kin, 2 * I, I, E, out, workspace, workspace_bytes,
+                            (hipStream_t)stream);
+  return rc;
+}
+
+extern "C" int mtx_swiglu(const void* h, int dtype, int64_t M, int64_t I, void* out, void* stream) {
+  if (M < 0 || I < 0 || (dtype != MTX_F32 && dtype != MTX_BF16)) return MTX_ERR_ARG;
+  if (M == 0 || I == 0) return MTX_OK;
+  if (!h || !out) return MTX_ERR_ARG;
+  return launch_swiglu(h, dtype, M, I, out, (hipStream_t)stream);
+}
+
+extern "C" int mtx_tgmm(const void* x, const void* g, const int32_t* group_sizes, int dtype, int64_t M, int64_t K,
+                        int64_t N, int64_t E, void* dw, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (dtype != MTX_F32 && dtype != MTX_BF16) return MTX_ERR_ARG;
+  int rc = common_checks(M, E, workspace, workspace_bytes, kMinBM);
+  if (rc != MTX_OK) return rc;
+  if (K < 0 || N < 0 || K > INT32_MAX / 2 || N > INT32_MAX / 2) return MTX_ERR_ARG;
+  if (K == 0 || N == 0) return MTX_OK;
+  if (!dw || !group_sizes || (M > 0 && (!x || !g))) return MTX_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  GmmWs wsp = gmm_ws(workspace, E);
+  rc = launch_build_tiles(group_sizes, E, M, kMinBM, wsp, st);
+  if (rc) return rc;
+  const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)g % 16 == 0);
+  if (dtype == MTX_BF16 && aligned && K % 128 == 0 && N % 128 == 0 && M > 0) {
+    mf::Args a;
+    a.A = (const uint16_t*)x;
+    a.B = (const uint16_t*)g;
+    a.C = (uint16_t*)dw;
+    a.count = wsp.count;
+    a.offsets = wsp.offsets;
+    a.order = wsp.order;
+    a.tiles = wsp.tiles;
+    a.M = (int)M;
+    a.Kred = 0;
+    a.N = (int)N;
+    a.Kd = (int)K;
+    a.ldc = (int)N;
+    a.I = 0;
+    a.E = (int)E;
+    if (K % 256 == 0 && N % 256 == 0) {
+      const int64_t grid = round_up(E * (K / 256) * (N / 256), 8);
+      return launch_mfma<256, 256, 2, 2, mf::TGMM, mf::EPI_STORE>(a, grid, st);
+    }
+    const int64_t grid = round_up(E * (K / 128) * (N / 128), 8);
+    return launch_mfma<128, 128, 2, 2, mf::TGMM, mf::EPI_STORE>(a, grid, st);
+  }
+  dim3 grid((unsigned)E, (unsigned)ceil_div(K, 64), (unsigned)ceil_div(N, 64));
+  if (dtype == MTX_F32)
+    hipLaunchKernelGGL(tgmm_generic_kernel<float>, grid, dim3(256), 0, st, (const float*)x, (const float*)g,
+                       wsp.offsets, K, N, (float*)dw);
+  else
+    hipLaunchKernelGGL(tgmm_generic_kernel<uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)x,
+                       (const uint16_t*)g, wsp.offsets, K, N, (uint16_t*)dw);
+  return check_launch();
+}
+
+extern "C" int mtx_swiglu_bwd(const void* h, const void* dy, int dtype, int64_t M, int64_t I, void* dh, void* stream) {
+  if (M < 0 || I < 0 || (dtype != MTX_F32 && dtype != MTX_BF16)) return MTX_ERR_ARG;
+  if (M == 0 || I == 0) return MTX_OK;
+  if (!h || !dy || !dh) return MTX_ERR_ARG;
+  int64_t blocks = ceil_div(M * I, 256);
+  if (blocks > 65536) blocks = 65536;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == MTX_F32)
+    hipLaunchKernelGGL(swiglu_bwd_kernel<float>, dim3(blocks), dim3(256), 0, st, (const float*)h, (const float*)dy, M,
+                       I, (float*)dh);
+  else
+    hipLaunchKernelGGL(swiglu_bwd_kernel<uint16_t>, dim3(blocks), dim3(256), 0, st, (const uint16_t*)h,
+                       (const uint16_t*)dy, M, I, (uint16_t*)dh);
+  return check_launch();
+}

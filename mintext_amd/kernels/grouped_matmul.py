@@ -1,0 +1,184 @@
+"""Grouped matrix multiplication x[group_i] @ weights[i] per expert, on gfx950.
+
+Drop-in for bzantium/mintext ``mintext/kernels/grouped_matmul.py`` (same names, arguments,
+output dtypes and differentiability):
+
+* ``grouped_matmul(x, weights, group_sizes, *, tiling=None)`` (grouped_matmul.py:58-76)
+* ``grouped_matmul_vjp(x, weights, group_sizes, *, tiling=(128,)*9, mosaic_fusion=True)``
+  (:83-114) -- forward gmm, backward dlhs = g @ W^T and drhs = tgmm(x, g) (:151-187)
+* ``tgmm(lhs, rhs, group_sizes)`` (:197-235) -- per-group x^T @ g, zeros for empty groups
+
+``tiling`` / ``mosaic_fusion`` are TPU XLA hints in the reference; they are accepted (and
+padded to 9 entries like the reference) and do not change results.  ``group_sizes`` never
+leaves the device.  Extra entry points beyond the reference: ``grouped_matmul_swiglu``
+(gate_up GEMM with the SwiGLU of moe.py:195-196 fused into the epilogue) and ``swiglu``.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib as L
+
+
+def _gs(group_sizes: torch.Tensor) -> torch.Tensor:
+    g = group_sizes if group_sizes.dtype == torch.int32 else group_sizes.to(torch.int32)
+    return g.contiguous()
+
+
+def _check_float(*ts):
+    for t in ts:
+        if t.dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError(f"grouped GEMM takes float32 or bfloat16 operands, got {t.dtype}")
+    if len({t.dtype for t in ts}) != 1:
+        raise TypeError("grouped GEMM operands must share one dtype")
+
+
+def _gmm_fwd(x: torch.Tensor, w: torch.Tensor, gs: torch.Tensor) -> torch.Tensor:
+    dev = L.require_device(x, w, gs)
+    _check_float(x, w)
+    x = x.contiguous()
+    w = w.contiguous()
+    M, Kin = x.shape
+    E, Kin2, Kout = w.shape
+    if Kin2 != Kin or gs.numel() != E:
+        raise ValueError(f"shape mismatch: x {tuple(x.shape)}, weights {tuple(w.shape)}, group_sizes {gs.numel()}")
+    out = torch.empty((M, Kout), dtype=x.dtype, device=dev)
+    ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
+    L.call("mtx_gmm", L.ptr(x), L.ptr(w), L.ptr(gs), L.dtype_code(x.dtype), M, Kin, Kout, E, L.ptr(out),
+           L.ptr(ws), ws.numel(), L.stream(dev))
+    return out
+
+
+def _gmm_dlhs(g: torch.Tensor, w: torch.Tensor, gs: torch.Tensor) -> torch.Tensor:
+    dev = L.require_device(g, w, gs)
+    g = g.contiguous()
+    w = w.contiguous()
+    if g.dtype != w.dtype:
+        g = g.to(w.dtype)
+    M, Kout = g.shape
+    E, Kin, Kout2 = w.shape
+    if Kout2 != Kout:
+        raise ValueError("dlhs shape mismatch")
+    dx = torch.empty((M, Kin), dtype=w.dtype, device=dev)
+    ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
+    L.call("mtx_gmm_dlhs", L.ptr(g), L.ptr(w), L.ptr(gs), L.dtype_code(w.dtype), M, Kin, Kout, E, L.ptr(dx),
+           L.ptr(ws), ws.numel(), L.stream(dev))
+    return dx
+
+
+def tgmm(lhs: torch.Tensor, rhs: torch.Tensor, group_sizes: torch.Tensor) -> torch.Tensor:
+    """Transposed grouped matmul: out[i] = lhs[group_i]^T @ rhs[group_i] (grouped_matmul.py:197-235).
+
+    Args:
+        lhs: [M, K] (activations of the forward pass).
+        rhs: [M, N] (upstream gradient).
+        group_sizes: [E] int32.
+
+    Returns:
+        [E, K, N] per-expert weight gradients in the operand dtype; empty groups give zeros.
+    """
+    gs = _gs(group_sizes)
+    dev = L.require_device(lhs, rhs, gs)
+    _check_float(lhs, rhs)
+    lhs = lhs.contiguous()
+    rhs = rhs.contiguous()
+    M, K = lhs.shape
+    M2, N = rhs.shape
+    if M2 != M:
+        raise ValueError("tgmm: lhs and rhs need the same number of rows")
+    E = gs.numel()
+    out = torch.empty((E, K, N), dtype=lhs.dtype, device=dev)
+    ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
+    L.call("mtx_tgmm", L.ptr(lhs), L.ptr(rhs), L.ptr(gs), L.dtype_code(lhs.dtype), M, K, N, E, L.ptr(out),
+           L.ptr(ws), ws.numel(), L.stream(dev))
+    return out
+
+
+class _GMM(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weights, group_sizes):
+        gs = _gs(group_sizes)
+        out = _gmm_fwd(x, weights, gs)
+        ctx.save_for_backward(x, weights, gs)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        x, w, gs = ctx.saved_tensors
+        grad = grad.contiguous().to(w.dtype)
+        dx = _gmm_dlhs(grad, w, gs) if ctx.needs_input_grad[0] else None
+        dw = tgmm(x, grad, gs) if ctx.needs_input_grad[1] else None
+        return dx, dw, None
+
+
+def _pad_tiling(tiling) -> tuple:
+    t = tuple(tiling)
+    if len(t) < 9:
+        base = t[:3] if len(t) >= 3 else (128, 128, 128)
+        t = (base * 3)[:9]
+    return t
+
+
+def grouped_matmul(x: torch.Tensor, weights: torch.Tensor, group_sizes: torch.Tensor, *,
+                   tiling=None) -> torch.Tensor:
+    """Grouped matrix multiplication: x[group_i] @ weights[i] (grouped_matmul.py:58-76).
+
+    Args:
+        x: [M, K_in] sorted tokens (contiguous per expert).
+        weights: [E, K_in, K_out].
+        group_sizes: [E] int32, tokens per expert (rows past the sum are zero in the output).
+        tiling: accepted for signature compatibility; does not change results.
+
+    Returns:
+        [M, K_out] in x's dtype.
+    """
+    del tiling
+    return _GMM.apply(x, weights, group_sizes)
+
+
+def grouped_matmul_vjp(x: torch.Tensor, weights: torch.Tensor, group_sizes: torch.Tensor, *,
+                       tiling=(128, 128, 128, 128, 128, 128, 128, 128, 128),
+                       mosaic_fusion: bool = True) -> torch.Tensor:
+    """Grouped matmul with the custom backward (grouped_matmul.py:83-114, 151-187).
+
+    Forward: gmm.  Backward: dlhs = grad @ W^T per group, drhs = tgmm(x, grad).
+    ``tiling`` (3 or 9 ints) and ``mosaic_fusion`` are accepted and ignored.
+    """
+    _pad_tiling(tiling)
+    del mosaic_fusion
+    return _GMM.apply(x, weights, group_sizes)
+
+
+def grouped_matmul_swiglu(x: torch.Tensor, weights: torch.Tensor, group_sizes: torch.Tensor) -> torch.Tensor:
+    """silu(h[:, :I]) * h[:, I:] with h = grouped_matmul(x, weights) -- fused, h never stored.
+
+    weights: [E, K_in, 2I] with the gate columns first (the fused gate_up layout of
+    mintext/modules/moe.py:125-132).  Returns [M, I] in x's dtype.  Forward only.
+    """
+    gs = _gs(group_sizes)
+    dev = L.require_device(x, weights, gs)
+    _check_float(x, weights)
+    x = x.contiguous()
+    w = weights.contiguous()
+    M, Kin = x.shape
+    E, Kin2, two_i = w.shape
+    if Kin2 != Kin or two_i % 2 or gs.numel() != E:
+        raise ValueError("grouped_matmul_swiglu shape mismatch")
+    I = two_i // 2
+    out = torch.empty((M, I), dtype=x.dtype, device=dev)
+    ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
+    L.call("mtx_gmm_swiglu", L.ptr(x), L.ptr(w), L.ptr(gs), L.dtype_code(x.dtype), M, Kin, I, E, L.ptr(out),
+           L.ptr(ws), ws.numel(), L.stream(dev))
+    return out
+
+
+def swiglu(h: torch.Tensor) -> torch.Tensor:
+    """silu(h[:, :I]) * h[:, I:] (mintext/modules/moe.py:195-196) as one HIP kernel."""
+    dev = L.require_device(h)
+    _check_float(h)
+    h = h.contiguous()
+    M, two_i = h.shape
+    I = two_i // 2
+    out = torch.empty((M, I), dtype=h.dtype, device=dev)
+    L.call("mtx_swiglu", L.ptr(h), L.dtype_code(h.dtype), M, I, L.ptr(out), L.stream(dev))
+    return out

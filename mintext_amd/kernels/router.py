@@ -1,0 +1,58 @@
+"""Router top-k on gfx950 (one HIP kernel, ``mtx_router_topk``).
+
+``route_topk(logits, k, scoring="sigmoid_group", ...)`` reproduces bzantium/mintext
+``MoERouter.__call__`` after the gate GEMM (mintext/modules/moe.py:53-67) together with
+``_group_topk_routing`` (moe.py:69-103): sigmoid scores in float32, the loss-free
+``e_score_correction_bias`` added for selection only, group score = sum of the top-2
+biased scores per group, top ``topk_group`` groups kept, top-k of the biased scores in the
+kept groups (descending, ties to the lower expert id), weights = unbiased scores,
+``w / (sum(w) + 1e-20)`` when ``norm_topk_prob``, times ``routed_scaling_factor``.
+
+``scoring="softmax"`` is the Mixtral / Qwen3-MoE router, which the reference does not
+have: top-k on the logits (the order of the float32 softmax), weights renormalised over
+the top-k (or the full-softmax probabilities when ``norm_topk_prob`` is False).
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib as L
+
+_SCORING = {"softmax": L.MTX_SCORING_SOFTMAX, "sigmoid_group": L.MTX_SCORING_SIGMOID_GROUP,
+            "sigmoid": L.MTX_SCORING_SIGMOID_GROUP}
+
+
+def route_topk(logits: torch.Tensor, k: int, *, scoring: str = "softmax", bias: torch.Tensor | None = None,
+               n_group: int = 1, topk_group: int = 1, norm_topk_prob: bool = True,
+               routed_scaling_factor: float = 1.0, return_scores: bool = False):
+    """Select the top-k experts per token.
+
+    Args:
+        logits: [T, E] router logits (float32 or bfloat16), i.e. the gate Linear output.
+        k: experts per token.
+        scoring: "softmax" or "sigmoid_group".
+        bias: [E] float32 e_score_correction_bias (sigmoid_group only; None = zeros).
+
+    Returns:
+        (topk_indices [T,k] int32, topk_weights [T,k] float32) and, with return_scores,
+        scores [T,E] float32 (sigmoid scores, or softmax probabilities).
+    """
+    if scoring not in _SCORING:
+        raise ValueError(f"unknown scoring {scoring!r}")
+    dev = L.require_device(logits)
+    lg = logits.contiguous()
+    if lg.dtype not in (torch.float32, torch.bfloat16):
+        lg = lg.float()
+    T, E = lg.shape
+    idx = torch.empty((T, k), dtype=torch.int32, device=dev)
+    w = torch.empty((T, k), dtype=torch.float32, device=dev)
+    scores = torch.empty((T, E), dtype=torch.float32, device=dev) if return_scores else None
+    b = None
+    if bias is not None:
+        b = bias.to(device=dev, dtype=torch.float32).contiguous()
+    L.call("mtx_router_topk", L.ptr(lg), L.dtype_code(lg.dtype), T, E, k, _SCORING[scoring], L.ptr(b),
+           n_group, topk_group, int(bool(norm_topk_prob)), float(routed_scaling_factor), L.ptr(idx), L.ptr(w),
+           L.ptr(scores), L.stream(dev))
+    if return_scores:
+        return idx, w, scores
+    return idx, w

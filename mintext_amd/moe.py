@@ -1,0 +1,80 @@
+"""MoE expert layer composed from the gfx950 kernels.
+
+``moe_experts_forward`` is the composition of bzantium/mintext
+``MoEExperts._forward_kernel`` (mintext/modules/moe.py:161-221): cast the expert weights to
+the compute dtype (:170-171), ``route`` (:174-176), gate_up grouped GEMM (:189-192), SwiGLU
+(:195-196), down grouped GEMM (:199-202), ``unroute`` (:221).  Without autograd the gate_up
+GEMM and the SwiGLU run as one fused kernel.
+
+``moe_layer_forward`` prepends the router top-k on given gate logits (moe.py:52-67) and,
+optionally, a shared expert (moe.py:256-258) evaluated as a one-group grouped GEMM.
+
+``moe_experts_forward_fp8`` is the blockwise-fp8 variant (no reference counterpart):
+activations quantised in 1x128 groups, routed with their scales, fp8 gate_up GEMM with the
+SwiGLU and the 1x128 re-quantisation fused, fp8 down GEMM to bf16, float32 combine.
+"""
+from __future__ import annotations
+
+import torch
+
+from .kernels.grouped_matmul import grouped_matmul_swiglu, grouped_matmul_vjp
+from .kernels.moe_dispatch import route, route_with_scales, unroute
+from .kernels.router import route_topk
+from .kernels.swiglu import swiglu_autograd
+
+
+def moe_experts_forward(x: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
+                        gate_up: torch.Tensor, down: torch.Tensor, *, fuse_swiglu: bool | None = None) -> torch.Tensor:
+    """[N, D] tokens -> [N, D] in result_type(x, topk_weights) (float32 for bf16 + f32 weights)."""
+    gate_up = gate_up.to(x.dtype)
+    down = down.to(x.dtype)
+    E = gate_up.shape[0]
+    sorted_tokens, sort_indices, group_sizes = route(x, topk_indices, E)
+    needs_grad = torch.is_grad_enabled() and (
+        x.requires_grad or gate_up.requires_grad or down.requires_grad or topk_weights.requires_grad)
+    if fuse_swiglu is None:
+        fuse_swiglu = not needs_grad
+    if fuse_swiglu:
+        inter = grouped_matmul_swiglu(sorted_tokens, gate_up, group_sizes)
+    else:
+        h = grouped_matmul_vjp(sorted_tokens, gate_up, group_sizes)
+        inter = swiglu_autograd(h)
+    out = grouped_matmul_vjp(inter, down, group_sizes)
+    return unroute(out, sort_indices, topk_weights, topk_indices.shape[1])
+
+
+def moe_layer_forward(logits: torch.Tensor, x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, *,
+                      k: int, scoring: str = "softmax", bias: torch.Tensor | None = None, n_group: int = 1,
+                      topk_group: int = 1, norm_topk_prob: bool = True, routed_scaling_factor: float = 1.0,
+                      shared_gate_up: torch.Tensor | None = None, shared_down: torch.Tensor | None = None):
+    """Router top-k + routed experts (+ shared expert).  Returns (out [T,D] f32, topk_indices, topk_weights)."""
+    idx, w = route_topk(logits, k, scoring=scoring, bias=bias, n_group=n_group, topk_group=topk_group,
+                        norm_topk_prob=norm_topk_prob, routed_scaling_factor=routed_scaling_factor)
+    out = moe_experts_forward(x, idx, w, gate_up, down)
+    if shared_gate_up is not None:
+        out = out + shared_expert_forward(x, shared_gate_up, shared_down).to(out.dtype)
+    return out, idx, w
+
+
+def shared_expert_forward(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor) -> torch.Tensor:
+    """Dense SwiGLU MLP (mintext/modules/linear.py:164-228 as used at moe.py:231-236) as a
+    one-group grouped GEMM: gate_up [D, 2I] or [1, D, 2I], down [I, D] or [1, I, D]."""
+    gu = gate_up.reshape(1, *gate_up.shape[-2:]).to(x.dtype)
+    dn = down.reshape(1, *down.shape[-2:]).to(x.dtype)
+    gs = torch.full((1,), x.shape[0], dtype=torch.int32, device=x.device)
+    inter = grouped_matmul_swiglu(x, gu, gs)
+    return grouped_matmul_vjp(inter, dn, gs)
+
+
+def moe_experts_forward_fp8(x: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
+                            gate_up_q: torch.Tensor, gate_up_scale: torch.Tensor, down_q: torch.Tensor,
+                            down_scale: torch.Tensor) -> torch.Tensor:
+    """Blockwise-fp8 expert layer; weights from ``quantize_fp8_weights`` ([E, Kout, Kin] e4m3)."""
+    from .kernels.fp8 import grouped_matmul_fp8, grouped_matmul_fp8_swiglu, quantize_fp8_rows
+
+    E = gate_up_q.shape[0]
+    xq, xs = quantize_fp8_rows(x)
+    sq, ss, sort_indices, group_sizes, _ = route_with_scales(xq, xs, topk_indices, E)
+    yq, ys = grouped_matmul_fp8_swiglu(sq, ss, gate_up_q, gate_up_scale, group_sizes)
+    out = grouped_matmul_fp8(yq, ys, down_q, down_scale, group_sizes)
+    return unroute(out, sort_indices, topk_weights, topk_indices.shape[1])

@@ -1,0 +1,377 @@
+"""CPU oracle of the bzantium/mintext MoE hot path -- TEST INFRASTRUCTURE ONLY.
+
+This module is the checker for the HIP kernels.  Only ``tests/``, ``__graft_entry__.smoke()``
+and the ``cpu_baseline`` leg of ``bench.py`` may import it; the product package
+(``mintext_amd``) never does.  It restates, in numpy, the reference algorithm of each
+function on the hot path, citing the reference file:line it follows (paths relative to the
+reference repository root).  Integer outputs (indices, permutations, group sizes, fp8
+codes) are exact; floating-point outputs are computed in float64 unless a function states
+otherwise.
+
+Pinning (what checks each function, beyond restating it): see tests/test_oracle.py --
+golden fixtures written by tests/golden/make_golden.py from independent implementations
+(HF transformers routers and experts, torch.sort(stable=True), torch float64 matmul, torch's
+float8_e4m3fn cast), brute force on tiny inputs and closed-form invariants.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+# ---------------------------------------------------------------------------------------------
+# number formats
+# ---------------------------------------------------------------------------------------------
+
+
+def bf16_round(x) -> np.ndarray:
+    """float32 -> nearest bfloat16 (RNE), returned as float32 values.  NaN stays NaN."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    u = x.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    out = r.astype(np.uint32).view(np.float32).copy()
+    nan = np.isnan(x)
+    out[nan] = np.nan
+    return out
+
+
+def bf16_bits(x) -> np.ndarray:
+    return (bf16_round(x).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def bf16_from_bits(b) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint32) << 16).view(np.float32)
+
+
+E4M3_MAX = 448.0
+
+
+def e4m3_encode(x) -> np.ndarray:
+    """float32 -> OCP e4m3fn code (uint8), round-to-nearest-even, saturating at +-448.
+
+    Format: 1 sign, 4 exponent bits (bias 7), 3 mantissa bits, no infinities, S.1111.111
+    = NaN; exponent field 0 holds subnormals m * 2^-9.
+    """
+    x = np.asarray(x, dtype=np.float32)
+    sign = np.signbit(x).astype(np.uint8) << 7
+    a = np.abs(x).astype(np.float64)
+    out = np.zeros(x.shape, dtype=np.uint8)
+    nan = np.isnan(x)
+    sat = (a >= E4M3_MAX) & ~nan
+    sub = (a < 2.0 ** -6) & ~nan
+    # subnormal: m = rne(a / 2^-9) in [0, 8]
+    m_sub = np.rint(a * 512.0)  # np.rint is round-half-even
+    out = np.where(sub, m_sub.astype(np.uint8), out)
+    # normal: a = 2^e * (1 + f/8)
+    norm = ~(sub | sat | nan)
+    e = np.floor(np.log2(np.where(norm, a, 1.0)))
+    # guard log2 rounding at exact powers of two
+    e = np.where(norm & (2.0 ** e > a), e - 1, e)
+    e = np.where(norm & (2.0 ** (e + 1) <= a), e + 1, e)
+    frac = np.where(norm, a / 2.0 ** e - 1.0, 0.0) * 8.0
+    f = np.rint(frac)
+    carry = f >= 8
+    f = np.where(carry, 0, f)
+    e = np.where(carry, e + 1, e)
+    code = ((e + 7).astype(np.int64) << 3) | f.astype(np.int64)
+    code = np.where(code > 0x7E, 0x7E, code)  # rounding up past 448 saturates
+    out = np.where(norm, code.astype(np.uint8), out)
+    out = np.where(sat, np.uint8(0x7E), out)
+    out = np.where(nan, np.uint8(0x7F), out)
+    return (out | sign).astype(np.uint8)
+
+
+def e4m3_decode(q) -> np.ndarray:
+    q = np.asarray(q, dtype=np.uint8)
+    s = np.where(q & 0x80, -1.0, 1.0)
+    e = ((q >> 3) & 0xF).astype(np.int64)
+    m = (q & 7).astype(np.float64)
+    val = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * 2.0 ** (e - 7).astype(np.float64))
+    val = np.where((e == 0xF) & (m == 7), np.nan, val)
+    return (s * val).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------------------------
+# router top-k   (mintext/modules/moe.py:41-103; softmax router: HF mixtral/qwen3_moe routers)
+# ---------------------------------------------------------------------------------------------
+
+
+def topk_desc(values: np.ndarray, k: int) -> np.ndarray:
+    """Indices of the k largest entries per row, descending, ties to the lower index.
+
+    This is the order lax.top_k returns (moe.py:79,83,98).  Restated as a stable sort on the
+    negated values: np.lexsort keys (index, -value) -> primary -value, secondary index.
+    """
+    values = np.asarray(values)
+    T, E = values.shape
+    idx = np.arange(E)
+    out = np.empty((T, k), dtype=np.int32)
+    for t in range(T):
+        order = np.lexsort((idx, -values[t].astype(np.float64)))
+        out[t] = order[:k]
+    return out
+
+
+def sigmoid_f32(logits) -> np.ndarray:
+    """jax.nn.sigmoid(float32(logits)) as 1 / (1 + exp(-x)) in float32 (moe.py:53)."""
+    x = np.asarray(logits, dtype=np.float32)
+    with np.errstate(over="ignore"):
+        return (np.float32(1.0) / (np.float32(1.0) + np.exp(-x))).astype(np.float32)
+
+
+def select_sigmoid_group(scores: np.ndarray, bias, k: int, n_group: int, topk_group: int):
+    """Expert selection of MoERouter._group_topk_routing (moe.py:69-103) given float32 scores.
+
+    Returns (topk_indices [T,k] int32, masked routing scores [T,E] float32).
+    Exact given the float32 scores: the only arithmetic is s + bias and a + b of the two
+    largest per group, both single float32 roundings.
+    """
+    s = np.asarray(scores, dtype=np.float32)
+    T, E = s.shape
+    b = np.zeros(E, np.float32) if bias is None else np.asarray(bias, np.float32)
+    r = (s + b).astype(np.float32)  # moe.py:56
+    if n_group > 1 and topk_group < n_group:
+        epg = E // n_group
+        grouped = r.reshape(T, n_group, epg)  # moe.py:76
+        top2 = -np.sort(-grouped, axis=-1)[..., : min(2, epg)]  # moe.py:79
+        gscore = top2[..., 0].copy()
+        if top2.shape[-1] == 2:
+            gscore = (top2[..., 0] + top2[..., 1]).astype(np.float32)  # moe.py:80
+        gsel = topk_desc(gscore, topk_group)  # moe.py:83
+        gmask = np.zeros((T, n_group), dtype=bool)
+        gmask[np.arange(T)[:, None], gsel] = True  # moe.py:86-89
+        emask = np.repeat(gmask, epg, axis=1)  # moe.py:92
+        r = np.where(emask, r, np.float32(-np.inf)).astype(np.float32)  # moe.py:95
+    return topk_desc(r, k), r
+
+
+def router_sigmoid_group(logits, k: int, bias=None, n_group: int = 1, topk_group: int = 1,
+                         norm_topk_prob: bool = True, routed_scaling_factor: float = 1.0, scores=None):
+    """MoERouter.__call__ after the gate GEMM (moe.py:52-67).
+
+    ``scores`` may be passed in (float32) to reproduce the selection on given scores.
+    Returns (idx int32 [T,k], weights float64 [T,k], scores float32 [T,E]).
+    """
+    s = sigmoid_f32(logits) if scores is None else np.asarray(scores, np.float32)
+    idx, _ = select_sigmoid_group(s, bias, k, n_group, topk_group)
+    w = np.take_along_axis(s.astype(np.float64), idx, axis=1)  # moe.py:101
+    if norm_topk_prob:
+        w = w / (w.sum(-1, keepdims=True) + 1e-20)  # moe.py:63-64
+    w = w * routed_scaling_factor  # moe.py:66
+    return idx, w, s
+
+
+def router_softmax(logits, k: int, norm_topk_prob: bool = True, routed_scaling_factor: float = 1.0):
+    """Softmax top-k router (HF mixtral/modeling_mixtral.py:104-111, qwen3_moe:258-267).
+
+    Selection on the float32 logits (softmax is monotone); weights in float64:
+    exp(l - lmax) / sum_topk exp(l - lmax) when renormalised, else the softmax probability.
+    Returns (idx int32 [T,k], weights float64 [T,k], probs float64 [T,E]).
+    """
+    lg = np.asarray(logits, dtype=np.float32)
+    idx = topk_desc(lg, k)
+    l64 = lg.astype(np.float64)
+    ex = np.exp(l64 - l64.max(-1, keepdims=True))
+    probs = ex / ex.sum(-1, keepdims=True)
+    top = np.take_along_axis(ex, idx, axis=1)
+    if norm_topk_prob:
+        w = top / top.sum(-1, keepdims=True)
+    else:
+        w = np.take_along_axis(probs, idx, axis=1)
+    return idx, w * routed_scaling_factor, probs
+
+
+# ---------------------------------------------------------------------------------------------
+# dispatch / combine   (mintext/kernels/moe_dispatch.py)
+# ---------------------------------------------------------------------------------------------
+
+
+def stable_counting_sort(keys: np.ndarray, num_buckets: int) -> np.ndarray:
+    """Stable argsort of small non-negative integer keys (counting sort).
+
+    Equals jnp.argsort(keys, stable=True) (moe_dispatch.py:73) for keys in [0, num_buckets).
+    """
+    keys = np.asarray(keys, dtype=np.int64).ravel()
+    counts = np.bincount(keys, minlength=num_buckets)
+    start = np.concatenate([[0], np.cumsum(counts)[:-1]])
+    perm = np.empty(keys.size, dtype=np.int32)
+    nxt = start.copy()
+    for p, kk in enumerate(keys):
+        perm[nxt[kk]] = p
+        nxt[kk] += 1
+    return perm
+
+
+def route(tokens, topk_indices, num_experts: int):
+    """route (moe_dispatch.py:47-81): (sorted_tokens [N*K,D], sort_indices [N*K], group_sizes [E]).
+
+    Expert ids outside [0,E) go to a trailing bucket and are not counted (the kernels'
+    documented behaviour; the reference does not define it).
+    """
+    idx = np.asarray(topk_indices, dtype=np.int64)
+    N, K = idx.shape
+    flat = idx.ravel()  # moe_dispatch.py:70
+    key = np.where((flat < 0) | (flat >= num_experts), num_experts, flat)
+    perm = stable_counting_sort(key, num_experts + 1)  # :73
+    tokens = np.asarray(tokens)
+    sorted_tokens = tokens[perm // K]  # repeat (:67) then gather (:76)
+    gs = np.bincount(key, minlength=num_experts + 1)[:num_experts].astype(np.int32)  # :79
+    return sorted_tokens, perm, gs
+
+
+def invert_permutation(perm) -> np.ndarray:
+    perm = np.asarray(perm, dtype=np.int64)
+    inv = np.empty(perm.size, dtype=np.int32)
+    inv[perm] = np.arange(perm.size, dtype=np.int32)  # == argsort(perm) (moe_dispatch.py:102)
+    return inv
+
+
+def unroute(sorted_output, sort_indices, topk_weights, k: int) -> np.ndarray:
+    """unroute (moe_dispatch.py:84-111) in float64: out[n] = sum_k w[n,k] Y[inv[n*K+k]]."""
+    Y = np.asarray(sorted_output, dtype=np.float64)
+    inv = invert_permutation(sort_indices)
+    w = np.asarray(topk_weights, dtype=np.float64)
+    N = w.shape[0]
+    u = Y[inv].reshape(N, k, -1)  # :103-108
+    return np.einsum("nkd,nk->nd", u, w)  # :111
+
+
+def unroute_f32(sorted_output, sort_indices, topk_weights, k: int) -> np.ndarray:
+    """unroute with float32 arithmetic, k ascending (the fp32 path's rounding model)."""
+    Y = np.asarray(sorted_output, dtype=np.float32)
+    inv = invert_permutation(sort_indices)
+    w = np.asarray(topk_weights, dtype=np.float32)
+    N = w.shape[0]
+    u = Y[inv].reshape(N, k, -1)
+    acc = np.zeros((N, u.shape[-1]), dtype=np.float32)
+    for kk in range(k):
+        acc = (acc + w[:, kk : kk + 1] * u[:, kk]).astype(np.float32)
+    return acc
+
+
+# ---------------------------------------------------------------------------------------------
+# grouped GEMM   (mintext/kernels/grouped_matmul.py)
+# ---------------------------------------------------------------------------------------------
+
+
+def group_offsets(group_sizes, M: int) -> np.ndarray:
+    gs = np.maximum(np.asarray(group_sizes, dtype=np.int64), 0)
+    off = np.concatenate([[0], np.cumsum(gs)])
+    return np.minimum(off, M)
+
+
+def gmm(x, w, group_sizes) -> np.ndarray:
+    """ragged_dot (grouped_matmul.py:58-76, 242-277) in float64; rows past sum(gs) are 0."""
+    x = np.asarray(x, dtype=np.float64)
+    w = np.asarray(w, dtype=np.float64)
+    M = x.shape[0]
+    off = group_offsets(group_sizes, M)
+    out = np.zeros((M, w.shape[2]))
+    for e in range(w.shape[0]):
+        a, b = off[e], off[e + 1]
+        if b > a:
+            out[a:b] = x[a:b] @ w[e]
+    return out
+
+
+def gmm_dlhs(g, w, group_sizes) -> np.ndarray:
+    """dlhs = ragged_dot(g, swapaxes(W,1,2)) (grouped_matmul.py:162-176), float64."""
+    return gmm(g, np.swapaxes(np.asarray(w, np.float64), 1, 2), group_sizes)
+
+
+def tgmm(x, g, group_sizes) -> np.ndarray:
+    """tgmm (grouped_matmul.py:197-235) as per-group x^T g in float64; empty group -> 0."""
+    x = np.asarray(x, dtype=np.float64)
+    g = np.asarray(g, dtype=np.float64)
+    M = x.shape[0]
+    E = np.asarray(group_sizes).size
+    off = group_offsets(group_sizes, M)
+    out = np.zeros((E, x.shape[1], g.shape[1]))
+    for e in range(E):
+        a, b = off[e], off[e + 1]
+        if b > a:
+            out[e] = x[a:b].T @ g[a:b]
+    return out
+
+
+def silu(x):
+    x = np.asarray(x, dtype=np.float64)
+    return x / (1.0 + np.exp(-x))
+
+
+def swiglu(h) -> np.ndarray:
+    """gate, up = split(h, 2, -1); silu(gate) * up (mintext/modules/moe.py:195-196)."""
+    h = np.asarray(h, dtype=np.float64)
+    i = h.shape[-1] // 2
+    return silu(h[..., :i]) * h[..., i:]
+
+
+def swiglu_bwd(h, dy) -> np.ndarray:
+    h = np.asarray(h, dtype=np.float64)
+    dy = np.asarray(dy, dtype=np.float64)
+    i = h.shape[-1] // 2
+    g, u = h[..., :i], h[..., i:]
+    s = 1.0 / (1.0 + np.exp(-g))
+    return np.concatenate([dy * u * s * (1 + g * (1 - s)), dy * g * s], axis=-1)
+
+
+# ---------------------------------------------------------------------------------------------
+# blockwise fp8 (no reference counterpart; conventions of mintext/modules/linear.py:37-57)
+# ---------------------------------------------------------------------------------------------
+
+
+def quant_fp8_rows(x, group: int = 128):
+    """1 x 128 groups: scale = amax/448 (1 if amax == 0), q = RNE(x / scale) in float32."""
+    x = np.asarray(x, dtype=np.float32)
+    M, D = x.shape
+    g = x.reshape(M, D // group, group)
+    amax = np.abs(g).max(-1)
+    s = (amax / np.float32(E4M3_MAX)).astype(np.float32)
+    s = np.where(s == 0, np.float32(1.0), s).astype(np.float32)
+    q = e4m3_encode((g / s[..., None]).astype(np.float32)).reshape(M, D)
+    return q, s
+
+
+def quant_fp8_weights(w, block: int = 128):
+    """128 x 128 blocks over (Kin, Kout) of w [E,Kin,Kout]; returns the k-contiguous
+    transposed codes wq [E,Kout,Kin] and scales ws [E,Kout/128,Kin/128]."""
+    w = np.asarray(w, dtype=np.float32)
+    E, Kin, Kout = w.shape
+    blk = w.reshape(E, Kin // block, block, Kout // block, block)
+    amax = np.abs(blk).max(axis=(2, 4))  # [E, Kin/128, Kout/128]
+    s = (amax / np.float32(E4M3_MAX)).astype(np.float32)
+    s = np.where(s == 0, np.float32(1.0), s).astype(np.float32)
+    q = e4m3_encode((blk / s[:, :, None, :, None]).astype(np.float32)).reshape(E, Kin, Kout)
+    return np.ascontiguousarray(np.swapaxes(q, 1, 2)), np.ascontiguousarray(np.swapaxes(s, 1, 2))
+
+
+def dequant_rows(q, s, group: int = 128) -> np.ndarray:
+    q = e4m3_decode(q).astype(np.float64)
+    M, D = q.shape
+    return (q.reshape(M, D // group, group) * np.asarray(s, np.float64)[..., None]).reshape(M, D)
+
+
+def dequant_weights(wq, ws, block: int = 128) -> np.ndarray:
+    """wq [E,Kout,Kin], ws [E,Kout/128,Kin/128] -> W [E,Kin,Kout] float64 (reference layout)."""
+    q = e4m3_decode(wq).astype(np.float64)
+    E, Kout, Kin = q.shape
+    blk = q.reshape(E, Kout // block, block, Kin // block, block) * np.asarray(ws, np.float64)[:, :, None, :, None]
+    return np.swapaxes(blk.reshape(E, Kout, Kin), 1, 2)
+
+
+def gmm_fp8(xq, xs, wq, ws, group_sizes) -> np.ndarray:
+    """Blockwise-fp8 grouped GEMM = dequantise, then float64 gmm."""
+    return gmm(dequant_rows(xq, xs), dequant_weights(wq, ws), group_sizes)
+
+
+# ---------------------------------------------------------------------------------------------
+# composition  (MoEExperts._forward_kernel, mintext/modules/moe.py:161-221)
+# ---------------------------------------------------------------------------------------------
+
+
+def moe_experts(x, topk_indices, topk_weights, gate_up, down) -> np.ndarray:
+    """route -> gmm(gate_up) -> SwiGLU -> gmm(down) -> unroute, all in float64."""
+    E = np.asarray(gate_up).shape[0]
+    k = np.asarray(topk_indices).shape[1]
+    sorted_tokens, perm, gs = route(np.asarray(x, np.float64), topk_indices, E)
+    h = gmm(sorted_tokens, gate_up, gs)
+    y = gmm(swiglu(h), down, gs)
+    return unroute(y, perm, topk_weights, k)

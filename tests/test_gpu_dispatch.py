@@ -1,0 +1,167 @@
+"""GPU parity: route / unroute / _sort_with_vjp (HIP, through the C-ABI) vs the oracle.
+
+Integer outputs (sort_indices, group_sizes, the gathered rows) must be bit-exact; the f32
+combine is checked at 1e-5 relative.  Mirrors tests/test_moe_kernels.py:22-134 of the reference.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden, rel_err
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return t if dtype is None else t.to(dtype)
+
+
+def test_route_matches_golden_fixtures(dev):
+    from mintext_amd.kernels import route
+
+    g = golden("dispatch")
+    for n in sorted({k.split("__")[0] for k in g.files}):
+        idx, E = g[f"{n}__idx"], int(g[f"{n}__E"])
+        N, K = idx.shape
+        x = np.random.default_rng(0).standard_normal((N, 64)).astype(np.float32)
+        for dt in (torch.float32, torch.bfloat16):
+            st, si, gs = route(_t(x, dev, dt), _t(idx, dev), E)
+            np.testing.assert_array_equal(si.cpu().numpy(), g[f"{n}__perm"], err_msg=n)
+            np.testing.assert_array_equal(gs.cpu().numpy(), g[f"{n}__gs"], err_msg=n)
+            ref = torch.from_numpy(x).to(dt)[torch.from_numpy(g[f"{n}__perm"].astype(np.int64) // K)]
+            assert torch.equal(st.cpu(), ref), n
+
+
+@pytest.mark.parametrize("N,K,E,D", [(16384, 8, 128, 2048), (4096, 8, 256, 512), (8192, 2, 8, 4096), (3, 1, 1, 8)])
+def test_route_large_bit_exact(dev, N, K, E, D):
+    from mintext_amd.kernels import route
+
+    rng = np.random.default_rng(N + E)
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(min(N, 64))]) if K > 1 else rng.integers(0, E, (N, K))
+    if K > 1:
+        idx = np.concatenate([idx, rng.integers(0, E, (N - idx.shape[0], K))])  # duplicates allowed too
+    x = torch.randn(N, D, device=dev, dtype=torch.bfloat16)
+    st, si, gs = route(x, _t(idx.astype(np.int32), dev), E)
+    perm = np.argsort(idx.ravel(), kind="stable")
+    np.testing.assert_array_equal(si.cpu().numpy(), perm)
+    np.testing.assert_array_equal(gs.cpu().numpy(), np.bincount(idx.ravel(), minlength=E))
+    assert torch.equal(st, x[torch.from_numpy(perm // K).to(dev)])
+
+
+def test_route_out_of_range_ids_sorted_last(dev):
+    from mintext_amd.kernels import route
+
+    idx = np.array([[1, 7], [0, -1], [2, 1], [9, 0]], np.int32)  # E = 4: 7, -1, 9 invalid
+    x = np.arange(4 * 8, dtype=np.float32).reshape(4, 8)
+    st, si, gs = route(_t(x, dev), _t(idx, dev), 4)
+    _, perm, gso = O.route(x, idx, 4)
+    np.testing.assert_array_equal(si.cpu().numpy(), perm)
+    np.testing.assert_array_equal(gs.cpu().numpy(), gso)
+    assert gs.sum().item() == 5
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_unroute_matches_oracle(dev, dt):
+    from mintext_amd.kernels import route, unroute
+
+    rng = np.random.default_rng(3)
+    N, D, K, E = 1000, 200, 4, 16
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(N)]).astype(np.int32)
+    y = rng.standard_normal((N * K, D)).astype(np.float32)
+    w = rng.random((N, K)).astype(np.float32)
+    _, si, _ = route(_t(rng.standard_normal((N, D)).astype(np.float32), dev), _t(idx, dev), E)
+    yt = _t(y, dev, dt)
+    out = unroute(yt, si, _t(w, dev), K)
+    assert out.dtype == torch.float32  # result_type(bf16, f32) = f32 as in moe_dispatch.py:111
+    ref = O.unroute(yt.float().cpu().numpy(), si.cpu().numpy(), w, K)
+    np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-5)
+    # without route's cached inverse (fresh sort_indices tensor)
+    out2 = unroute(yt, si.clone(), _t(w, dev), K)
+    assert torch.equal(out, out2)
+
+
+def test_route_unroute_gradients(dev):
+    """tests/test_moe_kernels.py:69-103: grad of sum(unroute(route(x))) and finite differences."""
+    from mintext_amd.kernels import route, unroute
+
+    rng = np.random.default_rng(42)
+    N, D, K, E = 32, 64, 2, 4
+    x = _t(rng.standard_normal((N, D)).astype(np.float32), dev).requires_grad_(True)
+    idx = _t(rng.integers(0, E, (N, K)).astype(np.int32), dev)
+    w = _t(rng.random((N, K)).astype(np.float32), dev).requires_grad_(True)
+
+    def fn(tok, ww):
+        st, si, _ = route(tok, idx, E)
+        return unroute(st, si, ww, K).sum()
+
+    loss = fn(x, w)
+    loss.backward()
+    # closed form: d/dx = sum_k w[n,k]; d/dw[n,k] = sum_d x[n,d]
+    np.testing.assert_allclose(x.grad.cpu().numpy(), np.repeat(w.detach().cpu().numpy().sum(1, keepdims=True), D, 1),
+                               rtol=1e-6)
+    np.testing.assert_allclose(w.grad.cpu().numpy(), np.repeat(x.detach().cpu().numpy().sum(1, keepdims=True), K, 1),
+                               rtol=1e-5, atol=1e-5)
+    eps = 1e-3
+    xr = x.detach()
+    for i, j in [(0, 0), (5, 7), (31, 63), (17, 30)]:
+        xp, xm = xr.clone(), xr.clone()
+        xp[i, j] += eps
+        xm[i, j] -= eps
+        num = (fn(xp, w.detach()) - fn(xm, w.detach())).item() / (2 * eps)
+        np.testing.assert_allclose(x.grad[i, j].item(), num, rtol=0.02, atol=1e-4)
+
+
+def test_unroute_backward_matches_oracle(dev):
+    from mintext_amd.kernels import route, unroute
+
+    rng = np.random.default_rng(8)
+    N, D, K, E = 300, 96, 3, 8
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(N)]).astype(np.int32)
+    _, si, _ = route(_t(np.zeros((N, D), np.float32), dev), _t(idx, dev), E)
+    y = _t(rng.standard_normal((N * K, D)).astype(np.float32), dev).requires_grad_(True)
+    w = _t(rng.random((N, K)).astype(np.float32), dev).requires_grad_(True)
+    g = rng.standard_normal((N, D)).astype(np.float32)
+    out = unroute(y, si, w, K)
+    out.backward(_t(g, dev))
+    perm = si.cpu().numpy()
+    inv = O.invert_permutation(perm)
+    Y = y.detach().cpu().numpy()
+    W = w.detach().cpu().numpy()
+    dY = np.empty_like(Y)
+    dY[inv] = (W.reshape(-1, 1) * np.repeat(g, K, axis=0))
+    dW = np.einsum("nkd,nd->nk", Y[inv].reshape(N, K, D), g)
+    np.testing.assert_allclose(y.grad.cpu().numpy(), dY, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(w.grad.cpu().numpy(), dW, rtol=1e-5, atol=1e-4)
+
+
+def test_single_and_empty_expert_edge_cases(dev):
+    """tests/test_moe_kernels.py:105-134."""
+    from mintext_amd.kernels import route, unroute
+
+    x = torch.randn(8, 16, device=dev)
+    st, si, gs = route(x, torch.zeros(8, 1, dtype=torch.int32, device=dev), 4)
+    assert gs.cpu().tolist() == [8, 0, 0, 0]
+    out = unroute(st, si, torch.ones(8, 1, device=dev), 1)
+    assert torch.equal(out, x)
+    idx = torch.randint(0, 2, (8, 1), device=dev, dtype=torch.int32)
+    st, si, gs = route(x, idx, 4)
+    assert gs[2].item() == 0 and gs[3].item() == 0 and gs.sum().item() == 8
+    assert torch.isfinite(unroute(st, si, torch.ones(8, 1, device=dev), 1)).all()
+
+
+def test_sort_with_vjp(dev):
+    from mintext_amd.kernels import _sort_with_vjp
+
+    x = torch.randn(50, 12, device=dev, requires_grad=True)
+    p = torch.randperm(50, device=dev).to(torch.int32)
+    y = _sort_with_vjp(x, p)
+    assert torch.equal(y, x.detach()[p.long()])
+    g = torch.randn(50, 12, device=dev)
+    y.backward(g)
+    expect = torch.empty_like(g)
+    expect[p.long()] = g
+    assert torch.equal(x.grad, expect)

@@ -1,0 +1,203 @@
+"""GPU parity: grouped GEMM forward / fused SwiGLU / dlhs / tgmm (HIP) vs the oracle.
+
+Tolerances (north star): fp32 path 1e-5 relative against float64; bf16 path 2e-2 relative
+against a float64 reference computed from the same bf16-rounded operands.  Shapes cover the
+reference tests (tests/test_moe_kernels.py:140-490) on the exact-fp32 path, and the MFMA
+tilings (256- and 128-row tiles, 256- and 128-column tiles) with ragged, empty and skewed
+groups on the bf16 path.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden, rel_err
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return t if dtype is None else t.to(dtype)
+
+
+def _close(got, ref, rtol):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert rel_err(got, ref) < rtol, rel_err(got, ref)
+    scale = np.abs(ref).max() if ref.size else 1.0
+    np.testing.assert_allclose(got, ref, rtol=rtol, atol=rtol * scale)
+
+
+# --------------------------------------------------------------------- exact fp32 fixtures
+def test_gmm_fp32_golden(dev):
+    from mintext_amd.kernels import grouped_matmul, grouped_matmul_vjp, tgmm
+
+    g = golden("gmm")
+    for n in sorted({k.split("__")[0] for k in g.files}):
+        gs, x, w, gr = g[f"{n}__gs"], g[f"{n}__x"], g[f"{n}__w"], g[f"{n}__g"]
+        out = grouped_matmul(_t(x, dev), _t(w, dev), _t(gs, dev))
+        _close(out.cpu().numpy(), g[f"{n}__out"], 1e-5)
+        out2 = grouped_matmul_vjp(_t(x, dev), _t(w, dev), _t(gs, dev), tiling=(64, 64, 64))
+        assert torch.equal(out, out2)
+        tg = tgmm(_t(x, dev), _t(gr, dev), _t(gs, dev))
+        _close(tg.cpu().numpy(), g[f"{n}__tgmm"], 1e-5)
+        empty = np.flatnonzero(gs == 0)
+        assert (tg[torch.from_numpy(empty).to(dev)] == 0).all()
+        xt = _t(x, dev).requires_grad_(True)
+        wt = _t(w, dev).requires_grad_(True)
+        grouped_matmul_vjp(xt, wt, _t(gs, dev)).backward(_t(gr, dev))
+        _close(xt.grad.cpu().numpy(), g[f"{n}__dlhs"], 1e-5)
+        _close(wt.grad.cpu().numpy(), g[f"{n}__tgmm"], 1e-5)
+
+
+def test_gmm_rows_past_group_sum_are_zero(dev):
+    from mintext_amd.kernels import grouped_matmul
+
+    x = torch.randn(300, 64, device=dev)
+    w = torch.randn(3, 64, 32, device=dev)
+    gs = torch.tensor([100, 0, 150], dtype=torch.int32, device=dev)
+    out = grouped_matmul(x, w, gs)
+    assert (out[250:] == 0).all()
+    xb, wb = x.bfloat16(), torch.randn(3, 64, 256, device=dev).bfloat16()
+    outb = grouped_matmul(xb, wb, gs)
+    assert (outb[250:] == 0).all()
+    _close(outb[:250].float().cpu().numpy(), O.gmm(xb.float().cpu().numpy(), wb.float().cpu().numpy(), [100, 0, 150])[:250],
+           2e-2)
+
+
+def test_gmm_finite_difference(dev):
+    """tests/test_moe_kernels.py:209-231,358-403 (dx and dW by central differences)."""
+    from mintext_amd.kernels import grouped_matmul_vjp
+
+    torch.manual_seed(0)
+    x = torch.randn(8, 4, device=dev, dtype=torch.float32)
+    w = torch.randn(2, 4, 4, device=dev)
+    gs = torch.tensor([4, 4], dtype=torch.int32, device=dev)
+    xg = x.clone().requires_grad_(True)
+    wg = w.clone().requires_grad_(True)
+    grouped_matmul_vjp(xg, wg, gs).sum().backward()
+    eps = 1e-3
+    for i in range(4):
+        for j in range(4):
+            xp, xm = x.clone(), x.clone()
+            xp[i, j] += eps
+            xm[i, j] -= eps
+            num = (grouped_matmul_vjp(xp, w, gs).sum() - grouped_matmul_vjp(xm, w, gs).sum()).item() / (2 * eps)
+            np.testing.assert_allclose(xg.grad[i, j].item(), num, rtol=0.02, atol=1e-4)
+    for e in range(2):
+        for i in range(2):
+            for j in range(2):
+                wp, wm = w.clone(), w.clone()
+                wp[e, i, j] += eps
+                wm[e, i, j] -= eps
+                num = (grouped_matmul_vjp(x, wp, gs).sum() - grouped_matmul_vjp(x, wm, gs).sum()).item() / (2 * eps)
+                np.testing.assert_allclose(wg.grad[e, i, j].item(), num, rtol=0.02, atol=1e-4)
+
+
+# ----------------------------------------------------------------------------- bf16 MFMA
+def _groups(rng, M, E, kind):
+    if kind == "uniform":
+        gs = np.full(E, M // E)
+        gs[: M - gs.sum()] += 1
+    elif kind == "skew":
+        p = 1.0 / np.arange(1, E + 1) ** 1.2
+        p = p[rng.permutation(E)]
+        gs = rng.multinomial(M, p / p.sum())
+        gs[rng.integers(0, E)] = 0
+        gs[0] += M - gs.sum()
+    else:  # ragged with empties
+        cut = np.sort(rng.integers(0, M + 1, E - 1))
+        gs = np.diff(np.concatenate([[0], cut, [M]]))
+        gs[1] = gs[1] + gs[2]
+        gs[2] = 0
+    return gs.astype(np.int32)
+
+
+BF16_SHAPES = [
+    # (M, E, Kin, Kout, groups)  -- tiles: M/E >= 192 -> 256-row tiles, else 128-row
+    (2048, 4, 256, 512, "uniform"),
+    (2048, 8, 128, 768, "ragged"),
+    (1500, 16, 192, 256, "skew"),
+    (640, 8, 64, 384, "ragged"),  # Kout % 256 != 0 -> 128-column tiles
+    (96, 3, 64, 256, "ragged"),
+]
+
+
+@pytest.mark.parametrize("M,E,Kin,Kout,kind", BF16_SHAPES)
+def test_gmm_bf16_mfma(dev, M, E, Kin, Kout, kind):
+    from mintext_amd.kernels import grouped_matmul
+    from mintext_amd.kernels.grouped_matmul import _gmm_dlhs
+
+    rng = np.random.default_rng(M + Kin)
+    gs = _groups(rng, M, E, kind)
+    x = torch.randn(M, Kin, device=dev).bfloat16()
+    w = (torch.randn(E, Kin, Kout, device=dev) * 0.05).bfloat16()
+    out = grouped_matmul(x, w, _t(gs, dev))
+    assert out.dtype == torch.bfloat16
+    xr, wr = x.float().cpu().numpy(), w.float().cpu().numpy()
+    _close(out.float().cpu().numpy(), O.gmm(xr, wr, gs), 2e-2)
+    # dlhs (reduction over Kout; output Kin columns)
+    gr = torch.randn(M, Kout, device=dev).bfloat16()
+    dx = _gmm_dlhs(gr, w, _t(gs, dev))
+    _close(dx.float().cpu().numpy(), O.gmm_dlhs(gr.float().cpu().numpy(), wr, gs), 2e-2)
+
+
+@pytest.mark.parametrize("M,E,Kin,I,kind", [(2048, 4, 256, 256, "uniform"), (1000, 8, 128, 384, "ragged"),
+                                            (300, 5, 64, 128, "skew")])
+def test_gmm_swiglu_fused(dev, M, E, Kin, I, kind):
+    from mintext_amd.kernels import grouped_matmul_swiglu
+
+    rng = np.random.default_rng(I + M)
+    gs = _groups(rng, M, E, kind)
+    for dt, tol in ((torch.bfloat16, 2e-2), (torch.float32, 1e-5)):
+        x = torch.randn(M, Kin, device=dev).to(dt)
+        w = (torch.randn(E, Kin, 2 * I, device=dev) * 0.1).to(dt)
+        y = grouped_matmul_swiglu(x, w, _t(gs, dev))
+        ref = O.swiglu(O.gmm(x.float().cpu().numpy(), w.float().cpu().numpy(), gs))
+        _close(y.float().cpu().numpy(), ref, tol)
+
+
+@pytest.mark.parametrize("M,E,K,N,kind", [(2048, 4, 256, 512, "uniform"), (1700, 8, 128, 256, "skew"),
+                                          (900, 6, 256, 128, "ragged")])
+def test_tgmm_bf16_mfma(dev, M, E, K, N, kind):
+    from mintext_amd.kernels import tgmm
+
+    rng = np.random.default_rng(K + N + M)
+    gs = _groups(rng, M, E, kind)
+    x = torch.randn(M, K, device=dev).bfloat16()
+    g = torch.randn(M, N, device=dev).bfloat16()
+    out = tgmm(x, g, _t(gs, dev))
+    ref = O.tgmm(x.float().cpu().numpy(), g.float().cpu().numpy(), gs)
+    _close(out.float().cpu().numpy(), ref, 2e-2)
+    for e in np.flatnonzero(gs == 0):
+        assert (out[int(e)] == 0).all()
+
+
+def test_gmm_bf16_sampled_mixtral_shape(dev):
+    """C2 gate_up shape (M=16384, Kin=4096, Kout=28672, E=8): sampled rows/columns vs float64."""
+    from mintext_amd.kernels import grouped_matmul_swiglu
+
+    M, E, D, I = 16384, 8, 4096, 14336
+    rng = np.random.default_rng(2)
+    gs = _groups(rng, M, E, "uniform")
+    gs[3] += 37
+    gs[5] -= 37
+    x = torch.randn(M, D, device=dev).bfloat16()
+    w = (torch.randn(E, D, 2 * I, device=dev) * 0.02).bfloat16()
+    y = grouped_matmul_swiglu(x, w, _t(gs, dev))
+    off = np.concatenate([[0], np.cumsum(gs)])
+    rows = np.sort(rng.choice(M, 48, replace=False))
+    cols = np.sort(rng.choice(I, 40, replace=False))
+    xs = x[torch.from_numpy(rows).to(dev)].float().cpu().numpy().astype(np.float64)
+    ref = np.empty((rows.size, cols.size))
+    for i, r in enumerate(rows):
+        e = int(np.searchsorted(off, r, side="right") - 1)
+        we = w[e].float()
+        gate = we[:, torch.from_numpy(cols).to(dev)].cpu().numpy().astype(np.float64)
+        up = we[:, torch.from_numpy(cols + I).to(dev)].cpu().numpy().astype(np.float64)
+        ref[i] = O.silu(xs[i] @ gate) * (xs[i] @ up)
+    got = y[torch.from_numpy(rows).to(dev)][:, torch.from_numpy(cols).to(dev)].float().cpu().numpy()
+    _close(got, ref, 2e-2)

@@ -1,0 +1,96 @@
+"""GPU parity: router top-k (HIP) vs the oracle and the HF-derived fixtures.
+
+Indices must be bit-exact.  Softmax mode selects on the logits, so its indices are exact for
+any input; sigmoid mode selects on float32 scores computed on the GPU, which can differ from
+numpy's sigmoid by an ulp, so its indices are checked bit-exactly against the oracle's
+selection run on the GPU's own scores (the scores themselves at 1e-6 relative).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def test_softmax_router_fixtures(dev):
+    from mintext_amd.kernels import route_topk
+
+    g = golden("routers")
+    for key, k in (("mixtral", 2), ("qwen", 8)):
+        idx, w = route_topk(torch.from_numpy(g[f"{key}_logits"]).to(dev), k, scoring="softmax")
+        np.testing.assert_array_equal(idx.cpu().numpy(), g[f"{key}_idx"])
+        np.testing.assert_allclose(w.cpu().numpy(), g[f"{key}_w"], rtol=1e-5, atol=1e-7)
+    idx, w = route_topk(torch.from_numpy(g["qwen_logits"]).to(dev), 8, scoring="softmax", norm_topk_prob=False)
+    np.testing.assert_array_equal(idx.cpu().numpy(), g["qwen_idx_nonorm"])
+    np.testing.assert_allclose(w.cpu().numpy(), g["qwen_w_nonorm"], rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("key", ["ds", "ds3"])
+def test_sigmoid_group_router_fixtures(dev, key):
+    from mintext_amd.kernels import route_topk
+
+    g = golden("routers")
+    idx, w, s = route_topk(torch.from_numpy(g[f"{key}_logits"]).to(dev), 8, scoring="sigmoid_group",
+                           bias=torch.from_numpy(g[f"{key}_bias"]), n_group=8, topk_group=4,
+                           routed_scaling_factor=2.5, return_scores=True)
+    s = s.cpu().numpy()
+    np.testing.assert_allclose(s, g[f"{key}_scores"], rtol=1e-6)
+    oi, ow, _ = O.router_sigmoid_group(None, 8, bias=g[f"{key}_bias"], n_group=8, topk_group=4,
+                                       routed_scaling_factor=2.5, scores=s)
+    np.testing.assert_array_equal(idx.cpu().numpy(), oi)
+    np.testing.assert_array_equal(idx.cpu().numpy(), g[f"{key}_idx"])
+    np.testing.assert_allclose(w.cpu().numpy(), ow, rtol=1e-5)
+
+
+@pytest.mark.parametrize("T,E,k,dt", [(16384, 128, 8, torch.bfloat16), (8192, 8, 2, torch.bfloat16),
+                                      (4096, 256, 8, torch.float32), (1000, 64, 6, torch.float32),
+                                      (777, 5, 3, torch.float32)])
+def test_softmax_router_large(dev, T, E, k, dt):
+    from mintext_amd.kernels import route_topk
+
+    logits = (torch.randn(T, E, device=dev) * 1.3).to(dt)
+    idx, w = route_topk(logits, k, scoring="softmax")
+    lg = logits.float().cpu().numpy()
+    oi, ow, _ = O.router_softmax(lg, k)
+    np.testing.assert_array_equal(idx.cpu().numpy(), oi)
+    np.testing.assert_allclose(w.cpu().numpy(), ow, rtol=1e-5, atol=1e-7)
+
+
+def test_softmax_router_ties_lower_index_first(dev):
+    from mintext_amd.kernels import route_topk
+
+    lg = np.random.default_rng(4).integers(0, 3, (512, 16)).astype(np.float32)  # heavy ties
+    idx, _ = route_topk(torch.from_numpy(lg).to(dev), 5, scoring="softmax")
+    np.testing.assert_array_equal(idx.cpu().numpy(), O.topk_desc(lg, 5))
+
+
+def test_deepseek_router_full_size(dev):
+    """C3 routing: T=4096, E=256, 8 groups / top-4, k=8, bias, scale 2.5."""
+    from mintext_amd.kernels import route_topk
+
+    T, E = 4096, 256
+    logits = torch.randn(T, E, device=dev).to(torch.bfloat16)
+    bias = torch.randn(E, device=dev) * 1e-3
+    idx, w, s = route_topk(logits, 8, scoring="sigmoid_group", bias=bias, n_group=8, topk_group=4,
+                           routed_scaling_factor=2.5, return_scores=True)
+    s = s.cpu().numpy()
+    np.testing.assert_allclose(s, O.sigmoid_f32(logits.float().cpu().numpy()), rtol=1e-6)
+    oi, ow, _ = O.router_sigmoid_group(None, 8, bias=bias.cpu().numpy(), n_group=8, topk_group=4,
+                                       routed_scaling_factor=2.5, scores=s)
+    np.testing.assert_array_equal(idx.cpu().numpy(), oi)
+    np.testing.assert_allclose(w.cpu().numpy(), ow, rtol=1e-5)
+
+
+def test_bias_steers_selection(dev):
+    """tests/test_model.py:468-478 of the reference: bias [10,0,0,0] always selects expert 0."""
+    from mintext_amd.kernels import route_topk
+
+    idx, _ = route_topk(torch.randn(64, 4, device=dev), 2, scoring="sigmoid_group",
+                        bias=torch.tensor([10.0, 0, 0, 0]), n_group=2, topk_group=1)
+    assert (idx[:, 0] == 0).all()
+    assert ((idx >= 0) & (idx < 4)).all()

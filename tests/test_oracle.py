@@ -1,0 +1,284 @@
+"""Pin the CPU oracle (oracle/moe_oracle.py) before trusting it as the GPU checker.
+
+Each oracle function is checked against something that does not share its code: golden
+fixtures written by tests/golden/make_golden.py from HF transformers, torch.sort(stable=True)
+and torch float64 matmuls; brute force on tiny inputs; closed forms and invariants.  A check
+that merely re-types the oracle's formula is avoided; each comparison is chosen so that a
+plausible slip (dropped bias, wrong tie order, transposed operand, unstable sort, wrong
+group offset) fails it.
+"""
+from __future__ import annotations
+
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden, rel_err
+from oracle import moe_oracle as O
+
+
+# ---------------------------------------------------------------------------- number formats
+def test_bf16_round_matches_torch():
+    x = np.random.default_rng(0).standard_normal(50000).astype(np.float32) * 30
+    x = np.concatenate([x, np.float32([0, -0.0, 1 + 2 ** -8, 1 + 3 * 2 ** -8, 65504, 3.4e38])])
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(O.bf16_round(x), ref)
+
+
+def test_e4m3_encode_matches_torch_fixture():
+    g = golden("fp8")
+    np.testing.assert_array_equal(O.e4m3_encode(g["values"]), g["codes"])
+
+
+def test_e4m3_decode_all_codes():
+    codes = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    got = O.e4m3_decode(codes)
+    both_nan = np.isnan(ref) & np.isnan(got)
+    np.testing.assert_array_equal(got[~both_nan], ref[~both_nan])
+    # every finite code round-trips
+    fin = ~np.isnan(ref)
+    np.testing.assert_array_equal(O.e4m3_encode(ref[fin]), codes[fin])
+
+
+def test_e4m3_saturates():
+    assert O.e4m3_encode(np.float32([1000.0]))[0] == 0x7E
+    assert O.e4m3_encode(np.float32([-470.0]))[0] == 0xFE
+
+
+# --------------------------------------------------------------------------------- routers
+def test_topk_ties_go_to_lower_index_bruteforce():
+    rng = np.random.default_rng(1)
+    vals = rng.integers(0, 3, size=(200, 6)).astype(np.float32)  # many ties
+    got = O.topk_desc(vals, 3)
+    for t in range(vals.shape[0]):
+        brute = sorted(range(6), key=lambda e: (-vals[t, e], e))[:3]
+        assert list(got[t]) == brute
+
+
+def test_softmax_router_matches_hf_mixtral():
+    g = golden("routers")
+    idx, w, _ = O.router_softmax(g["mixtral_logits"], 2)
+    np.testing.assert_array_equal(idx, g["mixtral_idx"])
+    np.testing.assert_allclose(w, g["mixtral_w"], rtol=1e-6, atol=1e-7)
+
+
+def test_softmax_router_matches_hf_qwen3():
+    g = golden("routers")
+    idx, w, _ = O.router_softmax(g["qwen_logits"], 8)
+    np.testing.assert_array_equal(idx, g["qwen_idx"])
+    np.testing.assert_allclose(w, g["qwen_w"], rtol=1e-6, atol=1e-7)
+    idx2, w2, _ = O.router_softmax(g["qwen_logits"], 8, norm_topk_prob=False)
+    np.testing.assert_array_equal(idx2, g["qwen_idx_nonorm"])
+    np.testing.assert_allclose(w2, g["qwen_w_nonorm"], rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("key", ["ds", "ds3"])
+def test_sigmoid_group_router_matches_hf_deepseek(key):
+    g = golden("routers")
+    idx, w, s = O.router_sigmoid_group(g[f"{key}_logits"], 8, bias=g[f"{key}_bias"], n_group=8, topk_group=4,
+                                       norm_topk_prob=True, routed_scaling_factor=2.5)
+    # sigmoid bits differ by a few ulp across libms; selection below is still exact
+    np.testing.assert_allclose(s, g[f"{key}_scores"], rtol=5e-7, atol=0)
+    np.testing.assert_array_equal(idx, g[f"{key}_idx"])
+    np.testing.assert_allclose(w, g[f"{key}_w"], rtol=1e-6)
+
+
+def test_group_limited_selection_bruteforce():
+    """Tiny E: enumerate group choices explicitly (moe.py:76-98 read as a definition)."""
+    rng = np.random.default_rng(7)
+    E, ng, tg, k = 8, 4, 2, 3
+    for _ in range(200):
+        s = rng.random((1, E)).astype(np.float32)
+        s[0, rng.integers(0, E)] = s[0, rng.integers(0, E)]  # occasional ties
+        b = (rng.standard_normal(E) * 0.05).astype(np.float32)
+        idx, _ = O.select_sigmoid_group(s, b, k, ng, tg)
+        r = (s[0] + b).astype(np.float32)
+        gsc = [float(np.float32(sorted(r[2 * q:2 * q + 2])[-1]) + np.float32(sorted(r[2 * q:2 * q + 2])[-2]))
+               for q in range(ng)]
+        groups = sorted(range(ng), key=lambda q: (-np.float32(gsc[q]), q))[:tg]
+        cand = [e for e in range(E) if e // 2 in groups]
+        best = sorted(cand, key=lambda e: (-r[e], e))[:k]
+        assert list(idx[0]) == best
+
+
+def test_bias_steers_selection():
+    """The reference's router test: bias [10,0,0,0] makes expert 0 always selected (test_model.py:468-478)."""
+    lg = np.random.default_rng(3).standard_normal((32, 4)).astype(np.float32)
+    idx, _, _ = O.router_sigmoid_group(lg, 2, bias=np.float32([10, 0, 0, 0]), n_group=2, topk_group=1)
+    assert (idx[:, 0] == 0).all()
+
+
+# -------------------------------------------------------------------------------- dispatch
+def _dispatch_cases():
+    g = golden("dispatch")
+    names = sorted({k.split("__")[0] for k in g.files})
+    return g, names
+
+
+def test_route_matches_torch_stable_sort_fixtures():
+    g, names = _dispatch_cases()
+    for n in names:
+        idx, E = g[f"{n}__idx"], int(g[f"{n}__E"])
+        K = idx.shape[1]
+        x = np.arange(idx.shape[0] * 3, dtype=np.float32).reshape(idx.shape[0], 3)
+        st, perm, gs = O.route(x, idx, E)
+        np.testing.assert_array_equal(perm, g[f"{n}__perm"], err_msg=n)
+        np.testing.assert_array_equal(gs, g[f"{n}__gs"], err_msg=n)
+        np.testing.assert_array_equal(st, x[g[f"{n}__perm"] // K])
+
+
+def test_counting_sort_equals_numpy_stable_argsort():
+    rng = np.random.default_rng(11)
+    for E in (1, 3, 8, 129, 256):
+        keys = rng.integers(0, E, 5000)
+        np.testing.assert_array_equal(O.stable_counting_sort(keys, E), np.argsort(keys, kind="stable"))
+
+
+def test_route_invariants_reference_tests():
+    """tests/test_moe_kernels.py:47-60: sum(gs) == N*K and expert ids non-decreasing."""
+    rng = np.random.default_rng(5)
+    idx = rng.integers(0, 4, (32, 2))
+    _, perm, gs = O.route(np.zeros((32, 1)), idx, 4)
+    assert gs.sum() == 64
+    assert (np.diff(idx.ravel()[perm]) >= 0).all()
+    # stability: within one expert the flat positions ascend
+    e_sorted = idx.ravel()[perm]
+    for e in range(4):
+        assert (np.diff(perm[e_sorted == e]) > 0).all()
+
+
+def test_unroute_closed_form():
+    """unroute(route(x)) with weights w gives sum_k w[n,k] * x[n] (combine of K copies)."""
+    rng = np.random.default_rng(6)
+    N, D, K, E = 50, 7, 3, 5
+    x = rng.standard_normal((N, D))
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(N)])
+    w = rng.random((N, K))
+    st, perm, _ = O.route(x, idx, E)
+    np.testing.assert_allclose(O.unroute(st, perm, w, K), x * w.sum(1, keepdims=True), rtol=1e-12)
+    np.testing.assert_allclose(O.unroute_f32(st, perm, w, K), x * w.sum(1, keepdims=True), rtol=1e-5)
+
+
+def test_invert_permutation_is_argsort():
+    p = np.random.default_rng(8).permutation(1000)
+    np.testing.assert_array_equal(O.invert_permutation(p), np.argsort(p))
+
+
+# ------------------------------------------------------------------------------------- gmm
+def _gmm_cases():
+    g = golden("gmm")
+    return g, sorted({k.split("__")[0] for k in g.files})
+
+
+def test_gmm_dlhs_tgmm_match_torch_fixtures():
+    g, names = _gmm_cases()
+    for n in names:
+        gs, x, w, gr = g[f"{n}__gs"], g[f"{n}__x"], g[f"{n}__w"], g[f"{n}__g"]
+        np.testing.assert_allclose(O.gmm(x, w, gs), g[f"{n}__out"], rtol=1e-12, atol=1e-12, err_msg=n)
+        np.testing.assert_allclose(O.gmm_dlhs(gr, w, gs), g[f"{n}__dlhs"], rtol=1e-12, atol=1e-12, err_msg=n)
+        np.testing.assert_allclose(O.tgmm(x, gr, gs), g[f"{n}__tgmm"], rtol=1e-12, atol=1e-12, err_msg=n)
+
+
+def test_tgmm_empty_group_exact_zero():
+    x = np.ones((16, 4))
+    g = np.ones((16, 4))
+    out = O.tgmm(x, g, [8, 0, 8])
+    assert (out[1] == 0).all() and (out[0] == 8).all()
+
+
+def test_gmm_rows_past_group_sum_are_zero():
+    out = O.gmm(np.ones((10, 3)), np.ones((2, 3, 2)), [4, 3])
+    assert (out[7:] == 0).all() and (out[:7] == 3).all()
+
+
+def test_gmm_vjp_identities():
+    """<gmm(x,W), g> = <x, dlhs(g,W)> = sum_e <W_e, tgmm(x,g)_e> (adjointness pins both VJPs)."""
+    rng = np.random.default_rng(9)
+    gs = [5, 0, 7, 3]
+    x = rng.standard_normal((15, 6))
+    W = rng.standard_normal((4, 6, 4))
+    g = rng.standard_normal((15, 4))
+    lhs = np.sum(O.gmm(x, W, gs) * g)
+    assert np.isclose(lhs, np.sum(x * O.gmm_dlhs(g, W, gs)), rtol=1e-12)
+    assert np.isclose(lhs, np.sum(W * O.tgmm(x, g, gs)), rtol=1e-12)
+
+
+def test_swiglu_and_bwd():
+    rng = np.random.default_rng(10)
+    h = rng.standard_normal((5, 8))
+    y = O.swiglu(h)
+    np.testing.assert_allclose(y, h[:, :4] / (1 + np.exp(-h[:, :4])) * h[:, 4:], rtol=1e-14)
+    dy = rng.standard_normal((5, 4))
+    dh = O.swiglu_bwd(h, dy)
+    eps = 1e-6
+    for i, j in itertools.product(range(5), range(8)):
+        hp, hm = h.copy(), h.copy()
+        hp[i, j] += eps
+        hm[i, j] -= eps
+        num = np.sum((O.swiglu(hp) - O.swiglu(hm)) * dy) / (2 * eps)
+        assert abs(num - dh[i, j]) < 1e-6
+
+
+# ------------------------------------------------------------------------------------- fp8
+def test_quant_rows_roundtrip_bound():
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((16, 512)).astype(np.float32) * 3
+    q, s = O.quant_fp8_rows(x)
+    assert q.dtype == np.uint8 and s.shape == (16, 4)
+    # the group max maps exactly to +-448
+    amax_codes = np.abs(O.e4m3_decode(q).reshape(16, 4, 128)).max(-1)
+    np.testing.assert_array_equal(amax_codes, 448.0)
+    # e4m3 has 3 mantissa bits: relative error <= 2^-4 per normal element
+    deq = O.dequant_rows(q, s)
+    big = np.abs(x) > 2.0 ** -6 * s.repeat(128, axis=1)
+    assert (np.abs(deq - x)[big] <= np.abs(x)[big] * 2.0 ** -4 + 1e-12).all()
+
+
+def test_quant_weights_layout_and_dequant():
+    rng = np.random.default_rng(13)
+    w = rng.standard_normal((2, 256, 384)).astype(np.float32) * 0.02
+    wq, ws = O.quant_fp8_weights(w)
+    assert wq.shape == (2, 384, 256) and ws.shape == (2, 3, 2)
+    # block (e=1, kin-block 1, kout-block 2) scale is its amax / 448
+    assert np.isclose(ws[1, 2, 1], np.abs(w[1, 128:256, 256:384]).max() / 448.0, rtol=1e-7)
+    # transposed layout: wq[e, n, k] encodes w[e, k, n]
+    np.testing.assert_array_equal(wq[0, 5, 7], O.e4m3_encode(np.float32(w[0, 7, 5] / ws[0, 0, 0])))
+    assert rel_err(O.dequant_weights(wq, ws), w) < 0.04
+
+
+def test_gmm_fp8_equals_dequantised_gmm():
+    rng = np.random.default_rng(14)
+    gs = [40, 0, 88]
+    x = rng.standard_normal((128, 256)).astype(np.float32)
+    w = (rng.standard_normal((3, 256, 128)) * 0.05).astype(np.float32)
+    xq, xs = O.quant_fp8_rows(x)
+    wq, ws = O.quant_fp8_weights(w)
+    got = O.gmm_fp8(xq, xs, wq, ws, gs)
+    assert rel_err(got, O.gmm(x, w, gs)) < 6e-2
+
+
+# ---------------------------------------------------------------------------- composition
+def test_tiny_moe_layer_matches_hf_mixtral():
+    """C1 (T=256, D=128, E=8, K=2, I=256): oracle router + experts == HF MixtralSparseMoeBlock (float64)."""
+    g = golden("moe_tiny")
+    rng = np.random.default_rng(1)
+    T, D, E, I = 256, 128, 8, 256
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    rng.standard_normal((D, E))  # gate weights (the fixture stores the logits)
+    gate_up = (rng.standard_normal((E, D, 2 * I)) * 0.02).astype(np.float32)
+    down = (rng.standard_normal((E, I, D)) * 0.02).astype(np.float32)
+    idx, w, _ = O.router_softmax(g["logits"], 2)
+    np.testing.assert_array_equal(idx, g["idx"])
+    out = O.moe_experts(x, idx, w, gate_up, down)
+    np.testing.assert_allclose(out, g["out"], rtol=1e-5, atol=1e-7)
+
+
+def test_planted_mistake_is_caught():
+    """A transposed-operand slip in the GEMM (a plausible bug) fails the fixture comparison."""
+    g = golden("gmm")
+    gs, x, w = g["uniform_e4__gs"], g["uniform_e4__x"], g["uniform_e4__w"]
+    wrong = O.gmm(x, w[::-1], gs)  # experts in reversed order
+    assert rel_err(wrong, g["uniform_e4__out"]) > 0.5
