@@ -230,8 +230,7 @@ def run(cfg_name, steps, warmup, cpu_baseline=True):
     gu_ms, dn_ms = t_gu.mean_ms(), t_dn.mean_ms()
     peak = PEAK_FP8_TFLOPS if fp8 else PEAK_BF16_TFLOPS
     if cfg_name == "qwen3_bwd":
-        kern_flops = 2 * (2.0 * M * I * D) + 0  # dlhs pair: [M,D]x[D..]: 2*M*D*I + 2*M*2I*D
-        kern_flops = 2.0 * M * D * I + 2.0 * M * 2 * I * D
+        kern_flops = 2.0 * M * D * I + 2.0 * M * 2 * I * D  # both dlhs GEMMs
         achieved = kern_flops / (gu_ms * 1e-3) / 1e12
         dominant = "gmm_dlhs (both expert GEMMs)"
     else:
@@ -285,7 +284,21 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="mixtral", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 3 plain 256 MiB device copies (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     a = ap.parse_args(argv)
+    if a.copy_calibration:
+        import torch
+
+        n = 256 << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda")
+        src.fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "dispatches": 3}))
+        return 0
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (no expert parallelism or "
               "collectives); run with --gpus 1", file=sys.stderr)

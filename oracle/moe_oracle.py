@@ -375,3 +375,18 @@ def moe_experts(x, topk_indices, topk_weights, gate_up, down) -> np.ndarray:
     h = gmm(sorted_tokens, gate_up, gs)
     y = gmm(swiglu(h), down, gs)
     return unroute(y, perm, topk_weights, k)
+
+
+def moe_experts_fp8(x, topk_indices, topk_weights, gu_q, gu_s, dn_q, dn_s) -> np.ndarray:
+    """The blockwise-fp8 expert layer with the kernels' quantisation points: x quantised in
+    1x128 groups, routed with its scales, fp8 gate_up GEMM, SwiGLU, re-quantisation of the
+    SwiGLU output in 1x128 groups, fp8 down GEMM rounded to bf16, float64 combine."""
+    k = np.asarray(topk_indices).shape[1]
+    E = np.asarray(gu_q).shape[0]
+    xq, xs = quant_fp8_rows(np.asarray(x, np.float32))
+    sq, perm, gs = route(xq, topk_indices, E)
+    ss = xs[perm // k]
+    y = swiglu(gmm_fp8(sq, ss, gu_q, gu_s, gs)).astype(np.float32)
+    yq, ys = quant_fp8_rows(y)
+    o = bf16_round(gmm_fp8(yq, ys, dn_q, dn_s, gs).astype(np.float32))
+    return unroute(o, perm, topk_weights, k)

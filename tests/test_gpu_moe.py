@@ -68,9 +68,17 @@ def test_fp8_layer_matches_oracle(dev):
     guq, gus = quantize_fp8_weights(gate_up)
     dnq, dns = quantize_fp8_weights(down)
     out = moe_experts_forward_fp8(x, idx, w, guq, gus, dnq, dns)
+    u8 = lambda t: t.view(torch.uint8).cpu().numpy()
+    # same quantisation points as the kernels: only f32-vs-f64 accumulation, the bf16 output
+    # rounding and the resulting one-step code flips in the re-quantisation differ
+    ref_q = O.moe_experts_fp8(x.float().cpu().numpy(), idx.cpu().numpy(), w.cpu().numpy(), u8(guq), gus.cpu().numpy(),
+                              u8(dnq), dns.cpu().numpy())
+    assert rel_err(out.cpu().numpy(), ref_q) < 2e-2
+    # against the unquantised float64 layer: each GEMM is within 6e-2 (test_gpu_fp8); the layer
+    # quantises activations twice in series (x, then the SwiGLU output), so its bound is 1e-1
     ref = O.moe_experts(x.float().cpu().numpy(), idx.cpu().numpy(), w.cpu().numpy(), gate_up.float().cpu().numpy(),
                         down.float().cpu().numpy())
-    assert rel_err(out.cpu().numpy(), ref) < 6e-2
+    assert rel_err(out.cpu().numpy(), ref) < 1e-1
 
 
 def test_block_backward_matches_oracle(dev):
