@@ -24,6 +24,7 @@
 // f32 path (and shapes the MFMA tiling does not cover): an LDS-tiled exact-fp32 FMA kernel.
 #include "common.h"
 #include <type_traits>
+#include <algorithm>
 
 namespace mtx {
 
@@ -116,7 +117,10 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
     t.pad = 0;
     tiles[s_total[1] + e] = t;
   }
-  if (e == 0) count[0] = s_total[1] + ntail;
+  if (e == 0) {
+    count[0] = s_total[1] + ntail;
+    count[1] = s_total[1];  // tiles with an expert (the rest are zero tiles)
+  }
   // expert order by descending group size (ties: lower id first), used by tgmm
   if (e < E) {
     int rank = 0;
@@ -600,6 +604,241 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_mfma_kernel(Args p) {
   }
 }
 
+// Epilogue helpers of the MFMA path (bf16 outputs).
+__device__ __forceinline__ uint16_t bf16_bits_hw(float f) {
+  const __bf16 h = (__bf16)f;  // v_cvt_pk_bf16_f32: round-to-nearest-even
+  return __builtin_bit_cast(uint16_t, h);
+}
+// silu(g) * u with the hardware exp2 / reciprocal (about 1e-6 relative; used for bf16 outputs).
+__device__ __forceinline__ float swiglu_fast(float g, float u) {
+  return g * u * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
+
+
+// ---- v3: direct-to-LDS loads, 4-stage ring, transpose reads (FWD / SWIGLU / DLHS) ----------------
+// 256x256 output tile, 8 waves (2 per SIMD) with 128x64 wave tiles, BK = 32.  Every global
+// load is a global_load_lds_dwordx4 straight into a 4-deep LDS ring (no staging registers, no
+// ds_write, no VALU transposes); stage s is loaded three steps before it is consumed.  Layouts
+// per stage (32 KB):
+//   A   : 256 rows x 64 B (k-contiguous), 16-byte chunk c of row r at chunk c ^ ((r>>2)&3)
+//   W   : FWD: 32 k-rows x 512 B (n-contiguous, as in HBM), chunk c of row k at c ^ 4(k&3);
+//         the MFMA operand (8 consecutive k of one n per lane) is assembled with two
+//         ds_read_b64_tr_b16, whose 16-lane groups return B[k0+j][n0+lane] for j = 0..3 when
+//         lane r of the group addresses B[k0 + r/4][n0 + 4(r%4)].
+//         DLHS: 256 n-rows x 64 B like A.
+// Each lane of a load instruction writes LDS byte (M0 + 16*lane), so the swizzle is realised by
+// choosing the global source of each lane.  Both swizzles make the fragment reads conflict-free.
+namespace v3 {
+constexpr int BM = 256, BN = 256, BKS = 32, NSTAGE = 4;
+constexpr int A_BYTES = BM * BKS * 2, B_BYTES = BN * BKS * 2, STAGE = A_BYTES + B_BYTES;
+__device__ __forceinline__ int a_off(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
+__device__ __forceinline__ int bn_off(int k, int c) { return k * 512 + ((c ^ ((k & 3) << 2)) << 4); }
+}  // namespace v3
+
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+typedef __attribute__((address_space(3))) char lds_char;
+// 16-byte direct global->LDS load: lane l writes LDS byte lds_base + 16*l (lds_base is
+// wave-uniform).  Issued as inline asm so that the compiler does not serialise the LDS reads
+// of other ring stages behind these loads; the kernel waits for them with MTX_VMCNT.
+__device__ __forceinline__ void gload_lds16(const void* gptr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base)
+               : "memory", "m0");
+}
+// s_waitcnt immediate (GFX9 encoding) that waits for vmcnt <= N only.
+#define MTX_VMCNT(N) ((((N) & 0xF)) | (0x7 << 4) | (0xF << 8) | ((((N) >> 4) & 0x3) << 14))
+typedef __attribute__((address_space(1))) const char gbl_char;
+
+template <int MODE, int EPI, int WM, int WN>
+__global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
+  using namespace v3;
+  constexpr int NT = WM * WN * 64;
+  constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
+  constexpr int A_INSTR = A_BYTES / 1024 / (NT / 64);  // load instructions per wave per stage
+  constexpr int B_INSTR = B_BYTES / 1024 / (NT / 64);
+  static_assert(MODE == FWD || MODE == DLHS, "v3 covers the forward and dlhs GEMMs");
+  constexpr bool B_T = (MODE == FWD);
+  __shared__ __attribute__((aligned(1024))) char lds[NSTAGE * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  const int nn = (EPI == EPI_SWIGLU) ? (p.I / (BN / 2)) : (p.N / BN);
+  const int cnt = p.count[0];
+  const int total = cnt * nn;
+  const int pid = blockIdx.x;
+  const int total8 = (total + 7) & ~7;
+  if (pid >= total8) return;
+  const int lid = (pid & 7) * (total8 >> 3) + (pid >> 3);
+  if (lid >= total) return;
+  constexpr int GM = 8;
+  const int grp = lid / (GM * nn);
+  const int first_m = grp * GM;
+  const int gsz = min(GM, cnt - first_m);
+  const int local = lid - grp * GM * nn;
+  const int mt = first_m + local % gsz;
+  const int n_tile = local / gsz;
+  const MTile t = p.tiles[mt];
+  const int e = t.e, r0 = t.r0, r1 = t.r1;
+  const int col0 = n_tile * BN;
+  if (e < 0) {
+    const int ncols = (EPI == EPI_SWIGLU) ? BN / 2 : BN;
+    const int c0 = (EPI == EPI_SWIGLU) ? n_tile * (BN / 2) : col0;
+    for (int i = tid; i < BM * ncols; i += NT) {
+      const int r = r0 + i / ncols;
+      if (r < r1) p.C[(int64_t)r * p.ldc + c0 + i % ncols] = 0;
+    }
+    return;
+  }
+
+  // ---- per-lane global sources of the load instructions (byte offsets at k-step 0) -----
+  const char* Ab = (const char*)p.A;
+  const char* Bb = (const char*)(p.B + (int64_t)e * p.Kred * p.N);
+  uint32_t aoff[A_INSTR], boff[B_INSTR];
+#pragma unroll
+  for (int i = 0; i < A_INSTR; ++i) {
+    const int seg = wave * A_INSTR + i;            // 1 KB segment of the A region
+    const int r = seg * 16 + (lane >> 2), pc = lane & 3;
+    const int c = pc ^ ((r >> 2) & 3);
+    int gr = r0 + r;
+    gr = gr < p.M ? gr : p.M - 1;
+    aoff[i] = ((uint32_t)gr * (uint32_t)p.Kred + (uint32_t)(c * 8)) * 2u;
+  }
+#pragma unroll
+  for (int i = 0; i < B_INSTR; ++i) {
+    const int seg = wave * B_INSTR + i;
+    if (B_T) {
+      const int k = seg * 2 + (lane >> 5), pc = lane & 31;
+      const int c = pc ^ ((k & 3) << 2);
+      const int tc = c * 8;  // tile-local column
+      int gc;
+      if (EPI == EPI_SWIGLU) {
+        const int w_ = tc / WTN, within = tc % WTN;
+        const int half = within / (WTN / 2), o = within % (WTN / 2);
+        gc = half * p.I + n_tile * (BN / 2) + w_ * (WTN / 2) + o;
+      } else {
+        gc = col0 + tc;
+      }
+      boff[i] = ((uint32_t)k * (uint32_t)p.N + (uint32_t)gc) * 2u;
+    } else {
+      const int r = seg * 16 + (lane >> 2), pc = lane & 3;
+      const int c = pc ^ ((r >> 2) & 3);
+      boff[i] = ((uint32_t)(col0 + r) * (uint32_t)p.Kred + (uint32_t)(c * 8)) * 2u;
+    }
+  }
+  const uint32_t a_step = BKS * 2;
+  const uint32_t b_step = B_T ? (uint32_t)BKS * (uint32_t)p.N * 2u : (uint32_t)BKS * 2u;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_char*)lds;
+  const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+  auto issue_stage = [&](int kt) {
+    const uint32_t st = lds_base + (uint32_t)((kt & (NSTAGE - 1)) * STAGE);
+#pragma unroll
+    for (int i = 0; i < A_INSTR; ++i)
+      gload_lds16(Ab + aoff[i] + (uint32_t)kt * a_step, st + (wave_u * A_INSTR + i) * 1024u);
+#pragma unroll
+    for (int i = 0; i < B_INSTR; ++i)
+      gload_lds16(Bb + boff[i] + (uint32_t)kt * b_step, st + (uint32_t)A_BYTES + (wave_u * B_INSTR + i) * 1024u);
+  };
+
+  // ---- fragments ---------------------------------------------------------------------
+  bf16x8 fa[2][TM], fb[2][TN];
+  const int frow = lane & 31, fhalf = lane >> 5;
+  auto read_frags = [&](int kt, int kk, int buf) {
+    const char* st = lds + (kt & (NSTAGE - 1)) * STAGE;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = wm * WTM + i * 32 + frow;
+      fa[buf][i] = *(const bf16x8*)(st + a_off(r, kk * 2 + fhalf));
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      if (B_T) {
+        const int n = wn * WTN + j * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+        const int k = kk * 16 + 8 * fhalf + ((lane & 15) >> 2);
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(st + A_BYTES + bn_off(k, n >> 3) + (n & 7) * 2));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(st + A_BYTES + bn_off(k + 4, n >> 3) + (n & 7) * 2));
+        const s16x4 both[2] = {lo, hi};
+        fb[buf][j] = __builtin_bit_cast(bf16x8, both);
+      } else {
+        const int r = wn * WTN + j * 32 + frow;
+        fb[buf][j] = *(const bf16x8*)(st + A_BYTES + a_off(r, kk * 2 + fhalf));
+      }
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  const int nk = p.Kred / BKS;
+  constexpr int LPS = A_INSTR + B_INSTR;  // load instructions per stage per thread
+  // prologue: stages 0..2 in flight; stages 0 and 1 landed and visible
+  issue_stage(0);
+  if (nk > 1) issue_stage(1);
+  if (nk > 2) issue_stage(2);
+  if (nk > 2) __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS));  // (vmcnt counts outstanding loads)
+  else __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));
+  __syncthreads();
+  read_frags(0, 0, 0);
+
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 3 < nk) issue_stage(kt + 3);
+    // substep 0: prefetch substep 1 of this stage
+    read_frags(kt, 1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[0][i], fb[0][j], acc[i][j], 0, 0, 0);
+    // substep 1: prefetch substep 0 of the next stage (visible since the last barrier).  On
+    // the last step this reads an unused ring slot: in bounds, and branch-free so that the
+    // MFMAs below only wait for the fragments they use.
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(kt + 1, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[1][i], fb[1][j], acc[i][j], 0, 0, 0);
+    // stage kt+2 must have landed before the barrier makes it visible to every wave
+    if (kt + 3 < nk) __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS));
+    else __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));
+    __syncthreads();
+  }
+
+  const int ccol = lane & 31, rhalf = (lane >> 5) * 4;
+  if (EPI == EPI_SWIGLU) {
+    const int ycol0 = n_tile * (BN / 2) + wn * (WTN / 2);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN / 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = r0 + wm * WTM + i * 32 + 8 * (v >> 2) + rhalf + (v & 3);
+          if (row < r1) {
+            const float gt = acc[i][j][v], up = acc[i][j + TN / 2][v];
+            p.C[(int64_t)row * p.ldc + ycol0 + j * 32 + ccol] = bf16_bits_hw(swiglu_fast(gt, up));
+          }
+        }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = r0 + wm * WTM + i * 32 + 8 * (v >> 2) + rhalf + (v & 3);
+          if (row < r1) p.C[(int64_t)row * p.ldc + col0 + wn * WTN + j * 32 + ccol] = bf16_bits_hw(acc[i][j][v]);
+        }
+  }
+}
+
 }  // namespace mf
 
 // ---- host-side dispatch ----------------------------------------------------------------------
@@ -610,6 +849,20 @@ struct MfmaCfg {
 static int launch_build_tiles(const int32_t* gs, int64_t E, int64_t M, int BM, const GmmWs& w, hipStream_t st) {
   hipLaunchKernelGGL(build_tiles_kernel, dim3(1), dim3(1024), 0, st, gs, (int)E, (int)M, BM, w.count, w.offsets,
                      w.order, w.tiles);
+  return check_launch();
+}
+
+#ifndef MTX_V3_WM
+#define MTX_V3_WM 2
+#define MTX_V3_WN 4
+#endif
+
+template <int MODE, int EPI>
+static int launch_v3(const mf::Args& a, int64_t grid, hipStream_t st) {
+  if (grid <= 0) return MTX_OK;
+  grid = round_up(grid, 8);
+  hipLaunchKernelGGL((mf::gmm_v3_kernel<MODE, EPI, MTX_V3_WM, MTX_V3_WN>), dim3((unsigned)grid),
+                     dim3(MTX_V3_WM * MTX_V3_WN * 64), 0, st, a);
   return check_launch();
 }
 
@@ -631,6 +884,10 @@ static int common_checks(int64_t M, int64_t E, void* ws, int64_t ws_bytes, int64
 
 // Smallest m-tile any path uses is 64 rows, so the workspace bound uses BM = 64.
 static constexpr int kMinBM = 64;
+
+// The large-group path (mean group >= 192 rows) uses the 256x256 direct-to-LDS kernel.
+#define MTX_BIG_BM 256
+#define MTX_BIG_BN 256
 
 // FWD / DLHS / SWIGLU driver. mode: 0 fwd, 1 dlhs, 2 swiglu
 static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs, int dtype, int64_t M, int64_t Kred,
@@ -663,24 +920,24 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
     a.I = (int)I;
     a.E = (int)E;
     // tile shape: 256-row tiles when groups are large on average, else 128
-    const bool big_m = (M / E) >= 192;
+    const bool big_m = (M / E) >= 192 && Kred % mf::v3::BKS == 0 && M * Kred * 2 < (int64_t(1) << 32) &&
+                       Kred * Nout * 2 < (int64_t(1) << 32);
     if (mode == 2 && I % 128 == 0) {
-      if (big_m) {
-        rc = launch_build_tiles(gs, E, M, 256, wsp, st);
+      if (big_m && I % (MTX_BIG_BN / 2) == 0) {
+        rc = launch_build_tiles(gs, E, M, MTX_BIG_BM, wsp, st);
         if (rc) return rc;
-        return launch_mfma<256, 256, 2, 2, mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 256) * (I / 128), st);
+        return launch_v3<mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, MTX_BIG_BM) * (I / (MTX_BIG_BN / 2)), st);
       }
       rc = launch_build_tiles(gs, E, M, 128, wsp, st);
       if (rc) return rc;
       return launch_mfma<128, 256, 1, 2, mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 128) * (I / 128), st);
     }
     if (mode != 2 && Nout % 256 == 0) {
-      if (big_m) {
-        rc = launch_build_tiles(gs, E, M, 256, wsp, st);
+      if (big_m && Nout % MTX_BIG_BN == 0) {
+        rc = launch_build_tiles(gs, E, M, MTX_BIG_BM, wsp, st);
         if (rc) return rc;
-        const int64_t grid = gmm_max_tiles(M, E, 256) * (Nout / 256);
-        return mode == 0 ? launch_mfma<256, 256, 2, 2, mf::FWD, mf::EPI_STORE>(a, grid, st)
-                         : launch_mfma<256, 256, 2, 2, mf::DLHS, mf::EPI_STORE>(a, grid, st);
+        const int64_t grid = gmm_max_tiles(M, E, MTX_BIG_BM) * (Nout / MTX_BIG_BN);
+        return mode == 0 ? launch_v3<mf::FWD, mf::EPI_STORE>(a, grid, st) : launch_v3<mf::DLHS, mf::EPI_STORE>(a, grid, st);
       }
       rc = launch_build_tiles(gs, E, M, 128, wsp, st);
       if (rc) return rc;
