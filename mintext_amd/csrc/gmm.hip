@@ -655,58 +655,99 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
   constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
   constexpr int A_INSTR = A_BYTES / 1024 / (NT / 64);  // load instructions per wave per stage
   constexpr int B_INSTR = B_BYTES / 1024 / (NT / 64);
-  static_assert(MODE == FWD || MODE == DLHS, "v3 covers the forward and dlhs GEMMs");
-  constexpr bool B_T = (MODE == FWD);
+  static_assert(MODE == FWD || MODE == DLHS || MODE == TGMM, "v3 mode");
+  constexpr bool A_T = (MODE == TGMM);                 // A tile stored [reduction][row] (transpose reads)
+  constexpr bool B_T = (MODE == FWD || MODE == TGMM);  // B tile stored [reduction][col]
   __shared__ __attribute__((aligned(1024))) char lds[NSTAGE * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
-  const int nn = (EPI == EPI_SWIGLU) ? (p.I / (BN / 2)) : (p.N / BN);
-  const int cnt = p.count[0];
-  const int total = cnt * nn;
-  const int pid = blockIdx.x;
-  const int total8 = (total + 7) & ~7;
-  if (pid >= total8) return;
-  const int lid = (pid & 7) * (total8 >> 3) + (pid >> 3);
-  if (lid >= total) return;
-  constexpr int GM = 8;
-  const int grp = lid / (GM * nn);
-  const int first_m = grp * GM;
-  const int gsz = min(GM, cnt - first_m);
-  const int local = lid - grp * GM * nn;
-  const int mt = first_m + local % gsz;
-  const int n_tile = local / gsz;
-  const MTile t = p.tiles[mt];
-  const int e = t.e, r0 = t.r0, r1 = t.r1;
-  const int col0 = n_tile * BN;
-  if (e < 0) {
-    const int ncols = (EPI == EPI_SWIGLU) ? BN / 2 : BN;
-    const int c0 = (EPI == EPI_SWIGLU) ? n_tile * (BN / 2) : col0;
-    for (int i = tid; i < BM * ncols; i += NT) {
-      const int r = r0 + i / ncols;
-      if (r < r1) p.C[(int64_t)r * p.ldc + c0 + i % ncols] = 0;
+  // ---- which output tile --------------------------------------------------------------
+  // FWD/DLHS: rows [r0,r1) of A, output columns from col0.  TGMM: reduction rows [r0,r1) of
+  // x and g (expert e's group), output block dW[e][row0:+BM][col0:+BN]; experts are visited
+  // in descending group size so that the longest reductions start first.
+  int e, r0, r1, col0, n_tile, row0 = 0;
+  if constexpr (MODE == TGMM) {
+    const int ntiles = p.N / BN, per_e = (p.Kd / BM) * ntiles;
+    const int lid = blockIdx.x;
+    if (lid >= p.E * per_e) return;
+    e = p.order[lid / per_e];
+    const int rem = lid % per_e;
+    row0 = (rem / ntiles) * BM;
+    n_tile = rem % ntiles;
+    col0 = n_tile * BN;
+    r0 = p.offsets[e];
+    r1 = p.offsets[e + 1];
+    if (r1 <= r0) {  // empty group: dW[e] = 0
+      uint16_t* out = p.C + (int64_t)e * p.Kd * p.N;
+      for (int i = tid; i < BM * BN / 8; i += NT) {
+        const int r = i / (BN / 8), c = (i % (BN / 8)) * 8;
+        *(u32x4*)(out + (int64_t)(row0 + r) * p.N + col0 + c) = u32x4{0u, 0u, 0u, 0u};
+      }
+      return;
     }
-    return;
+  } else {
+    const int nn = (EPI == EPI_SWIGLU) ? (p.I / (BN / 2)) : (p.N / BN);
+    const int cnt = p.count[0];
+    const int total = cnt * nn;
+    const int pid = blockIdx.x;
+    const int total8 = (total + 7) & ~7;
+    if (pid >= total8) return;
+    const int lid = (pid & 7) * (total8 >> 3) + (pid >> 3);
+    if (lid >= total) return;
+    constexpr int GM = 8;
+    const int grp = lid / (GM * nn);
+    const int first_m = grp * GM;
+    const int gsz = min(GM, cnt - first_m);
+    const int local = lid - grp * GM * nn;
+    const int mt = first_m + local % gsz;
+    n_tile = local / gsz;
+    const MTile t = p.tiles[mt];
+    e = t.e;
+    r0 = t.r0;
+    r1 = t.r1;
+    col0 = n_tile * BN;
+    if (e < 0) {
+      const int ncols = (EPI == EPI_SWIGLU) ? BN / 2 : BN;
+      const int c0 = (EPI == EPI_SWIGLU) ? n_tile * (BN / 2) : col0;
+      for (int i = tid; i < BM * ncols; i += NT) {
+        const int r = r0 + i / ncols;
+        if (r < r1) p.C[(int64_t)r * p.ldc + c0 + i % ncols] = 0;
+      }
+      return;
+    }
   }
 
   // ---- per-lane global sources of the load instructions (byte offsets at k-step 0) -----
+  // A row-major operand (FWD/DLHS): lane l of segment s fills row 16s + l/4, chunk slot l%4.
+  // Transposed operands (W in FWD, x and g in TGMM): lane l fills reduction row 2s + l/32,
+  // chunk slot l%32.  TGMM rows are expert-relative and clamped to M-1 at issue time (the
+  // reduction tail past r1 is zeroed in the fragments).
   const char* Ab = (const char*)p.A;
-  const char* Bb = (const char*)(p.B + (int64_t)e * p.Kred * p.N);
+  const char* Bb = (MODE == TGMM) ? (const char*)p.B : (const char*)(p.B + (int64_t)e * p.Kred * p.N);
   uint32_t aoff[A_INSTR], boff[B_INSTR];
+  int arow[A_T ? A_INSTR : 1], brow[(MODE == TGMM) ? B_INSTR : 1];
 #pragma unroll
   for (int i = 0; i < A_INSTR; ++i) {
-    const int seg = wave * A_INSTR + i;            // 1 KB segment of the A region
-    const int r = seg * 16 + (lane >> 2), pc = lane & 3;
-    const int c = pc ^ ((r >> 2) & 3);
-    int gr = r0 + r;
-    gr = gr < p.M ? gr : p.M - 1;
-    aoff[i] = ((uint32_t)gr * (uint32_t)p.Kred + (uint32_t)(c * 8)) * 2u;
+    const int seg = wave * A_INSTR + i;  // 1 KB segment of the A region
+    if constexpr (A_T) {
+      const int k = seg * 2 + (lane >> 5), pc = lane & 31;
+      const int c = pc ^ ((k & 3) << 2);
+      arow[i] = r0 + k;
+      aoff[i] = (uint32_t)(row0 + c * 8) * 2u;
+    } else {
+      const int r = seg * 16 + (lane >> 2), pc = lane & 3;
+      const int c = pc ^ ((r >> 2) & 3);
+      int gr = r0 + r;
+      gr = gr < p.M ? gr : p.M - 1;
+      aoff[i] = ((uint32_t)gr * (uint32_t)p.Kred + (uint32_t)(c * 8)) * 2u;
+    }
   }
 #pragma unroll
   for (int i = 0; i < B_INSTR; ++i) {
     const int seg = wave * B_INSTR + i;
-    if (B_T) {
+    if constexpr (B_T) {
       const int k = seg * 2 + (lane >> 5), pc = lane & 31;
       const int c = pc ^ ((k & 3) << 2);
       const int tc = c * 8;  // tile-local column
@@ -718,7 +759,12 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
       } else {
         gc = col0 + tc;
       }
-      boff[i] = ((uint32_t)k * (uint32_t)p.N + (uint32_t)gc) * 2u;
+      if constexpr (MODE == TGMM) {
+        brow[i] = r0 + k;
+        boff[i] = (uint32_t)gc * 2u;
+      } else {
+        boff[i] = ((uint32_t)k * (uint32_t)p.N + (uint32_t)gc) * 2u;
+      }
     } else {
       const int r = seg * 16 + (lane >> 2), pc = lane & 3;
       const int c = pc ^ ((r >> 2) & 3);
@@ -729,42 +775,77 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
   const uint32_t b_step = B_T ? (uint32_t)BKS * (uint32_t)p.N * 2u : (uint32_t)BKS * 2u;
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_char*)lds;
   const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+  const int mlast = p.M - 1;
   auto issue_stage = [&](int kt) {
     const uint32_t st = lds_base + (uint32_t)((kt & (NSTAGE - 1)) * STAGE);
+    if constexpr (MODE == TGMM) {
 #pragma unroll
-    for (int i = 0; i < A_INSTR; ++i)
-      gload_lds16(Ab + aoff[i] + (uint32_t)kt * a_step, st + (wave_u * A_INSTR + i) * 1024u);
+      for (int i = 0; i < A_INSTR; ++i) {
+        const uint32_t row = (uint32_t)min(arow[i] + kt * BKS, mlast);
+        gload_lds16(Ab + row * (uint32_t)(p.Kd * 2) + aoff[i], st + (wave_u * A_INSTR + i) * 1024u);
+      }
 #pragma unroll
-    for (int i = 0; i < B_INSTR; ++i)
-      gload_lds16(Bb + boff[i] + (uint32_t)kt * b_step, st + (uint32_t)A_BYTES + (wave_u * B_INSTR + i) * 1024u);
+      for (int i = 0; i < B_INSTR; ++i) {
+        const uint32_t row = (uint32_t)min(brow[i] + kt * BKS, mlast);
+        gload_lds16(Bb + row * (uint32_t)(p.N * 2) + boff[i], st + (uint32_t)A_BYTES + (wave_u * B_INSTR + i) * 1024u);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < A_INSTR; ++i)
+        gload_lds16(Ab + aoff[i] + (uint32_t)kt * a_step, st + (wave_u * A_INSTR + i) * 1024u);
+#pragma unroll
+      for (int i = 0; i < B_INSTR; ++i)
+        gload_lds16(Bb + boff[i] + (uint32_t)kt * b_step, st + (uint32_t)A_BYTES + (wave_u * B_INSTR + i) * 1024u);
+    }
   };
 
   // ---- fragments ---------------------------------------------------------------------
   bf16x8 fa[2][TM], fb[2][TN];
   const int frow = lane & 31, fhalf = lane >> 5;
+  // One 32-wide MFMA operand from a [reduction][col] tile via two transpose reads: lane l gets
+  // reduction rows kk*16 + 8*(l/32) + 0..7 of column c0 + l%32.
+  auto read_tr = [&](const char* region, int c0, int kk) -> bf16x8 {
+    const int n = c0 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const int k = kk * 16 + 8 * fhalf + ((lane & 15) >> 2);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(region + bn_off(k, n >> 3) + (n & 7) * 2));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(region + bn_off(k + 4, n >> 3) + (n & 7) * 2));
+    const s16x4 both[2] = {lo, hi};
+    return __builtin_bit_cast(bf16x8, both);
+  };
   auto read_frags = [&](int kt, int kk, int buf) {
     const char* st = lds + (kt & (NSTAGE - 1)) * STAGE;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      const int r = wm * WTM + i * 32 + frow;
-      fa[buf][i] = *(const bf16x8*)(st + a_off(r, kk * 2 + fhalf));
+      if constexpr (A_T) {
+        fa[buf][i] = read_tr(st, wm * WTM + i * 32, kk);
+      } else {
+        const int r = wm * WTM + i * 32 + frow;
+        fa[buf][i] = *(const bf16x8*)(st + a_off(r, kk * 2 + fhalf));
+      }
     }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      if (B_T) {
-        const int n = wn * WTN + j * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-        const int k = kk * 16 + 8 * fhalf + ((lane & 15) >> 2);
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(st + A_BYTES + bn_off(k, n >> 3) + (n & 7) * 2));
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(st + A_BYTES + bn_off(k + 4, n >> 3) + (n & 7) * 2));
-        const s16x4 both[2] = {lo, hi};
-        fb[buf][j] = __builtin_bit_cast(bf16x8, both);
+      if constexpr (B_T) {
+        fb[buf][j] = read_tr(st + A_BYTES, wn * WTN + j * 32, kk);
       } else {
         const int r = wn * WTN + j * 32 + frow;
         fb[buf][j] = *(const bf16x8*)(st + A_BYTES + a_off(r, kk * 2 + fhalf));
       }
     }
+  };
+  // TGMM reduction tail: keep only the first `rem` rows of the last step (both operands, so
+  // rows of other groups never reach the accumulators).
+  auto mask_frags = [&](int buf, int kk, int rem) {
+    const int nv = min(max(rem - kk * 16 - 8 * fhalf, 0), 8);
+    u32x4 m;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) m[d] = (2 * d + 1 < nv) ? 0xFFFFFFFFu : ((2 * d < nv) ? 0xFFFFu : 0u);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[buf][i] = __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, fa[buf][i]) & m);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[buf][j] = __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, fb[buf][j]) & m);
   };
 
   f32x16 acc[TM][TN];
@@ -775,7 +856,8 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  const int nk = p.Kred / BKS;
+  const int nk = (MODE == TGMM) ? (r1 - r0 + BKS - 1) / BKS : p.Kred / BKS;
+  const int tail = (MODE == TGMM) ? (r1 - r0) - (nk - 1) * BKS : BKS;  // rows in the last step
   constexpr int LPS = A_INSTR + B_INSTR;  // load instructions per stage per thread
   // prologue: stages 0..2 in flight; stages 0 and 1 landed and visible
   issue_stage(0);
@@ -790,6 +872,7 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
     if (kt + 3 < nk) issue_stage(kt + 3);
     // substep 0: prefetch substep 1 of this stage
     read_frags(kt, 1, 1);
+    if (MODE == TGMM && tail < BKS && kt == nk - 1) mask_frags(0, 0, tail);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -800,6 +883,7 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
     // MFMAs below only wait for the fragments they use.
     __builtin_amdgcn_sched_barrier(0);
     read_frags(kt + 1, 0, 0);
+    if (MODE == TGMM && tail < BKS && kt == nk - 1) mask_frags(1, 1, tail);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -812,7 +896,18 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
   }
 
   const int ccol = lane & 31, rhalf = (lane >> 5) * 4;
-  if (EPI == EPI_SWIGLU) {
+  if constexpr (MODE == TGMM) {
+    uint16_t* out = p.C + (int64_t)e * p.Kd * p.N;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = row0 + wm * WTM + i * 32 + 8 * (v >> 2) + rhalf + (v & 3);
+          out[(int64_t)row * p.N + col0 + wn * WTN + j * 32 + ccol] = bf16_bits_hw(acc[i][j][v]);
+        }
+  } else if (EPI == EPI_SWIGLU) {
     const int ycol0 = n_tile * (BN / 2) + wn * (WTN / 2);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -1055,6 +1150,8 @@ extern "C" int mtx_tgmm(const void* x, const void* g, const int32_t* group_sizes
     a.ldc = (int)N;
     a.I = 0;
     a.E = (int)E;
+    if (K % 256 == 0 && N % 256 == 0 && M * K * 2 < (int64_t(1) << 32) && M * N * 2 < (int64_t(1) << 32))
+      return launch_v3<mf::TGMM, mf::EPI_STORE>(a, E * (K / 256) * (N / 256), st);
     if (K % 256 == 0 && N % 256 == 0) {
       const int64_t grid = round_up(E * (K / 256) * (N / 256), 8);
       return launch_mfma<256, 256, 2, 2, mf::TGMM, mf::EPI_STORE>(a, grid, st);

@@ -161,7 +161,10 @@ def test_gmm_swiglu_fused(dev, M, E, Kin, I, kind):
 
 
 @pytest.mark.parametrize("M,E,K,N,kind", [(2048, 4, 256, 512, "uniform"), (1700, 8, 128, 256, "skew"),
-                                          (900, 6, 256, 128, "ragged")])
+                                          (900, 6, 256, 128, "ragged"),
+                                          # 256x256 direct-to-LDS path: ragged tails, empty groups
+                                          (1000, 8, 512, 256, "ragged"), (5000, 16, 256, 768, "skew"),
+                                          (333, 3, 256, 256, "ragged")])
 def test_tgmm_bf16_mfma(dev, M, E, K, N, kind):
     from mintext_amd.kernels import tgmm
 
@@ -201,3 +204,29 @@ def test_gmm_bf16_sampled_mixtral_shape(dev):
         ref[i] = O.silu(xs[i] @ gate) * (xs[i] @ up)
     got = y[torch.from_numpy(rows).to(dev)][:, torch.from_numpy(cols).to(dev)].float().cpu().numpy()
     _close(got, ref, 2e-2)
+
+
+def test_tgmm_bf16_sampled_qwen3_shape(dev):
+    """C5 tgmm shape (M=131072, K=2048, N=1536, E=128, Zipf-skewed groups): sampled blocks vs float64."""
+    from mintext_amd.kernels import tgmm
+
+    M, E, K, N = 131072, 128, 2048, 1536
+    rng = np.random.default_rng(5)
+    gs = _groups(rng, M, E, "skew")
+    x = torch.randn(M, K, device=dev).bfloat16()
+    g = torch.randn(M, N, device=dev).bfloat16()
+    out = tgmm(x, g, _t(gs, dev))
+    off = np.concatenate([[0], np.cumsum(gs)])
+    experts = [int(np.argmax(gs)), int(np.argmin(gs)), int(rng.integers(0, E)), int(rng.integers(0, E))]
+    ks = np.sort(rng.choice(K, 24, replace=False))
+    ns = np.sort(rng.choice(N, 24, replace=False))
+    for e in experts:
+        r0, r1 = int(off[e]), int(off[e + 1])
+        xs = x[r0:r1][:, torch.from_numpy(ks).to(dev)].float().cpu().numpy().astype(np.float64)
+        gsm = g[r0:r1][:, torch.from_numpy(ns).to(dev)].float().cpu().numpy().astype(np.float64)
+        ref = xs.T @ gsm
+        got = out[e][torch.from_numpy(ks).to(dev)][:, torch.from_numpy(ns).to(dev)].float().cpu().numpy()
+        if r1 == r0:
+            assert (got == 0).all()
+        else:
+            _close(got, ref, 2e-2)
