@@ -629,13 +629,19 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
 // Each lane of a load instruction writes LDS byte (M0 + 16*lane), so the swizzle is realised by
 // choosing the global source of each lane.  Both swizzles make the fragment reads conflict-free.
 namespace v3 {
-constexpr int BM = 256, BN = 256, BKS = 32, NSTAGE = 4;
+#ifndef MTX_V3_NSTAGE
+#define MTX_V3_NSTAGE 4
+#endif
+constexpr int BM = 256, BN = 256, BKS = 32, NSTAGE = MTX_V3_NSTAGE;
+constexpr int PD = NSTAGE - 1;  // stages in flight ahead of the one being computed
+__device__ __forceinline__ int slot(int kt) { return (NSTAGE & (NSTAGE - 1)) == 0 ? (kt & (NSTAGE - 1)) : kt % NSTAGE; }
 constexpr int A_BYTES = BM * BKS * 2, B_BYTES = BN * BKS * 2, STAGE = A_BYTES + B_BYTES;
 __device__ __forceinline__ int a_off(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
 __device__ __forceinline__ int bn_off(int k, int c) { return k * 512 + ((c ^ ((k & 3) << 2)) << 4); }
 }  // namespace v3
 
 typedef __attribute__((ext_vector_type(4))) short s16x4;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
 typedef __attribute__((address_space(3))) char lds_char;
 // 16-byte direct global->LDS load: lane l writes LDS byte lds_base + 16*l (lds_base is
 // wave-uniform).  Issued as inline asm so that the compiler does not serialise the LDS reads
@@ -647,6 +653,14 @@ __device__ __forceinline__ void gload_lds16(const void* gptr, uint32_t lds_base)
 // s_waitcnt immediate (GFX9 encoding) that waits for vmcnt <= N only.
 #define MTX_VMCNT(N) ((((N) & 0xF)) | (0x7 << 4) | (0xF << 8) | ((((N) >> 4) & 0x3) << 14))
 typedef __attribute__((address_space(1))) const char gbl_char;
+#ifndef MTX_V3_SB
+#define MTX_V3_SB 0
+#endif
+#if MTX_V3_SB
+#define MTX_V3_SCHED_BARRIER() __builtin_amdgcn_sched_barrier(0)
+#else
+#define MTX_V3_SCHED_BARRIER() ((void)0)
+#endif
 
 template <int MODE, int EPI, int WM, int WN>
 __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
@@ -777,7 +791,7 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
   const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
   const int mlast = p.M - 1;
   auto issue_stage = [&](int kt) {
-    const uint32_t st = lds_base + (uint32_t)((kt & (NSTAGE - 1)) * STAGE);
+    const uint32_t st = lds_base + (uint32_t)(slot(kt) * STAGE);
     if constexpr (MODE == TGMM) {
 #pragma unroll
       for (int i = 0; i < A_INSTR; ++i) {
@@ -815,7 +829,7 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
     return __builtin_bit_cast(bf16x8, both);
   };
   auto read_frags = [&](int kt, int kk, int buf) {
-    const char* st = lds + (kt & (NSTAGE - 1)) * STAGE;
+    const char* st = lds + slot(kt) * STAGE;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       if constexpr (A_T) {
@@ -859,78 +873,94 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
   const int nk = (MODE == TGMM) ? (r1 - r0 + BKS - 1) / BKS : p.Kred / BKS;
   const int tail = (MODE == TGMM) ? (r1 - r0) - (nk - 1) * BKS : BKS;  // rows in the last step
   constexpr int LPS = A_INSTR + B_INSTR;  // load instructions per stage per thread
-  // prologue: stages 0..2 in flight; stages 0 and 1 landed and visible
-  issue_stage(0);
-  if (nk > 1) issue_stage(1);
-  if (nk > 2) issue_stage(2);
-  if (nk > 2) __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS));  // (vmcnt counts outstanding loads)
+  // prologue: stages 0..PD-1 in flight; stages 0 and 1 landed and visible
+#pragma unroll
+  for (int s = 0; s < PD; ++s)
+    if (nk > s) issue_stage(s);
+  if (nk >= PD) __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));  // (vmcnt counts outstanding loads)
   else __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));
   __syncthreads();
   read_frags(0, 0, 0);
 
   for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 3 < nk) issue_stage(kt + 3);
+    if (kt + PD < nk) issue_stage(kt + PD);
     // substep 0: prefetch substep 1 of this stage
     read_frags(kt, 1, 1);
     if (MODE == TGMM && tail < BKS && kt == nk - 1) mask_frags(0, 0, tail);
-    __builtin_amdgcn_sched_barrier(0);
+    MTX_V3_SCHED_BARRIER();
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[0][i], fb[0][j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[0][j], fa[0][i], acc[i][j], 0, 0, 0);
     // substep 1: prefetch substep 0 of the next stage (visible since the last barrier).  On
     // the last step this reads an unused ring slot: in bounds, and branch-free so that the
     // MFMAs below only wait for the fragments they use.
-    __builtin_amdgcn_sched_barrier(0);
+    MTX_V3_SCHED_BARRIER();
     read_frags(kt + 1, 0, 0);
     if (MODE == TGMM && tail < BKS && kt == nk - 1) mask_frags(1, 1, tail);
-    __builtin_amdgcn_sched_barrier(0);
+    MTX_V3_SCHED_BARRIER();
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[1][i], fb[1][j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
     // stage kt+2 must have landed before the barrier makes it visible to every wave
-    if (kt + 3 < nk) __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS));
+    if (kt + PD < nk) __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
     else __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));
     __syncthreads();
   }
 
-  const int ccol = lane & 31, rhalf = (lane >> 5) * 4;
+  // ---- epilogue: the MFMAs computed C^T blocks (operands swapped), so acc[i][j][4g+q] of lane
+  // l is C[row i*32 + l%32][col j*32 + 8g + 4(l/32) + q]: four consecutive columns per lane,
+  // written as one 8-byte store of packed bf16.
+  const int erow = wm * WTM + (lane & 31), ecol = wn * WTN + 4 * (lane >> 5);
+  auto pack4 = [](float a, float b, float c, float d) -> bf16x4 {
+    return bf16x4{(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
+  };
   if constexpr (MODE == TGMM) {
     uint16_t* out = p.C + (int64_t)e * p.Kd * p.N;
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i) {
+      uint16_t* orow = out + (int64_t)(row0 + erow + i * 32) * p.N + col0 + ecol;
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int row = row0 + wm * WTM + i * 32 + 8 * (v >> 2) + rhalf + (v & 3);
-          out[(int64_t)row * p.N + col0 + wn * WTN + j * 32 + ccol] = bf16_bits_hw(acc[i][j][v]);
-        }
+        for (int g = 0; g < 4; ++g)
+          *(bf16x4*)(orow + j * 32 + 8 * g) =
+              pack4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+    }
   } else if (EPI == EPI_SWIGLU) {
-    const int ycol0 = n_tile * (BN / 2) + wn * (WTN / 2);
+    const int ycol = n_tile * (BN / 2) + wn * (WTN / 2) + 4 * (lane >> 5);
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i) {
+      const int row = r0 + erow + i * 32;
+      if (row < r1) {
+        uint16_t* orow = p.C + (int64_t)row * p.ldc + ycol;
 #pragma unroll
-      for (int j = 0; j < TN / 2; ++j)
+        for (int j = 0; j < TN / 2; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int row = r0 + wm * WTM + i * 32 + 8 * (v >> 2) + rhalf + (v & 3);
-          if (row < r1) {
-            const float gt = acc[i][j][v], up = acc[i][j + TN / 2][v];
-            p.C[(int64_t)row * p.ldc + ycol0 + j * 32 + ccol] = bf16_bits_hw(swiglu_fast(gt, up));
+          for (int g = 0; g < 4; ++g) {
+            const f32x16& gt = acc[i][j];
+            const f32x16& up = acc[i][j + TN / 2];
+            *(bf16x4*)(orow + j * 32 + 8 * g) =
+                pack4(swiglu_fast(gt[4 * g], up[4 * g]), swiglu_fast(gt[4 * g + 1], up[4 * g + 1]),
+                      swiglu_fast(gt[4 * g + 2], up[4 * g + 2]), swiglu_fast(gt[4 * g + 3], up[4 * g + 3]));
           }
-        }
+      }
+    }
   } else {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i) {
+      const int row = r0 + erow + i * 32;
+      if (row < r1) {
+        uint16_t* orow = p.C + (int64_t)row * p.ldc + col0 + ecol;
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int row = r0 + wm * WTM + i * 32 + 8 * (v >> 2) + rhalf + (v & 3);
-          if (row < r1) p.C[(int64_t)row * p.ldc + col0 + wn * WTN + j * 32 + ccol] = bf16_bits_hw(acc[i][j][v]);
-        }
+          for (int g = 0; g < 4; ++g)
+            *(bf16x4*)(orow + j * 32 + 8 * g) =
+                pack4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+      }
+    }
   }
 }
 
