@@ -629,13 +629,17 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
 // Each lane of a load instruction writes LDS byte (M0 + 16*lane), so the swizzle is realised by
 // choosing the global source of each lane.  Both swizzles make the fragment reads conflict-free.
 namespace v3 {
-#ifndef MTX_V3_NSTAGE
-#define MTX_V3_NSTAGE 4
-#endif
-constexpr int BM = 256, BN = 256, BKS = 32, NSTAGE = MTX_V3_NSTAGE;
-constexpr int PD = NSTAGE - 1;  // stages in flight ahead of the one being computed
-__device__ __forceinline__ int slot(int kt) { return (NSTAGE & (NSTAGE - 1)) == 0 ? (kt & (NSTAGE - 1)) : kt % NSTAGE; }
-constexpr int A_BYTES = BM * BKS * 2, B_BYTES = BN * BKS * 2, STAGE = A_BYTES + B_BYTES;
+constexpr int BKS = 32;  // reduction elements per ring stage
+// Block tile BM x 256 with an NST-deep ring of stages.
+template <int BM_, int NST_>
+struct Cfg {
+  static constexpr int BM = BM_, BN = 256, NSTAGE = NST_;
+  static constexpr int PD = NSTAGE - 1;  // stages in flight ahead of the one being computed
+  static constexpr int A_BYTES = BM * BKS * 2, B_BYTES = BN * BKS * 2, STAGE = A_BYTES + B_BYTES;
+  static __device__ __forceinline__ int slot(int kt) {
+    return (NSTAGE & (NSTAGE - 1)) == 0 ? (kt & (NSTAGE - 1)) : kt % NSTAGE;
+  }
+};
 __device__ __forceinline__ int a_off(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
 __device__ __forceinline__ int bn_off(int k, int c) { return k * 512 + ((c ^ ((k & 3) << 2)) << 4); }
 }  // namespace v3
@@ -662,9 +666,14 @@ typedef __attribute__((address_space(1))) const char gbl_char;
 #define MTX_V3_SCHED_BARRIER() ((void)0)
 #endif
 
-template <int MODE, int EPI, int WM, int WN>
-__global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
-  using namespace v3;
+template <int MODE, int EPI, int WM, int WN, int BM_, int NST_>
+__global__ __launch_bounds__(WM* WN * 64, 2) void gmm_v3_kernel(Args p) {
+  using v3::BKS;
+  using v3::a_off;
+  using v3::bn_off;
+  using C = v3::Cfg<BM_, NST_>;
+  constexpr int BM = C::BM, BN = C::BN, NSTAGE = C::NSTAGE, PD = C::PD;
+  constexpr int A_BYTES = C::A_BYTES, B_BYTES = C::B_BYTES, STAGE = C::STAGE;
   constexpr int NT = WM * WN * 64;
   constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
   constexpr int A_INSTR = A_BYTES / 1024 / (NT / 64);  // load instructions per wave per stage
@@ -753,8 +762,9 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
     } else {
       const int r = seg * 16 + (lane >> 2), pc = lane & 3;
       const int c = pc ^ ((r >> 2) & 3);
+      // rows past the tile's group repeat its last row: never used, and cache hits
       int gr = r0 + r;
-      gr = gr < p.M ? gr : p.M - 1;
+      gr = gr < r1 ? gr : r1 - 1;
       aoff[i] = ((uint32_t)gr * (uint32_t)p.Kred + (uint32_t)(c * 8)) * 2u;
     }
   }
@@ -791,7 +801,7 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
   const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
   const int mlast = p.M - 1;
   auto issue_stage = [&](int kt) {
-    const uint32_t st = lds_base + (uint32_t)(slot(kt) * STAGE);
+    const uint32_t st = lds_base + (uint32_t)(C::slot(kt) * STAGE);
     if constexpr (MODE == TGMM) {
 #pragma unroll
       for (int i = 0; i < A_INSTR; ++i) {
@@ -828,10 +838,11 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
     const s16x4 both[2] = {lo, hi};
     return __builtin_bit_cast(bf16x8, both);
   };
-  auto read_frags = [&](int kt, int kk, int buf) {
-    const char* st = lds + slot(kt) * STAGE;
+  auto read_frags = [&](int kt, int kk, int buf, int nb) {
+    const char* st = lds + C::slot(kt) * STAGE;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
+      if (i >= nb) continue;
       if constexpr (A_T) {
         fa[buf][i] = read_tr(st, wm * WTM + i * 32, kk);
       } else {
@@ -880,34 +891,48 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_v3_kernel(Args p) {
   if (nk >= PD) __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));  // (vmcnt counts outstanding loads)
   else __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));
   __syncthreads();
-  read_frags(0, 0, 0);
+  // 32-row blocks of this wave that hold rows of the group (FWD/DLHS tiles of small groups
+  // are partly empty): MFMAs and A reads of empty blocks are skipped.
+  const int nbi = (MODE == TGMM) ? TM : min(max((r1 - r0 - wm * WTM + 31) / 32, 0), TM);
+  read_frags(0, 0, 0, nbi);
 
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + PD < nk) issue_stage(kt + PD);
-    // substep 0: prefetch substep 1 of this stage
-    read_frags(kt, 1, 1);
-    if (MODE == TGMM && tail < BKS && kt == nk - 1) mask_frags(0, 0, tail);
-    MTX_V3_SCHED_BARRIER();
+  auto main_loop = [&](auto full_tag) {
+    constexpr bool FULL = decltype(full_tag)::value;
+    const int nb = FULL ? TM : nbi;
+    for (int kt = 0; kt < nk; ++kt) {
+      if (kt + PD < nk) issue_stage(kt + PD);
+      // substep 0: prefetch substep 1 of this stage
+      read_frags(kt, 1, 1, nb);
+      if (MODE == TGMM && tail < BKS && kt == nk - 1) mask_frags(0, 0, tail);
+      MTX_V3_SCHED_BARRIER();
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i) {
+        if (!FULL && i >= nb) continue;
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[0][j], fa[0][i], acc[i][j], 0, 0, 0);
-    // substep 1: prefetch substep 0 of the next stage (visible since the last barrier).  On
-    // the last step this reads an unused ring slot: in bounds, and branch-free so that the
-    // MFMAs below only wait for the fragments they use.
-    MTX_V3_SCHED_BARRIER();
-    read_frags(kt + 1, 0, 0);
-    if (MODE == TGMM && tail < BKS && kt == nk - 1) mask_frags(1, 1, tail);
-    MTX_V3_SCHED_BARRIER();
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[0][j], fa[0][i], acc[i][j], 0, 0, 0);
+      }
+      // substep 1: prefetch substep 0 of the next stage (visible since the last barrier).  On
+      // the last step this reads an unused ring slot: in bounds, and branch-free so that the
+      // MFMAs below only wait for the fragments they use.
+      MTX_V3_SCHED_BARRIER();
+      read_frags(kt + 1, 0, 0, nb);
+      if (MODE == TGMM && tail < BKS && kt == nk - 1) mask_frags(1, 1, tail);
+      MTX_V3_SCHED_BARRIER();
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i) {
+        if (!FULL && i >= nb) continue;
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
-    // stage kt+2 must have landed before the barrier makes it visible to every wave
-    if (kt + PD < nk) __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
-    else __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));
-    __syncthreads();
-  }
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
+      }
+      // stage kt+2 must have landed before the barrier makes it visible to every wave
+      if (kt + PD < nk) __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
+      else __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));
+      __syncthreads();
+    }
+  };
+  // Both loop versions execute the same barriers, so waves of one workgroup may take either.
+  if (MODE == TGMM || nbi == TM) main_loop(std::integral_constant<bool, true>());
+  else main_loop(std::integral_constant<bool, false>());
 
   // ---- epilogue: the MFMAs computed C^T blocks (operands swapped), so acc[i][j][4g+q] of lane
   // l is C[row i*32 + l%32][col j*32 + 8g + 4(l/32) + q]: four consecutive columns per lane,
@@ -977,17 +1002,29 @@ static int launch_build_tiles(const int32_t* gs, int64_t E, int64_t M, int BM, c
   return check_launch();
 }
 
-#ifndef MTX_V3_WM
-#define MTX_V3_WM 2
-#define MTX_V3_WN 4
+// v3 configurations: 256x256 tiles with 8 waves (128x64 wave tiles) and a 4-deep ring (one
+// workgroup per CU) for large groups; 128x256 tiles with 4 waves (64x128 wave tiles) and a
+// 3-deep ring (72 KB, two workgroups per CU) for groups of about a hundred rows.
+// Mean group size below which the 128-row configuration is used (0: always 256-row tiles,
+// whose empty 32-row blocks skip their MFMAs, so each expert's weights stream once).
+#ifndef MTX_V3_NSTAGE
+#define MTX_V3_NSTAGE 4
 #endif
-
+#ifndef MTX_V3_SMALL_MEAN
+#define MTX_V3_SMALL_MEAN 0
+#endif
 template <int MODE, int EPI>
 static int launch_v3(const mf::Args& a, int64_t grid, hipStream_t st) {
   if (grid <= 0) return MTX_OK;
   grid = round_up(grid, 8);
-  hipLaunchKernelGGL((mf::gmm_v3_kernel<MODE, EPI, MTX_V3_WM, MTX_V3_WN>), dim3((unsigned)grid),
-                     dim3(MTX_V3_WM * MTX_V3_WN * 64), 0, st, a);
+  hipLaunchKernelGGL((mf::gmm_v3_kernel<MODE, EPI, 2, 4, 256, MTX_V3_NSTAGE>), dim3((unsigned)grid), dim3(512), 0, st, a);
+  return check_launch();
+}
+template <int MODE, int EPI>
+static int launch_v3_small(const mf::Args& a, int64_t grid, hipStream_t st) {
+  if (grid <= 0) return MTX_OK;
+  grid = round_up(grid, 8);
+  hipLaunchKernelGGL((mf::gmm_v3_kernel<MODE, EPI, 2, 2, 128, 3>), dim3((unsigned)grid), dim3(256), 0, st, a);
   return check_launch();
 }
 
@@ -1010,9 +1047,6 @@ static int common_checks(int64_t M, int64_t E, void* ws, int64_t ws_bytes, int64
 // Smallest m-tile any path uses is 64 rows, so the workspace bound uses BM = 64.
 static constexpr int kMinBM = 64;
 
-// The large-group path (mean group >= 192 rows) uses the 256x256 direct-to-LDS kernel.
-#define MTX_BIG_BM 256
-#define MTX_BIG_BN 256
 
 // FWD / DLHS / SWIGLU driver. mode: 0 fwd, 1 dlhs, 2 swiglu
 static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs, int dtype, int64_t M, int64_t Kred,
@@ -1045,28 +1079,33 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
     a.I = (int)I;
     a.E = (int)E;
     // tile shape: 256-row tiles when groups are large on average, else 128
-    const bool big_m = (M / E) >= 192 && Kred % mf::v3::BKS == 0 && M * Kred * 2 < (int64_t(1) << 32) &&
-                       Kred * Nout * 2 < (int64_t(1) << 32);
+    const bool v3ok = Kred % mf::v3::BKS == 0 && M * Kred * 2 < (int64_t(1) << 32) &&
+                      Kred * Nout * 2 < (int64_t(1) << 32);
+    const bool big_m = v3ok && (M / E) >= MTX_V3_SMALL_MEAN;
     if (mode == 2 && I % 128 == 0) {
-      if (big_m && I % (MTX_BIG_BN / 2) == 0) {
-        rc = launch_build_tiles(gs, E, M, MTX_BIG_BM, wsp, st);
+      if (big_m) {
+        rc = launch_build_tiles(gs, E, M, 256, wsp, st);
         if (rc) return rc;
-        return launch_v3<mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, MTX_BIG_BM) * (I / (MTX_BIG_BN / 2)), st);
+        return launch_v3<mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 256) * (I / 128), st);
       }
       rc = launch_build_tiles(gs, E, M, 128, wsp, st);
       if (rc) return rc;
+      if (v3ok) return launch_v3_small<mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 128) * (I / 128), st);
       return launch_mfma<128, 256, 1, 2, mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 128) * (I / 128), st);
     }
     if (mode != 2 && Nout % 256 == 0) {
-      if (big_m && Nout % MTX_BIG_BN == 0) {
-        rc = launch_build_tiles(gs, E, M, MTX_BIG_BM, wsp, st);
+      if (big_m) {
+        rc = launch_build_tiles(gs, E, M, 256, wsp, st);
         if (rc) return rc;
-        const int64_t grid = gmm_max_tiles(M, E, MTX_BIG_BM) * (Nout / MTX_BIG_BN);
+        const int64_t grid = gmm_max_tiles(M, E, 256) * (Nout / 256);
         return mode == 0 ? launch_v3<mf::FWD, mf::EPI_STORE>(a, grid, st) : launch_v3<mf::DLHS, mf::EPI_STORE>(a, grid, st);
       }
       rc = launch_build_tiles(gs, E, M, 128, wsp, st);
       if (rc) return rc;
       const int64_t grid = gmm_max_tiles(M, E, 128) * (Nout / 256);
+      if (v3ok)
+        return mode == 0 ? launch_v3_small<mf::FWD, mf::EPI_STORE>(a, grid, st)
+                         : launch_v3_small<mf::DLHS, mf::EPI_STORE>(a, grid, st);
       return mode == 0 ? launch_mfma<128, 256, 1, 2, mf::FWD, mf::EPI_STORE>(a, grid, st)
                        : launch_mfma<128, 256, 1, 2, mf::DLHS, mf::EPI_STORE>(a, grid, st);
     }

@@ -206,6 +206,39 @@ def test_gmm_bf16_sampled_mixtral_shape(dev):
     _close(got, ref, 2e-2)
 
 
+def test_gmm_bf16_sampled_deepseek_shape(dev):
+    """C3 shapes (E=256, ~128 rows per expert): gate_up+SwiGLU and down, sampled rows vs float64."""
+    from mintext_amd.kernels import grouped_matmul, grouped_matmul_swiglu
+
+    M, E, D, I = 32768, 256, 7168, 2048
+    rng = np.random.default_rng(3)
+    gs = rng.multinomial(M, np.full(E, 1.0 / E)).astype(np.int32)
+    gs[7] = 0
+    gs[8] += M - gs.sum()
+    x = torch.randn(M, D, device=dev).bfloat16()
+    wgu = (torch.randn(E, D, 2 * I, device=dev) * 0.006).bfloat16()
+    y = grouped_matmul_swiglu(x, wgu, _t(gs, dev))
+    wd = (torch.randn(E, I, D, device=dev) * 0.006).bfloat16()
+    o = grouped_matmul(y, wd, _t(gs, dev))
+    off = np.concatenate([[0], np.cumsum(gs)])
+    rows = np.sort(rng.choice(M, 24, replace=False))
+    cols = np.sort(rng.choice(I, 32, replace=False))
+    ocols = np.sort(rng.choice(D, 32, replace=False))
+    tc, toc = torch.from_numpy(cols).to(dev), torch.from_numpy(ocols).to(dev)
+    ref_y = np.empty((rows.size, cols.size))
+    ref_o = np.empty((rows.size, ocols.size))
+    for i, r in enumerate(rows):
+        e = int(np.searchsorted(off, r, side="right") - 1)
+        xr = x[int(r)].double().cpu().numpy()
+        gate = wgu[e][:, tc].double().cpu().numpy()
+        up = wgu[e][:, tc + I].double().cpu().numpy()
+        ref_y[i] = O.silu(xr @ gate) * (xr @ up)
+        ref_o[i] = y[int(r)].double().cpu().numpy() @ wd[e][:, toc].double().cpu().numpy()
+    tr = torch.from_numpy(rows).to(dev)
+    _close(y[tr][:, tc].float().cpu().numpy(), ref_y, 2e-2)
+    _close(o[tr][:, toc].float().cpu().numpy(), ref_o, 2e-2)
+
+
 def test_tgmm_bf16_sampled_qwen3_shape(dev):
     """C5 tgmm shape (M=131072, K=2048, N=1536, E=128, Zipf-skewed groups): sampled blocks vs float64."""
     from mintext_amd.kernels import tgmm
