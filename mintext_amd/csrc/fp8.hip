@@ -12,6 +12,8 @@
 // f32 on the partial sums) and a bf16 output, or -- for the gate_up GEMM -- the SwiGLU and
 // a 1x128 re-quantisation of its output fused into the epilogue.
 #include "common.h"
+#include "lds_dma.h"
+#include <type_traits>
 
 namespace mtx {
 
@@ -409,6 +411,302 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gmm_fp8_kernel(Args p) {
     }
 }
 
+
+// ---- v3: direct-to-LDS ring (256x256 tiles, 8 waves) ---------------------------------------------
+// Both operands are k-contiguous, so a ring stage holds 64 k-bytes of 256 x-rows and of 256
+// weight rows (32 KB), loaded with global_load_lds_dwordx4 three stages ahead; 16-byte chunk c
+// of row r sits at chunk c ^ ((r>>2)&3), which keeps the 32-byte fragment reads conflict-free.
+// One v_mfma_scale_f32_32x32x64_f8f6f4 per 32x32 block and stage, operands swapped so that each
+// lane owns four consecutive output columns.  Block scales: the accumulators are kept in units of
+// the current 128-k block's scale s = xs[row,kb] * ws[nblk,kb]; between blocks they are multiplied
+// by s_kb / s_kb+1 (one multiply per accumulator per 128 k, no second accumulator set), and by the
+// last block's scale at the end, which gives sum_kb s_kb * P_kb.  The tile's scales are staged in
+// LDS once.  Scales must be finite and nonzero (the quantisers never produce 0).
+namespace v3 {
+constexpr int BM = 256, BN = 256, BKB = 64, NSTAGE = 4, PD = 3;
+constexpr int A_BYTES = BM * BKB, B_BYTES = BN * BKB, STAGE = A_BYTES + B_BYTES;
+constexpr int MAX_KB = 24;  // K <= 3072
+__device__ __forceinline__ int a_off(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
+}  // namespace v3
+
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+
+template <int EPI>
+__global__ __launch_bounds__(512, 2) void gmm_fp8_v3_kernel(Args p) {
+  using namespace v3;
+  constexpr int WN = 4, NT = 512, WTM = 128, WTN = 64, TM = 4, TN = 2;
+  constexpr int A_INSTR = 2, B_INSTR = 2, LPS = A_INSTR + B_INSTR;
+  __shared__ __attribute__((aligned(1024))) char lds[NSTAGE * STAGE];
+  __shared__ float s_sa[MAX_KB * BM];  // [kb][tile row]
+  __shared__ float s_sb[2 * MAX_KB];   // [weight-row half][kb]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  const int nn = (EPI == EPI_SWIGLU_Q) ? (p.I / 128) : (p.N / BN);
+  const int cnt = p.count[0];
+  const int total = cnt * nn;
+  const int pid = blockIdx.x;
+  const int total8 = (total + 7) & ~7;
+  if (pid >= total8) return;
+  const int lid = (pid & 7) * (total8 >> 3) + (pid >> 3);
+  if (lid >= total) return;
+  constexpr int GM = 8;
+  const int grp = lid / (GM * nn);
+  const int first_m = grp * GM;
+  const int gsz = min(GM, cnt - first_m);
+  const int local = lid - grp * GM * nn;
+  const int mt = first_m + local % gsz;
+  const int n_tile = local / gsz;
+  const MTileF8 t = p.tiles[mt];
+  const int e = t.e, r0 = t.r0, r1 = t.r1;
+  const int col0 = n_tile * BN;
+  if (e < 0) {  // rows past sum(group_sizes)
+    if (EPI == EPI_SWIGLU_Q) {
+      const int c0 = n_tile * 128;
+      for (int i = tid; i < BM * 128; i += NT) {
+        const int r = r0 + i / 128;
+        if (r < r1) {
+          p.outq[(int64_t)r * p.I + c0 + i % 128] = 0;
+          if (p.out) p.out[(int64_t)r * p.I + c0 + i % 128] = 0;
+        }
+      }
+      for (int i = tid; i < BM; i += NT)
+        if (r0 + i < r1) p.outs[(int64_t)(r0 + i) * (p.I / 128) + n_tile] = 1.0f;
+    } else {
+      for (int i = tid; i < BM * BN; i += NT) {
+        const int r = r0 + i / BN;
+        if (r < r1) p.out[(int64_t)r * p.ldc + col0 + i % BN] = 0;
+      }
+    }
+    return;
+  }
+  const int nkb = p.K / 128, nk = p.K / BKB;
+  // weight row of tile-local column c: the SwiGLU tile pairs gate rows n_tile*128 + [0,128)
+  // with up rows I + n_tile*128 + [0,128), 32 of each per wave
+  auto b_row = [&](int c) -> int {
+    if (EPI == EPI_SWIGLU_Q) {
+      const int w_ = c / WTN, within = c % WTN;
+      return (within / 32) * p.I + n_tile * 128 + w_ * 32 + within % 32;
+    }
+    return col0 + c;
+  };
+
+  // ---- scales of this tile -> LDS (before the ring loads, so their waits stay separate) ----
+  {
+    const float* wsc = p.ws + (int64_t)e * (p.N / 128) * nkb;
+    for (int i = tid; i < BM * nkb; i += NT) {
+      const int kb = i / BM, r = i % BM;
+      const int gr = min(r0 + r, r1 - 1);
+      s_sa[kb * BM + r] = p.xs[(int64_t)gr * nkb + kb];
+    }
+    if (tid < 2 * nkb) {
+      const int h = tid / nkb, kb = tid % nkb;
+      const int nblk = (EPI == EPI_SWIGLU_Q) ? (h * (p.I / 128) + n_tile) : (col0 / 128 + h);
+      s_sb[h * MAX_KB + kb] = wsc[(int64_t)nblk * nkb + kb];
+    }
+  }
+
+  // ---- per-lane global sources: lane l of segment s fills row 16s + l/4, chunk slot l%4 ----
+  const uint8_t* Bb = p.wq + (int64_t)e * p.N * p.K;
+  uint32_t aoff[A_INSTR], boff[B_INSTR];
+#pragma unroll
+  for (int i = 0; i < A_INSTR; ++i) {
+    const int seg = wave * A_INSTR + i;
+    const int r = seg * 16 + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
+    const int gr = min(r0 + r, r1 - 1);  // rows past the group repeat its last row (unused)
+    aoff[i] = (uint32_t)gr * (uint32_t)p.K + (uint32_t)(c * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < B_INSTR; ++i) {
+    const int seg = wave * B_INSTR + i;
+    const int r = seg * 16 + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
+    boff[i] = (uint32_t)b_row(r) * (uint32_t)p.K + (uint32_t)(c * 16);
+  }
+  const uint32_t lds_base = lds_addr(lds);
+  const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+  // Stages past the end re-read the last one (in bounds) into a ring slot that is no longer
+  // read, which keeps the loop body free of branches.
+  auto issue_stage = [&](int kt) {
+    const uint32_t st = lds_base + (uint32_t)((kt & (NSTAGE - 1)) * STAGE);
+    const uint32_t kofs = (uint32_t)min(kt, nk - 1) * BKB;
+#pragma unroll
+    for (int i = 0; i < A_INSTR; ++i) gload_lds16(p.xq + aoff[i] + kofs, st + (wave_u * A_INSTR + i) * 1024u);
+#pragma unroll
+    for (int i = 0; i < B_INSTR; ++i)
+      gload_lds16(Bb + boff[i] + kofs, st + (uint32_t)A_BYTES + (wave_u * B_INSTR + i) * 1024u);
+  };
+
+  // ---- fragments: lane l holds row l%32, k bytes 32*(l/32) .. +31 of the stage ------------
+  i32x8 fa[2][TM], fb[2][TN];
+  const int frow = lane & 31, fhalf = lane >> 5;
+  auto ld32 = [&](const char* base, int r) -> i32x8 {
+    const u32x4 lo = *(const u32x4*)(base + a_off(r, 2 * fhalf));
+    const u32x4 hi = *(const u32x4*)(base + a_off(r, 2 * fhalf + 1));
+    return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  };
+  auto read_frags = [&](int kt, int buf, int nb) {
+    const char* st = lds + (kt & (NSTAGE - 1)) * STAGE;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      if (i < nb) fa[buf][i] = ld32(st, wm * WTM + i * 32 + frow);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[buf][j] = ld32(st + A_BYTES, wn * WTN + j * 32 + frow);
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  // weight-scale half of accumulator column block j
+  auto half_of = [&](int j) -> int { return (EPI == EPI_SWIGLU_Q) ? j : (wn >> 1); };
+  auto scale_of = [&](int i, int j, int kb) -> float {
+    return s_sa[kb * BM + wm * WTM + i * 32 + frow] * s_sb[half_of(j) * MAX_KB + kb];
+  };
+
+  // 32-row blocks of this wave that hold rows of the group
+  const int nbi = min(max((r1 - r0 - wm * WTM + 31) / 32, 0), TM);
+
+#pragma unroll
+  for (int s = 0; s < PD; ++s)
+    if (nk > s) issue_stage(s);
+  if (nk >= PD) __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
+  else __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));
+  __syncthreads();  // stages 0 and 1 and the scales are visible
+  read_frags(0, 0, nbi);
+
+  // One iteration per 128-k scale block: ring stages 2kb (fragment buffer 0) and 2kb+1
+  // (buffer 1), so every fragment index is a compile-time constant.
+  auto main_loop = [&](auto full_tag) {
+    constexpr bool FULL = decltype(full_tag)::value;
+    const int nb = FULL ? TM : nbi;
+    auto mfmas = [&](int buf) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        if (!FULL && i >= nb) continue;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[buf][j], fa[buf][i], acc[i][j], 0, 0, 0, 127,
+                                                                      0, 127);
+      }
+    };
+    auto finish_stage = [&]() {
+      // stage kt+2 must have landed before the barrier makes it visible to every wave (stage
+      // kt+3, possibly a re-read past the end, may still be in flight)
+      __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
+      __syncthreads();
+    };
+    for (int kb = 0; kb < nkb; ++kb) {
+      const int kt = 2 * kb;
+      const bool more = kb + 1 < nkb;
+      // scale factors s_kb / s_kb+1 (read now, applied after this block's MFMAs)
+      float f[TM][TN];
+      if (more) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) f[i][j] = scale_of(i, j, kb) * __builtin_amdgcn_rcpf(scale_of(i, j, kb + 1));
+      }
+      issue_stage(kt + PD);
+      read_frags(kt + 1, 1, nb);
+      mfmas(0);
+      finish_stage();
+      issue_stage(kt + 1 + PD);
+      read_frags(kt + 2, 0, nb);  // the last step reads an unused ring slot (in bounds)
+      mfmas(1);
+      if (more) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          if (!FULL && i >= nb) continue;
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] *= f[i][j];
+        }
+      }
+      finish_stage();
+    }
+  };
+  if (nbi == TM) main_loop(std::integral_constant<bool, true>());
+  else main_loop(std::integral_constant<bool, false>());
+  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));  // no ring load may land after the workgroup ends
+
+  // ---- epilogue: acc[i][j][4g+q] of lane l is C[row i*32 + l%32][col j*32 + 8g + 4(l/32) + q]
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const float f = scale_of(i, j, nkb - 1);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] *= f;
+    }
+  const int erow = wm * WTM + frow;
+  if (EPI == EPI_STORE) {
+    const int ecol = col0 + wn * WTN + 4 * fhalf;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row = r0 + erow + i * 32;
+      if (row < r1) {
+        uint16_t* orow = p.out + (int64_t)row * p.ldc + ecol;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            *(bf16x4*)(orow + j * 32 + 8 * g) = bf16x4{(__bf16)acc[i][j][4 * g], (__bf16)acc[i][j][4 * g + 1],
+                                                       (__bf16)acc[i][j][4 * g + 2], (__bf16)acc[i][j][4 * g + 3]};
+      }
+    }
+    return;
+  }
+  // SwiGLU (gate block j = 0, up block j = 1) and 1x128 re-quantisation: the tile holds output
+  // columns [n_tile*128, +128), wave wn columns wn*32 + [0,32); the row maximum is combined
+  // over the two lanes of a row and over the four waves through LDS (the ring is free now).
+  float y[TM][16];
+  float* red = (float*)lds;  // [256 rows][4 waves]
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    float m = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      y[i][v] = acc[i][0][v] * acc[i][1][v] * __builtin_amdgcn_rcpf(1.0f + __expf(-acc[i][0][v]));
+      m = fmaxf(m, fabsf(y[i][v]));
+    }
+    m = fmaxf(m, __shfl_xor(m, 32));
+    if (fhalf == 0) red[(erow + i * 32) * 4 + wn] = m;
+  }
+  __syncthreads();
+  const int ycol = n_tile * 128 + wn * 32 + 4 * fhalf;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int rl = erow + i * 32, row = r0 + rl;
+    const f32x4 mx = *(const f32x4*)(red + rl * 4);
+    float sc = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])) / 448.0f;
+    if (sc == 0.0f) sc = 1.0f;
+    if (row < r1) {
+      uint8_t* qrow = p.outq + (int64_t)row * p.I + ycol;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint32_t q = (uint32_t)f32_to_e4m3(y[i][4 * g] / sc) | ((uint32_t)f32_to_e4m3(y[i][4 * g + 1] / sc) << 8) |
+                           ((uint32_t)f32_to_e4m3(y[i][4 * g + 2] / sc) << 16) |
+                           ((uint32_t)f32_to_e4m3(y[i][4 * g + 3] / sc) << 24);
+        *(uint32_t*)(qrow + 8 * g) = q;
+      }
+      if (p.out) {
+        uint16_t* brow = p.out + (int64_t)row * p.I + ycol;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *(bf16x4*)(brow + 8 * g) = bf16x4{(__bf16)y[i][4 * g], (__bf16)y[i][4 * g + 1], (__bf16)y[i][4 * g + 2],
+                                            (__bf16)y[i][4 * g + 3]};
+      }
+      if (wn == 0 && fhalf == 0) p.outs[(int64_t)row * (p.I / 128) + n_tile] = sc;
+    }
+  }
+}
+
 }  // namespace f8
 
 static inline int64_t f8_ws_bytes(int64_t M, int64_t E, int64_t BM) {
@@ -417,6 +715,19 @@ static inline int64_t f8_ws_bytes(int64_t M, int64_t E, int64_t BM) {
 
 template <int EPI>
 static int launch_fp8(const f8::Args& a, const int32_t* gs, int64_t E, int64_t nn, void* ws, hipStream_t st) {
+  const bool v3ok = a.K <= 128 * f8::v3::MAX_KB && (int64_t)a.M * a.K < (int64_t(1) << 32) &&
+                    (int64_t)a.N * a.K < (int64_t(1) << 32);
+  if (v3ok) {
+    int* count = (int*)ws;
+    MTileF8* tiles = (MTileF8*)((char*)ws + 256);
+    hipLaunchKernelGGL(f8::build_tiles_f8_kernel, dim3(1), dim3(1024), 0, st, gs, (int)E, a.M, 256, count, tiles);
+    f8::Args b = a;
+    b.count = count;
+    b.tiles = tiles;
+    const int64_t grid = round_up((ceil_div(a.M, 256) + E + 1) * nn, 8);
+    hipLaunchKernelGGL((f8::gmm_fp8_v3_kernel<EPI>), dim3((unsigned)grid), dim3(512), 0, st, b);
+    return check_launch();
+  }
   constexpr int BM = 128, BN = 256;
   int* count = (int*)ws;
   MTileF8* tiles = (MTileF8*)((char*)ws + 256);

@@ -23,6 +23,7 @@
 // tgmm) are loaded as 8x8 blocks and transposed in registers with v_perm_b32.
 // f32 path (and shapes the MFMA tiling does not cover): an LDS-tiled exact-fp32 FMA kernel.
 #include "common.h"
+#include "lds_dma.h"
 #include <type_traits>
 #include <algorithm>
 
@@ -646,17 +647,6 @@ __device__ __forceinline__ int bn_off(int k, int c) { return k * 512 + ((c ^ ((k
 
 typedef __attribute__((ext_vector_type(4))) short s16x4;
 typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
-typedef __attribute__((address_space(3))) char lds_char;
-// 16-byte direct global->LDS load: lane l writes LDS byte lds_base + 16*l (lds_base is
-// wave-uniform).  Issued as inline asm so that the compiler does not serialise the LDS reads
-// of other ring stages behind these loads; the kernel waits for them with MTX_VMCNT.
-__device__ __forceinline__ void gload_lds16(const void* gptr, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base)
-               : "memory", "m0");
-}
-// s_waitcnt immediate (GFX9 encoding) that waits for vmcnt <= N only.
-#define MTX_VMCNT(N) ((((N) & 0xF)) | (0x7 << 4) | (0xF << 8) | ((((N) >> 4) & 0x3) << 14))
-typedef __attribute__((address_space(1))) const char gbl_char;
 #ifndef MTX_V3_SB
 #define MTX_V3_SB 0
 #endif

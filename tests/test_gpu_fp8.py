@@ -51,14 +51,19 @@ def _groups(rng, M, E):
     return gs
 
 
-@pytest.mark.parametrize("M,E,Kin,Kout", [(1024, 4, 512, 512), (700, 8, 256, 256), (2000, 16, 128, 768)])
+@pytest.mark.parametrize("M,E,Kin,Kout", [(1024, 4, 512, 512), (700, 8, 256, 256), (2000, 16, 128, 768),
+                                           (1500, 6, 2048, 256), (600, 3, 3072, 512),
+                                           (400, 2, 3200, 256)])  # K > 3072: register-staged kernel
 def test_gmm_fp8(dev, M, E, Kin, Kout):
     from mintext_amd.kernels.fp8 import grouped_matmul_fp8, quantize_fp8_rows, quantize_fp8_weights
 
     rng = np.random.default_rng(M)
     gs = _groups(rng, M, E)
-    x = torch.randn(M, Kin, device=dev).bfloat16()
-    w = (torch.randn(E, Kin, Kout, device=dev) * 0.02).bfloat16()
+    # per-128-block magnitudes spread over 1e-3 .. 1e3 exercise the block-to-block rescaling
+    blk = torch.from_numpy(10.0 ** rng.uniform(-3, 3, (M, Kin // 128))).float().to(dev)
+    x = (torch.randn(M, Kin, device=dev) * blk.repeat_interleave(128, 1)).bfloat16()
+    wblk = torch.from_numpy(10.0 ** rng.uniform(-1, 1, (E, Kin // 128, 1))).float().to(dev)
+    w = (torch.randn(E, Kin, Kout, device=dev) * 0.02 * wblk.repeat_interleave(128, 1)).bfloat16()
     xq, xs = quantize_fp8_rows(x)
     wq, ws = quantize_fp8_weights(w)
     out = grouped_matmul_fp8(xq, xs, wq, ws, _t(gs, dev))
@@ -71,7 +76,7 @@ def test_gmm_fp8(dev, M, E, Kin, Kout):
     assert (out[tot:] == 0).all()
 
 
-@pytest.mark.parametrize("M,E,Kin,I", [(1024, 4, 256, 256), (900, 8, 512, 384)])
+@pytest.mark.parametrize("M,E,Kin,I", [(1024, 4, 256, 256), (900, 8, 512, 384), (2048, 8, 2048, 768)])
 def test_gmm_fp8_swiglu_requant(dev, M, E, Kin, I):
     from mintext_amd.kernels.fp8 import grouped_matmul_fp8_swiglu, quantize_fp8_rows, quantize_fp8_weights
 
