@@ -732,6 +732,9 @@ __global__ __launch_bounds__(WM* WN * 64, 2) void gmm_v3_kernel(Args p) {
     }
   }
 
+  const int nk = (MODE == TGMM) ? (r1 - r0 + BKS - 1) / BKS : p.Kred / BKS;
+  const int tail = (MODE == TGMM) ? (r1 - r0) - (nk - 1) * BKS : BKS;  // rows in the last step
+
   // ---- per-lane global sources of the load instructions (byte offsets at k-step 0) -----
   // A row-major operand (FWD/DLHS): lane l of segment s fills row 16s + l/4, chunk slot l%4.
   // Transposed operands (W in FWD, x and g in TGMM): lane l fills reduction row 2s + l/32,
@@ -790,8 +793,11 @@ __global__ __launch_bounds__(WM* WN * 64, 2) void gmm_v3_kernel(Args p) {
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_char*)lds;
   const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
   const int mlast = p.M - 1;
-  auto issue_stage = [&](int kt) {
-    const uint32_t st = lds_base + (uint32_t)(C::slot(kt) * STAGE);
+  // Stages past the end re-read the last one (in bounds) into a ring slot that is no longer
+  // read, which keeps the main loop free of branches.
+  auto issue_stage = [&](int kt_) {
+    const uint32_t st = lds_base + (uint32_t)(C::slot(kt_) * STAGE);
+    const int kt = min(kt_, nk - 1);
     if constexpr (MODE == TGMM) {
 #pragma unroll
       for (int i = 0; i < A_INSTR; ++i) {
@@ -871,15 +877,11 @@ __global__ __launch_bounds__(WM* WN * 64, 2) void gmm_v3_kernel(Args p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  const int nk = (MODE == TGMM) ? (r1 - r0 + BKS - 1) / BKS : p.Kred / BKS;
-  const int tail = (MODE == TGMM) ? (r1 - r0) - (nk - 1) * BKS : BKS;  // rows in the last step
   constexpr int LPS = A_INSTR + B_INSTR;  // load instructions per stage per thread
   // prologue: stages 0..PD-1 in flight; stages 0 and 1 landed and visible
 #pragma unroll
-  for (int s = 0; s < PD; ++s)
-    if (nk > s) issue_stage(s);
-  if (nk >= PD) __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));  // (vmcnt counts outstanding loads)
-  else __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));
+  for (int s = 0; s < PD; ++s) issue_stage(s);
+  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));  // (vmcnt counts outstanding loads)
   __syncthreads();
   // 32-row blocks of this wave that hold rows of the group (FWD/DLHS tiles of small groups
   // are partly empty): MFMAs and A reads of empty blocks are skipped.
@@ -890,7 +892,7 @@ __global__ __launch_bounds__(WM* WN * 64, 2) void gmm_v3_kernel(Args p) {
     constexpr bool FULL = decltype(full_tag)::value;
     const int nb = FULL ? TM : nbi;
     for (int kt = 0; kt < nk; ++kt) {
-      if (kt + PD < nk) issue_stage(kt + PD);
+      issue_stage(kt + PD);
       // substep 0: prefetch substep 1 of this stage
       read_frags(kt, 1, 1, nb);
       if (MODE == TGMM && tail < BKS && kt == nk - 1) mask_frags(0, 0, tail);
@@ -914,15 +916,16 @@ __global__ __launch_bounds__(WM* WN * 64, 2) void gmm_v3_kernel(Args p) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
       }
-      // stage kt+2 must have landed before the barrier makes it visible to every wave
-      if (kt + PD < nk) __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
-      else __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));
+      // stage kt+2 must have landed before the barrier makes it visible to every wave (later
+      // stages, possibly re-reads past the end, may still be in flight)
+      __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
       __syncthreads();
     }
   };
   // Both loop versions execute the same barriers, so waves of one workgroup may take either.
   if (MODE == TGMM || nbi == TM) main_loop(std::integral_constant<bool, true>());
   else main_loop(std::integral_constant<bool, false>());
+  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));  // no ring load may land after the workgroup ends
 
   // ---- epilogue: the MFMAs computed C^T blocks (operands swapped), so acc[i][j][4g+q] of lane
   // l is C[row i*32 + l%32][col j*32 + 8g + 4(l/32) + q]: four consecutive columns per lane,
