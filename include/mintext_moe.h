@@ -149,7 +149,9 @@ int mtx_swiglu_bwd(const void* h, const void* dy, int dtype, int64_t M, int64_t 
  * Activations: 1x128 groups along the row, scale = amax/448 (1 when amax == 0),
  * q = RNE(x / scale).  Weights: 128x128 blocks over (Kout, Kin), stored k-contiguous
  * w_q [E,Kout,Kin] with w_scale [E,Kout/128,Kin/128] (the per-expert nn.Linear layout).
- * Kin, Kout (and I) must be multiples of 128.                                           */
+ * Kin, Kout (and I) must be multiples of 128.  The block scales passed to the GEMMs must be
+ * finite and nonzero (the quantisers never produce 0).  mtx_quant_fp8_rows needs x 16-byte
+ * and xq 8-byte aligned (MTX_ERR_ARG otherwise).                                          */
 int mtx_quant_fp8_rows(const void* x, int dtype, int64_t M, int64_t D,
                        uint8_t* xq, float* x_scale, void* stream);
 /* w [E,Kin,Kout] (F32/BF16, reference layout) -> w_q [E,Kout,Kin], w_scale [E,Kout/128,Kin/128] */

@@ -65,38 +65,63 @@ __global__ __launch_bounds__(kRouteThreads) void route_count_kernel(
     counts[(int64_t)blockIdx.x * nb + b] = hist[b];
 }
 
-// Single workgroup of 1024 threads; nb <= 1024.
+// Single workgroup of 1024 threads; nb <= 1024.  counts[c][b] (per-chunk bucket counts) become
+// the exclusive offsets of chunk c's keys b in the stable order.  Thread (g, b) owns bucket b
+// for chunk group g (G = 1024 / nb groups of consecutive chunks), so the serial part is one
+// group's chunks.
 __global__ __launch_bounds__(1024) void route_scan_kernel(
     int32_t* __restrict__ counts, int nchunks, int nb, int E, int32_t* __restrict__ group_sizes) {
+  __shared__ int part[1024];  // [g][b] group sums, then group bases
   __shared__ int wsum[16];
-  const int b = threadIdx.x;
+  __shared__ int bucket_base[1024];
+  const int tid = threadIdx.x;
+  const int G = max(1, min(1024 / nb, nchunks));
+  const int cpg = (nchunks + G - 1) / G;
+  const int g = tid / nb, b = tid - g * nb;
+  const bool act = g < G;
+  const int c0 = g * cpg, c1 = min(c0 + cpg, nchunks);
   int sum = 0;
-  if (b < nb)
-    for (int c = 0; c < nchunks; ++c) sum += counts[(int64_t)c * nb + b];
-  // block-wide exclusive scan of sum over b (wave scan + scan of wave totals)
-  const int lane = b & 63, w = b >> 6;
-  int incl = sum;
+  if (act)
+    for (int c = c0; c < c1; ++c) sum += counts[(int64_t)c * nb + b];
+  if (act) part[g * nb + b] = sum;
+  __syncthreads();
+  // per bucket: exclusive scan over groups, and the bucket total
+  int total = 0;
+  if (tid < nb) {
+    for (int q = 0; q < G; ++q) {
+      const int x = part[q * nb + tid];
+      part[q * nb + tid] = total;
+      total += x;
+    }
+  }
+  // exclusive scan of bucket totals over b (wave scan + scan of wave totals)
+  const int lane = tid & 63, w = tid >> 6;
+  const int v = (tid < nb) ? total : 0;
+  int incl = v;
   for (int off = 1; off < 64; off <<= 1) {
     const int o = __shfl_up(incl, off);
     if (lane >= off) incl += o;
   }
   if (lane == 63) wsum[w] = incl;
   __syncthreads();
-  if (b == 0) {
+  if (tid == 0) {
     int run = 0;
-    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) { const int x = wsum[i]; wsum[i] = run; run += x; }
+    for (int i = 0; i < 16; ++i) { const int x = wsum[i]; wsum[i] = run; run += x; }
   }
   __syncthreads();
-  const int excl = incl - sum + wsum[w];
-  if (b < nb) {
-    int base = excl;
-    for (int c = 0; c < nchunks; ++c) {
+  if (tid < nb) {
+    bucket_base[tid] = incl - v + wsum[w];
+    if (tid < E) group_sizes[tid] = total;
+  }
+  __syncthreads();
+  if (act) {
+    int base = bucket_base[b] + part[g * nb + b];
+    for (int c = c0; c < c1; ++c) {
       const int64_t o = (int64_t)c * nb + b;
       const int x = counts[o];
       counts[o] = base;
       base += x;
     }
-    if (b < E) group_sizes[b] = sum;
   }
 }
 
@@ -168,6 +193,39 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(
   }
 }
 
+// 16-byte-aligned rows: out[j] = src[index[j] / div] as a flat list of 16-byte items (row j,
+// chunk c); each thread moves UNR items per step with all loads issued before the stores, so
+// short rows (fp8 scale rows of 64 bytes) keep every lane busy and long rows keep UNR loads in
+// flight per lane.
+template <int UNR>
+__global__ __launch_bounds__(256) void gather_chunks_kernel(
+    const char* __restrict__ src, int64_t src_rows, int64_t cpr, int cpr_shift,
+    const int32_t* __restrict__ index, int64_t rows, int64_t div, char* __restrict__ out) {
+  const int64_t total = rows * cpr;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t base = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; base < total; base += stride * UNR) {
+    u32x4 v[UNR];
+    int64_t dst[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int64_t it = base + u * stride;
+      dst[u] = -1;
+      if (it < total) {
+        const int64_t j = cpr_shift >= 0 ? (it >> cpr_shift) : it / cpr;
+        const int64_t c = it - j * cpr;
+        const int p = index[j];
+        const int64_t r = (p >= 0) ? (int64_t)(p / (int)div) : -1;
+        dst[u] = it;
+        if (r >= 0 && r < src_rows) v[u] = ((const u32x4*)src)[r * cpr + c];
+        else v[u] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+      if (dst[u] >= 0) ((u32x4*)out)[dst[u]] = v[u];
+  }
+}
+
 // out[index[j]] = src[j]
 template <typename VT>
 __global__ __launch_bounds__(256) void scatter_rows_kernel(
@@ -202,10 +260,19 @@ static int launch_gather(const void* src, int64_t src_rows, int64_t row_bytes, c
   if (blocks > 65536) blocks = 65536;
   const bool a16 = (row_bytes % 16 == 0) && ((uintptr_t)src % 16 == 0) && ((uintptr_t)out % 16 == 0);
   const bool a4 = (row_bytes % 4 == 0) && ((uintptr_t)src % 4 == 0) && ((uintptr_t)out % 4 == 0);
-  if (a16)
-    hipLaunchKernelGGL(gather_rows_kernel<u32x4>, dim3(blocks), dim3(256), 0, st, (const char*)src,
-                       src_rows, row_bytes, index, rows, div, (char*)out);
-  else if (a4)
+  if (a16) {
+    const int64_t cpr = row_bytes / 16;
+    int shift = -1;
+    if ((cpr & (cpr - 1)) == 0) {
+      shift = 0;
+      while ((int64_t(1) << shift) < cpr) ++shift;
+    }
+    constexpr int UNR = 8;
+    int64_t gb = ceil_div(rows * cpr, 256 * UNR);
+    if (gb > 16384) gb = 16384;
+    hipLaunchKernelGGL(gather_chunks_kernel<UNR>, dim3(gb), dim3(256), 0, st, (const char*)src, src_rows, cpr,
+                       shift, index, rows, div, (char*)out);
+  } else if (a4)
     hipLaunchKernelGGL(gather_rows_kernel<uint32_t>, dim3(blocks), dim3(256), 0, st, (const char*)src,
                        src_rows, row_bytes, index, rows, div, (char*)out);
   else
@@ -245,8 +312,11 @@ __device__ __forceinline__ void store8(uint16_t* p, const float* v) {
                           pack_bf16x2(v[6], v[7]));
 }
 
-// One wave per token; VEC8 = D % 8 == 0 and aligned pointers.
-template <typename YT, typename WT, typename OT, bool VEC8>
+// One wave per token; VEC8 = D % 8 == 0 and aligned pointers.  With KMAX > 0 (K <= KMAX) the
+// token's K row indices and weights are read first and the K rows of each 512-element slice are
+// loaded together (K independent 16-byte loads in flight per lane) before they are summed in
+// k order; the arithmetic is the same fmaf chain as the generic path.
+template <typename YT, typename WT, typename OT, bool VEC8, int KMAX>
 __global__ __launch_bounds__(256) void unroute_kernel(
     const YT* __restrict__ Y, const int32_t* __restrict__ inv, const WT* __restrict__ w,
     int64_t N, int K, int64_t D, OT* __restrict__ out) {
@@ -254,7 +324,39 @@ __global__ __launch_bounds__(256) void unroute_kernel(
   const int64_t n = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   if (n >= N) return;
   const int64_t M = N * (int64_t)K;
-  if (VEC8) {
+  if constexpr (VEC8 && KMAX > 0) {
+    int64_t jj[KMAX];
+    float ww[KMAX];
+    bool ok[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      ok[k] = false;
+      jj[k] = 0;
+      ww[k] = 0.0f;
+      if (k < K) {
+        const int64_t j = inv[n * K + k];
+        ok[k] = (j >= 0 && j < M);
+        jj[k] = ok[k] ? j : 0;
+        ww[k] = w ? ldf<WT>(w, n * K + k) : 1.0f;
+      }
+    }
+    for (int64_t d = (int64_t)lane * 8; d < D; d += 512) {
+      float y[KMAX][8];
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k)
+        if (k < K) load8(Y + jj[k] * D + d, y[k]);
+      float acc[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k)
+        if (k < K && ok[k]) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] = fmaf(ww[k], y[k][i], acc[i]);
+        }
+      store8(out + n * D + d, acc);
+    }
+  } else if constexpr (VEC8) {
     for (int64_t d = (int64_t)lane * 8; d < D; d += 512) {
       float acc[8];
 #pragma unroll
@@ -289,12 +391,15 @@ static void launch_unroute_t(const void* Y, const int32_t* inv, const void* w, i
                              int64_t D, void* out, hipStream_t st) {
   const int64_t blocks = ceil_div(N, 4);
   const bool v8 = (D % 8 == 0) && ((uintptr_t)Y % 16 == 0) && ((uintptr_t)out % 16 == 0);
-  if (v8)
-    hipLaunchKernelGGL((unroute_kernel<YT, WT, OT, true>), dim3(blocks), dim3(256), 0, st,
-                       (const YT*)Y, inv, (const WT*)w, N, K, D, (OT*)out);
-  else
-    hipLaunchKernelGGL((unroute_kernel<YT, WT, OT, false>), dim3(blocks), dim3(256), 0, st,
-                       (const YT*)Y, inv, (const WT*)w, N, K, D, (OT*)out);
+#define MTX_UNROUTE(V, KM)                                                                                  \
+  hipLaunchKernelGGL((unroute_kernel<YT, WT, OT, V, KM>), dim3(blocks), dim3(256), 0, st, (const YT*)Y, inv, \
+                     (const WT*)w, N, K, D, (OT*)out)
+  if (v8 && K <= 2) MTX_UNROUTE(true, 2);
+  else if (v8 && K <= 4) MTX_UNROUTE(true, 4);
+  else if (v8 && K <= 8) MTX_UNROUTE(true, 8);
+  else if (v8) MTX_UNROUTE(true, 0);
+  else MTX_UNROUTE(false, 0);
+#undef MTX_UNROUTE
 }
 
 // unroute backward, one wave per token n (reference VJP of moe_dispatch.py:102-111):

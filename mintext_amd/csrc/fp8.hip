@@ -33,33 +33,53 @@ constexpr int BK = 128;  // bytes of k per step == one scale block
 __device__ __forceinline__ int lds_off(int r, int c) { return r * 128 + ((c ^ (r & 7) ^ ((r >> 3) & 7)) << 4); }
 
 // ---- quantisers ------------------------------------------------------------------------------
-// One wave per (row, 128-group): 2 elements per lane.
+// 16 bytes per lane: a 128-group spans LPG = 128 / EPL lanes (16 for bf16, 32 for f32), so a
+// wave quantises 64 / LPG groups per step; the group maximum is a butterfly within those lanes.
 template <typename T>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const T* __restrict__ x, int64_t M, int64_t D,
                                                          uint8_t* __restrict__ xq, float* __restrict__ xs) {
+  constexpr int EPL = 16 / sizeof(T), LPG = 128 / EPL, GPW = 64 / LPG;
   const int lane = threadIdx.x & 63;
+  const int sub = lane / LPG, gl = lane % LPG;
   const int64_t ng = D / 128;
+  const int64_t total = M * ng;
   const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
-  for (int64_t t = wid; t < M * ng; t += nw) {
-    const int64_t r = t / ng, g = t % ng;
-    const int64_t base = r * D + g * 128 + lane * 2;
-    float a, b;
+  for (int64_t t0 = wid * GPW; t0 < total; t0 += nw * GPW) {
+    const int64_t t = t0 + sub;
+    const bool ok = t < total;
+    const int64_t tt = ok ? t : total - 1;
+    const int64_t r = tt / ng, g = tt % ng;
+    const int64_t base = r * D + g * 128 + gl * EPL;
+    float v[EPL];
+    const u32x4 raw = *(const u32x4*)(x + base);
     if constexpr (sizeof(T) == 4) {
-      a = ((const float*)x)[base];
-      b = ((const float*)x)[base + 1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(raw[i]);
     } else {
-      const uint32_t u = *(const uint32_t*)((const uint16_t*)x + base);
-      a = __uint_as_float(u << 16);
-      b = __uint_as_float(u & 0xffff0000u);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(raw[i] << 16);
+        v[2 * i + 1] = __uint_as_float(raw[i] & 0xffff0000u);
+      }
     }
-    float m = fmaxf(fabsf(a), fabsf(b));
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    float s = m / 448.0f;
-    if (s == 0.0f) s = 1.0f;
-    const uint16_t q = (uint16_t)f32_to_e4m3(a / s) | ((uint16_t)f32_to_e4m3(b / s) << 8);
-    *(uint16_t*)(xq + base) = q;
-    if (lane == 0) xs[r * ng + g] = s;
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) m = fmaxf(m, fabsf(v[i]));
+#pragma unroll
+    for (int off = LPG / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    float sc = m / 448.0f;
+    if (sc == 0.0f) sc = 1.0f;
+    uint32_t q[EPL / 4];
+#pragma unroll
+    for (int i = 0; i < EPL / 4; ++i)
+      q[i] = (uint32_t)f32_to_e4m3(v[4 * i] / sc) | ((uint32_t)f32_to_e4m3(v[4 * i + 1] / sc) << 8) |
+             ((uint32_t)f32_to_e4m3(v[4 * i + 2] / sc) << 16) | ((uint32_t)f32_to_e4m3(v[4 * i + 3] / sc) << 24);
+    if (ok) {
+      if constexpr (EPL == 8) *(uint2*)(xq + base) = make_uint2(q[0], q[1]);
+      else *(uint32_t*)(xq + base) = q[0];
+      if (gl == 0) xs[r * ng + g] = sc;
+    }
   }
 }
 
@@ -749,8 +769,9 @@ extern "C" int mtx_quant_fp8_rows(const void* x, int dtype, int64_t M, int64_t D
   if (M < 0 || D < 0 || D % 128 != 0 || (dtype != MTX_F32 && dtype != MTX_BF16)) return MTX_ERR_ARG;
   if (M == 0 || D == 0) return MTX_OK;
   if (!x || !xq || !x_scale) return MTX_ERR_ARG;
-  int64_t blocks = ceil_div(M * (D / 128), 4);
-  if (blocks > 65536) blocks = 65536;
+  if (((uintptr_t)x % 16) || ((uintptr_t)xq % 8)) return MTX_ERR_ARG;
+  int64_t blocks = ceil_div(M * (D / 128), 16);
+  if (blocks > 16384) blocks = 16384;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MTX_F32)
     hipLaunchKernelGGL(f8::quant_rows_kernel<float>, dim3(blocks), dim3(256), 0, st, (const float*)x, M, D, xq,
