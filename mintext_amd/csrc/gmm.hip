@@ -1003,6 +1003,9 @@ static int launch_build_tiles(const int32_t* gs, int64_t E, int64_t M, int BM, c
 #ifndef MTX_V3_NSTAGE
 #define MTX_V3_NSTAGE 4
 #endif
+#ifndef MTX_V3_WN
+#define MTX_V3_WN 4
+#endif
 #ifndef MTX_V3_SMALL_MEAN
 #define MTX_V3_SMALL_MEAN 0
 #endif
@@ -1010,7 +1013,8 @@ template <int MODE, int EPI>
 static int launch_v3(const mf::Args& a, int64_t grid, hipStream_t st) {
   if (grid <= 0) return MTX_OK;
   grid = round_up(grid, 8);
-  hipLaunchKernelGGL((mf::gmm_v3_kernel<MODE, EPI, 2, 4, 256, MTX_V3_NSTAGE>), dim3((unsigned)grid), dim3(512), 0, st, a);
+  hipLaunchKernelGGL((mf::gmm_v3_kernel<MODE, EPI, 2, MTX_V3_WN, 256, MTX_V3_NSTAGE>), dim3((unsigned)grid),
+                     dim3(128 * MTX_V3_WN), 0, st, a);
   return check_launch();
 }
 template <int MODE, int EPI>
