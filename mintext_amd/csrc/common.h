@@ -78,6 +78,22 @@ __device__ __forceinline__ uint8_t f32_to_e4m3(float f) {
   return (uint8_t)(sign | (uint8_t)(exp << 3) | (uint8_t)keep);
 }
 
+// Four values -> four e4m3fn codes (byte i = value i) with the same results as f32_to_e4m3:
+// the value is clamped to +-448 and converted by v_cvt_pk_fp8_f32 (OCP e4m3, RNE on gfx950,
+// checked against f32_to_e4m3 over every f32 with |x| in [2^-30, 2^10)); NaN keeps its sign.
+__device__ __forceinline__ uint32_t e4m3_pack4(float a, float b, float c, float d) {
+  auto cl = [](float x) { return fminf(fmaxf(x, -448.0f), 448.0f); };
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(cl(a), cl(b), 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(cl(c), cl(d), w, true);
+  uint32_t q = (uint32_t)w;
+  const float v[4] = {a, b, c, d};
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (__builtin_expect(v[i] != v[i], 0))
+      q = (q & ~(0xffu << (8 * i))) | ((uint32_t)(f32_to_e4m3(v[i])) << (8 * i));
+  return q;
+}
+
 __device__ __forceinline__ float e4m3_to_f32(uint8_t v) {
   uint32_t sign = (v & 0x80u) ? 0x80000000u : 0u;
   uint32_t e = (v >> 3) & 0xfu, m = v & 7u;

@@ -73,8 +73,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const T* __restrict__ x
     uint32_t q[EPL / 4];
 #pragma unroll
     for (int i = 0; i < EPL / 4; ++i)
-      q[i] = (uint32_t)f32_to_e4m3(v[4 * i] / sc) | ((uint32_t)f32_to_e4m3(v[4 * i + 1] / sc) << 8) |
-             ((uint32_t)f32_to_e4m3(v[4 * i + 2] / sc) << 16) | ((uint32_t)f32_to_e4m3(v[4 * i + 3] / sc) << 24);
+      q[i] = e4m3_pack4(v[4 * i] / sc, v[4 * i + 1] / sc, v[4 * i + 2] / sc, v[4 * i + 3] / sc);
     if (ok) {
       if constexpr (EPL == 8) *(uint2*)(xq + base) = make_uint2(q[0], q[1]);
       else *(uint32_t*)(xq + base) = q[0];
@@ -727,6 +726,321 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v3_kernel(Args p) {
   }
 }
 
+
+// ---- v4: persistent workgroups, block scales streamed through the ring -------------------------
+// Same tile, fragments and accumulation as v3, but (1) each workgroup walks a list of tiles and
+// the ring keeps loading across tile boundaries (the next tile's first stages are in flight
+// while the current tile finishes and stores), and (2) the scales travel with the data: the
+// even stage of every 128-k block also carries that block's 256 x-row scales (global_load_lds
+// of 4 bytes per lane, waves 0-3) and its two weight-block scales (wave 4), so no tile prologue
+// waits on memory.  Needs K >= 256 (four stages per tile, three in flight).
+namespace v4 {
+constexpr int BM = 256, BN = 256, BKB = 64, NSTAGE = 4, PD = 3;
+constexpr int A_BYTES = BM * BKB, B_BYTES = BN * BKB;
+constexpr int S_OFF = A_BYTES + B_BYTES;  // per slot: [0,1K) x-row scales, [1K,1K+8) weight scales
+constexpr int STAGE = S_OFF + 2048;
+constexpr int GM = 8;
+struct Tile {
+  int e, r0, r1, n_tile, zero;
+};
+}  // namespace v4
+
+template <int EPI>
+__global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
+  using namespace v4;
+  using v3::a_off;
+  constexpr int WN = 4, WTM = 128, WTN = 64, TM = 4, TN = 2;
+  constexpr int LPS = 4;  // data loads per wave and stage; even stages add one scale load
+  __shared__ __attribute__((aligned(1024))) char lds[NSTAGE * STAGE];
+  __shared__ float red[BM * 4];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int nn = (EPI == EPI_SWIGLU_Q) ? (p.I / 128) : (p.N / BN);
+  const int cnt = p.count[0];
+  const int total = cnt * nn;
+  // XCD x (= blockIdx % 8) sweeps tiles [x*per, (x+1)*per) with its gridDim/8 workgroups
+  const int nx = (int)(gridDim.x >> 3), xcd = (int)(blockIdx.x & 7), q = (int)(blockIdx.x >> 3);
+  const int per = (total + 7) >> 3;
+  const int lid_end = min((xcd + 1) * per, total);
+  int lid = xcd * per + q;
+  if (lid >= lid_end) return;
+  const int nkb = p.K / 128, nk = p.K / BKB;
+
+  auto decode = [&](int l) -> Tile {
+    const int grp = l / (GM * nn);
+    const int first_m = grp * GM;
+    const int gsz = min(GM, cnt - first_m);
+    const int local = l - grp * GM * nn;
+    const MTileF8 t = p.tiles[first_m + local % gsz];
+    Tile T;
+    T.zero = t.e < 0;
+    T.e = t.e < 0 ? 0 : t.e;  // rows past sum(group_sizes): computed with expert 0, stored as 0
+    T.r0 = t.r0;
+    T.r1 = t.r1;
+    T.n_tile = local / gsz;
+    return T;
+  };
+  // weight row of tile-local column c (SwiGLU tiles pair gate and up rows, 32 of each per wave)
+  auto b_row = [&](const Tile& T, int c) -> int {
+    if (EPI == EPI_SWIGLU_Q) {
+      const int w_ = c / WTN, within = c % WTN;
+      return (within / 32) * p.I + T.n_tile * 128 + w_ * 32 + within % 32;
+    }
+    return T.n_tile * BN + c;
+  };
+  struct Src {
+    uint32_t aoff[2], boff[2];
+    const uint8_t* B;
+    const float* sp;  // this lane's scale source for k-block 0 (stride 1 float per block)
+  };
+  auto make_src = [&](const Tile& T) -> Src {
+    Src S;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int seg = wave * 2 + i;
+      const int r = seg * 16 + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
+      S.aoff[i] = (uint32_t)min(T.r0 + r, T.r1 - 1) * (uint32_t)p.K + (uint32_t)(c * 16);
+      S.boff[i] = (uint32_t)b_row(T, r) * (uint32_t)p.K + (uint32_t)(c * 16);
+    }
+    S.B = p.wq + (int64_t)T.e * p.N * p.K;
+    if (wave < 4) {
+      S.sp = p.xs + (int64_t)min(T.r0 + 64 * wave + lane, T.r1 - 1) * nkb;
+    } else if (wave == 4) {
+      const int h = lane & 1;
+      const int nblk = (EPI == EPI_SWIGLU_Q) ? (h * (p.I / 128) + T.n_tile) : (T.n_tile * 2 + h);
+      S.sp = p.ws + ((int64_t)T.e * (p.N / 128) + nblk) * nkb;
+    } else {
+      S.sp = p.xs + (int64_t)T.r0 * nkb;  // filler load, keeps the per-wave load count uniform
+    }
+    return S;
+  };
+
+  Tile cur = decode(lid);
+  int lid_next = lid + nx;
+  Tile nxt = lid_next < lid_end ? decode(lid_next) : cur;
+  Src scur = make_src(cur), snxt = make_src(nxt);
+
+  const uint32_t lds_base = lds_addr(lds);
+  const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+  // issue ring step g = stage kt of the current tile, or of the next one when kt >= nk
+  auto issue = [&](int g, int kt, bool even) {
+    const bool in = kt < nk;
+    const int k = in ? kt : kt - nk;
+    const uint32_t st = lds_base + (uint32_t)((g & (NSTAGE - 1)) * STAGE);
+    const uint32_t kofs = (uint32_t)k * BKB;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      gload_lds16(p.xq + (in ? scur.aoff[i] : snxt.aoff[i]) + kofs, st + (wave_u * 2 + i) * 1024u);
+    const uint8_t* B = in ? scur.B : snxt.B;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      gload_lds16(B + (in ? scur.boff[i] : snxt.boff[i]) + kofs, st + (uint32_t)A_BYTES + (wave_u * 2 + i) * 1024u);
+    if (even) gload_lds4((in ? scur.sp : snxt.sp) + (k >> 1), st + (uint32_t)S_OFF + wave_u * 256u);
+  };
+
+  i32x8 fa[2][TM], fb[2][TN];
+  const int frow = lane & 31, fhalf = lane >> 5;
+  auto ld32 = [&](const char* base, int r) -> i32x8 {
+    const u32x4 lo = *(const u32x4*)(base + a_off(r, 2 * fhalf));
+    const u32x4 hi = *(const u32x4*)(base + a_off(r, 2 * fhalf + 1));
+    return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  };
+  auto read_frags = [&](int g, int buf) {
+    const char* st = lds + (g & (NSTAGE - 1)) * STAGE;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[buf][i] = ld32(st, wm * WTM + i * 32 + frow);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[buf][j] = ld32(st + A_BYTES, wn * WTN + j * 32 + frow);
+  };
+  // scales of the k-block whose even stage sits in ring step g
+  float sa_c[TM], sb_c[2], sa_n[TM], sb_n[2];
+  auto read_scales = [&](int g, float* sa, float* sb) {
+    const float* sc = (const float*)(lds + (g & (NSTAGE - 1)) * STAGE + S_OFF);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) sa[i] = sc[wm * WTM + i * 32 + frow];
+    sb[0] = sc[256];
+    sb[1] = sc[257];
+  };
+  auto half_of = [&](int j) -> int { return (EPI == EPI_SWIGLU_Q) ? j : (wn >> 1); };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  // prologue: ring steps 0..2; steps 0 and 1 landed (step 2 = LPS + 1 loads may be in flight)
+  issue(0, 0, true);
+  issue(1, 1, false);
+  issue(2, 2, true);
+  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));
+  __syncthreads();
+  read_scales(0, sa_c, sb_c);
+  read_frags(0, 0);
+  int g = 0;
+
+  auto mfmas = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[buf][j], fa[buf][i], acc[i][j], 0, 0, 0, 127,
+                                                                    0, 127);
+  };
+
+  for (;;) {
+    for (int kb = 0; kb < nkb; ++kb) {
+      const int kt = 2 * kb;
+      // even stage kt (ring step g)
+      issue(g + PD, kt + PD, false);
+      read_frags(g + 1, 1);
+      mfmas(0);
+      __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS));  // step g+2 landed (g+3 may be in flight)
+      __syncthreads();
+      // odd stage kt+1 (ring step g+1)
+      issue(g + 1 + PD, kt + 1 + PD, true);
+      read_frags(g + 2, 0);              // next block's first stage (or the next tile's)
+      read_scales(g + 2, sa_n, sb_n);    // and its scales
+      mfmas(1);
+      if (kb + 1 < nkb) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            const float f = (sa_c[i] * sb_c[half_of(j)]) * __builtin_amdgcn_rcpf(sa_n[i] * sb_n[half_of(j)]);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] *= f;
+          }
+#pragma unroll
+        for (int i = 0; i < TM; ++i) sa_c[i] = sa_n[i];
+        sb_c[0] = sb_n[0];
+        sb_c[1] = sb_n[1];
+      }
+      __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));  // step g+3 landed (g+4 may be in flight)
+      __syncthreads();
+      g += 2;
+    }
+
+    // ---- epilogue of the current tile (the next tile's first stages are in flight) ---------
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const float f = sa_c[i] * sb_c[half_of(j)];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = cur.zero ? 0.0f : acc[i][j][v] * f;  // (not 0 * x: x may be NaN)
+      }
+    // Outputs are staged through ring slot g-1 (the tile's last stage, consumed; the next DMA
+    // into it is issued after the closing barrier) so that every global store writes 16
+    // contiguous bytes per lane and whole 128-byte lines per group of 8 lanes (32 KB used).
+    char* stg = lds + ((g - 1) & (NSTAGE - 1)) * STAGE;
+    const int erow = wm * WTM + frow;
+    if (EPI == EPI_STORE) {
+      // per wave: 32 rows x 64 bf16 columns (128 bytes) at a time; 16-byte chunk c of row r is
+      // stored at chunk c ^ (r & 7)
+      char* wst = stg + wave * 4096;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq)
+            *(bf16x4*)(wst + frow * 128 + (((4 * j + gq) ^ (frow & 7)) << 4) + 8 * fhalf) =
+                bf16x4{(__bf16)acc[i][j][4 * gq], (__bf16)acc[i][j][4 * gq + 1], (__bf16)acc[i][j][4 * gq + 2],
+                       (__bf16)acc[i][j][4 * gq + 3]};
+        __builtin_amdgcn_s_waitcnt(MTX_LGKMCNT0);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int rloc = rr * 8 + (lane >> 3);
+          const u32x4 v = *(const u32x4*)(wst + rloc * 128 + (((lane & 7) ^ (rloc & 7)) << 4));
+          const int row = cur.r0 + wm * WTM + i * 32 + rloc;
+          if (row < cur.r1)
+            *(u32x4*)(p.out + (int64_t)row * p.ldc + cur.n_tile * BN + wn * WTN + (lane & 7) * 8) = v;
+        }
+        __builtin_amdgcn_s_waitcnt(MTX_LGKMCNT0);  // reads done before the next block overwrites
+      }
+      __syncthreads();  // staging slot free before the next tile's first ring load
+    } else {
+      float y[TM][16];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        float m = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          y[i][v] = acc[i][0][v] * acc[i][1][v] * __builtin_amdgcn_rcpf(1.0f + __expf(-acc[i][0][v]));
+          m = fmaxf(m, fabsf(y[i][v]));
+        }
+        m = fmaxf(m, __shfl_xor(m, 32));
+        if (fhalf == 0) red[(erow + i * 32) * 4 + wn] = m;
+      }
+      __syncthreads();
+      // e4m3 codes of the tile's 128 output columns: [256 rows][128 bytes], 16-byte chunk c of
+      // row r at chunk c ^ (r & 7)
+      const int ycol = wn * 32 + 4 * fhalf;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int rl = erow + i * 32, row = cur.r0 + rl;
+        const f32x4 mx = *(const f32x4*)(red + rl * 4);
+        float sc = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])) / 448.0f;
+        if (sc == 0.0f) sc = 1.0f;
+        const float inv = 1.0f / sc;
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const uint32_t qv = e4m3_pack4(y[i][4 * gq] * inv, y[i][4 * gq + 1] * inv, y[i][4 * gq + 2] * inv,
+                                         y[i][4 * gq + 3] * inv);
+          const int cb = ycol + 8 * gq;
+          *(uint32_t*)(stg + rl * 128 + (((cb >> 4) ^ (rl & 7)) << 4) + (cb & 15)) = qv;
+        }
+        if (row < cur.r1) {
+          if (p.out) {
+            uint16_t* brow = p.out + (int64_t)row * p.I + cur.n_tile * 128 + ycol;
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq)
+              *(bf16x4*)(brow + 8 * gq) = bf16x4{(__bf16)y[i][4 * gq], (__bf16)y[i][4 * gq + 1],
+                                                 (__bf16)y[i][4 * gq + 2], (__bf16)y[i][4 * gq + 3]};
+          }
+          if (wn == 0 && fhalf == 0) p.outs[(int64_t)row * (p.I / 128) + cur.n_tile] = sc;
+        }
+      }
+      __syncthreads();
+      // 256 rows x 128 bytes: 8 lanes per row, 8 rows per wave instruction
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int rl = wave * 32 + rr * 8 + (lane >> 3);
+        const u32x4 v = *(const u32x4*)(stg + rl * 128 + (((lane & 7) ^ (rl & 7)) << 4));
+        const int row = cur.r0 + rl;
+        if (row < cur.r1) *(u32x4*)(p.outq + (int64_t)row * p.I + cur.n_tile * 128 + (lane & 7) * 16) = v;
+      }
+      __syncthreads();  // red and the staging slot are reused by the next tile
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    // ---- next tile ------------------------------------------------------------------------
+    lid = lid_next;
+    if (lid >= lid_end) break;
+    cur = nxt;
+    scur = snxt;
+    lid_next = lid + nx;
+    if (lid_next < lid_end) {
+      nxt = decode(lid_next);
+      snxt = make_src(nxt);
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) sa_c[i] = sa_n[i];
+    sb_c[0] = sb_n[0];
+    sb_c[1] = sb_n[1];
+  }
+  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));  // filler loads of the last steps land before exit
+}
+
 }  // namespace f8
 
 static inline int64_t f8_ws_bytes(int64_t M, int64_t E, int64_t BM) {
@@ -735,8 +1049,20 @@ static inline int64_t f8_ws_bytes(int64_t M, int64_t E, int64_t BM) {
 
 template <int EPI>
 static int launch_fp8(const f8::Args& a, const int32_t* gs, int64_t E, int64_t nn, void* ws, hipStream_t st) {
-  const bool v3ok = a.K <= 128 * f8::v3::MAX_KB && (int64_t)a.M * a.K < (int64_t(1) << 32) &&
-                    (int64_t)a.N * a.K < (int64_t(1) << 32);
+  const bool off32 = (int64_t)a.M * a.K < (int64_t(1) << 32) && (int64_t)a.N * a.K < (int64_t(1) << 32);
+  if (off32 && a.K >= 256) {
+    int* count = (int*)ws;
+    MTileF8* tiles = (MTileF8*)((char*)ws + 256);
+    hipLaunchKernelGGL(f8::build_tiles_f8_kernel, dim3(1), dim3(1024), 0, st, gs, (int)E, a.M, 256, count, tiles);
+    f8::Args b = a;
+    b.count = count;
+    b.tiles = tiles;
+    int64_t grid = round_up((ceil_div(a.M, 256) + E + 1) * nn, 8);
+    if (grid > 256) grid = 256;  // persistent: one workgroup per CU
+    hipLaunchKernelGGL((f8::gmm_fp8_v4_kernel<EPI>), dim3((unsigned)grid), dim3(512), 0, st, b);
+    return check_launch();
+  }
+  const bool v3ok = a.K <= 128 * f8::v3::MAX_KB && off32;
   if (v3ok) {
     int* count = (int*)ws;
     MTileF8* tiles = (MTileF8*)((char*)ws + 256);

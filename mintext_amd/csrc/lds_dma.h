@@ -15,6 +15,12 @@ __device__ __forceinline__ void gload_lds16(const void* gptr, uint32_t lds_base)
                : "memory", "m0");
 }
 
+// 4-byte direct global->LDS load: lane l writes LDS byte lds_base + 4*l.
+__device__ __forceinline__ void gload_lds4(const void* gptr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(gptr), "s"(lds_base)
+               : "memory", "m0");
+}
+
 // LDS byte address of a __shared__ array (for M0).
 template <typename T>
 __device__ __forceinline__ uint32_t lds_addr(T* p) {

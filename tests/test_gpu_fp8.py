@@ -52,8 +52,8 @@ def _groups(rng, M, E):
 
 
 @pytest.mark.parametrize("M,E,Kin,Kout", [(1024, 4, 512, 512), (700, 8, 256, 256), (2000, 16, 128, 768),
-                                           (1500, 6, 2048, 256), (600, 3, 3072, 512),
-                                           (400, 2, 3200, 256)])  # K > 3072: register-staged kernel
+                                           (1500, 6, 2048, 256), (600, 3, 3072, 512), (400, 2, 3200, 256),
+                                           (20000, 8, 512, 2048)])  # more tiles than workgroups
 def test_gmm_fp8(dev, M, E, Kin, Kout):
     from mintext_amd.kernels.fp8 import grouped_matmul_fp8, quantize_fp8_rows, quantize_fp8_weights
 
@@ -76,7 +76,8 @@ def test_gmm_fp8(dev, M, E, Kin, Kout):
     assert (out[tot:] == 0).all()
 
 
-@pytest.mark.parametrize("M,E,Kin,I", [(1024, 4, 256, 256), (900, 8, 512, 384), (2048, 8, 2048, 768)])
+@pytest.mark.parametrize("M,E,Kin,I", [(1024, 4, 256, 256), (900, 8, 512, 384), (2048, 8, 2048, 768),
+                                       (12000, 8, 1024, 768)])
 def test_gmm_fp8_swiglu_requant(dev, M, E, Kin, I):
     from mintext_amd.kernels.fp8 import grouped_matmul_fp8_swiglu, quantize_fp8_rows, quantize_fp8_weights
 
@@ -97,3 +98,28 @@ def test_gmm_fp8_swiglu_requant(dev, M, E, Kin, I):
     assert rel_err(deq[:tot], ref[:tot]) < 6e-2
     amax = np.abs(O.e4m3_decode(_u8(yq))[:tot].reshape(tot, I // 128, 128)).max(-1)
     assert ((amax == 448.0) | (ys.cpu().numpy()[:tot] == 1.0)).all()
+
+
+@pytest.mark.parametrize("Kin", [128, 512])
+def test_gmm_fp8_rows_past_group_sum(dev, Kin):
+    """Rows past sum(group_sizes) come out as zeros even when their inputs hold NaN codes."""
+    from mintext_amd.kernels.fp8 import (grouped_matmul_fp8, grouped_matmul_fp8_swiglu, quantize_fp8_rows,
+                                         quantize_fp8_weights)
+
+    M, E, N, I = 1000, 4, 512, 256
+    rng = np.random.default_rng(Kin)
+    gs = np.array([300, 0, 350, 250], np.int32)  # sum 900 < M
+    x = torch.randn(M, Kin, device=dev).bfloat16()
+    xq, xs = quantize_fp8_rows(x)
+    xq[900:] = 0x7F  # e4m3fn NaN
+    w = (torch.randn(E, Kin, N, device=dev) * 0.05).bfloat16()
+    wq, ws = quantize_fp8_weights(w)
+    out = grouped_matmul_fp8(xq, xs, wq, ws, _t(gs, dev))
+    assert (out[900:] == 0).all()
+    assert torch.isfinite(out.float()).all()
+    deq = O.gmm_fp8(_u8(xq)[:900], xs.cpu().numpy()[:900], _u8(wq), ws.cpu().numpy(), gs)
+    assert rel_err(out.float().cpu().numpy()[:900], deq) < 1e-2
+    w2 = (torch.randn(E, Kin, 2 * I, device=dev) * 0.05).bfloat16()
+    wq2, ws2 = quantize_fp8_weights(w2)
+    yq, ys, yb = grouped_matmul_fp8_swiglu(xq, xs, wq2, ws2, _t(gs, dev), return_bf16=True)
+    assert (yq[900:] == 0).all() and (yb[900:] == 0).all() and (ys[900:] == 1.0).all()
