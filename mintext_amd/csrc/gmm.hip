@@ -928,57 +928,69 @@ __global__ __launch_bounds__(WM* WN * 64, 2) void gmm_v3_kernel(Args p) {
   __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));  // no ring load may land after the workgroup ends
 
   // ---- epilogue: the MFMAs computed C^T blocks (operands swapped), so acc[i][j][4g+q] of lane
-  // l is C[row i*32 + l%32][col j*32 + 8g + 4(l/32) + q]: four consecutive columns per lane,
-  // written as one 8-byte store of packed bf16.
-  const int erow = wm * WTM + (lane & 31), ecol = wn * WTN + 4 * (lane >> 5);
+  // l is C[row i*32 + l%32][col j*32 + 8g + 4(l/32) + q]: four consecutive columns per lane.
+  // The tile is staged in the (now idle) ring as packed bf16 rows, 16-byte chunk c of row r at
+  // chunk c ^ (r & 15), and written back with 16 contiguous bytes per lane so that every row
+  // of the tile goes out as whole 128-byte lines.
+  constexpr int OCOLS = (EPI == EPI_SWIGLU) ? BN / 2 : BN;  // bf16 output columns of the tile
+  constexpr int OROW = OCOLS * 2;                           // staged row bytes
+  constexpr int OCH = OROW / 16;                            // 16-byte chunks per row
+  static_assert(BM * OROW <= NSTAGE * STAGE, "staging fits the ring");
   auto pack4 = [](float a, float b, float c, float d) -> bf16x4 {
     return bf16x4{(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
   };
-  if constexpr (MODE == TGMM) {
-    uint16_t* out = p.C + (int64_t)e * p.Kd * p.N;
+  auto stage8 = [&](int r, int col, bf16x4 v) {  // col: tile column, multiple of 4
+    const int c = col >> 3;
+    *(bf16x4*)(lds + r * OROW + ((c ^ (r & 15)) << 4) + (col & 7) * 2) = v;
+  };
+  __syncthreads();  // every wave is done with the ring
+  {
+    const int frow = lane & 31, h4 = 4 * (lane >> 5);
+    if constexpr (EPI == EPI_SWIGLU) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      uint16_t* orow = out + (int64_t)(row0 + erow + i * 32) * p.N + col0 + ecol;
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-          *(bf16x4*)(orow + j * 32 + 8 * g) =
-              pack4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
-    }
-  } else if (EPI == EPI_SWIGLU) {
-    const int ycol = n_tile * (BN / 2) + wn * (WTN / 2) + 4 * (lane >> 5);
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int row = r0 + erow + i * 32;
-      if (row < r1) {
-        uint16_t* orow = p.C + (int64_t)row * p.ldc + ycol;
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN / 2; ++j)
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const f32x16& gt = acc[i][j];
             const f32x16& up = acc[i][j + TN / 2];
-            *(bf16x4*)(orow + j * 32 + 8 * g) =
-                pack4(swiglu_fast(gt[4 * g], up[4 * g]), swiglu_fast(gt[4 * g + 1], up[4 * g + 1]),
-                      swiglu_fast(gt[4 * g + 2], up[4 * g + 2]), swiglu_fast(gt[4 * g + 3], up[4 * g + 3]));
+            stage8(wm * WTM + i * 32 + frow, wn * (WTN / 2) + j * 32 + 8 * g + h4,
+                   pack4(swiglu_fast(gt[4 * g], up[4 * g]), swiglu_fast(gt[4 * g + 1], up[4 * g + 1]),
+                         swiglu_fast(gt[4 * g + 2], up[4 * g + 2]), swiglu_fast(gt[4 * g + 3], up[4 * g + 3])));
           }
-      }
-    }
-  } else {
+    } else {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int row = r0 + erow + i * 32;
-      if (row < r1) {
-        uint16_t* orow = p.C + (int64_t)row * p.ldc + col0 + ecol;
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
           for (int g = 0; g < 4; ++g)
-            *(bf16x4*)(orow + j * 32 + 8 * g) =
-                pack4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
-      }
+            stage8(wm * WTM + i * 32 + frow, wn * WTN + j * 32 + 8 * g + h4,
+                   pack4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]));
     }
+  }
+  __syncthreads();
+  uint16_t* obase;
+  int64_t ld;
+  int rbase, rlimit;
+  if constexpr (MODE == TGMM) {
+    obase = p.C + (int64_t)e * p.Kd * p.N + col0;
+    ld = p.N;
+    rbase = row0;
+    rlimit = row0 + BM;
+  } else {
+    obase = p.C + ((EPI == EPI_SWIGLU) ? n_tile * (BN / 2) : col0);
+    ld = p.ldc;
+    rbase = r0;
+    rlimit = r1;
+  }
+  constexpr int RPI = 64 / OCH;  // rows per wave instruction
+  for (int rr = wave * RPI + lane / OCH; rr < BM; rr += NT / OCH) {
+    const int c = lane % OCH;
+    const u32x4 v = *(const u32x4*)(lds + rr * OROW + ((c ^ (rr & 15)) << 4));
+    const int row = rbase + rr;
+    if (row < rlimit) *(u32x4*)(obase + (int64_t)row * ld + c * 8) = v;
   }
 }
 
