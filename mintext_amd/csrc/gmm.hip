@@ -57,7 +57,8 @@ static inline GmmWs gmm_ws(void* ws, int64_t E) {
 // One workgroup of 1024 threads, E <= 1024.
 __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __restrict__ gs, int E, int M, int BM,
                                                            int* __restrict__ count, int* __restrict__ offsets,
-                                                           int* __restrict__ order, MTile* __restrict__ tiles) {
+                                                           int* __restrict__ order, MTile* __restrict__ tiles,
+                                                           int need_order) {
   __shared__ int wsum[16];
   __shared__ int s_gs[1024];
   __shared__ int s_total[2];
@@ -123,7 +124,7 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
     count[1] = s_total[1];  // tiles with an expert (the rest are zero tiles)
   }
   // expert order by descending group size (ties: lower id first), used by tgmm
-  if (e < E) {
+  if (need_order && e < E) {
     int rank = 0;
     for (int h = 0; h < E; ++h) {
       const int o = s_gs[h];
@@ -1001,9 +1002,10 @@ struct MfmaCfg {
   int BM, BN;
 };
 
-static int launch_build_tiles(const int32_t* gs, int64_t E, int64_t M, int BM, const GmmWs& w, hipStream_t st) {
+static int launch_build_tiles(const int32_t* gs, int64_t E, int64_t M, int BM, const GmmWs& w, hipStream_t st,
+                              bool need_order = false) {
   hipLaunchKernelGGL(build_tiles_kernel, dim3(1), dim3(1024), 0, st, gs, (int)E, (int)M, BM, w.count, w.offsets,
-                     w.order, w.tiles);
+                     w.order, w.tiles, need_order ? 1 : 0);
   return check_launch();
 }
 
@@ -1209,7 +1211,7 @@ extern "C" int mtx_tgmm(const void* x, const void* g, const int32_t* group_sizes
   if (!dw || !group_sizes || (M > 0 && (!x || !g))) return MTX_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
   GmmWs wsp = gmm_ws(workspace, E);
-  rc = launch_build_tiles(group_sizes, E, M, kMinBM, wsp, st);
+  rc = launch_build_tiles(group_sizes, E, M, kMinBM, wsp, st, true);
   if (rc) return rc;
   const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)g % 16 == 0);
   if (dtype == MTX_BF16 && aligned && K % 128 == 0 && N % 128 == 0 && M > 0) {

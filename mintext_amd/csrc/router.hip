@@ -1,8 +1,8 @@
 // Router top-k for the MoE layer on gfx950.
 //
-// One token is owned by a group of L = min(64, pow2ceil(E)) lanes of a wave; each lane
-// holds V = ceil(E/L) candidates (expert e = lane_in_group + L*v, so the logits row is
-// read coalesced).  Top-K is K rounds of a lane-group arg-max butterfly on
+// One token is owned by a group of L = clamp(max(pow2ceil(E)/8, K), 1, 64) lanes of a wave; each lane
+// holds V = ceil(E/L) <= 16 candidates (expert e = lane_in_group + L*v, so the logits row is
+// read in L-wide runs).  Top-K is K rounds of a lane-group arg-max butterfly on
 // (value, expert id) with ties going to the lower id, the order lax.top_k returns.
 //
 // Semantics (bzantium/mintext):
@@ -190,8 +190,13 @@ extern "C" int mtx_router_topk(const void* logits, int logits_dtype, int64_t T, 
   if (scoring == MTX_SCORING_SIGMOID_GROUP && (E % n_group != 0 || topk_group > n_group)) return MTX_ERR_ARG;
   if (T == 0) return MTX_OK;
   if (!logits || !topk_idx || !topk_w) return MTX_ERR_ARG;
-  int L = 1;
-  while (L < E && L < 64) L <<= 1;
+  // L lanes per token with up to 8 candidates each: few butterfly steps per round and several
+  // tokens per wave (E = 8: one lane per token; E = 128: 16 lanes; E >= 512: 64 lanes)
+  int P = 1;
+  while (P < E) P <<= 1;
+  int L = P / 8 < 1 ? 1 : P / 8;
+  while (L < K) L <<= 1;  // lane li < K of a token holds the round-li winner (K <= 64)
+  if (L > 64) L = 64;
   const int V = (int)ceil_div(E, L);
   const int tpb = 4 * (64 / L);
   const int grid = (int)ceil_div(T, tpb);

@@ -49,7 +49,8 @@ def test_sigmoid_group_router_fixtures(dev, key):
 
 @pytest.mark.parametrize("T,E,k,dt", [(16384, 128, 8, torch.bfloat16), (8192, 8, 2, torch.bfloat16),
                                       (4096, 256, 8, torch.float32), (1000, 64, 6, torch.float32),
-                                      (777, 5, 3, torch.float32)])
+                                      (777, 5, 3, torch.float32), (300, 1024, 8, torch.float32),
+                                      (100, 3, 1, torch.float32), (64, 40, 40, torch.float32)])
 def test_softmax_router_large(dev, T, E, k, dt):
     from mintext_amd.kernels import route_topk
 
