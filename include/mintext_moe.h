@@ -85,6 +85,8 @@ int mtx_router_topk(const void* logits, int logits_dtype, int64_t T, int64_t E, 
  * group_sizes [E], and optionally inverse [N*K] (inverse[sort_indices[j]] = j; may be NULL).
  * tokens / sorted_tokens may both be NULL to compute only the permutation.
  * token_scales [N,D/128] f32 (may be NULL) are gathered alongside into sorted_scales.
+ * Rows are moved in token order (each token row read once, written to its K positions);
+ * with inverse == NULL the inverse permutation is kept in the workspace.
  * Expert ids outside [0,E) are sorted after every valid id and not counted.          */
 int64_t mtx_route_workspace_size(int64_t N, int64_t K, int64_t E);
 int mtx_route(const void* tokens, int dtype, const int32_t* topk_idx,

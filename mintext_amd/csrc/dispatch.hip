@@ -15,6 +15,7 @@
 //   4. gather_rows   : one wave per output row, 16-byte vector copies.
 // unroute (moe_dispatch.py:84-111) inverts the permutation (scatter of j to perm[j]) and
 // combines out[n] = sum_k w[n,k] * Y[inv[n*K+k]] in f32 with k ascending, one wave per token.
+#include <type_traits>
 #include "common.h"
 
 namespace mtx {
@@ -226,6 +227,51 @@ __global__ __launch_bounds__(256) void gather_chunks_kernel(
   }
 }
 
+// Dispatch in token order (moe_dispatch.py:67,76 without the materialised repeat): token row n
+// is read once and written to its K sorted positions, out[inv[n*K+k]] = src[n].  Items are
+// 16-byte chunks (n, c) of the data rows (cpr chunks per row) followed by those of the optional
+// scale rows (spr chunks per row), so both matrices move in one launch.  Each thread loads UNR
+// items before storing any of them (UNR loads and UNR*K stores in flight per lane).
+template <int UNR>
+__global__ __launch_bounds__(256) void dispatch_rows_kernel(
+    const u32x4* __restrict__ src, int64_t N, int64_t cpr, int cpr_shift, const u32x4* __restrict__ ssrc,
+    int64_t spr, const int32_t* __restrict__ inv, int K, u32x4* __restrict__ out, u32x4* __restrict__ sout) {
+  const int64_t nd = N * cpr;
+  const int64_t total = nd + N * spr;
+  const int64_t M = N * (int64_t)K;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t base = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; base < total; base += stride * UNR) {
+    u32x4 v[UNR];
+    int64_t n[UNR], c[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int64_t it = base + u * stride;
+      n[u] = -1;
+      if (it < nd) {
+        n[u] = cpr_shift >= 0 ? (it >> cpr_shift) : it / cpr;
+        c[u] = it - n[u] * cpr;
+        v[u] = src[it];
+      } else if (it < total) {
+        const int64_t i2 = it - nd;
+        n[u] = i2 / spr;
+        c[u] = i2 - n[u] * spr;
+        v[u] = ssrc[i2];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      if (n[u] < 0) continue;
+      const bool data = (base + u * stride) < nd;
+      for (int k = 0; k < K; ++k) {
+        const int64_t j = inv[n[u] * K + k];
+        if (j < 0 || j >= M) continue;
+        if (data) out[j * cpr + c[u]] = v[u];
+        else sout[j * spr + c[u]] = v[u];
+      }
+    }
+  }
+}
+
 // out[index[j]] = src[j]
 template <typename VT>
 __global__ __launch_bounds__(256) void scatter_rows_kernel(
@@ -340,21 +386,30 @@ __global__ __launch_bounds__(256) void unroute_kernel(
         ww[k] = w ? ldf<WT>(w, n * K + k) : 1.0f;
       }
     }
-    for (int64_t d = (int64_t)lane * 8; d < D; d += 512) {
-      float y[KMAX][8];
+    // S slices of 512 elements per step, so that S*K 16-byte loads are in flight per lane
+    constexpr int S = KMAX >= 8 ? 1 : 8 / KMAX;
+    for (int64_t d0 = (int64_t)lane * 8; d0 < D; d0 += 512 * S) {
+      float y[S][KMAX][8];
 #pragma unroll
-      for (int k = 0; k < KMAX; ++k)
-        if (k < K) load8(Y + jj[k] * D + d, y[k]);
-      float acc[8];
+      for (int s = 0; s < S; ++s)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+        for (int k = 0; k < KMAX; ++k)
+          if (k < K && d0 + 512 * s < D) load8(Y + jj[k] * D + d0 + 512 * s, y[s][k]);
 #pragma unroll
-      for (int k = 0; k < KMAX; ++k)
-        if (k < K && ok[k]) {
+      for (int s = 0; s < S; ++s) {
+        const int64_t d = d0 + 512 * s;
+        if (d >= D) break;
+        float acc[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[i] = fmaf(ww[k], y[k][i], acc[i]);
-        }
-      store8(out + n * D + d, acc);
+        for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k)
+          if (k < K && ok[k]) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = fmaf(ww[k], y[s][k][i], acc[i]);
+          }
+        store8(out + n * D + d, acc);
+      }
     }
   } else if constexpr (VEC8) {
     for (int64_t d = (int64_t)lane * 8; d < D; d += 512) {
@@ -386,6 +441,142 @@ __global__ __launch_bounds__(256) void unroute_kernel(
   }
 }
 
+// Flat combine: one thread per (token n, 8-element chunk c) item, UNR items per thread with all
+// of their K row loads issued before any sum, so that every lane keeps UNR*K 16-byte loads in
+// flight and no wave waits on a chain of dependent phases.  Same fmaf chain in k order as
+// unroute_kernel (K <= KMAX, D % 8 == 0, 16-byte aligned rows).
+template <typename YT, typename WT, typename OT, int KMAX, int UNR>
+__global__ __launch_bounds__(256) void unroute_flat_kernel(
+    const YT* __restrict__ Y, const int32_t* __restrict__ inv, const WT* __restrict__ w,
+    int64_t N, int K, int64_t D, int cpr_shift, OT* __restrict__ out) {
+  const int64_t cpr = D >> 3;
+  const int64_t total = N * cpr;
+  const int64_t M = N * (int64_t)K;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t base = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; base < total; base += stride * UNR) {
+    int64_t jj[UNR][KMAX];
+    float ww[UNR][KMAX];
+    int64_t n[UNR], c[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int64_t it = base + u * stride;
+      n[u] = -1;
+      c[u] = 0;
+      if (it < total) {
+        n[u] = cpr_shift >= 0 ? (it >> cpr_shift) : it / cpr;
+        c[u] = it - n[u] * cpr;
+      }
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k) {
+        jj[u][k] = -1;
+        ww[u][k] = 0.0f;
+        if (n[u] >= 0 && k < K) {
+          const int64_t j = inv[n[u] * K + k];
+          jj[u][k] = (j >= 0 && j < M) ? j : -1;
+          ww[u][k] = w ? ldf<WT>(w, n[u] * K + k) : 1.0f;
+        }
+      }
+    }
+    float y[UNR][KMAX][8];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k)
+        if (jj[u][k] >= 0) load8(Y + jj[u][k] * D + c[u] * 8, y[u][k]);
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      if (n[u] < 0) continue;
+      float acc[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k)
+        if (jj[u][k] >= 0) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] = fmaf(ww[u][k], y[u][k][i], acc[i]);
+        }
+      store8(out + n[u] * D + c[u] * 8, acc);
+    }
+  }
+}
+
+// Row-wise combine for bf16 expert outputs: one wave per token; the K rows of the token are
+// requested whole (S consecutive 1 KB slices of a row back to back, kept packed in registers),
+// so each gathered row reaches HBM as one contiguous burst rather than as slices a latency
+// apart.  Then the slices are summed in k order with the same fmaf chain as unroute_kernel.
+template <typename WT, typename OT, int KMAX, int S>
+__global__ __launch_bounds__(256) void unroute_rows_kernel(
+    const uint16_t* __restrict__ Y, const int32_t* __restrict__ inv, const WT* __restrict__ w,
+    int64_t N, int K, int64_t D, OT* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  if (n >= N) return;
+  const int64_t M = N * (int64_t)K;
+  int64_t jj[KMAX];
+  float ww[KMAX];
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    jj[k] = -1;
+    ww[k] = 0.0f;
+    if (k < K) {
+      const int64_t j = inv[n * K + k];
+      jj[k] = (j >= 0 && j < M) ? j : -1;
+      ww[k] = w ? ldf<WT>(w, n * K + k) : 1.0f;
+    }
+  }
+  for (int64_t d0 = (int64_t)lane * 8; d0 < D; d0 += 512 * S) {
+    u32x4 q[KMAX][S];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k)
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+        if (jj[k] >= 0 && d0 + 512 * s < D) q[k][s] = *(const u32x4*)(Y + jj[k] * D + d0 + 512 * s);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int64_t d = d0 + 512 * s;
+      if (d >= D) break;
+      float acc[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k)
+        if (jj[k] >= 0) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            acc[2 * i] = fmaf(ww[k], __uint_as_float(q[k][s][i] << 16), acc[2 * i]);
+            acc[2 * i + 1] = fmaf(ww[k], __uint_as_float(q[k][s][i] & 0xffff0000u), acc[2 * i + 1]);
+          }
+        }
+      store8(out + n * D + d, acc);
+    }
+  }
+}
+
+#ifndef MTX_UNROUTE_FLAT
+#define MTX_UNROUTE_FLAT 0
+#endif
+#ifndef MTX_UNROUTE_ROWS
+#define MTX_UNROUTE_ROWS 1
+#endif
+#ifndef MTX_UNROUTE_UNR
+#define MTX_UNROUTE_UNR 2
+#endif
+template <typename YT, typename WT, typename OT, int KMAX>
+static void launch_unroute_flat(const void* Y, const int32_t* inv, const void* w, int64_t N, int K, int64_t D,
+                                void* out, hipStream_t st) {
+  constexpr int UNR = KMAX >= 8 ? 1 : MTX_UNROUTE_UNR;
+  const int64_t cpr = D / 8;
+  int shift = -1;
+  if ((cpr & (cpr - 1)) == 0) {
+    shift = 0;
+    while ((int64_t(1) << shift) < cpr) ++shift;
+  }
+  int64_t gb = ceil_div(N * cpr, 256 * UNR);
+  if (gb > 65536) gb = 65536;
+  hipLaunchKernelGGL((unroute_flat_kernel<YT, WT, OT, KMAX, UNR>), dim3(gb), dim3(256), 0, st, (const YT*)Y, inv,
+                     (const WT*)w, N, K, D, shift, (OT*)out);
+}
+
 template <typename YT, typename WT, typename OT>
 static void launch_unroute_t(const void* Y, const int32_t* inv, const void* w, int64_t N, int K,
                              int64_t D, void* out, hipStream_t st) {
@@ -394,7 +585,20 @@ static void launch_unroute_t(const void* Y, const int32_t* inv, const void* w, i
 #define MTX_UNROUTE(V, KM)                                                                                  \
   hipLaunchKernelGGL((unroute_kernel<YT, WT, OT, V, KM>), dim3(blocks), dim3(256), 0, st, (const YT*)Y, inv, \
                      (const WT*)w, N, K, D, (OT*)out)
-  if (v8 && K <= 2) MTX_UNROUTE(true, 2);
+  if (MTX_UNROUTE_ROWS && std::is_same<YT, uint16_t>::value && v8 && K <= 8) {
+    const int64_t blocks_ = ceil_div(N, 4);
+#define MTX_UNROUTE_ROWS_L(KM, SS)                                                                           \
+  hipLaunchKernelGGL((unroute_rows_kernel<WT, OT, KM, SS>), dim3(blocks_), dim3(256), 0, st, (const uint16_t*)Y, \
+                     inv, (const WT*)w, N, K, D, (OT*)out)
+    if (K <= 2) MTX_UNROUTE_ROWS_L(2, 8);
+    else if (K <= 4) MTX_UNROUTE_ROWS_L(4, 8);
+    else MTX_UNROUTE_ROWS_L(8, 4);
+#undef MTX_UNROUTE_ROWS_L
+  } else if (MTX_UNROUTE_FLAT && v8 && K <= 8) {
+    if (K <= 2) launch_unroute_flat<YT, WT, OT, 2>(Y, inv, w, N, K, D, out, st);
+    else if (K <= 4) launch_unroute_flat<YT, WT, OT, 4>(Y, inv, w, N, K, D, out, st);
+    else launch_unroute_flat<YT, WT, OT, 8>(Y, inv, w, N, K, D, out, st);
+  } else if (v8 && K <= 2) MTX_UNROUTE(true, 2);
   else if (v8 && K <= 4) MTX_UNROUTE(true, 4);
   else if (v8 && K <= 8) MTX_UNROUTE(true, 8);
   else if (v8) MTX_UNROUTE(true, 0);
@@ -447,9 +651,11 @@ extern "C" const char* mtx_status_string(int s) {
 extern "C" int mtx_last_hip_error(void) { return g_last_hip_error; }
 extern "C" int mtx_version(void) { return 1; }
 
+// Workspace: per-chunk bucket counts, then room for the inverse permutation (used when the
+// caller passes inverse == NULL, since the row dispatch runs in token order).
 extern "C" int64_t mtx_route_workspace_size(int64_t N, int64_t K, int64_t E) {
   if (N < 0 || K < 1 || E < 1) return -1;
-  return route_plan(N, K, E).ws_counts;
+  return route_plan(N, K, E).ws_counts + round_up(N * K * 4, 256);
 }
 
 extern "C" int mtx_route(const void* tokens, int dtype, const int32_t* topk_idx,
@@ -465,9 +671,10 @@ extern "C" int mtx_route(const void* tokens, int dtype, const int32_t* topk_idx,
   if (N * K > INT32_MAX) return MTX_ERR_ARG;
   if (!sort_indices || !group_sizes) return MTX_ERR_ARG;
   const RoutePlan p = route_plan(N, K, E);
-  if (!workspace || workspace_bytes < p.ws_counts) return MTX_ERR_WORKSPACE;
+  if (!workspace || workspace_bytes < mtx_route_workspace_size(N, K, E)) return MTX_ERR_WORKSPACE;
   hipStream_t st = (hipStream_t)stream;
   int32_t* counts = (int32_t*)workspace;
+  if (!inverse && (tokens || token_scales)) inverse = (int32_t*)((char*)workspace + p.ws_counts);
   const size_t hist_shm = (size_t)p.nb * sizeof(int);
   hipLaunchKernelGGL(route_count_kernel, dim3(p.nchunks), dim3(kRouteThreads), hist_shm, st,
                      topk_idx, p.M, (int)E, p.nb, p.chunk, counts);
@@ -481,15 +688,38 @@ extern "C" int mtx_route(const void* tokens, int dtype, const int32_t* topk_idx,
                        p.M, (int)E, p.nb, nbits, p.chunk, counts, sort_indices, inverse);
   int rc = check_launch();
   if (rc != MTX_OK) return rc;
-  if (tokens) {
-    rc = launch_gather(tokens, N, D * dtype_size(dtype), sort_indices, p.M, K, sorted_tokens, st);
-    if (rc != MTX_OK) return rc;
+  if (p.M == 0 || (!tokens && !token_scales)) return MTX_OK;
+  const int64_t row_bytes = D * dtype_size(dtype);
+  const bool a16 = (!tokens || ((row_bytes % 16 == 0) && (uintptr_t)tokens % 16 == 0 &&
+                                (uintptr_t)sorted_tokens % 16 == 0)) &&
+                   (!token_scales || ((D / 128) % 4 == 0 && (uintptr_t)token_scales % 16 == 0 &&
+                                      (uintptr_t)sorted_scales % 16 == 0));
+  if (!a16) {  // unaligned rows: destination-order gathers
+    if (tokens) {
+      rc = launch_gather(tokens, N, row_bytes, sort_indices, p.M, K, sorted_tokens, st);
+      if (rc != MTX_OK) return rc;
+    }
+    if (token_scales) {
+      rc = launch_gather(token_scales, N, (D / 128) * 4, sort_indices, p.M, K, sorted_scales, st);
+      if (rc != MTX_OK) return rc;
+    }
+    return MTX_OK;
   }
-  if (token_scales) {
-    rc = launch_gather(token_scales, N, (D / 128) * 4, sort_indices, p.M, K, sorted_scales, st);
-    if (rc != MTX_OK) return rc;
+  const int64_t cpr = tokens ? row_bytes / 16 : 0;
+  const int64_t spr = token_scales ? (D / 128) * 4 / 16 : 0;
+  int shift = -1;
+  if (cpr > 0 && (cpr & (cpr - 1)) == 0) {
+    shift = 0;
+    while ((int64_t(1) << shift) < cpr) ++shift;
   }
-  return MTX_OK;
+  constexpr int UNR = 4;
+  int64_t gb = ceil_div(N * (cpr + spr), 256 * UNR);
+  if (gb > 16384) gb = 16384;
+  if (gb < 1) gb = 1;
+  hipLaunchKernelGGL(dispatch_rows_kernel<UNR>, dim3(gb), dim3(256), 0, st, (const u32x4*)tokens, N, cpr, shift,
+                     (const u32x4*)token_scales, spr, inverse, (int)K, (u32x4*)sorted_tokens,
+                     (u32x4*)sorted_scales);
+  return check_launch();
 }
 
 extern "C" int mtx_gather_rows(const void* src, int dtype, int64_t src_rows, int64_t D,

@@ -658,8 +658,14 @@ typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
 #define MTX_V3_SCHED_BARRIER() ((void)0)
 #endif
 
+#ifndef MTX_V3_WPE
+#define MTX_V3_WPE 2
+#endif
+#ifndef MTX_V3_SGB
+#define MTX_V3_SGB 1
+#endif
 template <int MODE, int EPI, int WM, int WN, int BM_, int NST_>
-__global__ __launch_bounds__(WM* WN * 64, 2) void gmm_v3_kernel(Args p) {
+__global__ __launch_bounds__(WM* WN * 64, MTX_V3_WPE) void gmm_v3_kernel(Args p) {
   using v3::BKS;
   using v3::a_off;
   using v3::bn_off;
@@ -895,6 +901,37 @@ __global__ __launch_bounds__(WM* WN * 64, 2) void gmm_v3_kernel(Args p) {
     const int nb = FULL ? TM : nbi;
     for (int kt = 0; kt < nk; ++kt) {
       issue_stage(kt + PD);
+#if MTX_V3_SGB
+      if constexpr (FULL && MODE != TGMM) {
+        // explicit interleave: one fragment read of the next substep after each MFMA
+        __builtin_amdgcn_sched_barrier(0);
+        read_frags(kt, 1, 1, nb);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[0][j], fa[0][i], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < TM * TN; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        read_frags(kt + 1, 0, 0, nb);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < TM * TN; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
+        __syncthreads();
+        continue;
+      }
+#endif
       // substep 0: prefetch substep 1 of this stage
       read_frags(kt, 1, 1, nb);
       if (MODE == TGMM && tail < BKS && kt == nk - 1) mask_frags(0, 0, tail);
