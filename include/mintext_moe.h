@@ -142,6 +142,20 @@ int mtx_gmm_dlhs(const void* g, const void* w, const int32_t* group_sizes, int d
 int mtx_tgmm(const void* x, const void* g, const int32_t* group_sizes, int dtype,
              int64_t M, int64_t K, int64_t N, int64_t E, void* dw,
              void* workspace, int64_t workspace_bytes, void* stream);
+/* The three GEMMs above with an explicit tile configuration (the `tiling` argument of the
+ * Python API and the autotuner's search space; no counterpart in the C form of the reference,
+ * which passes TPU tilings to XLA, grouped_matmul.py:58-76 / kernels/autotuner.py:177-310).
+ * op: MTX_GMM_OP_FWD (out [M,Kout]), MTX_GMM_OP_SWIGLU (Kout = I, w [E,Kin,2I], out [M,I]),
+ * MTX_GMM_OP_DLHS (x = g [M,Kout], out = dx [M,Kin]).  tile_m: 0 (shape heuristic), 128 or 256
+ * rows per m-tile of the bf16 MFMA path; tile_group: 0 (heuristic) or 1..64 m-tiles per
+ * scheduling group.  The f32 path and shapes outside the MFMA tiling ignore both.  Every
+ * configuration gives the same output bits.                                             */
+#define MTX_GMM_OP_FWD    0
+#define MTX_GMM_OP_SWIGLU 1
+#define MTX_GMM_OP_DLHS   2
+int mtx_gmm_tiled(int op, const void* x, const void* w, const int32_t* group_sizes, int dtype,
+                  int64_t M, int64_t Kin, int64_t Kout, int64_t E, int64_t tile_m, int64_t tile_group,
+                  void* out, void* workspace, int64_t workspace_bytes, void* stream);
 /* out[r,j] = silu(h[r,j]) * h[r,I+j]   h [M,2I] -> out [M,I] (F32/BF16)                */
 int mtx_swiglu(const void* h, int dtype, int64_t M, int64_t I, void* out, void* stream);
 /* VJP of mtx_swiglu: dh [M,2I] from h [M,2I] and dy [M,I]                              */

@@ -26,6 +26,7 @@ MTX_ERR_UNSUPPORTED = -3
 MTX_ERR_HIP = -4
 MTX_F32, MTX_BF16, MTX_FP8E4M3 = 0, 1, 2
 MTX_SCORING_SOFTMAX, MTX_SCORING_SIGMOID_GROUP = 0, 1
+MTX_GMM_OP_FWD, MTX_GMM_OP_SWIGLU, MTX_GMM_OP_DLHS = 0, 1, 2
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -50,6 +51,7 @@ SIGNATURES = {
     "mtx_gmm_swiglu": (_I, [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "mtx_gmm_dlhs": (_I, [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "mtx_tgmm": (_I, [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
+    "mtx_gmm_tiled": (_I, [_I, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "mtx_swiglu": (_I, [_P, _I, _I64, _I64, _P, _P]),
     "mtx_swiglu_bwd": (_I, [_P, _P, _I, _I64, _I64, _P, _P]),
     "mtx_quant_fp8_rows": (_I, [_P, _I, _I64, _I64, _P, _P, _P]),

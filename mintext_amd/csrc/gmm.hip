@@ -1100,9 +1100,12 @@ static int common_checks(int64_t M, int64_t E, void* ws, int64_t ws_bytes, int64
 static constexpr int kMinBM = 64;
 
 
-// FWD / DLHS / SWIGLU driver. mode: 0 fwd, 1 dlhs, 2 swiglu
+// FWD / DLHS / SWIGLU driver. mode: 0 fwd, 1 dlhs, 2 swiglu.  tile_m (0, 128 or 256 rows per
+// m-tile) and tile_group (0 or m-tiles per scheduling group) override the shape heuristics on the
+// bf16 MFMA path; every configuration computes each output element with the same MFMA sequence.
 static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs, int dtype, int64_t M, int64_t Kred,
-                      int64_t Nout, int64_t I, int64_t E, void* out, void* ws, int64_t ws_bytes, hipStream_t st) {
+                      int64_t Nout, int64_t I, int64_t E, void* out, void* ws, int64_t ws_bytes, hipStream_t st,
+                      int tile_m = 0, int tile_group = 0) {
   if (dtype != MTX_F32 && dtype != MTX_BF16) return MTX_ERR_ARG;
   int rc = common_checks(M, E, ws, ws_bytes, kMinBM);
   if (rc != MTX_OK) return rc;
@@ -1134,11 +1137,11 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
     // m-tiles per expert, 8 balances the re-reads of x and W through L2; with about one m-tile
     // per expert (W is read once whatever the order) 1 keeps each x tile in L2 while all its
     // n-tiles run (C3 shapes: 6-7 % less time than 8).
-    a.gm = (M / E) <= 256 ? MTX_GM_SMALL : 8;
+    a.gm = tile_group > 0 ? tile_group : ((M / E) <= 256 ? MTX_GM_SMALL : 8);
     // tile shape: 256-row tiles when groups are large on average, else 128
     const bool v3ok = Kred % mf::v3::BKS == 0 && M * Kred * 2 < (int64_t(1) << 32) &&
                       Kred * Nout * 2 < (int64_t(1) << 32);
-    const bool big_m = v3ok && (M / E) >= MTX_V3_SMALL_MEAN;
+    const bool big_m = v3ok && (tile_m == 256 || (tile_m == 0 && (M / E) >= MTX_V3_SMALL_MEAN));
     if (mode == 2 && I % 128 == 0) {
       if (big_m) {
         rc = launch_build_tiles(gs, E, M, 256, wsp, st);
@@ -1238,6 +1241,27 @@ extern "C" int mtx_gmm_swiglu(const void* x, const void* w, const int32_t* group
   const int rc = gmm_driver(2, x, w, group_sizes, dtype, M, Kin, 2 * I, I, E, out, workspace, workspace_bytes,
                             (hipStream_t)stream);
   return rc;
+}
+
+extern "C" int mtx_gmm_tiled(int op, const void* x, const void* w, const int32_t* group_sizes, int dtype, int64_t M,
+                             int64_t Kin, int64_t Kout, int64_t E, int64_t tile_m, int64_t tile_group, void* out,
+                             void* workspace, int64_t workspace_bytes, void* stream) {
+  if (tile_m != 0 && tile_m != 128 && tile_m != 256) return MTX_ERR_ARG;
+  if (tile_group < 0 || tile_group > 64) return MTX_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  const int tm = (int)tile_m, tg = (int)tile_group;
+  switch (op) {
+    case MTX_GMM_OP_FWD:
+      return gmm_driver(0, x, w, group_sizes, dtype, M, Kin, Kout, 0, E, out, workspace, workspace_bytes, st, tm, tg);
+    case MTX_GMM_OP_DLHS:
+      return gmm_driver(1, x, w, group_sizes, dtype, M, Kout, Kin, 0, E, out, workspace, workspace_bytes, st, tm, tg);
+    case MTX_GMM_OP_SWIGLU:
+      if (Kout < 0) return MTX_ERR_ARG;
+      return gmm_driver(2, x, w, group_sizes, dtype, M, Kin, 2 * Kout, Kout, E, out, workspace, workspace_bytes, st,
+                        tm, tg);
+    default:
+      return MTX_ERR_ARG;
+  }
 }
 
 extern "C" int mtx_swiglu(const void* h, int dtype, int64_t M, int64_t I, void* out, void* stream) {

@@ -8,9 +8,13 @@ output dtypes and differentiability):
   (:83-114) -- forward gmm, backward dlhs = g @ W^T and drhs = tgmm(x, g) (:151-187)
 * ``tgmm(lhs, rhs, group_sizes)`` (:197-235) -- per-group x^T @ g, zeros for empty groups
 
-``tiling`` / ``mosaic_fusion`` are TPU XLA hints in the reference; they are accepted (and
-padded to 9 entries like the reference) and do not change results.  ``group_sizes`` never
-leaves the device.  Extra entry points beyond the reference: ``grouped_matmul_swiglu``
+``tiling`` selects the HIP tile configuration (the reference passes TPU ``ragged_dot`` tilings
+to XLA): a 3-tuple ``(tm, tg, tn)`` per GEMM -- ``tm`` rows per m-tile (128 or 256; other values
+round to the nearer), ``tg`` m-tiles per XCD scheduling group (1..64), ``tn`` columns per n-tile
+(256 is the only width; accepted and ignored).  ``None`` keeps the shape heuristics.  The
+9-tuple of ``grouped_matmul_vjp`` is padded from 3 like the reference (fwd, dlhs, tgmm; the
+tgmm entry is not used).  Tile configurations never change the output bits.  ``mosaic_fusion``
+is accepted and ignored.  ``group_sizes`` never leaves the device.  Extra entry points beyond the reference: ``grouped_matmul_swiglu``
 (gate_up GEMM with the SwiGLU of moe.py:195-196 fused into the epilogue) and ``swiglu``.
 """
 from __future__ import annotations
@@ -33,7 +37,19 @@ def _check_float(*ts):
         raise TypeError("grouped GEMM operands must share one dtype")
 
 
-def _gmm_fwd(x: torch.Tensor, w: torch.Tensor, gs: torch.Tensor) -> torch.Tensor:
+def _tile_args(tiling) -> tuple[int, int]:
+    """(tile_m, tile_group) for the C-ABI from a (tm, tg, tn) tiling; (0, 0) = heuristics."""
+    if tiling is None:
+        return 0, 0
+    t = tuple(int(v) for v in tiling)
+    if len(t) < 2 or any(v <= 0 for v in t):
+        raise ValueError(f"tiling must hold positive ints (tm, tg, tn), got {tiling!r}")
+    tm = 128 if t[0] <= 128 else 256
+    tg = min(max(t[1], 1), 64)
+    return tm, tg
+
+
+def _gmm_fwd(x: torch.Tensor, w: torch.Tensor, gs: torch.Tensor, tiling=None) -> torch.Tensor:
     dev = L.require_device(x, w, gs)
     _check_float(x, w)
     x = x.contiguous()
@@ -44,12 +60,13 @@ def _gmm_fwd(x: torch.Tensor, w: torch.Tensor, gs: torch.Tensor) -> torch.Tensor
         raise ValueError(f"shape mismatch: x {tuple(x.shape)}, weights {tuple(w.shape)}, group_sizes {gs.numel()}")
     out = torch.empty((M, Kout), dtype=x.dtype, device=dev)
     ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
-    L.call("mtx_gmm", L.ptr(x), L.ptr(w), L.ptr(gs), L.dtype_code(x.dtype), M, Kin, Kout, E, L.ptr(out),
-           L.ptr(ws), ws.numel(), L.stream(dev))
+    tm, tg = _tile_args(tiling)
+    L.call("mtx_gmm_tiled", L.MTX_GMM_OP_FWD, L.ptr(x), L.ptr(w), L.ptr(gs), L.dtype_code(x.dtype), M, Kin, Kout,
+           E, tm, tg, L.ptr(out), L.ptr(ws), ws.numel(), L.stream(dev))
     return out
 
 
-def _gmm_dlhs(g: torch.Tensor, w: torch.Tensor, gs: torch.Tensor) -> torch.Tensor:
+def _gmm_dlhs(g: torch.Tensor, w: torch.Tensor, gs: torch.Tensor, tiling=None) -> torch.Tensor:
     dev = L.require_device(g, w, gs)
     g = g.contiguous()
     w = w.contiguous()
@@ -61,8 +78,9 @@ def _gmm_dlhs(g: torch.Tensor, w: torch.Tensor, gs: torch.Tensor) -> torch.Tenso
         raise ValueError("dlhs shape mismatch")
     dx = torch.empty((M, Kin), dtype=w.dtype, device=dev)
     ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
-    L.call("mtx_gmm_dlhs", L.ptr(g), L.ptr(w), L.ptr(gs), L.dtype_code(w.dtype), M, Kin, Kout, E, L.ptr(dx),
-           L.ptr(ws), ws.numel(), L.stream(dev))
+    tm, tg = _tile_args(tiling)
+    L.call("mtx_gmm_tiled", L.MTX_GMM_OP_DLHS, L.ptr(g), L.ptr(w), L.ptr(gs), L.dtype_code(w.dtype), M, Kin, Kout,
+           E, tm, tg, L.ptr(dx), L.ptr(ws), ws.numel(), L.stream(dev))
     return dx
 
 
@@ -96,19 +114,21 @@ def tgmm(lhs: torch.Tensor, rhs: torch.Tensor, group_sizes: torch.Tensor) -> tor
 
 class _GMM(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, weights, group_sizes):
+    def forward(ctx, x, weights, group_sizes, tiling9):
         gs = _gs(group_sizes)
-        out = _gmm_fwd(x, weights, gs)
+        out = _gmm_fwd(x, weights, gs, None if tiling9 is None else tiling9[0:3])
         ctx.save_for_backward(x, weights, gs)
+        ctx.tiling9 = tiling9
         return out
 
     @staticmethod
     def backward(ctx, grad):
         x, w, gs = ctx.saved_tensors
         grad = grad.contiguous().to(w.dtype)
-        dx = _gmm_dlhs(grad, w, gs) if ctx.needs_input_grad[0] else None
+        t9 = ctx.tiling9
+        dx = _gmm_dlhs(grad, w, gs, None if t9 is None else t9[3:6]) if ctx.needs_input_grad[0] else None
         dw = tgmm(x, grad, gs) if ctx.needs_input_grad[1] else None
-        return dx, dw, None
+        return dx, dw, None, None
 
 
 def _pad_tiling(tiling) -> tuple:
@@ -127,13 +147,13 @@ def grouped_matmul(x: torch.Tensor, weights: torch.Tensor, group_sizes: torch.Te
         x: [M, K_in] sorted tokens (contiguous per expert).
         weights: [E, K_in, K_out].
         group_sizes: [E] int32, tokens per expert (rows past the sum are zero in the output).
-        tiling: accepted for signature compatibility; does not change results.
+        tiling: (tm, tg, tn) HIP tile configuration or None (shape heuristics); does not
+            change results.
 
     Returns:
         [M, K_out] in x's dtype.
     """
-    del tiling
-    return _GMM.apply(x, weights, group_sizes)
+    return _GMM.apply(x, weights, group_sizes, None if tiling is None else _pad_tiling(tiling))
 
 
 def grouped_matmul_vjp(x: torch.Tensor, weights: torch.Tensor, group_sizes: torch.Tensor, *,
@@ -142,18 +162,21 @@ def grouped_matmul_vjp(x: torch.Tensor, weights: torch.Tensor, group_sizes: torc
     """Grouped matmul with the custom backward (grouped_matmul.py:83-114, 151-187).
 
     Forward: gmm.  Backward: dlhs = grad @ W^T per group, drhs = tgmm(x, grad).
-    ``tiling`` (3 or 9 ints) and ``mosaic_fusion`` are accepted and ignored.
+    ``tiling`` (3 or 9 ints, padded like grouped_matmul.py:108-112): entries 0-2 configure the
+    forward GEMM and 3-5 the dlhs GEMM as ``(tm, tg, tn)``; ``None`` keeps the heuristics.
+    ``mosaic_fusion`` is accepted and ignored.
     """
-    _pad_tiling(tiling)
     del mosaic_fusion
-    return _GMM.apply(x, weights, group_sizes)
+    return _GMM.apply(x, weights, group_sizes, None if tiling is None else _pad_tiling(tiling))
 
 
-def grouped_matmul_swiglu(x: torch.Tensor, weights: torch.Tensor, group_sizes: torch.Tensor) -> torch.Tensor:
+def grouped_matmul_swiglu(x: torch.Tensor, weights: torch.Tensor, group_sizes: torch.Tensor, *,
+                          tiling=None) -> torch.Tensor:
     """silu(h[:, :I]) * h[:, I:] with h = grouped_matmul(x, weights) -- fused, h never stored.
 
     weights: [E, K_in, 2I] with the gate columns first (the fused gate_up layout of
-    mintext/modules/moe.py:125-132).  Returns [M, I] in x's dtype.  Forward only.
+    mintext/modules/moe.py:125-132).  Returns [M, I] in x's dtype.  Forward only.  ``tiling``:
+    (tm, tg, tn) as for ``grouped_matmul``.
     """
     gs = _gs(group_sizes)
     dev = L.require_device(x, weights, gs)
@@ -167,8 +190,9 @@ def grouped_matmul_swiglu(x: torch.Tensor, weights: torch.Tensor, group_sizes: t
     I = two_i // 2
     out = torch.empty((M, I), dtype=x.dtype, device=dev)
     ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
-    L.call("mtx_gmm_swiglu", L.ptr(x), L.ptr(w), L.ptr(gs), L.dtype_code(x.dtype), M, Kin, I, E, L.ptr(out),
-           L.ptr(ws), ws.numel(), L.stream(dev))
+    tm, tg = _tile_args(tiling)
+    L.call("mtx_gmm_tiled", L.MTX_GMM_OP_SWIGLU, L.ptr(x), L.ptr(w), L.ptr(gs), L.dtype_code(x.dtype), M, Kin, I,
+           E, tm, tg, L.ptr(out), L.ptr(ws), ws.numel(), L.stream(dev))
     return out
 
 

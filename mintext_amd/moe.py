@@ -24,8 +24,14 @@ from .kernels.swiglu import swiglu_autograd
 
 
 def moe_experts_forward(x: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
-                        gate_up: torch.Tensor, down: torch.Tensor, *, fuse_swiglu: bool | None = None) -> torch.Tensor:
-    """[N, D] tokens -> [N, D] in result_type(x, topk_weights) (float32 for bf16 + f32 weights)."""
+                        gate_up: torch.Tensor, down: torch.Tensor, *, fuse_swiglu: bool | None = None,
+                        gate_up_tiling=None, down_tiling=None) -> torch.Tensor:
+    """[N, D] tokens -> [N, D] in result_type(x, topk_weights) (float32 for bf16 + f32 weights).
+
+    ``gate_up_tiling`` / ``down_tiling``: HIP tile configurations (``kernels.autotuner``), the
+    counterparts of ``MoEExperts.gate_up_tiling`` / ``down_tiling`` (moe.py:189-202) that the
+    reference's train.py:43-52 fills from the autotuner.
+    """
     gate_up = gate_up.to(x.dtype)
     down = down.to(x.dtype)
     E = gate_up.shape[0]
@@ -35,11 +41,11 @@ def moe_experts_forward(x: torch.Tensor, topk_indices: torch.Tensor, topk_weight
     if fuse_swiglu is None:
         fuse_swiglu = not needs_grad
     if fuse_swiglu:
-        inter = grouped_matmul_swiglu(sorted_tokens, gate_up, group_sizes)
+        inter = grouped_matmul_swiglu(sorted_tokens, gate_up, group_sizes, tiling=gate_up_tiling)
     else:
-        h = grouped_matmul_vjp(sorted_tokens, gate_up, group_sizes)
+        h = grouped_matmul_vjp(sorted_tokens, gate_up, group_sizes, tiling=gate_up_tiling)
         inter = swiglu_autograd(h)
-    out = grouped_matmul_vjp(inter, down, group_sizes)
+    out = grouped_matmul_vjp(inter, down, group_sizes, tiling=down_tiling)
     return unroute(out, sort_indices, topk_weights, topk_indices.shape[1])
 
 
