@@ -165,15 +165,21 @@ def _uniform_group_sizes(M: int, E: int, device):
 
 
 def _tune_one(x, w, gs, candidates, warmup_iters, bench_iters, name):
-    best_t = None
-    best = _benchmark_tiling(x, w, gs, None, warmup_iters, bench_iters)
-    logger.info("  %s heuristic tiling: %.1f GFLOPS", name, best)
-    for t in candidates:
-        g = _benchmark_tiling(x, w, gs, t, warmup_iters, bench_iters)
-        if g > best:
-            best, best_t = g, t
-            logger.info("  new best %s: %s -> %.1f GFLOPS", name, t, g)
-    return best_t, best
+    """Best (tiling, GFLOP/s) among the heuristic configuration (None) and ``candidates``.
+
+    Every configuration is timed twice, in forward then reverse order, and keeps its better
+    run, so that clock ramp-up and thermal drift do not favour the configurations timed last.
+    """
+    configs = [None] + list(candidates)
+    score = {i: 0.0 for i in range(len(configs))}
+    for order in (range(len(configs)), reversed(range(len(configs)))):
+        for i in order:
+            score[i] = max(score[i], _benchmark_tiling(x, w, gs, configs[i], warmup_iters, bench_iters))
+    logger.info("  %s heuristic tiling: %.1f GFLOPS", name, score[0])
+    best_i = max(score, key=lambda i: (score[i], i == 0))  # ties keep the heuristic
+    if best_i:
+        logger.info("  best %s: %s -> %.1f GFLOPS", name, configs[best_i], score[best_i])
+    return configs[best_i], score[best_i]
 
 
 def autotune_moe(config: MoETuningConfig, cache_dir: str | None = None, max_trials: int = 20,
