@@ -71,7 +71,7 @@ class EventTimer:
         return float(np.mean([a.elapsed_time(b) for a, b in self.pairs])) if self.pairs else 0.0
 
 
-def _cpu_baseline_layer(x, logits, gate_up, down, cfg, budget_s=12.0):
+def _cpu_baseline_layer(x, logits, gate_up, down, cfg, budget_s=12.0, shared=None):
     """Oracle forward (float64) on the first Ts tokens; Ts doubles until the run takes >= budget/3."""
     from oracle import moe_oracle as O
 
@@ -92,7 +92,10 @@ def _cpu_baseline_layer(x, logits, gate_up, down, cfg, budget_s=12.0):
             idx, w, _ = O.router_sigmoid_group(logits[:ts], cfg["K"], n_group=cfg.get("n_group", 1),
                                                topk_group=cfg.get("topk_group", 1),
                                                routed_scaling_factor=cfg.get("scale", 1.0))
-        O.moe_experts(x[:ts].astype(np.float64), idx, w, gu, dn)
+        if shared is None:
+            O.moe_experts(x[:ts].astype(np.float64), idx, w, gu, dn)
+        else:
+            O.moe_block(x[:ts].astype(np.float64), idx, w, gu, dn, shared[0], shared[1])
         dt = time.perf_counter() - t0
         best = (ts, dt)
         if dt >= budget_s / 3 or ts >= T:
@@ -109,7 +112,7 @@ def _zipf_bias(E, s, rng, beta=0.55):
     return (-beta * s * np.log(rank)).astype(np.float32)
 
 
-def run(cfg_name, steps, warmup, cpu_baseline=True):
+def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate"):
     import torch
 
     from mintext_amd import _lib
@@ -133,14 +136,24 @@ def run(cfg_name, steps, warmup, cpu_baseline=True):
     gate_up = (torch.randn(E, D, 2 * I, device=dev, generator=g) * cfg["wstd"]).to(cdt)
     down = (torch.randn(E, I, D, device=dev, generator=g) * cfg["wstd"]).to(cdt)
     shared = None
+    fold = False
     if cfg.get("shared"):
         shared = ((torch.randn(1, D, 2 * I * cfg["shared"], device=dev, generator=g) * cfg["wstd"]).to(cdt),
                   (torch.randn(1, I * cfg["shared"], D, device=dev, generator=g) * cfg["wstd"]).to(cdt))
+        fold = shared_mode == "folded" and cfg["shared"] == 1
+        if fold:
+            # load-time transform: the shared expert becomes expert E of the routed weights
+            from mintext_amd.moe import fold_shared_expert
+
+            gate_up, down = fold_shared_expert(gate_up, down, shared[0], shared[1])
     rkw = dict(scoring=cfg["scoring"], n_group=cfg.get("n_group", 1), topk_group=cfg.get("topk_group", 1),
                routed_scaling_factor=cfg.get("scale", 1.0))
 
     t_gu, t_dn, t_disp, t_comb = EventTimer(torch), EventTimer(torch), EventTimer(torch), EventTimer(torch)
-    flops_fwd = 2.0 * M * D * 2 * I + 2.0 * M * I * D
+    Mg = M + T if fold else M  # rows through the expert GEMMs (the folded shared expert adds T)
+    Kc = K + 1 if fold else K  # rows combined per token
+    Eg = E + 1 if fold else E  # groups
+    flops_fwd = 2.0 * Mg * D * 2 * I + 2.0 * Mg * I * D
     fp8 = cfg["dtype"] == "fp8"
     if fp8:
         from mintext_amd.kernels.fp8 import (grouped_matmul_fp8, grouped_matmul_fp8_swiglu, quantize_fp8_rows,
@@ -152,14 +165,14 @@ def run(cfg_name, steps, warmup, cpu_baseline=True):
 
     def step(timed):
         with torch.no_grad():
-            idx, w = route_topk(logits, K, **rkw)
+            idx, w = route_topk(logits, K, shared_expert=E if fold else None, **rkw)
             if timed:
                 t_disp.start()
             if fp8:
                 xq, xs = quantize_fp8_rows(x)
                 sq, ss, si, gs, _ = route_with_scales(xq, xs, idx, E)
             else:
-                st, si, gs = route(x, idx, E)
+                st, si, gs = route(x, idx, Eg)
             if timed:
                 t_disp.stop()
                 t_gu.start()
@@ -174,10 +187,10 @@ def run(cfg_name, steps, warmup, cpu_baseline=True):
             if timed:
                 t_dn.stop()
                 t_comb.start()
-            out = unroute(o, si, w, K)
+            out = unroute(o, si, w, Kc)
             if timed:
                 t_comb.stop()
-            if shared is not None:
+            if shared is not None and not fold:
                 from mintext_amd.moe import shared_expert_forward
 
                 out = out + shared_expert_forward(x, shared[0], shared[1]).float()
@@ -234,13 +247,13 @@ def run(cfg_name, steps, warmup, cpu_baseline=True):
         achieved = kern_flops / (gu_ms * 1e-3) / 1e12
         dominant = "gmm_dlhs (both expert GEMMs)"
     else:
-        kern_flops = 2.0 * M * D * 2 * I
+        kern_flops = 2.0 * Mg * D * 2 * I
         achieved = kern_flops / (gu_ms * 1e-3) / 1e12
         dominant = "gmm_fp8_swiglu (gate_up + SwiGLU + requant)" if fp8 else "gmm_swiglu (gate_up + fused SwiGLU)"
     tokens_per_s = T / (ms * 1e-3)
     gemm_ms = gu_ms + dn_ms
-    disp_b = T * D * (1 if fp8 else 2) + M * D * (1 if fp8 else 2) + T * K * 4 + M * 4 + E * 4
-    comb_b = M * D * 2 + T * K * 4 + M * 4 + T * D * 4
+    disp_b = T * D * (1 if fp8 else 2) + Mg * D * (1 if fp8 else 2) + T * Kc * 4 + Mg * 4 + Eg * 4
+    comb_b = Mg * D * 2 + T * Kc * 4 + Mg * 4 + T * D * 4
     res = {
         "metric": "MoE layer fwd tokens/s + grouped-GEMM TFLOP/s (% of peak), 1x MI355X",
         "value": round(tokens_per_s, 1),
@@ -257,7 +270,8 @@ def run(cfg_name, steps, warmup, cpu_baseline=True):
         "config": {"workload": f"{cfg_name} MoE layer forward" if cfg_name != "qwen3_bwd" else
                    "qwen3 grouped-GEMM backward (dlhs+tgmm), Zipf(1.2) skew",
                    "T": T, "d_model": D, "experts": E, "top_k": K, "d_ff": I, "routing": cfg["scoring"],
-                   "parallelism": "single GPU"},
+                   "parallelism": "single GPU",
+                   **({"shared_expert": shared_mode if fold else "separate"} if shared is not None else {})},
         "gemm": {"tflops": round(flops_fwd / (gemm_ms * 1e-3) / 1e12 if cfg_name != "qwen3_bwd" else
                                  flops_fwd / ((gu_ms + dn_ms) * 1e-3) / 1e12, 1),
                  "frac_of_peak": round((flops_fwd / (gemm_ms * 1e-3) / 1e12) / peak, 4),
@@ -272,8 +286,10 @@ def run(cfg_name, steps, warmup, cpu_baseline=True):
         "wall_s": round(wall, 3),
     }
     if cpu_baseline and cfg_name not in ("qwen3_bwd",):
+        sh = None if shared is None else (shared[0][0].float().cpu().numpy(), shared[1][0].float().cpu().numpy())
         res["cpu_baseline"] = _cpu_baseline_layer(x.float().cpu().numpy(), logits.float().cpu().numpy(),
-                                                  gate_up.float().cpu().numpy(), down.float().cpu().numpy(), cfg)
+                                                  gate_up[:E].float().cpu().numpy(), down[:E].float().cpu().numpy(),
+                                                  cfg, shared=sh)
     return res
 
 
@@ -284,6 +300,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="mixtral", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--shared", default="separate", choices=["folded", "separate"],
+                    help="deepseek: shared expert run as its own one-group GEMMs (default) or folded into the routed GEMMs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 plain 256 MiB device copies (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     a = ap.parse_args(argv)
@@ -303,7 +321,7 @@ def main(argv=None):
         print("bench.py measures one GPU only: this build has no multi-GPU path (no expert parallelism or "
               "collectives); run with --gpus 1", file=sys.stderr)
         return 2
-    res = run(a.config, a.steps, a.warmup, cpu_baseline=not a.no_cpu_baseline)
+    res = run(a.config, a.steps, a.warmup, cpu_baseline=not a.no_cpu_baseline, shared_mode=a.shared)
     print(json.dumps(res))
     return 0
 

@@ -12,6 +12,9 @@
  *   mtx_router_topk        <- MoERouter.__call__ / _group_topk_routing
  *                             (mintext/modules/moe.py:41-103); softmax mode has no
  *                             counterpart in the reference (Mixtral/Qwen3 router)
+ *   mtx_router_topk_shared <- the same with MoEBlock's shared expert (moe.py:231-236,256-258)
+ *                             folded in as an always-routed extra expert
+ *   mtx_expert_bias_update <- update_expert_biases (mintext/trainer.py:371-410), one layer
  *   mtx_route              <- route (mintext/kernels/moe_dispatch.py:47-81)
  *   mtx_gather_rows        <- _sort_with_vjp forward (moe_dispatch.py:21-24)
  *   mtx_scatter_rows       <- _sort_with_vjp backward (moe_dispatch.py:33-38)
@@ -78,6 +81,21 @@ int mtx_router_topk(const void* logits, int logits_dtype, int64_t T, int64_t E, 
                     int scoring, const float* bias, int64_t n_group, int64_t topk_group,
                     int norm_topk_prob, float routed_scaling_factor,
                     int32_t* topk_idx, float* topk_w, float* scores, void* stream);
+
+/* As mtx_router_topk, with a shared expert folded in as an always-routed extra expert
+ * (MoEBlock's shared expert, mintext/modules/moe.py:231-236,256-258, evaluated inside the
+ * routed grouped GEMMs): topk_idx / topk_w are [T,K+1]; columns 0..K-1 as mtx_router_topk,
+ * column K = shared_expert (>= E) with weight 1.0, so that the combine adds the shared output
+ * last, after the routed sum, as routed_out + shared_out does.                          */
+int mtx_router_topk_shared(const void* logits, int logits_dtype, int64_t T, int64_t E, int64_t K,
+                           int scoring, const float* bias, int64_t n_group, int64_t topk_group,
+                           int norm_topk_prob, float routed_scaling_factor, int64_t shared_expert,
+                           int32_t* topk_idx, float* topk_w, float* scores, void* stream);
+
+/* Loss-free load balancing for one MoE layer (update_expert_biases, mintext/trainer.py:371-410):
+ * bias[e] += rate * sign(float(sum(counts))/E - counts[e]).  expert_counts [E] int32 is the
+ * layer's bincount of topk_idx (trainer.py:297-308), i.e. the group_sizes mtx_route returns. */
+int mtx_expert_bias_update(const int32_t* expert_counts, int64_t E, float rate, float* bias, void* stream);
 
 /* ---- route (dispatch) ------------------------------------------------------------------
  * tokens [N,D] (F32/BF16/FP8E4M3), topk_idx [N,K] -> sorted_tokens [N*K,D] (same dtype),

@@ -33,7 +33,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     const void* __restrict__ logits, int ldt, int T, int E, int K, int L,
     int scoring, const float* __restrict__ bias, int n_group, int topk_group, int norm,
     float rscale, int32_t* __restrict__ idx_out, float* __restrict__ w_out,
-    float* __restrict__ scores_out) {
+    float* __restrict__ scores_out, int ldo, int extra) {
   extern __shared__ float smem[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -161,8 +161,13 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   w = w * rscale;
   (void)my_v;
   if (tok_ok && li < K) {
-    idx_out[t * K + li] = my_i;
-    w_out[t * K + li] = w;
+    idx_out[t * ldo + li] = my_i;
+    w_out[t * ldo + li] = w;
+  }
+  // always-routed extra expert (a folded shared expert) in column K with weight 1
+  if (tok_ok && extra >= 0 && li == 0) {
+    idx_out[t * ldo + K] = extra;
+    w_out[t * ldo + K] = 1.0f;
   }
   if (scores_out != nullptr) {
 #pragma unroll
@@ -178,10 +183,10 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
 
 using namespace mtx;
 
-extern "C" int mtx_router_topk(const void* logits, int logits_dtype, int64_t T, int64_t E, int64_t K,
-                               int scoring, const float* bias, int64_t n_group, int64_t topk_group,
-                               int norm_topk_prob, float routed_scaling_factor,
-                               int32_t* topk_idx, float* topk_w, float* scores, void* stream) {
+static int router_launch(const void* logits, int logits_dtype, int64_t T, int64_t E, int64_t K, int scoring,
+                         const float* bias, int64_t n_group, int64_t topk_group, int norm_topk_prob,
+                         float routed_scaling_factor, int32_t* topk_idx, float* topk_w, float* scores, int64_t ldo,
+                         int64_t extra, void* stream) {
   if (T < 0 || E < 1 || E > 1024 || K < 1 || K > E || K > 64) return MTX_ERR_ARG;
   if (logits_dtype != MTX_F32 && logits_dtype != MTX_BF16) return MTX_ERR_ARG;
   if (scoring != MTX_SCORING_SOFTMAX && scoring != MTX_SCORING_SIGMOID_GROUP) return MTX_ERR_ARG;
@@ -207,12 +212,59 @@ extern "C" int mtx_router_topk(const void* logits, int logits_dtype, int64_t T, 
 #define MTX_LAUNCH_TOPK(VV)                                                                      \
   hipLaunchKernelGGL(router_topk_kernel<VV>, dim3(grid), dim3(256), shm, st, logits, logits_dtype, \
                      (int)T, (int)E, (int)K, L, scoring, bias, (int)n_group, (int)topk_group,      \
-                     norm_topk_prob, routed_scaling_factor, topk_idx, topk_w, scores)
+                     norm_topk_prob, routed_scaling_factor, topk_idx, topk_w, scores, (int)ldo, (int)extra)
   if (V <= 1) MTX_LAUNCH_TOPK(1);
   else if (V <= 2) MTX_LAUNCH_TOPK(2);
   else if (V <= 4) MTX_LAUNCH_TOPK(4);
   else if (V <= 8) MTX_LAUNCH_TOPK(8);
   else MTX_LAUNCH_TOPK(16);
 #undef MTX_LAUNCH_TOPK
+  return check_launch();
+}
+
+extern "C" int mtx_router_topk(const void* logits, int logits_dtype, int64_t T, int64_t E, int64_t K,
+                               int scoring, const float* bias, int64_t n_group, int64_t topk_group,
+                               int norm_topk_prob, float routed_scaling_factor,
+                               int32_t* topk_idx, float* topk_w, float* scores, void* stream) {
+  return router_launch(logits, logits_dtype, T, E, K, scoring, bias, n_group, topk_group, norm_topk_prob,
+                       routed_scaling_factor, topk_idx, topk_w, scores, K, -1, stream);
+}
+
+extern "C" int mtx_router_topk_shared(const void* logits, int logits_dtype, int64_t T, int64_t E, int64_t K,
+                                      int scoring, const float* bias, int64_t n_group, int64_t topk_group,
+                                      int norm_topk_prob, float routed_scaling_factor, int64_t shared_expert,
+                                      int32_t* topk_idx, float* topk_w, float* scores, void* stream) {
+  if (shared_expert < E || shared_expert > INT32_MAX) return MTX_ERR_ARG;
+  return router_launch(logits, logits_dtype, T, E, K, scoring, bias, n_group, topk_group, norm_topk_prob,
+                       routed_scaling_factor, topk_idx, topk_w, scores, K + 1, shared_expert, stream);
+}
+
+// Loss-free load balancing (trainer.py:371-410 for one layer): bias[e] += rate * sign(mean - counts[e])
+// with mean = float(sum(counts)) / float(E), one workgroup.
+__global__ __launch_bounds__(1024) void expert_bias_update_kernel(const int32_t* __restrict__ counts, int E, float rate,
+                                                                  float* __restrict__ bias) {
+  __shared__ long long wsum[16];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  long long part = 0;
+  for (int e = tid; e < E; e += blockDim.x) part += counts[e];
+  for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off);
+  if (lane == 0) wsum[w] = part;
+  __syncthreads();
+  long long total = 0;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) total += wsum[i];
+  const float mean = (float)total / (float)E;
+  for (int e = tid; e < E; e += blockDim.x) {
+    const float d = mean - (float)counts[e];
+    const float sgn = d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f);
+    bias[e] = bias[e] + sgn * rate;
+  }
+}
+
+extern "C" int mtx_expert_bias_update(const int32_t* expert_counts, int64_t E, float rate, float* bias,
+                                      void* stream) {
+  if (E < 1 || E > (int64_t(1) << 20)) return MTX_ERR_ARG;
+  if (!expert_counts || !bias) return MTX_ERR_ARG;
+  hipLaunchKernelGGL(expert_bias_update_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, expert_counts, (int)E,
+                     rate, bias);
   return check_launch();
 }

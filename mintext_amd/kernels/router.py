@@ -24,7 +24,7 @@ _SCORING = {"softmax": L.MTX_SCORING_SOFTMAX, "sigmoid_group": L.MTX_SCORING_SIG
 
 def route_topk(logits: torch.Tensor, k: int, *, scoring: str = "softmax", bias: torch.Tensor | None = None,
                n_group: int = 1, topk_group: int = 1, norm_topk_prob: bool = True,
-               routed_scaling_factor: float = 1.0, return_scores: bool = False):
+               routed_scaling_factor: float = 1.0, return_scores: bool = False, shared_expert: int | None = None):
     """Select the top-k experts per token.
 
     Args:
@@ -32,10 +32,13 @@ def route_topk(logits: torch.Tensor, k: int, *, scoring: str = "softmax", bias: 
         k: experts per token.
         scoring: "softmax" or "sigmoid_group".
         bias: [E] float32 e_score_correction_bias (sigmoid_group only; None = zeros).
+        shared_expert: id (>= E) of a shared expert folded into the routed weights: the
+            outputs get a column k naming it with weight 1.0 (``mtx_router_topk_shared``).
 
     Returns:
-        (topk_indices [T,k] int32, topk_weights [T,k] float32) and, with return_scores,
-        scores [T,E] float32 (sigmoid scores, or softmax probabilities).
+        (topk_indices [T,k] int32, topk_weights [T,k] float32) -- [T,k+1] with a shared
+        expert -- and, with return_scores, scores [T,E] float32 (sigmoid scores, or softmax
+        probabilities).
     """
     if scoring not in _SCORING:
         raise ValueError(f"unknown scoring {scoring!r}")
@@ -44,15 +47,39 @@ def route_topk(logits: torch.Tensor, k: int, *, scoring: str = "softmax", bias: 
     if lg.dtype not in (torch.float32, torch.bfloat16):
         lg = lg.float()
     T, E = lg.shape
-    idx = torch.empty((T, k), dtype=torch.int32, device=dev)
-    w = torch.empty((T, k), dtype=torch.float32, device=dev)
+    kk = k if shared_expert is None else k + 1
+    idx = torch.empty((T, kk), dtype=torch.int32, device=dev)
+    w = torch.empty((T, kk), dtype=torch.float32, device=dev)
     scores = torch.empty((T, E), dtype=torch.float32, device=dev) if return_scores else None
     b = None
     if bias is not None:
         b = bias.to(device=dev, dtype=torch.float32).contiguous()
-    L.call("mtx_router_topk", L.ptr(lg), L.dtype_code(lg.dtype), T, E, k, _SCORING[scoring], L.ptr(b),
-           n_group, topk_group, int(bool(norm_topk_prob)), float(routed_scaling_factor), L.ptr(idx), L.ptr(w),
-           L.ptr(scores), L.stream(dev))
+    if shared_expert is None:
+        L.call("mtx_router_topk", L.ptr(lg), L.dtype_code(lg.dtype), T, E, k, _SCORING[scoring], L.ptr(b),
+               n_group, topk_group, int(bool(norm_topk_prob)), float(routed_scaling_factor), L.ptr(idx), L.ptr(w),
+               L.ptr(scores), L.stream(dev))
+    else:
+        L.call("mtx_router_topk_shared", L.ptr(lg), L.dtype_code(lg.dtype), T, E, k, _SCORING[scoring], L.ptr(b),
+               n_group, topk_group, int(bool(norm_topk_prob)), float(routed_scaling_factor), int(shared_expert),
+               L.ptr(idx), L.ptr(w), L.ptr(scores), L.stream(dev))
     if return_scores:
         return idx, w, scores
     return idx, w
+
+
+def update_expert_bias(bias: torch.Tensor, expert_counts: torch.Tensor, rate: float) -> torch.Tensor:
+    """Loss-free load balancing of one MoE layer, in place (update_expert_biases,
+    mintext/trainer.py:371-410): ``bias += rate * sign(mean(counts) - counts)``.
+
+    ``expert_counts`` is the layer's bincount of its top-k indices (trainer.py:297-308), which
+    is the ``group_sizes`` that ``route`` returns.  ``bias`` is the float32 [E]
+    ``e_score_correction_bias``; it is returned for chaining.
+    """
+    dev = L.require_device(bias, expert_counts)
+    if bias.dtype != torch.float32 or not bias.is_contiguous():
+        raise TypeError("bias must be a contiguous float32 tensor (updated in place)")
+    counts = expert_counts.to(torch.int32).contiguous()
+    if counts.numel() != bias.numel():
+        raise ValueError(f"expert_counts has {counts.numel()} entries for {bias.numel()} experts")
+    L.call("mtx_expert_bias_update", L.ptr(counts), bias.numel(), float(rate), L.ptr(bias), L.stream(dev))
+    return bias

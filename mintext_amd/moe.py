@@ -7,7 +7,10 @@ the compute dtype (:170-171), ``route`` (:174-176), gate_up grouped GEMM (:189-1
 GEMM and the SwiGLU run as one fused kernel.
 
 ``moe_layer_forward`` prepends the router top-k on given gate logits (moe.py:52-67) and,
-optionally, a shared expert (moe.py:256-258) evaluated as a one-group grouped GEMM.
+optionally, a shared expert (moe.py:256-258): either evaluated as a one-group grouped GEMM
+and added, or -- after the load-time ``fold_shared_expert`` -- folded into the routed GEMMs
+as an always-routed extra expert with weight 1, whose output the combine adds after the
+routed sum (the same sum, in the same order, as routed_out + shared_out).
 
 ``moe_experts_forward_fp8`` is the blockwise-fp8 variant (no reference counterpart):
 activations quantised in 1x128 groups, routed with their scales, fp8 gate_up GEMM with the
@@ -25,12 +28,14 @@ from .kernels.swiglu import swiglu_autograd
 
 def moe_experts_forward(x: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
                         gate_up: torch.Tensor, down: torch.Tensor, *, fuse_swiglu: bool | None = None,
-                        gate_up_tiling=None, down_tiling=None) -> torch.Tensor:
+                        gate_up_tiling=None, down_tiling=None, return_group_sizes: bool = False):
     """[N, D] tokens -> [N, D] in result_type(x, topk_weights) (float32 for bf16 + f32 weights).
 
     ``gate_up_tiling`` / ``down_tiling``: HIP tile configurations (``kernels.autotuner``), the
     counterparts of ``MoEExperts.gate_up_tiling`` / ``down_tiling`` (moe.py:189-202) that the
-    reference's train.py:43-52 fills from the autotuner.
+    reference's train.py:43-52 fills from the autotuner.  With ``return_group_sizes`` the
+    result is ``(out, group_sizes)``: the per-expert token counts (the bincount of
+    trainer.py:297-308) that ``route`` computed anyway.
     """
     gate_up = gate_up.to(x.dtype)
     down = down.to(x.dtype)
@@ -46,19 +51,58 @@ def moe_experts_forward(x: torch.Tensor, topk_indices: torch.Tensor, topk_weight
         h = grouped_matmul_vjp(sorted_tokens, gate_up, group_sizes, tiling=gate_up_tiling)
         inter = swiglu_autograd(h)
     out = grouped_matmul_vjp(inter, down, group_sizes, tiling=down_tiling)
-    return unroute(out, sort_indices, topk_weights, topk_indices.shape[1])
+    res = unroute(out, sort_indices, topk_weights, topk_indices.shape[1])
+    return (res, group_sizes) if return_group_sizes else res
+
+
+def fold_shared_expert(gate_up: torch.Tensor, down: torch.Tensor, shared_gate_up: torch.Tensor,
+                       shared_down: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Load-time transform: the shared expert appended as expert E of the routed weights.
+
+    gate_up [E, D, 2I] + shared [D, 2I] (or [1, D, 2I]) -> [E+1, D, 2I]; down [E, I, D] +
+    shared [I, D] -> [E+1, I, D].  The shared expert's intermediate size must equal the routed
+    one (DeepSeek-V3: n_shared_experts = 1, moe.py:231-236); the shared gate/up columns keep the
+    gate-first layout.  Done once when the weights are loaded, never per step.
+    """
+    E, D, two_i = gate_up.shape
+    sgu = shared_gate_up.reshape(-1, *shared_gate_up.shape[-2:])
+    sdn = shared_down.reshape(-1, *shared_down.shape[-2:])
+    if sgu.shape != (1, D, two_i) or sdn.shape != (1, two_i // 2, D) or down.shape != (E, two_i // 2, D):
+        raise ValueError(f"shared expert {tuple(shared_gate_up.shape)}/{tuple(shared_down.shape)} does not fold "
+                         f"into routed experts {tuple(gate_up.shape)}/{tuple(down.shape)} (intermediate sizes differ)")
+    return (torch.cat([gate_up, sgu.to(gate_up.dtype)], 0).contiguous(),
+            torch.cat([down, sdn.to(down.dtype)], 0).contiguous())
 
 
 def moe_layer_forward(logits: torch.Tensor, x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, *,
                       k: int, scoring: str = "softmax", bias: torch.Tensor | None = None, n_group: int = 1,
                       topk_group: int = 1, norm_topk_prob: bool = True, routed_scaling_factor: float = 1.0,
-                      shared_gate_up: torch.Tensor | None = None, shared_down: torch.Tensor | None = None):
-    """Router top-k + routed experts (+ shared expert).  Returns (out [T,D] f32, topk_indices, topk_weights)."""
-    idx, w = route_topk(logits, k, scoring=scoring, bias=bias, n_group=n_group, topk_group=topk_group,
-                        norm_topk_prob=norm_topk_prob, routed_scaling_factor=routed_scaling_factor)
-    out = moe_experts_forward(x, idx, w, gate_up, down)
-    if shared_gate_up is not None:
-        out = out + shared_expert_forward(x, shared_gate_up, shared_down).to(out.dtype)
+                      shared_gate_up: torch.Tensor | None = None, shared_down: torch.Tensor | None = None,
+                      shared_folded: bool = False, return_expert_counts: bool = False):
+    """Router top-k + routed experts (+ shared expert) -- MoEBlock.__call__ (moe.py:240-266) after
+    the gate GEMM.  Returns (out [T,D] f32, topk_indices [T,k], topk_weights [T,k]) and, with
+    ``return_expert_counts``, the [E] int32 per-expert token counts (trainer.py:297-308).
+
+    ``shared_folded``: ``gate_up`` / ``down`` come from ``fold_shared_expert`` (E routed experts
+    + the shared one as expert E, ``logits`` has E columns); the shared expert then runs inside
+    the routed grouped GEMMs.
+    """
+    rkw = dict(scoring=scoring, bias=bias, n_group=n_group, topk_group=topk_group, norm_topk_prob=norm_topk_prob,
+               routed_scaling_factor=routed_scaling_factor)
+    E = logits.shape[1]
+    if shared_folded:
+        if gate_up.shape[0] != E + 1:
+            raise ValueError(f"folded weights need {E + 1} experts (E routed + shared), got {gate_up.shape[0]}")
+        idx, w = route_topk(logits, k, shared_expert=E, **rkw)
+        out, gs = moe_experts_forward(x, idx, w, gate_up, down, return_group_sizes=True)
+        idx, w = idx[:, :k], w[:, :k]
+    else:
+        idx, w = route_topk(logits, k, **rkw)
+        out, gs = moe_experts_forward(x, idx, w, gate_up, down, return_group_sizes=True)
+        if shared_gate_up is not None:
+            out = out + shared_expert_forward(x, shared_gate_up, shared_down).to(out.dtype)
+    if return_expert_counts:
+        return out, idx, w, gs[:E]
     return out, idx, w
 
 

@@ -390,3 +390,26 @@ def moe_experts_fp8(x, topk_indices, topk_weights, gu_q, gu_s, dn_q, dn_s) -> np
     yq, ys = quant_fp8_rows(y)
     o = bf16_round(gmm_fp8(yq, ys, dn_q, dn_s, gs).astype(np.float32))
     return unroute(o, perm, topk_weights, k)
+
+
+def moe_block(x, topk_indices, topk_weights, gate_up, down, shared_gate_up=None, shared_down=None) -> np.ndarray:
+    """MoEBlock.__call__ after the router (mintext/modules/moe.py:246-266): routed experts plus,
+    when given, the shared expert MLP (moe.py:231-236, linear.py:164-228) on the same tokens,
+    output = routed_out + shared_out, float64.  shared_gate_up [D, 2I'] (gate columns first),
+    shared_down [I', D]."""
+    out = moe_experts(x, topk_indices, topk_weights, gate_up, down)
+    if shared_gate_up is not None:
+        x64 = np.asarray(x, np.float64)
+        h = x64 @ np.asarray(shared_gate_up, np.float64).reshape(x64.shape[1], -1)
+        out = out + swiglu(h) @ np.asarray(shared_down, np.float64).reshape(-1, x64.shape[1])
+    return out
+
+
+def expert_bias_update(expert_counts, rate: float, bias) -> np.ndarray:
+    """update_expert_biases (mintext/trainer.py:371-410) for one layer, float32 as under JAX with
+    x64 disabled: avg = float32(sum(counts)) / float32(E); bias + sign(avg - counts) * rate."""
+    c = np.asarray(expert_counts, np.int64)
+    E = c.shape[-1]
+    avg = np.float32(c.sum()) / np.float32(E)
+    direction = np.sign(avg - c.astype(np.float32)).astype(np.float32)
+    return (np.asarray(bias, np.float32) + direction * np.float32(rate)).astype(np.float32)

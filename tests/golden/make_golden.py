@@ -237,6 +237,50 @@ def make_moe_tiny():
                         w=w.numpy(), out=out.numpy())
 
 
+# ------------------------------------------------- DeepSeek-style block with a shared expert
+def moe_block_inputs():
+    """Inputs of the shared-expert block fixture (regenerated from a PCG64 seed by the tests)."""
+    T, D, E, K, I, G, TG = 64, 64, 16, 4, 32, 4, 2
+    r = _rng(21)
+    x = r.standard_normal((T, D)).astype(np.float32)
+    wg = (r.standard_normal((D, E)) * 0.2).astype(np.float32)
+    bias = (r.standard_normal(E) * 0.05).astype(np.float32)
+    gate_up = (r.standard_normal((E, D, 2 * I)) * 0.05).astype(np.float32)
+    down = (r.standard_normal((E, I, D)) * 0.05).astype(np.float32)
+    sgu = (r.standard_normal((D, 2 * I)) * 0.05).astype(np.float32)
+    sdn = (r.standard_normal((I, D)) * 0.05).astype(np.float32)
+    return dict(T=T, D=D, E=E, K=K, I=I, n_group=G, topk_group=TG, scale=2.5, x=x, wg=wg, bias=bias,
+                gate_up=gate_up, down=down, shared_gate_up=sgu, shared_down=sdn)
+
+
+def make_moe_block_shared():
+    """HF DeepseekV3MoE (float64 experts; its router computes float32 logits and scores):
+    sigmoid + bias, group-limited top-4 of 16 experts, norm, x2.5, one shared expert."""
+    from transformers import DeepseekV3Config
+    from transformers.models.deepseek_v3.modeling_deepseek_v3 import DeepseekV3MoE
+
+    p = moe_block_inputs()
+    D, E, K, I = p["D"], p["E"], p["K"], p["I"]
+    cfg = DeepseekV3Config(hidden_size=D, moe_intermediate_size=I, n_routed_experts=E, num_experts_per_tok=K,
+                           n_group=p["n_group"], topk_group=p["topk_group"], routed_scaling_factor=p["scale"],
+                           norm_topk_prob=True, n_shared_experts=1, hidden_act="silu")
+    blk = DeepseekV3MoE(cfg).double().eval()
+    t64 = lambda a: torch.from_numpy(np.ascontiguousarray(a)).double()
+    with torch.no_grad():
+        blk.gate.weight.copy_(t64(p["wg"].T))
+        blk.gate.e_score_correction_bias.copy_(t64(p["bias"]))
+        blk.experts.gate_up_proj.copy_(t64(np.swapaxes(p["gate_up"], 1, 2)))
+        blk.experts.down_proj.copy_(t64(np.swapaxes(p["down"], 1, 2)))
+        blk.shared_experts.gate_proj.weight.copy_(t64(p["shared_gate_up"][:, :I].T))
+        blk.shared_experts.up_proj.weight.copy_(t64(p["shared_gate_up"][:, I:].T))
+        blk.shared_experts.down_proj.weight.copy_(t64(p["shared_down"].T))
+        xt = t64(p["x"])
+        logits, w, idx = blk.gate(xt)
+        out = blk(xt[None]).reshape(p["T"], D)
+    np.savez_compressed(OUT / "moe_block_shared.npz", logits=logits.float().numpy(),
+                        idx=idx.numpy().astype(np.int32), w=w.float().numpy(), out=out.numpy())
+
+
 if __name__ == "__main__":
     torch.manual_seed(0)
     make_routers()
@@ -244,5 +288,6 @@ if __name__ == "__main__":
     make_gmm()
     make_fp8()
     make_moe_tiny()
+    make_moe_block_shared()
     for p in sorted(OUT.glob("*.npz")):
         print(p.name, p.stat().st_size)

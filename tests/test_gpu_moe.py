@@ -113,3 +113,94 @@ def test_block_backward_matches_oracle(dev):
             lm = L(args["x"], args["gate_up"], args["down"], args["w"])
             num = (lp - lm) / (2 * eps)
             np.testing.assert_allclose(grad.reshape(-1)[pos].item(), num, rtol=1e-3, atol=1e-4, err_msg=name)
+
+
+# ---- shared expert folded into the routed GEMMs, expert counts, loss-free bias update -------
+
+def _block_inputs():
+    import sys
+
+    from conftest import GOLDEN
+
+    sys.path.insert(0, str(GOLDEN))
+    from make_golden import moe_block_inputs
+
+    return moe_block_inputs()
+
+
+@pytest.mark.gpu
+def test_router_topk_shared_column(dev):
+    from mintext_amd.kernels import route_topk
+
+    p = _block_inputs()
+    lg = torch.from_numpy(golden("moe_block_shared")["logits"]).to(dev)
+    kw = dict(scoring="sigmoid_group", bias=torch.from_numpy(p["bias"]).to(dev), n_group=p["n_group"],
+              topk_group=p["topk_group"], routed_scaling_factor=p["scale"])
+    idx, w = route_topk(lg, p["K"], **kw)
+    idx2, w2 = route_topk(lg, p["K"], shared_expert=p["E"], **kw)
+    assert idx2.shape == (p["T"], p["K"] + 1)
+    assert torch.equal(idx2[:, :p["K"]], idx) and torch.equal(w2[:, :p["K"]], w)
+    assert (idx2[:, p["K"]] == p["E"]).all() and (w2[:, p["K"]] == 1.0).all()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_folded_shared_expert_block(dev, dtype):
+    from mintext_amd.moe import fold_shared_expert, moe_layer_forward
+
+    p = _block_inputs()
+    g = golden("moe_block_shared")
+    cdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(cdt)
+    x, gu, dn, sgu, sdn = t(p["x"]), t(p["gate_up"]), t(p["down"]), t(p["shared_gate_up"]), t(p["shared_down"])
+    lg = torch.from_numpy(g["logits"]).to(dev)
+    kw = dict(k=p["K"], scoring="sigmoid_group", bias=torch.from_numpy(p["bias"]).to(dev), n_group=p["n_group"],
+              topk_group=p["topk_group"], routed_scaling_factor=p["scale"])
+    out_s, idx_s, w_s, cnt_s = moe_layer_forward(lg, x, gu, dn, shared_gate_up=sgu, shared_down=sdn,
+                                                 return_expert_counts=True, **kw)
+    gu_f, dn_f = fold_shared_expert(gu, dn, sgu, sdn)
+    out_f, idx_f, w_f, cnt_f = moe_layer_forward(lg, x, gu_f, dn_f, shared_folded=True, return_expert_counts=True,
+                                                 **kw)
+    # same routing, same counts, same output bits as routed + shared evaluated separately
+    assert torch.equal(idx_f, idx_s) and torch.equal(w_f, w_s) and torch.equal(cnt_f, cnt_s)
+    assert torch.equal(out_f, out_s)
+    assert np.array_equal(cnt_f.cpu().numpy(), np.bincount(idx_f.cpu().numpy().ravel(), minlength=p["E"]))
+    tol = 1e-5 if dtype == "f32" else 2e-2
+    assert rel_err(out_f.double().cpu().numpy(), g["out"]) < tol
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("E", [8, 256, 1000])
+def test_expert_bias_update_matches_oracle(dev, E):
+    from mintext_amd.kernels import update_expert_bias
+
+    rng = np.random.default_rng(E)
+    counts = rng.integers(0, 3 * E, size=E).astype(np.int32)
+    counts[: E // 4] = int(counts.mean())  # some experts exactly at the (integer) mean
+    bias = (rng.standard_normal(E) * 0.01).astype(np.float32)
+    b = torch.from_numpy(bias).to(dev)
+    update_expert_bias(b, torch.from_numpy(counts).to(dev), 1e-3)
+    assert np.array_equal(b.cpu().numpy(), O.expert_bias_update(counts, 1e-3, bias))
+
+
+@pytest.mark.gpu
+def test_folded_shared_expert_mfma_shapes(dev):
+    # shapes on the bf16 MFMA kernels (D, I multiples of 256 / 128): folded == separate, bit for bit
+    from mintext_amd.moe import fold_shared_expert, moe_layer_forward
+
+    rng = np.random.default_rng(3)
+    T, D, E, K, I = 512, 512, 32, 8, 256
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev).bfloat16()
+    x = t(rng.standard_normal((T, D)))
+    gu, dn = t(rng.standard_normal((E, D, 2 * I)) * 0.03), t(rng.standard_normal((E, I, D)) * 0.03)
+    sgu, sdn = t(rng.standard_normal((D, 2 * I)) * 0.03), t(rng.standard_normal((I, D)) * 0.03)
+    lg = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32)).to(dev).bfloat16()
+    bias = torch.from_numpy((rng.standard_normal(E) * 1e-3).astype(np.float32)).to(dev)
+    kw = dict(k=K, scoring="sigmoid_group", bias=bias, n_group=8, topk_group=4, routed_scaling_factor=2.5)
+    out_s, idx, w = moe_layer_forward(lg, x, gu, dn, shared_gate_up=sgu, shared_down=sdn, **kw)
+    gu_f, dn_f = fold_shared_expert(gu, dn, sgu, sdn)
+    out_f, idx_f, w_f = moe_layer_forward(lg, x, gu_f, dn_f, shared_folded=True, **kw)
+    assert torch.equal(out_f, out_s)
+    f = lambda a: a.float().cpu().numpy()
+    ref = O.moe_block(f(x), idx.cpu().numpy(), w.cpu().numpy(), f(gu), f(dn), f(sgu), f(sdn))
+    assert rel_err(out_f.double().cpu().numpy(), ref) < 2e-2

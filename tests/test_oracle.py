@@ -276,6 +276,59 @@ def test_tiny_moe_layer_matches_hf_mixtral():
     np.testing.assert_allclose(out, g["out"], rtol=1e-5, atol=1e-7)
 
 
+def _block_inputs():
+    import sys
+
+    sys.path.insert(0, str(__import__("conftest").GOLDEN))
+    from make_golden import moe_block_inputs
+
+    return moe_block_inputs()
+
+
+def test_moe_block_with_shared_expert_matches_hf_deepseek():
+    # HF DeepseekV3MoE (routed experts + shared expert), float64 experts, float32 router
+    p, g = _block_inputs(), golden("moe_block_shared")
+    idx, w, _ = O.router_sigmoid_group(g["logits"], p["K"], bias=p["bias"], n_group=p["n_group"],
+                                       topk_group=p["topk_group"], routed_scaling_factor=p["scale"])
+    # HF returns its top-k unsorted: same set, same weight per expert
+    for t in range(p["T"]):
+        hf = dict(zip(g["idx"][t].tolist(), g["w"][t].tolist()))
+        ours = dict(zip(idx[t].tolist(), w[t].tolist()))
+        assert set(hf) == set(ours)
+        for e in hf:
+            assert abs(hf[e] - ours[e]) <= 1e-6 * abs(hf[e])
+    out = O.moe_block(p["x"], idx, w, p["gate_up"], p["down"], p["shared_gate_up"], p["shared_down"])
+    assert rel_err(out, g["out"]) < 1e-6
+    # the shared expert is a real term: without it the output differs
+    assert rel_err(O.moe_experts(p["x"], idx, w, p["gate_up"], p["down"]), g["out"]) > 1e-2
+
+
+def test_folded_shared_expert_equals_block():
+    # the shared expert as an always-routed extra expert (weight 1) gives the block's output
+    p = _block_inputs()
+    g = golden("moe_block_shared")
+    idx, w, _ = O.router_sigmoid_group(g["logits"], p["K"], bias=p["bias"], n_group=p["n_group"],
+                                       topk_group=p["topk_group"], routed_scaling_factor=p["scale"])
+    E = p["E"]
+    idx_f = np.concatenate([idx, np.full((p["T"], 1), E, np.int32)], 1)
+    w_f = np.concatenate([w, np.ones((p["T"], 1), np.float32)], 1)
+    gu_f = np.concatenate([p["gate_up"], p["shared_gate_up"][None]], 0)
+    dn_f = np.concatenate([p["down"], p["shared_down"][None]], 0)
+    folded = O.moe_experts(p["x"], idx_f, w_f, gu_f, dn_f)
+    assert rel_err(folded, g["out"]) < 1e-6
+
+
+def test_expert_bias_update_known_answers():
+    rate = 0.001
+    # mean 2: under-used experts (1, 0) go up, over-used (3, 4) go down
+    got = O.expert_bias_update([3, 1, 0, 4], rate, [0.5, 0.5, 0.5, 0.5])
+    assert np.array_equal(got, np.float32([0.5 - 0.001, 0.5 + 0.001, 0.5 + 0.001, 0.5 - 0.001]))
+    # balanced load: unchanged (sign(0) == 0)
+    assert np.array_equal(O.expert_bias_update([5, 5, 5], 0.1, [1.0, -2.0, 0.0]), np.float32([1.0, -2.0, 0.0]))
+    # fractional mean 1.5
+    assert np.array_equal(O.expert_bias_update([1, 2], 1.0, [0.0, 0.0]), np.float32([1.0, -1.0]))
+
+
 def test_planted_mistake_is_caught():
     """A transposed-operand slip in the GEMM (a plausible bug) fails the fixture comparison."""
     g = golden("gmm")
