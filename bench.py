@@ -293,6 +293,55 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate"):
     return res
 
 
+def gemm_power_study(steps=10, warmup=3):
+    """C2 gate_up grouped GEMM (fused SwiGLU) and a hipBLASLt dense GEMM of the same FLOPs
+    (torch.matmul [16384,4096] x [4096,28672]), each on N(0,1)/N(0,0.02) data and on all-zero
+    data: with zeros the MFMA datapath barely toggles, so the clock is not power-limited and
+    the difference isolates the data-dependent clock drop from the kernels' issue efficiency.
+    Not a benchmark of the path: one JSON line of timings for the DESIGN analysis."""
+    import torch
+
+    from mintext_amd import _lib
+    from mintext_amd.kernels import grouped_matmul_swiglu
+
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    M, D, I, E = 16384, 4096, 14336, 8
+    gs = torch.full((E,), M // E, dtype=torch.int32, device=dev)
+    x = torch.empty(M, D, dtype=torch.bfloat16, device=dev)
+    w = torch.empty(E, D, 2 * I, dtype=torch.bfloat16, device=dev)
+    flop = 2.0 * M * D * 2 * I
+
+    def t_ms(fn):
+        for _ in range(warmup):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            fn()
+        b.record()
+        b.synchronize()
+        return a.elapsed_time(b) / steps
+
+    out = {"study": "gemm-power", "shape": "C2 gate_up [16384,4096] x [8,4096,28672]", "steps": steps}
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    for data in ("normal", "zeros", "normal"):
+        if data == "normal":
+            x.copy_(torch.randn(M, D, device=dev, generator=g))
+            w.copy_(torch.randn(E, D, 2 * I, device=dev, generator=g) * 0.02)
+        else:
+            x.zero_()
+            w.zero_()
+        ours = t_ms(lambda: grouped_matmul_swiglu(x, w, gs))
+        dense = t_ms(lambda: torch.matmul(x, w[0]))
+        out.setdefault(data, []).append({"gmm_swiglu_ms": round(ours, 4), "gmm_swiglu_tflops": round(flop / ours / 1e9, 1),
+                                         "hipblaslt_dense_ms": round(dense, 4),
+                                         "hipblaslt_dense_tflops": round(flop / dense / 1e9, 1)})
+    print(json.dumps(out))
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -304,7 +353,11 @@ def main(argv=None):
                     help="deepseek: shared expert run as its own one-group GEMMs (default) or folded into the routed GEMMs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 plain 256 MiB device copies (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--study", choices=["gemm-power"], default=None,
+                    help="gemm-power: GEMM timings on normal vs all-zero data (clock / issue-efficiency study)")
     a = ap.parse_args(argv)
+    if a.study == "gemm-power":
+        return gemm_power_study(a.steps if a.steps != 20 else 10, a.warmup)
     if a.copy_calibration:
         import torch
 

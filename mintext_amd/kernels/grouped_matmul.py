@@ -9,9 +9,10 @@ output dtypes and differentiability):
 * ``tgmm(lhs, rhs, group_sizes)`` (:197-235) -- per-group x^T @ g, zeros for empty groups
 
 ``tiling`` selects the HIP tile configuration (the reference passes TPU ``ragged_dot`` tilings
-to XLA): a 3-tuple ``(tm, tg, tn)`` per GEMM -- ``tm`` rows per m-tile (128 or 256; other values
-round to the nearer), ``tg`` m-tiles per XCD scheduling group (1..64), ``tn`` columns per n-tile
-(256 is the only width; accepted and ignored).  ``None`` keeps the shape heuristics.  The
+to XLA): a 3-tuple ``(tm, tg, tn)`` per GEMM with ``tn == 256`` (the MFMA kernels' n-tile
+width) -- ``tm`` rows per m-tile (128 or 256; other values round to the nearer), ``tg`` m-tiles
+per XCD scheduling group (1..64).  ``None`` and any tuple with another ``tn`` (the reference's
+TPU tilings, such as its default (128, 128, 128)) keep the shape heuristics.  The
 9-tuple of ``grouped_matmul_vjp`` is padded from 3 like the reference (fwd, dlhs, tgmm; the
 tgmm entry is not used).  Tile configurations never change the output bits.  ``mosaic_fusion``
 is accepted and ignored.  ``group_sizes`` never leaves the device.  Extra entry points beyond the reference: ``grouped_matmul_swiglu``
@@ -37,13 +38,24 @@ def _check_float(*ts):
         raise TypeError("grouped GEMM operands must share one dtype")
 
 
+HIP_TN = 256  # n-tile width of the MFMA kernels; a tiling with another tn is a TPU hint
+
+
 def _tile_args(tiling) -> tuple[int, int]:
-    """(tile_m, tile_group) for the C-ABI from a (tm, tg, tn) tiling; (0, 0) = heuristics."""
+    """(tile_m, tile_group) for the C-ABI from a (tm, tg, tn) tiling; (0, 0) = heuristics.
+
+    Only tilings with tn == 256 (those of ``kernels.autotuner``) select a HIP configuration.
+    Any other tuple is a TPU ``ragged_dot`` tiling -- e.g. the (128, 128, 128) that the
+    reference passes when no tiling is configured (mintext/modules/moe.py:180-186) -- and
+    leaves the shape heuristics in charge.
+    """
     if tiling is None:
         return 0, 0
     t = tuple(int(v) for v in tiling)
-    if len(t) < 2 or any(v <= 0 for v in t):
+    if len(t) < 3 or any(v <= 0 for v in t):
         raise ValueError(f"tiling must hold positive ints (tm, tg, tn), got {tiling!r}")
+    if t[2] != HIP_TN:
+        return 0, 0
     tm = 128 if t[0] <= 128 else 256
     tg = min(max(t[1], 1), 64)
     return tm, tg

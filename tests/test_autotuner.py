@@ -96,8 +96,11 @@ def test_cached_result_needs_no_gpu(tmp_path):
 def test_tile_args_mapping():
     assert _tile_args(None) == (0, 0)
     assert _tile_args((256, 8, 256)) == (256, 8)
-    assert _tile_args((64, 1, 128)) == (128, 1)       # tm rounds to the nearer supported value
+    assert _tile_args((64, 1, 256)) == (128, 1)       # tm rounds to the nearer supported value
     assert _tile_args((512, 128, 256)) == (256, 64)   # tg clamps to 64
+    # TPU tilings (tn != 256), e.g. the reference's default (128, 128, 128): heuristics
+    assert _tile_args((128, 128, 128)) == (0, 0)
+    assert _tile_args((256, 512, 512)) == (0, 0)
     with pytest.raises(ValueError):
         _tile_args((0, 1, 256))
     # 3 -> 9 padding of grouped_matmul.py:108-112
@@ -160,14 +163,15 @@ def test_grouped_matmul_vjp_with_tiling_matches_default(dev):
     x0 = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(dev).bfloat16()
     w0 = torch.from_numpy((rng.standard_normal((E, K, N)) * 0.05).astype(np.float32)).to(dev).bfloat16()
     outs = []
-    for tiling in [(128,) * 9, (128, 2, 256, 256, 1, 256, 128, 128, 128)]:
+    for tiling in [(128,) * 9, (128, 2, 256, 256, 1, 256, 128, 128, 128), None]:
         x = x0.clone().requires_grad_(True)
         w = w0.clone().requires_grad_(True)
         y = grouped_matmul_vjp(x, w, gs, tiling=tiling)
         y.float().square().sum().backward()
         outs.append((y.detach(), x.grad, w.grad))
-    for a, b in zip(*outs):
-        assert torch.equal(a, b)
+    for other in outs[1:]:
+        for a, b in zip(outs[0], other):
+            assert torch.equal(a, b)
 
 
 @pytest.mark.gpu
@@ -180,3 +184,11 @@ def test_autotune_moe_tunes_and_caches(dev, tmp_path):
     for t in (r.gate_up_tiling, r.down_tiling):
         assert t is None or (len(t) == 3 and all(_pow2(v) for v in t))
     assert _load_cache(str(tmp_path), _cache_key(config)) == r
+
+
+def test_reference_default_tiling_keeps_heuristics():
+    from mintext_amd.kernels.grouped_matmul import _pad_tiling
+
+    # grouped_matmul_vjp's default and the reference's "no tiling configured" value
+    for t in [(128,) * 9, _pad_tiling((128, 128, 128))]:
+        assert _tile_args(t[0:3]) == (0, 0) and _tile_args(t[3:6]) == (0, 0)
