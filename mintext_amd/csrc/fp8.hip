@@ -924,20 +924,26 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
 #if MTX_F8_ROT
 #pragma unroll
     for (int j = 0; j < TN; ++j) fr_b[cb ^ 1][j] = rd_b(g_ + 1, j);
+    // accumulator q = i*TN + j is rescaled (block boundary only) one slot ahead of its MFMA,
+    // while the previous MFMA runs, so that no MFMA waits on the multiplies of its own input
+    auto rescale_acc = [&](int q) {
+      const int i = q / TN, j = q % TN;
+      const float fj = f[i][half_of(j)];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] *= fj;
+    };
+    if (rescale) rescale_acc(0);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        if (rescale) {
-          const float fj = f[i][half_of(j)];
-#pragma unroll
-          for (int v = 0; v < 16; ++v) acc[i][j][v] *= fj;
-        }
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr_b[cb][j], fr_a[i], acc[i][j], 0, 0, 0, 127,
                                                                     0, 127);
+        if (rescale && i * TN + j + 1 < TM * TN) rescale_acc(i * TN + j + 1);
       }
       fr_a[i] = rd_a(g_ + 1, i);
     }
+
 #endif
   };
   (void)rot_stage;
