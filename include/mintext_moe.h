@@ -36,6 +36,8 @@
  *   mtx_quant_fp8_weights  <- no counterpart; 128x128 weight blocks
  *   mtx_gmm_fp8            <- no counterpart; blockwise-fp8 form of mtx_gmm
  *   mtx_gmm_fp8_swiglu     <- no counterpart; blockwise-fp8 form of mtx_gmm_swiglu
+ *   mtx_transpose_batched  <- _import_expert_weights / _export_expert_weights
+ *                             (mintext/checkpoint/conversion.py:80-166), on the device
  */
 #ifndef MINTEXT_MOE_H
 #define MINTEXT_MOE_H
@@ -203,6 +205,18 @@ int mtx_gmm_fp8_swiglu(const uint8_t* xq, const float* x_scale, const uint8_t* w
                        int64_t M, int64_t Kin, int64_t I, int64_t E,
                        uint8_t* out_q, float* out_scale, void* out_bf16,
                        void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---- expert weight layouts -------------------------------------------------------------
+ * Batched transpose-copy (the per-expert HF <-> fused conversions of
+ * mintext/checkpoint/conversion.py:80-166, done on the device at load time):
+ * out[b*out_batch_stride + c*out_ld + r] = in[b*in_batch_stride + r*in_ld + c] for b < B,
+ * r < R, c < C (strides in elements; F32 or BF16).  HF gate [E,I,D] and up [E,I,D] land in the
+ * two halves of a fused gate_up [E,D,2I] with out_ld = 2I (up: out offset by I elements);
+ * HF down [E,D,I] -> down [E,I,D]; the reverse calls export.  Input and output must not
+ * overlap.  B <= 65535 and ceil(R/64) <= 65535.                                          */
+int mtx_transpose_batched(const void* in, int dtype, int64_t B, int64_t R, int64_t C,
+                          int64_t in_batch_stride, int64_t in_ld, void* out,
+                          int64_t out_batch_stride, int64_t out_ld, void* stream);
 
 #ifdef __cplusplus
 }

@@ -60,6 +60,7 @@ SIGNATURES = {
     "mtx_quant_fp8_weights": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _P]),
     "mtx_gmm_fp8": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "mtx_gmm_fp8_swiglu": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
+    "mtx_transpose_batched": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P]),
 }
 
 

@@ -413,3 +413,25 @@ def expert_bias_update(expert_counts, rate: float, bias) -> np.ndarray:
     avg = np.float32(c.sum()) / np.float32(E)
     direction = np.sign(avg - c.astype(np.float32)).astype(np.float32)
     return (np.asarray(bias, np.float32) + direction * np.float32(rate)).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------------------------
+# expert weight layouts  (mintext/checkpoint/conversion.py:80-166)
+# ---------------------------------------------------------------------------------------------
+
+
+def experts_from_hf(gate, up, down):
+    """_import_expert_weights (conversion.py:80-133) on stacked per-expert HF weights:
+    gate_up[e] = concatenate([gate[e].T, up[e].T], -1), down_f[e] = down[e].T."""
+    gate, up, down = (np.asarray(a) for a in (gate, up, down))
+    gate_up = np.stack([np.concatenate([gate[e].T, up[e].T], axis=-1) for e in range(gate.shape[0])])
+    return gate_up, np.stack([down[e].T for e in range(down.shape[0])])
+
+
+def experts_to_hf(gate_up, down):
+    """_export_expert_weights (conversion.py:136-166): (gate [E,I,D], up [E,I,D], down [E,D,I])."""
+    gate_up, down = np.asarray(gate_up), np.asarray(down)
+    i = gate_up.shape[2] // 2
+    gate = np.stack([gate_up[e, :, :i].T for e in range(gate_up.shape[0])])
+    up = np.stack([gate_up[e, :, i:].T for e in range(gate_up.shape[0])])
+    return gate, up, np.stack([down[e].T for e in range(down.shape[0])])

@@ -329,6 +329,28 @@ def test_expert_bias_update_known_answers():
     assert np.array_equal(O.expert_bias_update([1, 2], 1.0, [0.0, 0.0]), np.float32([1.0, -1.0]))
 
 
+def test_expert_layout_conversion_closed_form():
+    # conversion.py:80-166 on a hand-checkable case: gate_up[e, d, i] = gate[e, i, d] (i < I) and
+    # up[e, i - I, d] (i >= I); down_f[e, i, d] = down[e, d, i]; export inverts import
+    E, I, D = 3, 4, 5
+    gate = np.arange(E * I * D, dtype=np.float32).reshape(E, I, D)
+    up = -np.arange(E * I * D, dtype=np.float32).reshape(E, I, D) - 1
+    down = np.arange(E * D * I, dtype=np.float32).reshape(E, D, I) * 10
+    gu, dn = O.experts_from_hf(gate, up, down)
+    assert gu.shape == (E, D, 2 * I) and dn.shape == (E, I, D)
+    for e, d, i in itertools.product(range(E), range(D), range(2 * I)):
+        assert gu[e, d, i] == (gate[e, i, d] if i < I else up[e, i - I, d])
+    for e, i, d in itertools.product(range(E), range(I), range(D)):
+        assert dn[e, i, d] == down[e, d, i]
+    g2, u2, d2 = O.experts_to_hf(gu, dn)
+    assert np.array_equal(g2, gate) and np.array_equal(u2, up) and np.array_equal(d2, down)
+    # the fused layout feeds the expert layer exactly like HF's per-expert matmuls (SwiGLU MLP)
+    x = np.random.default_rng(0).standard_normal((7, D))
+    h = x @ gu[1].astype(np.float64)
+    hf = np.concatenate([x @ gate[1].T.astype(np.float64), x @ up[1].T.astype(np.float64)], -1)
+    assert np.allclose(h, hf)
+
+
 def test_planted_mistake_is_caught():
     """A transposed-operand slip in the GEMM (a plausible bug) fails the fixture comparison."""
     g = golden("gmm")
