@@ -843,6 +843,8 @@ __global__ __launch_bounds__(WM* WN * 64, MTX_V3_WPE) void gmm_v3_kernel(Args p)
     return __builtin_bit_cast(bf16x8, both);
   };
   auto read_frags = [&](int kt, int kk, int buf, int nb) {
+    // a wave with no rows of the group in this tile (small groups) runs no MFMA: no reads
+    if (MODE != TGMM && nb == 0) return;
     const char* st = lds + C::slot(kt) * STAGE;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
