@@ -441,65 +441,6 @@ __global__ __launch_bounds__(256) void unroute_kernel(
   }
 }
 
-// Flat combine: one thread per (token n, 8-element chunk c) item, UNR items per thread with all
-// of their K row loads issued before any sum, so that every lane keeps UNR*K 16-byte loads in
-// flight and no wave waits on a chain of dependent phases.  Same fmaf chain in k order as
-// unroute_kernel (K <= KMAX, D % 8 == 0, 16-byte aligned rows).
-template <typename YT, typename WT, typename OT, int KMAX, int UNR>
-__global__ __launch_bounds__(256) void unroute_flat_kernel(
-    const YT* __restrict__ Y, const int32_t* __restrict__ inv, const WT* __restrict__ w,
-    int64_t N, int K, int64_t D, int cpr_shift, OT* __restrict__ out) {
-  const int64_t cpr = D >> 3;
-  const int64_t total = N * cpr;
-  const int64_t M = N * (int64_t)K;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t base = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; base < total; base += stride * UNR) {
-    int64_t jj[UNR][KMAX];
-    float ww[UNR][KMAX];
-    int64_t n[UNR], c[UNR];
-#pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const int64_t it = base + u * stride;
-      n[u] = -1;
-      c[u] = 0;
-      if (it < total) {
-        n[u] = cpr_shift >= 0 ? (it >> cpr_shift) : it / cpr;
-        c[u] = it - n[u] * cpr;
-      }
-#pragma unroll
-      for (int k = 0; k < KMAX; ++k) {
-        jj[u][k] = -1;
-        ww[u][k] = 0.0f;
-        if (n[u] >= 0 && k < K) {
-          const int64_t j = inv[n[u] * K + k];
-          jj[u][k] = (j >= 0 && j < M) ? j : -1;
-          ww[u][k] = w ? ldf<WT>(w, n[u] * K + k) : 1.0f;
-        }
-      }
-    }
-    float y[UNR][KMAX][8];
-#pragma unroll
-    for (int u = 0; u < UNR; ++u)
-#pragma unroll
-      for (int k = 0; k < KMAX; ++k)
-        if (jj[u][k] >= 0) load8(Y + jj[u][k] * D + c[u] * 8, y[u][k]);
-#pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      if (n[u] < 0) continue;
-      float acc[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-#pragma unroll
-      for (int k = 0; k < KMAX; ++k)
-        if (jj[u][k] >= 0) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc[i] = fmaf(ww[u][k], y[u][k][i], acc[i]);
-        }
-      store8(out + n[u] * D + c[u] * 8, acc);
-    }
-  }
-}
-
 // Row-wise combine for bf16 expert outputs: one wave per token; the K rows of the token are
 // requested whole (S consecutive 1 KB slices of a row back to back, kept packed in registers),
 // so each gathered row reaches HBM as one contiguous burst rather than as slices a latency
@@ -552,31 +493,6 @@ __global__ __launch_bounds__(256) void unroute_rows_kernel(
   }
 }
 
-#ifndef MTX_UNROUTE_FLAT
-#define MTX_UNROUTE_FLAT 0
-#endif
-#ifndef MTX_UNROUTE_ROWS
-#define MTX_UNROUTE_ROWS 1
-#endif
-#ifndef MTX_UNROUTE_UNR
-#define MTX_UNROUTE_UNR 2
-#endif
-template <typename YT, typename WT, typename OT, int KMAX>
-static void launch_unroute_flat(const void* Y, const int32_t* inv, const void* w, int64_t N, int K, int64_t D,
-                                void* out, hipStream_t st) {
-  constexpr int UNR = KMAX >= 8 ? 1 : MTX_UNROUTE_UNR;
-  const int64_t cpr = D / 8;
-  int shift = -1;
-  if ((cpr & (cpr - 1)) == 0) {
-    shift = 0;
-    while ((int64_t(1) << shift) < cpr) ++shift;
-  }
-  int64_t gb = ceil_div(N * cpr, 256 * UNR);
-  if (gb > 65536) gb = 65536;
-  hipLaunchKernelGGL((unroute_flat_kernel<YT, WT, OT, KMAX, UNR>), dim3(gb), dim3(256), 0, st, (const YT*)Y, inv,
-                     (const WT*)w, N, K, D, shift, (OT*)out);
-}
-
 template <typename YT, typename WT, typename OT>
 static void launch_unroute_t(const void* Y, const int32_t* inv, const void* w, int64_t N, int K,
                              int64_t D, void* out, hipStream_t st) {
@@ -585,7 +501,7 @@ static void launch_unroute_t(const void* Y, const int32_t* inv, const void* w, i
 #define MTX_UNROUTE(V, KM)                                                                                  \
   hipLaunchKernelGGL((unroute_kernel<YT, WT, OT, V, KM>), dim3(blocks), dim3(256), 0, st, (const YT*)Y, inv, \
                      (const WT*)w, N, K, D, (OT*)out)
-  if (MTX_UNROUTE_ROWS && std::is_same<YT, uint16_t>::value && v8 && K <= 8) {
+  if (std::is_same<YT, uint16_t>::value && v8 && K <= 8) {
     const int64_t blocks_ = ceil_div(N, 4);
 #define MTX_UNROUTE_ROWS_L(KM, SS)                                                                           \
   hipLaunchKernelGGL((unroute_rows_kernel<WT, OT, KM, SS>), dim3(blocks_), dim3(256), 0, st, (const uint16_t*)Y, \
@@ -594,10 +510,6 @@ static void launch_unroute_t(const void* Y, const int32_t* inv, const void* w, i
     else if (K <= 4) MTX_UNROUTE_ROWS_L(4, 8);
     else MTX_UNROUTE_ROWS_L(8, 4);
 #undef MTX_UNROUTE_ROWS_L
-  } else if (MTX_UNROUTE_FLAT && v8 && K <= 8) {
-    if (K <= 2) launch_unroute_flat<YT, WT, OT, 2>(Y, inv, w, N, K, D, out, st);
-    else if (K <= 4) launch_unroute_flat<YT, WT, OT, 4>(Y, inv, w, N, K, D, out, st);
-    else launch_unroute_flat<YT, WT, OT, 8>(Y, inv, w, N, K, D, out, st);
   } else if (v8 && K <= 2) MTX_UNROUTE(true, 2);
   else if (v8 && K <= 4) MTX_UNROUTE(true, 4);
   else if (v8 && K <= 8) MTX_UNROUTE(true, 8);

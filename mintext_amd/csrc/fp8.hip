@@ -745,12 +745,6 @@ struct Tile {
 };
 }  // namespace v4
 
-#ifndef MTX_F8_LATE_RESCALE
-#define MTX_F8_LATE_RESCALE 1
-#endif
-#ifndef MTX_F8_ROT
-#define MTX_F8_ROT 1
-#endif
 template <int EPI>
 __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
   using namespace v4;
@@ -845,21 +839,12 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
     if (even) gload_lds4((in ? scur.sp : snxt.sp) + (k >> 1), st + (uint32_t)S_OFF + wave_u * 256u);
   };
 
-  i32x8 fa[2][TM], fb[2][TN];
   const int frow = lane & 31, fhalf = lane >> 5;
   auto ld32 = [&](const char* base, int r) -> i32x8 {
     const u32x4 lo = *(const u32x4*)(base + a_off(r, 2 * fhalf));
     const u32x4 hi = *(const u32x4*)(base + a_off(r, 2 * fhalf + 1));
     return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
   };
-  auto read_frags = [&](int g, int buf) {
-    const char* st = lds + (g & (NSTAGE - 1)) * STAGE;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) fa[buf][i] = ld32(st, wm * WTM + i * 32 + frow);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) fb[buf][j] = ld32(st + A_BYTES, wn * WTN + j * 32 + frow);
-  };
-#if MTX_F8_ROT
   // Rotating fragments: one A set fr_a[TM] and two B sets fr_b[2][TN].  During a stage the
   // A fragment of row block i is reloaded from the next stage right after its last MFMA, and
   // the next stage's B fragments go to the other B set, so the live fragments fit beside the
@@ -871,7 +856,6 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
   auto rd_b = [&](int g_, int j) -> i32x8 {
     return ld32(lds + (g_ & (NSTAGE - 1)) * STAGE + A_BYTES, wn * WTN + j * 32 + frow);
   };
-#endif
   // scales of the k-block whose even stage sits in ring step g
   float sa_c[TM], sb_c[2], sa_n[TM], sb_n[2];
   auto read_scales = [&](int g, float* sa, float* sb) {
@@ -898,30 +882,16 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
   __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));
   __syncthreads();
   read_scales(0, sa_c, sb_c);
-#if MTX_F8_ROT
 #pragma unroll
   for (int i = 0; i < TM; ++i) fr_a[i] = rd_a(0, i);
 #pragma unroll
   for (int j = 0; j < TN; ++j) fr_b[0][j] = rd_b(0, j);
-#else
-  read_frags(0, 0);
-#endif
   int g = 0;
 
-  auto mfmas = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[buf][j], fa[buf][i], acc[i][j], 0, 0, 0, 127,
-                                                                    0, 127);
-  };
-
   // One stage of the rotating schedule: MFMAs of ring step g_ on fr_a / fr_b[cb], with the
-  // fragments of step g_+1 read in between; rescale (k-block boundary) applied per accumulator
-  // just before its MFMA.
+  // fragments of step g_+1 read in between; at a k-block boundary each accumulator moves from
+  // the previous block's scale units to this block's (f = s_prev / s_this) before its MFMA.
   auto rot_stage = [&](int g_, int cb, bool rescale, const float (&f)[TM][2]) {
-#if MTX_F8_ROT
 #pragma unroll
     for (int j = 0; j < TN; ++j) fr_b[cb ^ 1][j] = rd_b(g_ + 1, j);
     // accumulator q = i*TN + j is rescaled (block boundary only) one slot ahead of its MFMA,
@@ -943,18 +913,14 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
       }
       fr_a[i] = rd_a(g_ + 1, i);
     }
-
-#endif
   };
-  (void)rot_stage;
 
   for (;;) {
-#if MTX_F8_ROT
     for (int kb = 0; kb < nkb; ++kb) {
       const int kt = 2 * kb;
       // even stage kt (ring step g): B fragments in set 0
       issue(g + PD, kt + PD, false);
-      float f[TM][2];
+      float f[TM][2] = {};
       if (kb > 0) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -978,70 +944,6 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
       __syncthreads();
       g += 2;
     }
-#else
-    for (int kb = 0; kb < nkb; ++kb) {
-      const int kt = 2 * kb;
-      // even stage kt (ring step g)
-      issue(g + PD, kt + PD, false);
-      read_frags(g + 1, 1);
-#if MTX_F8_LATE_RESCALE
-      if (kb > 0) {
-        // Accumulators move from block kb-1's scale units to block kb's just before their first
-        // MFMA of block kb: the multiplies of accumulator (i,j+1) overlap the MFMA of (i,j).
-        // Same product per element and same order as rescaling at the end of block kb-1.
-        float f[TM][2];
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) f[i][h] = (sa_c[i] * sb_c[h]) * __builtin_amdgcn_rcpf(sa_n[i] * sb_n[h]);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            const float fj = f[i][half_of(j)];
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] *= fj;
-            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[0][j], fa[0][i], acc[i][j], 0, 0, 0, 127,
-                                                                        0, 127);
-          }
-#pragma unroll
-        for (int i = 0; i < TM; ++i) sa_c[i] = sa_n[i];
-        sb_c[0] = sb_n[0];
-        sb_c[1] = sb_n[1];
-      } else {
-        mfmas(0);
-      }
-#else
-      mfmas(0);
-#endif
-      __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS));  // step g+2 landed (g+3 may be in flight)
-      __syncthreads();
-      // odd stage kt+1 (ring step g+1)
-      issue(g + 1 + PD, kt + 1 + PD, true);
-      read_frags(g + 2, 0);              // next block's first stage (or the next tile's)
-      read_scales(g + 2, sa_n, sb_n);    // and its scales
-      mfmas(1);
-#if !MTX_F8_LATE_RESCALE
-      if (kb + 1 < nkb) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            const float f = (sa_c[i] * sb_c[half_of(j)]) * __builtin_amdgcn_rcpf(sa_n[i] * sb_n[half_of(j)]);
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] *= f;
-          }
-#pragma unroll
-        for (int i = 0; i < TM; ++i) sa_c[i] = sa_n[i];
-        sb_c[0] = sb_n[0];
-        sb_c[1] = sb_n[1];
-      }
-#endif
-      __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));  // step g+3 landed (g+4 may be in flight)
-      __syncthreads();
-      g += 2;
-    }
-#endif
 
     // ---- epilogue of the current tile (the next tile's first stages are in flight) ---------
 #pragma unroll

@@ -649,14 +649,6 @@ __device__ __forceinline__ int bn_off(int k, int c) { return k * 512 + ((c ^ ((k
 
 typedef __attribute__((ext_vector_type(4))) short s16x4;
 typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
-#ifndef MTX_V3_SB
-#define MTX_V3_SB 0
-#endif
-#if MTX_V3_SB
-#define MTX_V3_SCHED_BARRIER() __builtin_amdgcn_sched_barrier(0)
-#else
-#define MTX_V3_SCHED_BARRIER() ((void)0)
-#endif
 
 #ifndef MTX_V3_WPE
 #define MTX_V3_WPE 2
@@ -937,7 +929,6 @@ __global__ __launch_bounds__(WM* WN * 64, MTX_V3_WPE) void gmm_v3_kernel(Args p)
       // substep 0: prefetch substep 1 of this stage
       read_frags(kt, 1, 1, nb);
       if (MODE == TGMM && tail < BKS && kt == nk - 1) mask_frags(0, 0, tail);
-      MTX_V3_SCHED_BARRIER();
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         if (!FULL && i >= nb) continue;
@@ -947,10 +938,8 @@ __global__ __launch_bounds__(WM* WN * 64, MTX_V3_WPE) void gmm_v3_kernel(Args p)
       // substep 1: prefetch substep 0 of the next stage (visible since the last barrier).  On
       // the last step this reads an unused ring slot: in bounds, and branch-free so that the
       // MFMAs below only wait for the fragments they use.
-      MTX_V3_SCHED_BARRIER();
       read_frags(kt + 1, 0, 0, nb);
       if (MODE == TGMM && tail < BKS && kt == nk - 1) mask_frags(1, 1, tail);
-      MTX_V3_SCHED_BARRIER();
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         if (!FULL && i >= nb) continue;
