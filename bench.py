@@ -112,7 +112,7 @@ def _zipf_bias(E, s, rng, beta=0.55):
     return (-beta * s * np.log(rank)).astype(np.float32)
 
 
-def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate"):
+def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_graph=False):
     import torch
 
     from mintext_amd import _lib
@@ -234,6 +234,21 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate"):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = start.elapsed_time(end) / steps
+    graph_ms = None
+    if use_graph:
+        # the same step captured once in a HIP graph and replayed: no per-kernel host launches
+        from mintext_amd.moe import CapturedLayer
+
+        cap = CapturedLayer(lambda: step(False))
+        for _ in range(warmup):
+            cap.replay()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(steps):
+            cap.replay()
+        end.record()
+        torch.cuda.synchronize()
+        graph_ms = start.elapsed_time(end) / steps
 
     gs_host = None
     with torch.no_grad():
@@ -285,6 +300,8 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate"):
                  "empty": int((gs_host == 0).sum())},
         "wall_s": round(wall, 3),
     }
+    if graph_ms is not None:
+        res["hip_graph"] = {"ms_per_step": round(graph_ms, 4), "tokens_per_s": round(T / (graph_ms * 1e-3), 1)}
     if cpu_baseline and cfg_name not in ("qwen3_bwd",):
         sh = None if shared is None else (shared[0][0].float().cpu().numpy(), shared[1][0].float().cpu().numpy())
         res["cpu_baseline"] = _cpu_baseline_layer(x.float().cpu().numpy(), logits.float().cpu().numpy(),
@@ -353,6 +370,8 @@ def main(argv=None):
                     help="deepseek: shared expert run as its own one-group GEMMs (default) or folded into the routed GEMMs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 plain 256 MiB device copies (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--graph", action="store_true",
+                    help="also time the step captured in a HIP graph and replayed (reported as hip_graph)")
     ap.add_argument("--study", choices=["gemm-power"], default=None,
                     help="gemm-power: GEMM timings on normal vs all-zero data (clock / issue-efficiency study)")
     a = ap.parse_args(argv)
@@ -374,7 +393,8 @@ def main(argv=None):
         print("bench.py measures one GPU only: this build has no multi-GPU path (no expert parallelism or "
               "collectives); run with --gpus 1", file=sys.stderr)
         return 2
-    res = run(a.config, a.steps, a.warmup, cpu_baseline=not a.no_cpu_baseline, shared_mode=a.shared)
+    res = run(a.config, a.steps, a.warmup, cpu_baseline=not a.no_cpu_baseline, shared_mode=a.shared,
+              use_graph=a.graph)
     print(json.dumps(res))
     return 0
 

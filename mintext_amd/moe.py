@@ -128,3 +128,30 @@ def moe_experts_forward_fp8(x: torch.Tensor, topk_indices: torch.Tensor, topk_we
     yq, ys = grouped_matmul_fp8_swiglu(sq, ss, gate_up_q, gate_up_scale, group_sizes)
     out = grouped_matmul_fp8(yq, ys, down_q, down_scale, group_sizes)
     return unroute(out, sort_indices, topk_weights, topk_indices.shape[1])
+
+
+class CapturedLayer:
+    """A MoE layer forward captured once in a HIP graph and replayed (for serving loops and
+    launch-bound shapes, where per-kernel host launches dominate).
+
+    ``fn(*inputs)`` must return a tensor or a tuple of tensors and run only device work (every
+    entry point of this package does: no host synchronisation, no allocation in the C-ABI, no
+    memset nodes).  ``inputs`` are the static input tensors: refill them in place (``copy_``)
+    between replays.  ``replay()`` returns the static outputs, overwritten by each replay.
+    """
+
+    def __init__(self, fn, *inputs, warmup: int = 2):
+        self.inputs = inputs
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side), torch.no_grad():
+            for _ in range(warmup):  # allocator and library state settle outside the capture
+                fn(*inputs)
+        torch.cuda.current_stream().wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph), torch.no_grad():
+            self.outputs = fn(*inputs)
+
+    def replay(self):
+        self.graph.replay()
+        return self.outputs
