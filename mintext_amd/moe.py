@@ -106,6 +106,30 @@ def moe_layer_forward(logits: torch.Tensor, x: torch.Tensor, gate_up: torch.Tens
     return out, idx, w
 
 
+def moe_block_forward(x: torch.Tensor, gate_weight: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, *,
+                      k: int, scoring: str = "sigmoid_group", bias: torch.Tensor | None = None, n_group: int = 1,
+                      topk_group: int = 1, norm_topk_prob: bool = True, routed_scaling_factor: float = 1.0,
+                      shared_gate_up: torch.Tensor | None = None, shared_down: torch.Tensor | None = None,
+                      shared_folded: bool = False):
+    """``MoEBlock.__call__`` (mintext/modules/moe.py:240-266) on [B, S, D] or [N, D] tokens.
+
+    The router gate is ``Linear.__call__`` (mintext/modules/linear.py:123-147): a plain dense
+    GEMM ``x @ gate_weight`` ([D, E], the reference's kernel layout) in the compute dtype, f32
+    accumulation and one rounding to the compute dtype -- served by hipBLASLt through
+    ``torch.matmul``; everything after the logits runs on this package's kernels.  Returns
+    ``(output [.., D] float32, {"topk_indices", "topk_weights", "expert_counts"})``, the
+    reference's aux data plus the counts of trainer.py:297-308.
+    """
+    shape = x.shape
+    xf = x.reshape(-1, shape[-1])
+    logits = torch.matmul(xf, gate_weight.to(xf.dtype))
+    out, idx, w, counts = moe_layer_forward(
+        logits, xf, gate_up, down, k=k, scoring=scoring, bias=bias, n_group=n_group, topk_group=topk_group,
+        norm_topk_prob=norm_topk_prob, routed_scaling_factor=routed_scaling_factor, shared_gate_up=shared_gate_up,
+        shared_down=shared_down, shared_folded=shared_folded, return_expert_counts=True)
+    return out.reshape(*shape[:-1], out.shape[-1]), {"topk_indices": idx, "topk_weights": w, "expert_counts": counts}
+
+
 def shared_expert_forward(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor) -> torch.Tensor:
     """Dense SwiGLU MLP (mintext/modules/linear.py:164-228 as used at moe.py:231-236) as a
     one-group grouped GEMM: gate_up [D, 2I] or [1, D, 2I], down [I, D] or [1, I, D]."""

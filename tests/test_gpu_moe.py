@@ -204,3 +204,35 @@ def test_folded_shared_expert_mfma_shapes(dev):
     f = lambda a: a.float().cpu().numpy()
     ref = O.moe_block(f(x), idx.cpu().numpy(), w.cpu().numpy(), f(gu), f(dn), f(sgu), f(sdn))
     assert rel_err(out_f.double().cpu().numpy(), ref) < 2e-2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_moe_block_forward_with_gate(dev, dtype):
+    # MoEBlock.__call__ from the tokens: hipBLASLt gate GEMM, then the HIP path; against the
+    # HF DeepseekV3MoE fixture (the gate is the identity-free Linear x @ Wg)
+    from mintext_amd.moe import moe_block_forward
+
+    p = _block_inputs()
+    g = golden("moe_block_shared")
+    cdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(cdt)
+    x = t(p["x"]).reshape(2, p["T"] // 2, p["D"])
+    out, aux = moe_block_forward(x, t(p["wg"]), t(p["gate_up"]), t(p["down"]), k=p["K"], scoring="sigmoid_group",
+                                 bias=torch.from_numpy(p["bias"]).to(dev), n_group=p["n_group"],
+                                 topk_group=p["topk_group"], routed_scaling_factor=p["scale"],
+                                 shared_gate_up=t(p["shared_gate_up"]), shared_down=t(p["shared_down"]))
+    assert out.shape == (2, p["T"] // 2, p["D"]) and out.dtype == torch.float32
+    idx = aux["topk_indices"].cpu().numpy()
+    assert np.array_equal(aux["expert_counts"].cpu().numpy(), np.bincount(idx.ravel(), minlength=p["E"]))
+    if dtype == "f32":
+        # f32 logits: the same expert sets as HF's router
+        for r in range(p["T"]):
+            assert set(idx[r].tolist()) == set(g["idx"][r].tolist())
+        assert rel_err(out.reshape(p["T"], p["D"]).double().cpu().numpy(), g["out"]) < 1e-5
+    else:
+        # bf16 logits may flip near-ties: check against the oracle block on the GPU's own routing
+        f = lambda a: a.float().cpu().numpy()
+        ref = O.moe_block(f(t(p["x"])), idx, aux["topk_weights"].cpu().numpy(), f(t(p["gate_up"])), f(t(p["down"])),
+                          f(t(p["shared_gate_up"])), f(t(p["shared_down"])))
+        assert rel_err(out.reshape(p["T"], p["D"]).double().cpu().numpy(), ref) < 2e-2
