@@ -144,7 +144,14 @@ int mtx_unroute_bwd(const void* dout, int g_dtype, const void* sorted_output, in
 /* ---- grouped GEMM ----------------------------------------------------------------------
  * Rows of x are grouped contiguously in group_sizes order (a device array that is never
  * read on the host).  Rows past sum(group_sizes) produce zeros.  F32 (exact fp32 FMA) or
- * BF16 (MFMA, f32 accumulate, one rounding).  Output dtype = input dtype.              */
+ * BF16 (MFMA, f32 accumulate, one rounding).  Output dtype = input dtype.
+ * The workspace holds the per-call tile lists and (64 MB) the f32 partial tiles of the
+ * split tail: on the 256-row bf16 path, when an XCD's last round of output tiles is at most
+ * half full, those tiles are split along the reduction into 2-4 pieces that run on the idle
+ * CUs; the last piece to finish adds the pieces in piece order.  Results are deterministic;
+ * a split tile's f32 sum is associated differently from a whole tile's, so outputs can differ
+ * from the unsplit schedule by a bf16 rounding.  A workspace smaller than the size returned
+ * here (but large enough for the tile lists) runs every tile whole.                      */
 int64_t mtx_gmm_workspace_size(int64_t M, int64_t E);
 /* out[r,:] = x[r,:] @ w[g(r)]       x [M,Kin], w [E,Kin,Kout] -> out [M,Kout]          */
 int mtx_gmm(const void* x, const void* w, const int32_t* group_sizes, int dtype,
@@ -169,7 +176,8 @@ int mtx_tgmm(const void* x, const void* g, const int32_t* group_sizes, int dtype
  * MTX_GMM_OP_DLHS (x = g [M,Kout], out = dx [M,Kin]).  tile_m: 0 (shape heuristic), 128 or 256
  * rows per m-tile of the bf16 MFMA path; tile_group: 0 (heuristic) or 1..64 m-tiles per
  * scheduling group.  The f32 path and shapes outside the MFMA tiling ignore both.  Every
- * configuration gives the same output bits.                                             */
+ * configuration computes the same f32 sums; they agree bit for bit unless the split tail
+ * (mtx_gmm_workspace_size) splits different tiles, and then to a bf16 rounding.          */
 #define MTX_GMM_OP_FWD    0
 #define MTX_GMM_OP_SWIGLU 1
 #define MTX_GMM_OP_DLHS   2

@@ -41,16 +41,36 @@ struct GmmWs {
   int* offsets;
   int* order;
   MTile* tiles;
+  int* split_cnt;     // arrival counters of split tiles (zeroed by build_tiles_kernel)
+  float* split_part;  // fp32 partial tiles of split pieces
 };
+// Split tail (256x256 store tiles, FWD/DLHS).  Workgroup pid is dispatched to XCD pid % 8 and
+// each CU holds one 256-row workgroup, so an XCD runs its tiles in rounds of (CUs per XCD).
+// When the last round holds at most half as many tiles as CUs (rem <= kSplitMaxRem), those rem
+// tiles are split along K into S = min(kSplitMaxS, CUs / rem) pieces, dispatched after the
+// whole tiles; each piece stores an f32 partial tile, and the piece that arrives last (per-tile
+// counter) sums the partials in piece order and runs the epilogue.  No workgroup waits on
+// another, and the sum does not depend on arrival order.  The dispatch assumption only
+// affects speed: any placement gives the same result.  At most kSplitItems pieces per XCD.
+constexpr int kSplitXcd = 8, kSplitItems = 32, kSplitMaxRem = 16, kSplitMaxS = 4;
+constexpr int64_t kSplitSlotFloats = 256 * 256;
 static inline int64_t gmm_ws_tiles_off(int64_t E) { return round_up((int64_t)(48 + 2 * E + 1) * 4, 256); }
 static inline int64_t gmm_max_tiles(int64_t M, int64_t E, int64_t BM) { return ceil_div(M, BM) + E + 1; }
-static inline GmmWs gmm_ws(void* ws, int64_t E) {
+static inline int64_t gmm_ws_split_off(int64_t M, int64_t E) {
+  return round_up(gmm_ws_tiles_off(E) + gmm_max_tiles(M, E, 64) * (int64_t)sizeof(MTile), 256);
+}
+static inline int64_t gmm_ws_split_bytes() {
+  return 1024 + (int64_t)kSplitXcd * kSplitItems * kSplitSlotFloats * 4;
+}
+static inline GmmWs gmm_ws(void* ws, int64_t M, int64_t E) {
   GmmWs w;
   int* b = (int*)ws;
   w.count = b;
   w.offsets = b + 16;
   w.order = b + 32 + E + 1;
   w.tiles = (MTile*)((char*)ws + gmm_ws_tiles_off(E));
+  w.split_cnt = (int*)((char*)ws + gmm_ws_split_off(M, E));
+  w.split_part = (float*)((char*)w.split_cnt + 1024);
   return w;
 }
 
@@ -58,8 +78,9 @@ static inline GmmWs gmm_ws(void* ws, int64_t E) {
 __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __restrict__ gs, int E, int M, int BM,
                                                            int* __restrict__ count, int* __restrict__ offsets,
                                                            int* __restrict__ order, MTile* __restrict__ tiles,
-                                                           int need_order) {
+                                                           int need_order, int* __restrict__ split_cnt) {
   __shared__ int wsum[16];
+  if (split_cnt && threadIdx.x < kSplitXcd * kSplitMaxRem) split_cnt[threadIdx.x] = 0;
   __shared__ int s_gs[1024];
   __shared__ int s_total[2];
   const int e = threadIdx.x, lane = e & 63, w = e >> 6;
@@ -363,6 +384,10 @@ struct Args {
   int I;       // SwiGLU intermediate size
   int E;
   int gm;      // m-tiles per scheduling group (consecutive tiles sweep gm m-tiles, then n)
+  int* split_cnt = nullptr;     // split tail (FWD/DLHS store tiles): arrival counters
+  float* split_part = nullptr;  //   fp32 partials, kSplitItems slots of BM x BN per XCD
+  int split_on = 0;             //   0: every tile runs whole
+  int ncu_x = 32;               //   CUs per XCD (one resident 256-row workgroup per CU)
 };
 
 // ---- tile loaders ------------------------------------------------------------------------------
@@ -672,6 +697,7 @@ __global__ __launch_bounds__(WM* WN * 64, MTX_V3_WPE) void gmm_v3_kernel(Args p)
   constexpr bool A_T = (MODE == TGMM);                 // A tile stored [reduction][row] (transpose reads)
   constexpr bool B_T = (MODE == FWD || MODE == TGMM);  // B tile stored [reduction][col]
   __shared__ __attribute__((aligned(1024))) char lds[NSTAGE * STAGE];
+  __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -681,6 +707,7 @@ __global__ __launch_bounds__(WM* WN * 64, MTX_V3_WPE) void gmm_v3_kernel(Args p)
   // x and g (expert e's group), output block dW[e][row0:+BM][col0:+BN]; experts are visited
   // in descending group size so that the longest reductions start first.
   int e, r0, r1, col0, n_tile, row0 = 0;
+  int piece = 0, npieces = 1, split_u = 0;  // k-piece of a split tail tile (1 piece: whole tile)
   if constexpr (MODE == TGMM) {
     const int ntiles = p.N / BN, per_e = (p.Kd / BM) * ntiles;
     const int lid = blockIdx.x;
@@ -706,9 +733,31 @@ __global__ __launch_bounds__(WM* WN * 64, MTX_V3_WPE) void gmm_v3_kernel(Args p)
     const int total = cnt * nn;
     const int pid = blockIdx.x;
     const int total8 = (total + 7) & ~7;
-    if (pid >= total8) return;
-    const int lid = (pid & 7) * (total8 >> 3) + (pid >> 3);
-    if (lid >= total) return;
+    const int xcd = pid & 7, q = pid >> 3, per = total8 >> 3;
+    int lid;
+    if (EPI == EPI_STORE && BM == 256 && MODE != TGMM && p.split_on) {
+      // XCD xcd runs tiles [xcd*per, xcd*per + tx) in dispatch order q; when its last round is
+      // at most half full (rem tiles on ncu_x CUs), those rem tiles are split along K into S
+      // pieces, dispatched after the whole tiles
+      const int tx = max(0, min(per, total - xcd * per));
+      const int rem = tx % p.ncu_x;
+      int S = (rem > 0 && rem <= kSplitMaxRem && 2 * rem <= p.ncu_x) ? min(kSplitMaxS, p.ncu_x / rem) : 1;
+      S = min(S, max(p.Kred / BKS, 1));
+      const int nwhole = (S > 1) ? tx - rem : tx;
+      if (q >= nwhole + (S > 1 ? rem * S : 0)) return;
+      if (q < nwhole) {
+        lid = xcd * per + q;
+      } else {
+        split_u = (q - nwhole) / S;
+        piece = (q - nwhole) % S;
+        npieces = S;
+        lid = xcd * per + nwhole + split_u;
+      }
+    } else {
+      if (pid >= total8) return;
+      lid = xcd * per + q;
+      if (lid >= total) return;
+    }
     const int GM = p.gm;
     const int grp = lid / (GM * nn);
     const int first_m = grp * GM;
@@ -722,6 +771,7 @@ __global__ __launch_bounds__(WM* WN * 64, MTX_V3_WPE) void gmm_v3_kernel(Args p)
     r1 = t.r1;
     col0 = n_tile * BN;
     if (e < 0) {
+      if (piece > 0) return;
       const int ncols = (EPI == EPI_SWIGLU) ? BN / 2 : BN;
       const int c0 = (EPI == EPI_SWIGLU) ? n_tile * (BN / 2) : col0;
       for (int i = tid; i < BM * ncols; i += NT) {
@@ -732,7 +782,10 @@ __global__ __launch_bounds__(WM* WN * 64, MTX_V3_WPE) void gmm_v3_kernel(Args p)
     }
   }
 
-  const int nk = (MODE == TGMM) ? (r1 - r0 + BKS - 1) / BKS : p.Kred / BKS;
+  // k-stages [kb0, kb0 + nk) of this workgroup (piece of npieces; the whole range when 1)
+  const int nk_all = (MODE == TGMM) ? (r1 - r0 + BKS - 1) / BKS : p.Kred / BKS;
+  const int kb0 = piece * nk_all / npieces;
+  const int nk = (piece + 1) * nk_all / npieces - kb0;
   const int tail = (MODE == TGMM) ? (r1 - r0) - (nk - 1) * BKS : BKS;  // rows in the last step
 
   // ---- per-lane global sources of the load instructions (byte offsets at k-step 0) -----
@@ -797,7 +850,7 @@ __global__ __launch_bounds__(WM* WN * 64, MTX_V3_WPE) void gmm_v3_kernel(Args p)
   // read, which keeps the main loop free of branches.
   auto issue_stage = [&](int kt_) {
     const uint32_t st = lds_base + (uint32_t)(C::slot(kt_) * STAGE);
-    const int kt = min(kt_, nk - 1);
+    const int kt = kb0 + min(kt_, nk - 1);
     if constexpr (MODE == TGMM) {
 #pragma unroll
       for (int i = 0; i < A_INSTR; ++i) {
@@ -957,6 +1010,49 @@ __global__ __launch_bounds__(WM* WN * 64, MTX_V3_WPE) void gmm_v3_kernel(Args p)
   else main_loop(std::integral_constant<bool, false>());
   __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));  // no ring load may land after the workgroup ends
 
+  if (npieces > 1) {
+    // Split tail piece: publish the fp32 partial tile; the piece that arrives last (by the
+    // tile's counter) reloads every piece and adds them in piece order -- the same sum
+    // whatever the arrival order -- then runs the epilogue.  Nothing waits on another
+    // workgroup.  A lane's partial is float4 chunks, one coalesced 1 KB row per wave store.
+    static_assert(BM * BN <= kSplitSlotFloats, "split slot");
+    typedef __attribute__((ext_vector_type(4))) float f32x4;
+    constexpr int64_t SLOT4 = kSplitSlotFloats / 4;
+    const int xcd_e = (int)(blockIdx.x & 7);
+    f32x4* part = (f32x4*)(p.split_part + (int64_t)(xcd_e * kSplitItems + split_u * npieces) * kSplitSlotFloats);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          part[piece * SLOT4 + ((i * TN + j) * 4 + g) * NT + tid] =
+              f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(p.split_cnt + xcd_e * kSplitMaxRem + split_u, 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == npieces - 1;
+    __syncthreads();
+    if (!s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+#pragma unroll
+    for (int s2 = 0; s2 < kSplitMaxS; ++s2) {  // unrolled: each piece's loads issue together
+      if (s2 >= npieces) break;
+      const f32x4* src = part + s2 * SLOT4;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const f32x4 v = src[((i * TN + j) * 4 + g) * NT + tid];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[i][j][4 * g + c] = (s2 == 0) ? v[c] : acc[i][j][4 * g + c] + v[c];
+          }
+    }
+  }
+
   // ---- epilogue: the MFMAs computed C^T blocks (operands swapped), so acc[i][j][4g+q] of lane
   // l is C[row i*32 + l%32][col j*32 + 8g + 4(l/32) + q]: four consecutive columns per lane.
   // The tile is staged in the (now idle) ring as packed bf16 rows, 16-byte chunk c of row r at
@@ -1032,10 +1128,23 @@ struct MfmaCfg {
 };
 
 static int launch_build_tiles(const int32_t* gs, int64_t E, int64_t M, int BM, const GmmWs& w, hipStream_t st,
-                              bool need_order = false) {
+                              bool need_order = false, bool reset_split = false) {
   hipLaunchKernelGGL(build_tiles_kernel, dim3(1), dim3(1024), 0, st, gs, (int)E, (int)M, BM, w.count, w.offsets,
-                     w.order, w.tiles, need_order ? 1 : 0);
+                     w.order, w.tiles, need_order ? 1 : 0, reset_split ? w.split_cnt : (int*)nullptr);
   return check_launch();
+}
+
+// CUs per XCD of the current device (one resident 256-row workgroup per CU), cached per device.
+static int cus_per_xcd() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev] = n / kSplitXcd;
+  }
+  return cache[dev];
 }
 
 // v3 configurations: 256x256 tiles with 8 waves (128x64 wave tiles) and a 4-deep ring (one
@@ -1103,7 +1212,7 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
   if (Kred < 0 || Nout < 0 || Kred > INT32_MAX / 2 || Nout > INT32_MAX / 2) return MTX_ERR_ARG;
   if (M == 0 || Nout == 0) return MTX_OK;
   if (!x || !w || !gs || !out) return MTX_ERR_ARG;
-  GmmWs wsp = gmm_ws(ws, E);
+  GmmWs wsp = gmm_ws(ws, M, E);
   const int64_t out_cols = (mode == 2) ? I : Nout;
   if (mode == 2 && Nout != 2 * I) return MTX_ERR_ARG;
   // bf16 MFMA eligibility
@@ -1146,9 +1255,20 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
     }
     if (mode != 2 && Nout % 256 == 0) {
       if (big_m) {
-        rc = launch_build_tiles(gs, E, M, 256, wsp, st);
+        // split tail when the workspace carries the partials region (mtx_gmm_workspace_size)
+        const int ncu = cus_per_xcd();
+        const bool split = ws_bytes >= gmm_ws_split_off(M, E) + gmm_ws_split_bytes() && ncu >= 2 &&
+                           ncu <= kSplitItems;
+        if (split) {
+          a.split_on = 1;
+          a.split_cnt = wsp.split_cnt;
+          a.split_part = wsp.split_part;
+          a.ncu_x = ncu;
+        }
+        rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, split);
         if (rc) return rc;
-        const int64_t grid = gmm_max_tiles(M, E, 256) * (Nout / 256);
+        // split pieces add at most ncu - rem < ncu workgroups per XCD
+        const int64_t grid = round_up(gmm_max_tiles(M, E, 256) * (Nout / 256), 8) + (split ? 8 * (int64_t)ncu : 0);
         return mode == 0 ? launch_v3<mf::FWD, mf::EPI_STORE>(a, grid, st) : launch_v3<mf::DLHS, mf::EPI_STORE>(a, grid, st);
       }
       rc = launch_build_tiles(gs, E, M, 128, wsp, st);
@@ -1206,9 +1326,12 @@ static int launch_swiglu(const void* h, int dtype, int64_t M, int64_t I, void* o
 
 using namespace mtx;
 
+// Tile lists, then the split-tail region (counters + fp32 partial tiles).  A workspace of at
+// least the tile-list part (common_checks) is accepted; the split tail runs only with the full
+// size returned here.
 extern "C" int64_t mtx_gmm_workspace_size(int64_t M, int64_t E) {
   if (M < 0 || E < 1) return -1;
-  return gmm_ws_tiles_off(E) + gmm_max_tiles(M, E, kMinBM) * (int64_t)sizeof(MTile);
+  return gmm_ws_split_off(M, E) + gmm_ws_split_bytes();
 }
 
 extern "C" int mtx_gmm(const void* x, const void* w, const int32_t* group_sizes, int dtype, int64_t M, int64_t Kin,
@@ -1271,7 +1394,7 @@ extern "C" int mtx_tgmm(const void* x, const void* g, const int32_t* group_sizes
   if (K == 0 || N == 0) return MTX_OK;
   if (!dw || !group_sizes || (M > 0 && (!x || !g))) return MTX_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
-  GmmWs wsp = gmm_ws(workspace, E);
+  GmmWs wsp = gmm_ws(workspace, M, E);
   rc = launch_build_tiles(group_sizes, E, M, kMinBM, wsp, st, true);
   if (rc) return rc;
   const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)g % 16 == 0);

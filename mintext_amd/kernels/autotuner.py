@@ -10,8 +10,9 @@ space is the HIP kernels' own tile configuration instead of TPU ``ragged_dot`` t
 * ``tn`` -- columns per n-tile, always 256 (the MFMA kernels' only width).
 
 A tiling is the tuple ``(tm, tg, tn)``; ``grouped_matmul(..., tiling=...)`` and
-``grouped_matmul_vjp`` take it directly.  No tiling changes the output bits, so tuning only
-trades time.  Candidates are timed with HIP events on the current stream.
+``grouped_matmul_vjp`` take it directly.  Every tiling computes the same f32 sums (outputs
+agree to a bf16 rounding, bit for bit where the kernels' split tail splits the same tiles),
+so tuning only trades time.  Candidates are timed with HIP events on the current stream.
 
 Reference: ``MoETuningConfig`` / ``MoETuningResult`` (autotuner.py:18-36), ``_cache_key``
 (:39-55), ``_load_cache`` / ``_save_cache`` (:58-86), ``_generate_candidates`` (:89-104),

@@ -119,9 +119,21 @@ def _groups(rng, M, E, skew=False):
     return g.astype(np.int32)
 
 
+def _same_sums(got, ref, tag):
+    """Same f32 sums up to summation order, each rounded once to bf16: tile configurations
+    whose 256-row schedule splits tail tiles along K add the k-pieces in another order, so
+    outputs agree to a bf16 rounding (plus the f32 error where a sum cancels), not bit for bit.
+    Each configuration is deterministic."""
+    import torch
+
+    d = (got.float() - ref.float()).abs()
+    bound = ref.float().abs() * 2.0 ** -7 + 1e-4 * ref.float().abs().max()
+    assert (d <= bound).all(), (tag, (d - bound).max().item())
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("skew", [False, True])
-def test_every_tiling_gives_the_same_bits(dev, skew):
+def test_every_tiling_gives_the_same_sums(dev, skew):
     import torch
 
     from mintext_amd.kernels.grouped_matmul import (_gmm_dlhs, grouped_matmul, grouped_matmul_swiglu)
@@ -137,9 +149,10 @@ def test_every_tiling_gives_the_same_bits(dev, skew):
     ref_d = _gmm_dlhs(g, w, gs)
     cands = _generate_candidates(M, K, N, E) + [(128, 64, 256), (256, 64, 256)]
     for t in cands:
-        assert torch.equal(grouped_matmul(x, w, gs, tiling=t), ref_f), t
-        assert torch.equal(grouped_matmul_swiglu(x, w, gs, tiling=t), ref_s), t
-        assert torch.equal(_gmm_dlhs(g, w, gs, t), ref_d), t
+        for got, ref in ((grouped_matmul(x, w, gs, tiling=t), ref_f),
+                         (grouped_matmul_swiglu(x, w, gs, tiling=t), ref_s), (_gmm_dlhs(g, w, gs, t), ref_d)):
+            _same_sums(got, ref, t)
+        assert torch.equal(grouped_matmul(x, w, gs, tiling=t), grouped_matmul(x, w, gs, tiling=t)), t
     # and the heuristic result is the grouped product (bf16 tolerance vs float64)
     xs, ws_, fs = x.double().cpu().numpy(), w.double().cpu().numpy(), ref_f.double().cpu().numpy()
     off = np.concatenate([[0], np.cumsum(gs.cpu().numpy())])
@@ -170,8 +183,9 @@ def test_grouped_matmul_vjp_with_tiling_matches_default(dev):
         y.float().square().sum().backward()
         outs.append((y.detach(), x.grad, w.grad))
     for other in outs[1:]:
-        for a, b in zip(outs[0], other):
-            assert torch.equal(a, b)
+        _same_sums(other[0], outs[0][0], "y")
+        for a, b in zip(outs[0][1:], other[1:]):  # gradients of a loss of y: relative norm
+            assert (torch.linalg.vector_norm((a - b).float()) / torch.linalg.vector_norm(b.float())).item() < 2e-3
 
 
 @pytest.mark.gpu

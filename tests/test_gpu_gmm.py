@@ -263,3 +263,62 @@ def test_tgmm_bf16_sampled_qwen3_shape(dev):
             assert (got == 0).all()
         else:
             _close(got, ref, 2e-2)
+
+
+# --------------------------------------------------------------- split tail (256-row tiles)
+SPLIT_SHAPES = [
+    # (group sizes, Kin, Kout): per-XCD tile counts whose last round is sparse, so the tail
+    # tiles run as k-pieces: 8 x 2080 rows, 1 n-tile -> 9 tiles per XCD, each in 3 pieces;
+    # 4 groups of ~9.5k rows (one empty), 2 n-tiles -> 37 tiles per XCD, the last 5 in 4 pieces
+    ([2080] * 8, 1024, 256),
+    ([9472, 0, 9500, 9444 + 9472], 256, 512),
+    ([300, 5, 257, 0, 1], 2048, 256),
+]
+
+
+@pytest.mark.parametrize("op", ["fwd", "dlhs"])
+@pytest.mark.parametrize("gs,Kin,Kout", SPLIT_SHAPES)
+def test_gmm_split_tail_matches_whole_tiles(dev, gs, Kin, Kout, op):
+    """The split tail (full workspace) against whole tiles (workspace without the partials
+    region) and the float64 oracle: same values to bf16 rounding, deterministic bits."""
+    from mintext_amd import _lib as L
+
+    rng = np.random.default_rng(len(gs) + Kin)
+    gs = np.asarray(gs, np.int32)
+    M, E = int(gs.sum()) + 7, len(gs)  # 7 rows past the groups -> zeros
+    if op == "fwd":
+        x = rng.standard_normal((M, Kin)).astype(np.float32)
+        w = (rng.standard_normal((E, Kin, Kout)) * 0.05).astype(np.float32)
+        n_red, n_out = Kin, Kout
+    else:  # dx = g @ w^T: the reduction runs over Kout
+        x = rng.standard_normal((M, Kout)).astype(np.float32)
+        w = (rng.standard_normal((E, Kin, Kout)) * 0.05).astype(np.float32)
+        n_red, n_out = Kout, Kin
+    xb, wb = _t(x, dev, torch.bfloat16), _t(w, dev, torch.bfloat16)
+    g = _t(gs, dev)
+    full = L.query("mtx_gmm_workspace_size", M, E)
+    st = L.stream(dev)
+    name = "mtx_gmm" if op == "fwd" else "mtx_gmm_dlhs"
+
+    def run(ws_bytes):
+        ws = L.workspace(full, dev)
+        out = torch.full((M, n_out), float("nan"), dtype=torch.bfloat16, device=dev)
+        L.call(name, xb.data_ptr(), wb.data_ptr(), g.data_ptr(), L.dtype_code(torch.bfloat16), M, Kin, Kout, E,
+               out.data_ptr(), ws.data_ptr(), ws_bytes, st)
+        torch.cuda.synchronize()
+        return out
+
+    split, split2 = run(full), run(full)
+    whole = run(full - (64 << 20))  # tile lists only: every tile runs whole
+    assert torch.equal(split, split2)
+    xf, wf = xb.float().cpu().numpy(), wb.float().cpu().numpy()
+    ref = O.gmm(xf, wf, gs) if op == "fwd" else O.gmm_dlhs(xf, wf, gs)
+    assert ref.shape == (M, n_out) and n_red > 0
+    for out in (split, whole):
+        assert (out[int(gs.sum()):] == 0).all()
+        _close(out.float().cpu().numpy(), ref, 2e-2)
+    # both round f32 sums of the same products, added in another order: a bf16 ulp apart at
+    # most, plus the f32 summation error where the sum cancels
+    d = (split.float() - whole.float()).abs()
+    bound = whole.float().abs() * 2.0 ** -7 + 1e-5 * float(np.abs(ref).max())
+    assert (d <= bound).all(), (d - bound).max().item()

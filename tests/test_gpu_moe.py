@@ -185,7 +185,9 @@ def test_expert_bias_update_matches_oracle(dev, E):
 
 @pytest.mark.gpu
 def test_folded_shared_expert_mfma_shapes(dev):
-    # shapes on the bf16 MFMA kernels (D, I multiples of 256 / 128): folded == separate, bit for bit
+    # shapes on the bf16 MFMA kernels (D, I multiples of 256 / 128): folded == separate up to the
+    # f32 summation order of split-K tail tiles (the two layouts split different tiles), i.e.
+    # within a bf16 rounding of each expert output
     from mintext_amd.moe import fold_shared_expert, moe_layer_forward
 
     rng = np.random.default_rng(3)
@@ -200,7 +202,9 @@ def test_folded_shared_expert_mfma_shapes(dev):
     out_s, idx, w = moe_layer_forward(lg, x, gu, dn, shared_gate_up=sgu, shared_down=sdn, **kw)
     gu_f, dn_f = fold_shared_expert(gu, dn, sgu, sdn)
     out_f, idx_f, w_f = moe_layer_forward(lg, x, gu_f, dn_f, shared_folded=True, **kw)
-    assert torch.equal(out_f, out_s)
+    assert torch.equal(idx_f, idx) and torch.equal(w_f, w)
+    scale = out_s.abs().max().item()
+    assert ((out_f - out_s).abs() <= 2.0 ** -7 * out_s.abs() + 2.0 ** -9 * scale).all()
     f = lambda a: a.float().cpu().numpy()
     ref = O.moe_block(f(x), idx.cpu().numpy(), w.cpu().numpy(), f(gu), f(dn), f(sgu), f(sdn))
     assert rel_err(out_f.double().cpu().numpy(), ref) < 2e-2
