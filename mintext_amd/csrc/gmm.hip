@@ -80,34 +80,36 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
                                                            int* __restrict__ order, MTile* __restrict__ tiles,
                                                            int need_order, int* __restrict__ split_cnt) {
   __shared__ int wsum[16];
+  __shared__ long long wsum64[16];
   if (split_cnt && threadIdx.x < kSplitXcd * kSplitMaxRem) split_cnt[threadIdx.x] = 0;
   __shared__ int s_gs[1024];
   __shared__ int s_total[2];
   const int e = threadIdx.x, lane = e & 63, w = e >> 6;
-  const int g = (e < E) ? max(gs[e], 0) : 0;
+  const int g = (e < E) ? min(max(gs[e], 0), M) : 0;  // rows past M are dropped
   s_gs[e] = g;
   // exclusive scan of g -> row offsets (64-bit safe: M < 2^31 is checked on the host)
-  int incl = g;
+  // row offsets in 64 bits: E groups of up to M rows each can sum past 2^31
+  long long incl64 = g;
   for (int off = 1; off < 64; off <<= 1) {
-    const int o = __shfl_up(incl, off);
-    if (lane >= off) incl += o;
+    const long long o = __shfl_up(incl64, off);
+    if (lane >= off) incl64 += o;
   }
-  if (lane == 63) wsum[w] = incl;
+  if (lane == 63) wsum64[w] = incl64;
   __syncthreads();
   if (e == 0) {
-    int run = 0;
-    for (int i = 0; i < 16; ++i) { const int x = wsum[i]; wsum[i] = run; run += x; }
-    s_total[0] = run;
+    long long run = 0;
+    for (int i = 0; i < 16; ++i) { const long long x = wsum64[i]; wsum64[i] = run; run += x; }
+    s_total[0] = (int)min(run, (long long)M);
   }
   __syncthreads();
-  const int start = incl - g + wsum[w];
-  const int r0 = min(start, M), r1 = min(start + g, M);
+  const long long start = incl64 - g + wsum64[w];
+  const int r0 = (int)min(start, (long long)M), r1 = (int)min(start + g, (long long)M);
   const int nt = (r1 - r0 + BM - 1) / BM;
   if (e < E) offsets[e] = r0;
   if (e == 0) offsets[E] = min(s_total[0], M);
   __syncthreads();
   // exclusive scan of tile counts
-  incl = nt;
+  int incl = nt;
   for (int off = 1; off < 64; off <<= 1) {
     const int o = __shfl_up(incl, off);
     if (lane >= off) incl += o;
@@ -132,13 +134,13 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
   // zero tiles for rows past sum(group_sizes)
   const int used = min(s_total[0], M);
   const int ntail = (M - used + BM - 1) / BM;
-  if (e < ntail) {
+  for (int z = e; z < ntail; z += blockDim.x) {  // may exceed the block when many rows are unused
     MTile t;
     t.e = -1;
-    t.r0 = used + e * BM;
-    t.r1 = min(used + (e + 1) * BM, M);
+    t.r0 = used + z * BM;
+    t.r1 = min(used + (z + 1) * BM, M);
     t.pad = 0;
-    tiles[s_total[1] + e] = t;
+    tiles[s_total[1] + z] = t;
   }
   if (e == 0) {
     count[0] = s_total[1] + ntail;

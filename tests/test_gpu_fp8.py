@@ -123,3 +123,19 @@ def test_gmm_fp8_rows_past_group_sum(dev, Kin):
     wq2, ws2 = quantize_fp8_weights(w2)
     yq, ys, yb = grouped_matmul_fp8_swiglu(xq, xs, wq2, ws2, _t(gs, dev), return_bf16=True)
     assert (yq[900:] == 0).all() and (yb[900:] == 0).all() and (ys[900:] == 1.0).all()
+
+
+def test_gmm_fp8_more_zero_tiles_than_threads(dev):
+    """Unused rows spanning more than 1024 zero tiles of 256 rows come out as zeros."""
+    from mintext_amd.kernels.fp8 import grouped_matmul_fp8, quantize_fp8_rows, quantize_fp8_weights
+
+    M, E, Kin, N = 270_000, 2, 256, 256
+    gs = np.array([300, 200], np.int32)
+    x = torch.randn(M, Kin, device=dev).bfloat16()
+    xq, xs = quantize_fp8_rows(x)
+    w = (torch.randn(E, Kin, N, device=dev) * 0.05).bfloat16()
+    wq, ws = quantize_fp8_weights(w)
+    out = grouped_matmul_fp8(xq, xs, wq, ws, _t(gs, dev))
+    assert (out[500:] == 0).all()
+    deq = O.gmm_fp8(_u8(xq)[:500], xs.cpu().numpy()[:500], _u8(wq), ws.cpu().numpy(), gs)
+    assert rel_err(out.float().cpu().numpy()[:500], deq) < 1e-2

@@ -322,3 +322,41 @@ def test_gmm_split_tail_matches_whole_tiles(dev, gs, Kin, Kout, op):
     d = (split.float() - whole.float()).abs()
     bound = whole.float().abs() * 2.0 ** -7 + 1e-5 * float(np.abs(ref).max())
     assert (d <= bound).all(), (d - bound).max().item()
+
+
+@pytest.mark.parametrize("dtype,M", [("bf16", 300_000), ("f32", 70_000)])
+def test_gmm_more_zero_tiles_than_threads(dev, dtype, M):
+    """Rows past sum(group_sizes) spanning more zero tiles than the tile builder's 1024 threads
+    (256-row tiles on the bf16 path, 64-row tiles on the f32 path) all come out as zeros."""
+    from mintext_amd.kernels import grouped_matmul, tgmm
+    from mintext_amd.kernels.grouped_matmul import _gmm_dlhs
+
+    cdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    gs = np.array([100, 0, 57], np.int32)
+    x = torch.randn(M, 64, device=dev).to(cdt)
+    w = (torch.randn(3, 64, 256, device=dev) * 0.1).to(cdt)
+    g = _t(gs, dev)
+    out = grouped_matmul(x, w, g)
+    assert (out[157:] == 0).all()
+    tol = 2e-2 if dtype == "bf16" else 1e-5
+    _close(out[:157].float().cpu().numpy(), O.gmm(x[:157].float().cpu().numpy(), w.float().cpu().numpy(), gs)[:157], tol)
+    dy = torch.randn(M, 256, device=dev).to(cdt)
+    dx = _gmm_dlhs(dy, w, g, None)
+    assert (dx[157:] == 0).all()
+    dw = tgmm(x, dy, g)
+    ref = O.tgmm(x[:157].float().cpu().numpy(), dy[:157].float().cpu().numpy(), gs)
+    _close(dw.float().cpu().numpy(), ref, tol)
+
+
+def test_gmm_group_sizes_past_m_are_clipped(dev):
+    """Group sizes summing past M (up to INT32_MAX) keep the first M rows: the oracle's
+    cumulative offsets clipped to M."""
+    from mintext_amd.kernels import grouped_matmul
+
+    M = 600
+    gs = np.array([2**31 - 1, 5, 7], np.int32)
+    for cdt, tol in ((torch.bfloat16, 2e-2), (torch.float32, 1e-5)):
+        x = torch.randn(M, 64, device=dev).to(cdt)
+        w = (torch.randn(3, 64, 256, device=dev) * 0.1).to(cdt)
+        out = grouped_matmul(x, w, _t(gs, dev))
+        _close(out.float().cpu().numpy(), O.gmm(x.float().cpu().numpy(), w.float().cpu().numpy(), gs), tol)
