@@ -118,6 +118,7 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
     from mintext_amd import _lib
     from mintext_amd.kernels import grouped_matmul_swiglu, grouped_matmul_vjp, route, route_topk, tgmm, unroute
     from mintext_amd.kernels.grouped_matmul import _gmm_dlhs
+    from mintext_amd.kernels.moe_dispatch import unroute_add
 
     _lib.lib()
     cfg = CONFIGS[cfg_name]
@@ -156,9 +157,8 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
     flops_fwd = 2.0 * Mg * D * 2 * I + 2.0 * Mg * I * D
     fp8 = cfg["dtype"] == "fp8"
     if fp8:
-        from mintext_amd.kernels.fp8 import (grouped_matmul_fp8, grouped_matmul_fp8_swiglu, quantize_fp8_rows,
-                                             quantize_fp8_weights)
-        from mintext_amd.kernels.moe_dispatch import route_with_scales
+        from mintext_amd.kernels.fp8 import grouped_matmul_fp8, grouped_matmul_fp8_swiglu, quantize_fp8_weights
+        from mintext_amd.kernels.moe_dispatch import route_quantize_fp8
 
         guq, gus = quantize_fp8_weights(gate_up)
         dnq, dns = quantize_fp8_weights(down)
@@ -169,8 +169,8 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
             if timed:
                 t_disp.start()
             if fp8:
-                xq, xs = quantize_fp8_rows(x)
-                sq, ss, si, gs, _ = route_with_scales(xq, xs, idx, E)
+                # 1x128 quantisation of the tokens fused into their dispatch
+                sq, ss, si, gs, _ = route_quantize_fp8(x, idx, E)
             else:
                 st, si, gs = route(x, idx, Eg)
             if timed:
@@ -186,14 +186,17 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
             o = grouped_matmul_fp8(yq, ys, dnq, dns, gs) if fp8 else grouped_matmul_vjp(y, down, gs)
             if timed:
                 t_dn.stop()
-                t_comb.start()
-            out = unroute(o, si, w, Kc)
-            if timed:
-                t_comb.stop()
+            sh_out = None
             if shared is not None and not fold:
                 from mintext_amd.moe import shared_expert_forward
 
-                out = out + shared_expert_forward(x, shared[0], shared[1]).float()
+                sh_out = shared_expert_forward(x, shared[0], shared[1])
+            if timed:
+                t_comb.start()
+            # combine; a separate shared expert's output is added in the same pass
+            out = unroute(o, si, w, Kc) if sh_out is None else unroute_add(o, si, w, Kc, sh_out)
+            if timed:
+                t_comb.stop()
             return out
 
     if cfg_name == "qwen3_bwd":
@@ -267,8 +270,14 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
         dominant = "gmm_fp8_swiglu (gate_up + SwiGLU + requant)" if fp8 else "gmm_swiglu (gate_up + fused SwiGLU)"
     tokens_per_s = T / (ms * 1e-3)
     gemm_ms = gu_ms + dn_ms
-    disp_b = T * D * (1 if fp8 else 2) + Mg * D * (1 if fp8 else 2) + T * Kc * 4 + Mg * 4 + Eg * 4
-    comb_b = Mg * D * 2 + T * Kc * 4 + Mg * 4 + T * D * 4
+    # dispatch: token rows read once (bf16; fp8 runs quantise them in the same pass), sorted rows
+    # written (fp8 codes + 1x128 f32 scales for fp8), indices; combine: expert rows, weights,
+    # permutation, f32 output (+ the bf16 shared-expert output when it is added in the pass)
+    xb = 4 if cfg["dtype"] == "f32" else 2  # bytes per element of the token rows and expert outputs
+    disp_b = T * D * xb + Mg * D * (1 if fp8 else xb) + T * Kc * 4 + Mg * 4 + Eg * 4
+    if fp8:
+        disp_b += Mg * (D // 128) * 4
+    comb_b = Mg * D * xb + T * Kc * 4 + Mg * 4 + T * D * 4 + (T * D * xb if shared is not None and not fold else 0)
     res = {
         "metric": "MoE layer fwd tokens/s + grouped-GEMM TFLOP/s (% of peak), 1x MI355X",
         "value": round(tokens_per_s, 1),

@@ -21,6 +21,7 @@
  *   mtx_invert_permutation <- jnp.argsort(sort_indices) (moe_dispatch.py:102)
  *   mtx_unroute            <- unroute (moe_dispatch.py:84-111); with topk_w == NULL it is
  *                             the route VJP (sum over the K copies, moe_dispatch.py:33-38,67)
+ *   mtx_unroute_add        <- unroute + `routed_out + shared_out` (mintext/modules/moe.py:256-258)
  *   mtx_unroute_bwd        <- VJP of unroute (_sort_bwd gather + einsum transpose,
  *                             moe_dispatch.py:33-38,102-111)
  *   mtx_gmm                <- grouped_matmul / _gmm_ragged_dot / _gmm_vjp_fwd
@@ -33,6 +34,7 @@
  *   mtx_swiglu_bwd         <- its autodiff VJP (taken by jax.grad through moe.py:195-196)
  *   mtx_quant_fp8_rows     <- no counterpart (per-tensor analogue: _fp8_matmul,
  *                             mintext/modules/linear.py:37-57); 1x128 activation groups
+ *   mtx_route_quant_fp8    <- quantise (no counterpart) + route (moe_dispatch.py:47-81) fused
  *   mtx_quant_fp8_weights  <- no counterpart; 128x128 weight blocks
  *   mtx_gmm_fp8            <- no counterpart; blockwise-fp8 form of mtx_gmm
  *   mtx_gmm_fp8_swiglu     <- no counterpart; blockwise-fp8 form of mtx_gmm_swiglu
@@ -135,6 +137,12 @@ int mtx_invert_permutation(const int32_t* perm, int64_t M, int32_t* inverse, voi
 int mtx_unroute(const void* sorted_output, int y_dtype, const int32_t* inverse,
                 const void* topk_w, int w_dtype, int64_t N, int64_t K, int64_t D,
                 void* out, int out_dtype, void* stream);
+/* mtx_unroute plus an [N,D] addend (F32/BF16), added in f32 after the k-sum:
+ * out = unroute(...) + addend -- `output = routed_out + shared_out` of MoEBlock.__call__
+ * (mintext/modules/moe.py:256-258) in the combine's pass (bit-identical to the two steps). */
+int mtx_unroute_add(const void* sorted_output, int y_dtype, const int32_t* inverse,
+                    const void* topk_w, int w_dtype, int64_t N, int64_t K, int64_t D,
+                    const void* addend, int add_dtype, void* out, int out_dtype, void* stream);
 /* VJP of mtx_unroute: d_sorted[inverse[n*K+k],:] = w[n,k] * dout[n,:]  (dtype y_dtype),
  * d_w[n,k] = sum_d dout[n,d] * sorted_output[inverse[n*K+k],d]  (dtype w_dtype; may be NULL). */
 int mtx_unroute_bwd(const void* dout, int g_dtype, const void* sorted_output, int y_dtype,
@@ -198,6 +206,15 @@ int mtx_swiglu_bwd(const void* h, const void* dy, int dtype, int64_t M, int64_t 
  * and xq 8-byte aligned (MTX_ERR_ARG otherwise).                                          */
 int mtx_quant_fp8_rows(const void* x, int dtype, int64_t M, int64_t D,
                        uint8_t* xq, float* x_scale, void* stream);
+/* mtx_quant_fp8_rows followed by mtx_route of the codes and scales, in one row pass: tokens
+ * [N,D] (F32/BF16, 16-byte aligned, D % 128 == 0) -> sorted_q [N*K,D] e4m3fn (8-byte aligned),
+ * sorted_scales [N*K,D/128] f32, sort_indices, group_sizes, inverse (may be NULL) exactly as
+ * the two calls produce them (route: mintext/kernels/moe_dispatch.py:47-81).  Workspace:
+ * mtx_route_workspace_size.                                                              */
+int mtx_route_quant_fp8(const void* tokens, int dtype, const int32_t* topk_idx, int64_t N,
+                        int64_t D, int64_t K, int64_t E, uint8_t* sorted_q, float* sorted_scales,
+                        int32_t* sort_indices, int32_t* group_sizes, int32_t* inverse,
+                        void* workspace, int64_t workspace_bytes, void* stream);
 /* w [E,Kin,Kout] (F32/BF16, reference layout) -> w_q [E,Kout,Kin], w_scale [E,Kout/128,Kin/128] */
 int mtx_quant_fp8_weights(const void* w, int dtype, int64_t E, int64_t Kin, int64_t Kout,
                           uint8_t* w_q, float* w_scale, void* stream);

@@ -47,6 +47,7 @@ SIGNATURES = {
     "mtx_scatter_rows": (_I, [_P, _I, _I64, _I64, _P, _P, _P]),
     "mtx_invert_permutation": (_I, [_P, _I64, _P, _P]),
     "mtx_unroute": (_I, [_P, _I, _P, _P, _I, _I64, _I64, _I64, _P, _I, _P]),
+    "mtx_unroute_add": (_I, [_P, _I, _P, _P, _I, _I64, _I64, _I64, _P, _I, _P, _I, _P]),
     "mtx_unroute_bwd": (_I, [_P, _I, _P, _I, _P, _P, _I, _I64, _I64, _I64, _P, _P, _P]),
     "mtx_gmm_workspace_size": (_I64, [_I64, _I64]),
     "mtx_gmm": (_I, [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
@@ -57,6 +58,7 @@ SIGNATURES = {
     "mtx_swiglu": (_I, [_P, _I, _I64, _I64, _P, _P]),
     "mtx_swiglu_bwd": (_I, [_P, _P, _I, _I64, _I64, _P, _P]),
     "mtx_quant_fp8_rows": (_I, [_P, _I, _I64, _I64, _P, _P, _P]),
+    "mtx_route_quant_fp8": (_I, [_P, _I, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "mtx_quant_fp8_weights": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _P]),
     "mtx_gmm_fp8": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "mtx_gmm_fp8_swiglu": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),

@@ -272,6 +272,75 @@ __global__ __launch_bounds__(256) void dispatch_rows_kernel(
   }
 }
 
+// Quantise-and-dispatch in token order: the 1x128 e4m3 quantiser of quant_rows_kernel (same
+// group maximum, scale = amax / 448 or 1 when the group is all zeros, codes of v / scale) fused
+// with the row dispatch, so each token row is read once in its compute dtype and only its fp8
+// codes and scales are written, to the token's K sorted positions inv[n*K+k].  A 128-group
+// spans LPG = 128 / EPL lanes (16 for bf16, 32 for f32); each lane loads UNR groups' 16-byte
+// slices before any store.
+template <typename T, int UNR>
+__global__ __launch_bounds__(256) void dispatch_quant_rows_kernel(const T* __restrict__ x, int64_t N, int64_t D,
+                                                                  const int32_t* __restrict__ inv, int K,
+                                                                  uint8_t* __restrict__ outq,
+                                                                  float* __restrict__ outs) {
+  constexpr int EPL = 16 / sizeof(T), LPG = 128 / EPL, GPW = 64 / LPG;
+  const int lane = threadIdx.x & 63;
+  const int sub = lane / LPG, gl = lane % LPG;
+  const int64_t ng = D / 128;
+  const int64_t total = N * ng;
+  const int64_t M = N * (int64_t)K;
+  const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t t0 = wid * GPW; t0 < total; t0 += nw * GPW * UNR) {
+    u32x4 raw[UNR];
+    int64_t tt[UNR];
+    bool ok[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int64_t t = t0 + (int64_t)u * nw * GPW + sub;
+      ok[u] = t < total;
+      tt[u] = ok[u] ? t : total - 1;
+      const int64_t r = tt[u] / ng, g = tt[u] - r * ng;
+      raw[u] = *(const u32x4*)(x + r * D + g * 128 + gl * EPL);
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      float v[EPL];
+      if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(raw[u][i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[2 * i] = __uint_as_float(raw[u][i] << 16);
+          v[2 * i + 1] = __uint_as_float(raw[u][i] & 0xffff0000u);
+        }
+      }
+      float m = 0.0f;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) m = fmaxf(m, fabsf(v[i]));
+#pragma unroll
+      for (int off = LPG / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+      float sc = m / 448.0f;
+      if (sc == 0.0f) sc = 1.0f;
+      uint32_t q[EPL / 4];
+#pragma unroll
+      for (int i = 0; i < EPL / 4; ++i)
+        q[i] = e4m3_pack4(v[4 * i] / sc, v[4 * i + 1] / sc, v[4 * i + 2] / sc, v[4 * i + 3] / sc);
+      if (!ok[u]) continue;
+      const int64_t r = tt[u] / ng, g = tt[u] - r * ng;
+      for (int k = 0; k < K; ++k) {
+        const int64_t j = inv[r * K + k];
+        if (j < 0 || j >= M) continue;
+        uint8_t* dst = outq + j * D + g * 128 + gl * EPL;
+        if constexpr (EPL == 8) *(uint2*)dst = make_uint2(q[0], q[1]);
+        else *(uint32_t*)dst = q[0];
+        if (gl == 0) outs[j * ng + g] = sc;
+      }
+    }
+  }
+}
+
 // out[index[j]] = src[j]
 template <typename VT>
 __global__ __launch_bounds__(256) void scatter_rows_kernel(
@@ -358,6 +427,25 @@ __device__ __forceinline__ void store8(uint16_t* p, const float* v) {
                           pack_bf16x2(v[6], v[7]));
 }
 
+// Optional [N, D] addend of the combine (F32 or BF16; p == nullptr: none), added in f32 after
+// the k-sum: out = sum_k w*Y + addend, the `routed_out + shared_out` of MoEBlock.__call__
+// (bzantium/mintext mintext/modules/moe.py:256-258) in one pass.
+struct Addend {
+  const void* p;
+  int dt;
+};
+__device__ __forceinline__ void add8(const Addend& a, int64_t off, float* acc) {
+  if (!a.p) return;
+  float v[8];
+  if (a.dt == MTX_BF16) load8((const uint16_t*)a.p + off, v);
+  else load8((const float*)a.p + off, v);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = acc[i] + v[i];
+}
+__device__ __forceinline__ float add1(const Addend& a, int64_t i, float acc) {
+  return a.p ? acc + load_as_f32(a.p, i, a.dt) : acc;
+}
+
 // One wave per token; VEC8 = D % 8 == 0 and aligned pointers.  With KMAX > 0 (K <= KMAX) the
 // token's K row indices and weights are read first and the K rows of each 512-element slice are
 // loaded together (K independent 16-byte loads in flight per lane) before they are summed in
@@ -365,7 +453,7 @@ __device__ __forceinline__ void store8(uint16_t* p, const float* v) {
 template <typename YT, typename WT, typename OT, bool VEC8, int KMAX>
 __global__ __launch_bounds__(256) void unroute_kernel(
     const YT* __restrict__ Y, const int32_t* __restrict__ inv, const WT* __restrict__ w,
-    int64_t N, int K, int64_t D, OT* __restrict__ out) {
+    int64_t N, int K, int64_t D, OT* __restrict__ out, Addend add) {
   const int lane = threadIdx.x & 63;
   const int64_t n = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   if (n >= N) return;
@@ -408,6 +496,7 @@ __global__ __launch_bounds__(256) void unroute_kernel(
 #pragma unroll
             for (int i = 0; i < 8; ++i) acc[i] = fmaf(ww[k], y[s][k][i], acc[i]);
           }
+        add8(add, n * D + d, acc);
         store8(out + n * D + d, acc);
       }
     }
@@ -425,6 +514,7 @@ __global__ __launch_bounds__(256) void unroute_kernel(
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] = fmaf(wk, y[i], acc[i]);
       }
+      add8(add, n * D + d, acc);
       store8(out + n * D + d, acc);
     }
   } else {
@@ -436,7 +526,7 @@ __global__ __launch_bounds__(256) void unroute_kernel(
         if (j < 0 || j >= M) continue;
         acc = fmaf(wk, ldf<YT>(Y, j * D + d), acc);
       }
-      stf<OT>(out, n * D + d, acc);
+      stf<OT>(out, n * D + d, add1(add, n * D + d, acc));
     }
   }
 }
@@ -448,7 +538,7 @@ __global__ __launch_bounds__(256) void unroute_kernel(
 template <typename WT, typename OT, int KMAX, int S>
 __global__ __launch_bounds__(256) void unroute_rows_kernel(
     const uint16_t* __restrict__ Y, const int32_t* __restrict__ inv, const WT* __restrict__ w,
-    int64_t N, int K, int64_t D, OT* __restrict__ out) {
+    int64_t N, int K, int64_t D, OT* __restrict__ out, Addend add) {
   const int lane = threadIdx.x & 63;
   const int64_t n = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   if (n >= N) return;
@@ -488,6 +578,7 @@ __global__ __launch_bounds__(256) void unroute_rows_kernel(
             acc[2 * i + 1] = fmaf(ww[k], __uint_as_float(q[k][s][i] & 0xffff0000u), acc[2 * i + 1]);
           }
         }
+      add8(add, n * D + d, acc);
       store8(out + n * D + d, acc);
     }
   }
@@ -495,17 +586,18 @@ __global__ __launch_bounds__(256) void unroute_rows_kernel(
 
 template <typename YT, typename WT, typename OT>
 static void launch_unroute_t(const void* Y, const int32_t* inv, const void* w, int64_t N, int K,
-                             int64_t D, void* out, hipStream_t st) {
+                             int64_t D, void* out, Addend add, hipStream_t st) {
   const int64_t blocks = ceil_div(N, 4);
-  const bool v8 = (D % 8 == 0) && ((uintptr_t)Y % 16 == 0) && ((uintptr_t)out % 16 == 0);
+  const bool v8 = (D % 8 == 0) && ((uintptr_t)Y % 16 == 0) && ((uintptr_t)out % 16 == 0) &&
+                  ((uintptr_t)add.p % 16 == 0);
 #define MTX_UNROUTE(V, KM)                                                                                  \
   hipLaunchKernelGGL((unroute_kernel<YT, WT, OT, V, KM>), dim3(blocks), dim3(256), 0, st, (const YT*)Y, inv, \
-                     (const WT*)w, N, K, D, (OT*)out)
+                     (const WT*)w, N, K, D, (OT*)out, add)
   if (std::is_same<YT, uint16_t>::value && v8 && K <= 8) {
     const int64_t blocks_ = ceil_div(N, 4);
 #define MTX_UNROUTE_ROWS_L(KM, SS)                                                                           \
   hipLaunchKernelGGL((unroute_rows_kernel<WT, OT, KM, SS>), dim3(blocks_), dim3(256), 0, st, (const uint16_t*)Y, \
-                     inv, (const WT*)w, N, K, D, (OT*)out)
+                     inv, (const WT*)w, N, K, D, (OT*)out, add)
     if (K <= 2) MTX_UNROUTE_ROWS_L(2, 8);
     else if (K <= 4) MTX_UNROUTE_ROWS_L(4, 8);
     else MTX_UNROUTE_ROWS_L(8, 4);
@@ -570,6 +662,23 @@ extern "C" int64_t mtx_route_workspace_size(int64_t N, int64_t K, int64_t E) {
   return route_plan(N, K, E).ws_counts + round_up(N * K * 4, 256);
 }
 
+// Stable counting sort of topk_idx: sort_indices, group_sizes and the inverse permutation.
+static int route_permutation(const RoutePlan& p, const int32_t* topk_idx, int64_t E, int32_t* counts,
+                             int32_t* sort_indices, int32_t* group_sizes, int32_t* inverse, hipStream_t st) {
+  const size_t hist_shm = (size_t)p.nb * sizeof(int);
+  hipLaunchKernelGGL(route_count_kernel, dim3(p.nchunks), dim3(kRouteThreads), hist_shm, st,
+                     topk_idx, p.M, (int)E, p.nb, p.chunk, counts);
+  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(1024), 0, st, counts, p.nchunks, p.nb, (int)E,
+                     group_sizes);
+  int nbits = 0;
+  while ((1 << nbits) < p.nb) ++nbits;
+  const size_t sc_shm = (size_t)5 * p.nb * sizeof(int);
+  if (p.M > 0)
+    hipLaunchKernelGGL(route_scatter_kernel, dim3(p.nchunks), dim3(kRouteThreads), sc_shm, st, topk_idx,
+                       p.M, (int)E, p.nb, nbits, p.chunk, counts, sort_indices, inverse);
+  return check_launch();
+}
+
 extern "C" int mtx_route(const void* tokens, int dtype, const int32_t* topk_idx,
                          int64_t N, int64_t D, int64_t K, int64_t E,
                          void* sorted_tokens, int32_t* sort_indices, int32_t* group_sizes,
@@ -587,18 +696,7 @@ extern "C" int mtx_route(const void* tokens, int dtype, const int32_t* topk_idx,
   hipStream_t st = (hipStream_t)stream;
   int32_t* counts = (int32_t*)workspace;
   if (!inverse && (tokens || token_scales)) inverse = (int32_t*)((char*)workspace + p.ws_counts);
-  const size_t hist_shm = (size_t)p.nb * sizeof(int);
-  hipLaunchKernelGGL(route_count_kernel, dim3(p.nchunks), dim3(kRouteThreads), hist_shm, st,
-                     topk_idx, p.M, (int)E, p.nb, p.chunk, counts);
-  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(1024), 0, st, counts, p.nchunks, p.nb, (int)E,
-                     group_sizes);
-  int nbits = 0;
-  while ((1 << nbits) < p.nb) ++nbits;
-  const size_t sc_shm = (size_t)5 * p.nb * sizeof(int);
-  if (p.M > 0)
-    hipLaunchKernelGGL(route_scatter_kernel, dim3(p.nchunks), dim3(kRouteThreads), sc_shm, st, topk_idx,
-                       p.M, (int)E, p.nb, nbits, p.chunk, counts, sort_indices, inverse);
-  int rc = check_launch();
+  int rc = route_permutation(p, topk_idx, E, counts, sort_indices, group_sizes, inverse, st);
   if (rc != MTX_OK) return rc;
   if (p.M == 0 || (!tokens && !token_scales)) return MTX_OK;
   const int64_t row_bytes = D * dtype_size(dtype);
@@ -631,6 +729,39 @@ extern "C" int mtx_route(const void* tokens, int dtype, const int32_t* topk_idx,
   hipLaunchKernelGGL(dispatch_rows_kernel<UNR>, dim3(gb), dim3(256), 0, st, (const u32x4*)tokens, N, cpr, shift,
                      (const u32x4*)token_scales, spr, inverse, (int)K, (u32x4*)sorted_tokens,
                      (u32x4*)sorted_scales);
+  return check_launch();
+}
+
+extern "C" int mtx_route_quant_fp8(const void* tokens, int dtype, const int32_t* topk_idx, int64_t N,
+                                   int64_t D, int64_t K, int64_t E, uint8_t* sorted_q, float* sorted_scales,
+                                   int32_t* sort_indices, int32_t* group_sizes, int32_t* inverse,
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
+  if (N < 0 || D < 0 || K < 1 || E < 1 || E > 1023) return MTX_ERR_ARG;
+  if (dtype != MTX_F32 && dtype != MTX_BF16) return MTX_ERR_ARG;
+  if (D % 128 != 0 || N * K > INT32_MAX) return MTX_ERR_ARG;
+  if (!sort_indices || !group_sizes || !topk_idx) return MTX_ERR_ARG;
+  if (N > 0 && D > 0 && (!tokens || !sorted_q || !sorted_scales)) return MTX_ERR_ARG;
+  if ((uintptr_t)tokens % 16 != 0 || (uintptr_t)sorted_q % 8 != 0 || (uintptr_t)sorted_scales % 4 != 0)
+    return MTX_ERR_ARG;
+  const RoutePlan p = route_plan(N, K, E);
+  if (!workspace || workspace_bytes < mtx_route_workspace_size(N, K, E)) return MTX_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  int32_t* counts = (int32_t*)workspace;
+  if (!inverse) inverse = (int32_t*)((char*)workspace + p.ws_counts);
+  int rc = route_permutation(p, topk_idx, E, counts, sort_indices, group_sizes, inverse, st);
+  if (rc != MTX_OK) return rc;
+  if (p.M == 0 || D == 0) return MTX_OK;
+  constexpr int UNR = 4;
+  const int64_t groups = N * (D / 128);
+  const int gpw = dtype == MTX_BF16 ? 4 : 2;  // 128-groups per wave and step
+  int64_t gb = ceil_div(groups, (int64_t)gpw * 4 * UNR);
+  if (gb > 16384) gb = 16384;
+  if (dtype == MTX_BF16)
+    hipLaunchKernelGGL((dispatch_quant_rows_kernel<uint16_t, UNR>), dim3(gb), dim3(256), 0, st,
+                       (const uint16_t*)tokens, N, D, inverse, (int)K, sorted_q, sorted_scales);
+  else
+    hipLaunchKernelGGL((dispatch_quant_rows_kernel<float, UNR>), dim3(gb), dim3(256), 0, st, (const float*)tokens,
+                       N, D, inverse, (int)K, sorted_q, sorted_scales);
   return check_launch();
 }
 
@@ -673,18 +804,18 @@ extern "C" int mtx_invert_permutation(const int32_t* perm, int64_t M, int32_t* i
   return check_launch();
 }
 
-extern "C" int mtx_unroute(const void* sorted_output, int y_dtype, const int32_t* inverse,
-                           const void* topk_w, int w_dtype, int64_t N, int64_t K, int64_t D,
-                           void* out, int out_dtype, void* stream) {
+static int unroute_entry(const void* sorted_output, int y_dtype, const int32_t* inverse, const void* topk_w,
+                         int w_dtype, int64_t N, int64_t K, int64_t D, Addend add, void* out, int out_dtype,
+                         void* stream) {
   if (N < 0 || K < 1 || K > 1024 || D < 0) return MTX_ERR_ARG;
   if ((y_dtype != MTX_F32 && y_dtype != MTX_BF16) || (w_dtype != MTX_F32 && w_dtype != MTX_BF16) ||
-      (out_dtype != MTX_F32 && out_dtype != MTX_BF16))
+      (out_dtype != MTX_F32 && out_dtype != MTX_BF16) || (add.p && add.dt != MTX_F32 && add.dt != MTX_BF16))
     return MTX_ERR_ARG;
   if (N == 0 || D == 0) return MTX_OK;
   if (!sorted_output || !inverse || !out) return MTX_ERR_ARG;  // topk_w == NULL: unit weights
   hipStream_t st = (hipStream_t)stream;
   const int k = (int)K;
-#define MTX_UNR(YT, WT, OT) launch_unroute_t<YT, WT, OT>(sorted_output, inverse, topk_w, N, k, D, out, st)
+#define MTX_UNR(YT, WT, OT) launch_unroute_t<YT, WT, OT>(sorted_output, inverse, topk_w, N, k, D, out, add, st)
   if (y_dtype == MTX_BF16) {
     if (w_dtype == MTX_F32) { if (out_dtype == MTX_F32) MTX_UNR(uint16_t, float, float); else MTX_UNR(uint16_t, float, uint16_t); }
     else { if (out_dtype == MTX_F32) MTX_UNR(uint16_t, uint16_t, float); else MTX_UNR(uint16_t, uint16_t, uint16_t); }
@@ -694,6 +825,21 @@ extern "C" int mtx_unroute(const void* sorted_output, int y_dtype, const int32_t
   }
 #undef MTX_UNR
   return check_launch();
+}
+
+extern "C" int mtx_unroute(const void* sorted_output, int y_dtype, const int32_t* inverse,
+                           const void* topk_w, int w_dtype, int64_t N, int64_t K, int64_t D,
+                           void* out, int out_dtype, void* stream) {
+  return unroute_entry(sorted_output, y_dtype, inverse, topk_w, w_dtype, N, K, D, Addend{nullptr, 0}, out,
+                       out_dtype, stream);
+}
+
+extern "C" int mtx_unroute_add(const void* sorted_output, int y_dtype, const int32_t* inverse,
+                               const void* topk_w, int w_dtype, int64_t N, int64_t K, int64_t D,
+                               const void* addend, int add_dtype, void* out, int out_dtype, void* stream) {
+  if (!addend) return MTX_ERR_ARG;
+  return unroute_entry(sorted_output, y_dtype, inverse, topk_w, w_dtype, N, K, D, Addend{addend, add_dtype}, out,
+                       out_dtype, stream);
 }
 
 extern "C" int mtx_unroute_bwd(const void* dout, int g_dtype, const void* sorted_output, int y_dtype,

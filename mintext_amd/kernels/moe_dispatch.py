@@ -182,6 +182,66 @@ def unroute(sorted_output: torch.Tensor, sort_indices: torch.Tensor, topk_weight
     return _Unroute.apply(sorted_output, sort_indices, topk_weights, int(num_experts_per_tok))
 
 
+def unroute_add(sorted_output: torch.Tensor, sort_indices: torch.Tensor, topk_weights: torch.Tensor,
+                num_experts_per_tok: int, addend: torch.Tensor) -> torch.Tensor:
+    """``unroute(...) + addend`` -- the combine followed by ``output = routed_out + shared_out``
+    of MoEBlock.__call__ (mintext/modules/moe.py:256-258) -- in one pass over the rows
+    (``mtx_unroute_add``; the same f32 bits as the two steps).  ``addend`` is [N, D] float32 or
+    bfloat16.  With autograd active it is computed as the two differentiable steps.
+    """
+    needs_grad = torch.is_grad_enabled() and (
+        sorted_output.requires_grad or topk_weights.requires_grad or addend.requires_grad)
+    out_dtype = torch.result_type(sorted_output, topk_weights)
+    if needs_grad:
+        return unroute(sorted_output, sort_indices, topk_weights, num_experts_per_tok) + addend.to(out_dtype)
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"unroute output dtype {out_dtype} not supported")
+    if addend.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"addend dtype {addend.dtype} not supported")
+    dev = L.require_device(sorted_output, sort_indices, topk_weights, addend)
+    K = int(num_experts_per_tok)
+    N = topk_weights.shape[0]
+    Y = sorted_output.contiguous()
+    D = Y.shape[1]
+    if tuple(addend.shape) != (N, D):
+        raise ValueError(f"addend shape {tuple(addend.shape)} != {(N, D)}")
+    inv = _inverse_of(sort_indices)
+    w = topk_weights.contiguous()
+    a = addend.contiguous()
+    out = torch.empty((N, D), dtype=out_dtype, device=dev)
+    L.call("mtx_unroute_add", L.ptr(Y), L.dtype_code(Y.dtype), L.ptr(inv), L.ptr(w), L.dtype_code(w.dtype), N, K, D,
+           L.ptr(a), L.dtype_code(a.dtype), L.ptr(out), L.dtype_code(out_dtype), L.stream(dev))
+    return out
+
+
+def route_quantize_fp8(tokens: torch.Tensor, topk_indices: torch.Tensor, num_experts: int):
+    """1x128 e4m3 quantisation fused into the dispatch: the results of
+    ``route_with_scales(*quantize_fp8_rows(tokens), topk_indices, num_experts)`` with each
+    token row read once in its compute dtype (``mtx_route_quant_fp8``).  tokens [N, D] f32/bf16,
+    D % 128 == 0.  Returns (sorted_q, sorted_scales, sort_indices, group_sizes, inverse).
+    """
+    dev = L.require_device(tokens, topk_indices)
+    x = tokens.contiguous()
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"route_quantize_fp8 needs float32 or bfloat16 tokens, got {x.dtype}")
+    idx = _as_i32(topk_indices).contiguous()
+    N, K = idx.shape
+    D = x.shape[1]
+    M = N * K
+    sorted_q = torch.empty((M, D), dtype=torch.float8_e4m3fn, device=dev)
+    sorted_s = torch.empty((M, D // 128), dtype=torch.float32, device=dev)
+    sort_indices = torch.empty((M,), dtype=torch.int32, device=dev)
+    group_sizes = torch.empty((num_experts,), dtype=torch.int32, device=dev)
+    inverse = torch.empty((M,), dtype=torch.int32, device=dev)
+    ws = L.workspace(L.query("mtx_route_workspace_size", N, K, num_experts), dev)
+    L.call("mtx_route_quant_fp8", L.ptr(x), L.dtype_code(x.dtype), L.ptr(idx), N, D, K, num_experts,
+           L.ptr(sorted_q), L.ptr(sorted_s), L.ptr(sort_indices), L.ptr(group_sizes), L.ptr(inverse),
+           L.ptr(ws), ws.numel(), L.stream(dev))
+    sort_indices._mtx_inverse = inverse
+    sort_indices._mtx_version = sort_indices._version
+    return sorted_q, sorted_s, sort_indices, group_sizes, inverse
+
+
 def route_with_scales(tokens_q: torch.Tensor, token_scales: torch.Tensor, topk_indices: torch.Tensor,
                       num_experts: int):
     """fp8 dispatch: route e4m3 tokens and their [N, D/128] f32 scales in one pass.

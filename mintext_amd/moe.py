@@ -21,21 +21,23 @@ from __future__ import annotations
 import torch
 
 from .kernels.grouped_matmul import grouped_matmul_swiglu, grouped_matmul_vjp
-from .kernels.moe_dispatch import route, route_with_scales, unroute
+from .kernels.moe_dispatch import route, route_quantize_fp8, unroute, unroute_add
 from .kernels.router import route_topk
 from .kernels.swiglu import swiglu_autograd
 
 
 def moe_experts_forward(x: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
                         gate_up: torch.Tensor, down: torch.Tensor, *, fuse_swiglu: bool | None = None,
-                        gate_up_tiling=None, down_tiling=None, return_group_sizes: bool = False):
+                        gate_up_tiling=None, down_tiling=None, return_group_sizes: bool = False,
+                        addend: torch.Tensor | None = None):
     """[N, D] tokens -> [N, D] in result_type(x, topk_weights) (float32 for bf16 + f32 weights).
 
     ``gate_up_tiling`` / ``down_tiling``: HIP tile configurations (``kernels.autotuner``), the
     counterparts of ``MoEExperts.gate_up_tiling`` / ``down_tiling`` (moe.py:189-202) that the
     reference's train.py:43-52 fills from the autotuner.  With ``return_group_sizes`` the
     result is ``(out, group_sizes)``: the per-expert token counts (the bincount of
-    trainer.py:297-308) that ``route`` computed anyway.
+    trainer.py:297-308) that ``route`` computed anyway.  ``addend`` ([N, D], e.g. the shared
+    expert's output) is added to the combined output in the combine's own pass.
     """
     gate_up = gate_up.to(x.dtype)
     down = down.to(x.dtype)
@@ -51,7 +53,10 @@ def moe_experts_forward(x: torch.Tensor, topk_indices: torch.Tensor, topk_weight
         h = grouped_matmul_vjp(sorted_tokens, gate_up, group_sizes, tiling=gate_up_tiling)
         inter = swiglu_autograd(h)
     out = grouped_matmul_vjp(inter, down, group_sizes, tiling=down_tiling)
-    res = unroute(out, sort_indices, topk_weights, topk_indices.shape[1])
+    if addend is None:
+        res = unroute(out, sort_indices, topk_weights, topk_indices.shape[1])
+    else:
+        res = unroute_add(out, sort_indices, topk_weights, topk_indices.shape[1], addend)
     return (res, group_sizes) if return_group_sizes else res
 
 
@@ -98,9 +103,9 @@ def moe_layer_forward(logits: torch.Tensor, x: torch.Tensor, gate_up: torch.Tens
         idx, w = idx[:, :k], w[:, :k]
     else:
         idx, w = route_topk(logits, k, **rkw)
-        out, gs = moe_experts_forward(x, idx, w, gate_up, down, return_group_sizes=True)
-        if shared_gate_up is not None:
-            out = out + shared_expert_forward(x, shared_gate_up, shared_down).to(out.dtype)
+        # the shared expert's output joins the combine's pass: routed_out + shared_out (moe.py:256-258)
+        shared = None if shared_gate_up is None else shared_expert_forward(x, shared_gate_up, shared_down)
+        out, gs = moe_experts_forward(x, idx, w, gate_up, down, return_group_sizes=True, addend=shared)
     if return_expert_counts:
         return out, idx, w, gs[:E]
     return out, idx, w
@@ -144,11 +149,11 @@ def moe_experts_forward_fp8(x: torch.Tensor, topk_indices: torch.Tensor, topk_we
                             gate_up_q: torch.Tensor, gate_up_scale: torch.Tensor, down_q: torch.Tensor,
                             down_scale: torch.Tensor) -> torch.Tensor:
     """Blockwise-fp8 expert layer; weights from ``quantize_fp8_weights`` ([E, Kout, Kin] e4m3)."""
-    from .kernels.fp8 import grouped_matmul_fp8, grouped_matmul_fp8_swiglu, quantize_fp8_rows
+    from .kernels.fp8 import grouped_matmul_fp8, grouped_matmul_fp8_swiglu
 
     E = gate_up_q.shape[0]
-    xq, xs = quantize_fp8_rows(x)
-    sq, ss, sort_indices, group_sizes, _ = route_with_scales(xq, xs, topk_indices, E)
+    # 1x128 quantisation of the tokens fused into their dispatch (each row read once)
+    sq, ss, sort_indices, group_sizes, _ = route_quantize_fp8(x, topk_indices, E)
     yq, ys = grouped_matmul_fp8_swiglu(sq, ss, gate_up_q, gate_up_scale, group_sizes)
     out = grouped_matmul_fp8(yq, ys, down_q, down_scale, group_sizes)
     return unroute(out, sort_indices, topk_weights, topk_indices.shape[1])

@@ -84,6 +84,28 @@ def test_unroute_matches_oracle(dev, dt):
     assert torch.equal(out, out2)
 
 
+@pytest.mark.parametrize("ydt,adt", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                     (torch.float32, torch.bfloat16), (torch.float32, torch.float32)])
+@pytest.mark.parametrize("N,K,D", [(513, 2, 512), (300, 8, 1024), (77, 3, 198)])
+def test_unroute_add_equals_two_steps(dev, ydt, adt, N, K, D):
+    """unroute_add = unroute + addend (routed_out + shared_out, moe.py:256-258), bit for bit,
+    on the row-wise (bf16, K <= 8), vectorised and scalar (D % 8 != 0) combine kernels."""
+    from mintext_amd.kernels import route, unroute
+    from mintext_amd.kernels.moe_dispatch import unroute_add
+
+    rng = np.random.default_rng(N + K)
+    E = 16
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(N)]).astype(np.int32)
+    _, si, _ = route(_t(rng.standard_normal((N, D)).astype(np.float32), dev), _t(idx, dev), E)
+    y = _t(rng.standard_normal((N * K, D)).astype(np.float32), dev, ydt)
+    w = _t(rng.random((N, K)).astype(np.float32), dev)
+    a = _t(rng.standard_normal((N, D)).astype(np.float32), dev, adt)
+    out = unroute_add(y, si, w, K, a)
+    ref = unroute(y, si, w, K) + a.to(torch.float32)
+    assert out.dtype == torch.float32
+    assert torch.equal(out, ref)
+
+
 def test_route_unroute_gradients(dev):
     """tests/test_moe_kernels.py:69-103: grad of sum(unroute(route(x))) and finite differences."""
     from mintext_amd.kernels import route, unroute

@@ -33,6 +33,31 @@ def test_quant_rows_bit_exact(dev, dt):
     np.testing.assert_array_equal(_u8(q), oq)
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("N,K,E,D", [(16384, 8, 128, 2048), (1000, 2, 8, 384), (5, 3, 4, 128)])
+def test_route_quantize_fp8_equals_quant_then_route(dev, dt, N, K, E, D):
+    """The fused quantise-and-dispatch gives the bits of quantize_fp8_rows + route_with_scales
+    (codes, scales, permutation, group sizes, inverse), and the codes/scales match the oracle."""
+    from mintext_amd.kernels.fp8 import quantize_fp8_rows
+    from mintext_amd.kernels.moe_dispatch import route_quantize_fp8, route_with_scales
+
+    rng = np.random.default_rng(N + D)
+    idx = _t(rng.integers(0, E, (N, K)).astype(np.int32), dev)
+    x = (torch.randn(N, D, device=dev) * 3).to(dt)
+    x[N // 2, :128] = 0  # all-zero group -> scale 1
+    q1, s1, p1, g1, i1 = route_quantize_fp8(x, idx, E)
+    xq, xs = quantize_fp8_rows(x)
+    q2, s2, p2, g2, i2 = route_with_scales(xq, xs, idx, E)
+    assert torch.equal(p1, p2) and torch.equal(g1, g2) and torch.equal(i1, i2)
+    assert torch.equal(s1, s2)
+    assert torch.equal(q1.view(torch.uint8), q2.view(torch.uint8))
+    rows = np.argsort(idx.cpu().numpy().ravel(), kind="stable") // K
+    sel = np.unique(np.linspace(0, N * K - 1, 64).astype(np.int64))
+    oq, os_ = O.quant_fp8_rows(x.float().cpu().numpy()[rows[sel]])
+    np.testing.assert_array_equal(_u8(q1)[sel], oq)
+    np.testing.assert_array_equal(s1.cpu().numpy()[sel], os_)
+
+
 def test_quant_weights_bit_exact(dev):
     from mintext_amd.kernels.fp8 import quantize_fp8_weights
 
