@@ -207,7 +207,7 @@ int mtx_swiglu_bwd(const void* h, const void* dy, int dtype, int64_t M, int64_t 
 int mtx_quant_fp8_rows(const void* x, int dtype, int64_t M, int64_t D,
                        uint8_t* xq, float* x_scale, void* stream);
 /* mtx_quant_fp8_rows followed by mtx_route of the codes and scales, in one row pass: tokens
- * [N,D] (F32/BF16, 16-byte aligned, D % 128 == 0) -> sorted_q [N*K,D] e4m3fn (8-byte aligned),
+ * [N,D] (F32/BF16, 16-byte aligned, D % 128 == 0) -> sorted_q [N*K,D] e4m3fn (16-byte aligned),
  * sorted_scales [N*K,D/128] f32, sort_indices, group_sizes, inverse (may be NULL) exactly as
  * the two calls produce them (route: mintext/kernels/moe_dispatch.py:47-81).  Workspace:
  * mtx_route_workspace_size.                                                              */

@@ -70,12 +70,31 @@ __global__ __launch_bounds__(kRouteThreads) void route_count_kernel(
 // the exclusive offsets of chunk c's keys b in the stable order.  Thread (g, b) owns bucket b
 // for chunk group g (G = 1024 / nb groups of consecutive chunks), so the serial part is one
 // group's chunks.
+// With STAGE the [nchunks][nb] counts are first copied to LDS (coalesced), scanned there and
+// written back coalesced, so the serial per-thread walks run at LDS rather than memory latency.
+template <bool STAGE>
 __global__ __launch_bounds__(1024) void route_scan_kernel(
-    int32_t* __restrict__ counts, int nchunks, int nb, int E, int32_t* __restrict__ group_sizes) {
+    int32_t* __restrict__ counts_g, int nchunks, int nb, int E, int32_t* __restrict__ group_sizes) {
   __shared__ int part[1024];  // [g][b] group sums, then group bases
   __shared__ int wsum[16];
   __shared__ int bucket_base[1024];
+  extern __shared__ int staged[];  // [nchunks][nb] when STAGE
   const int tid = threadIdx.x;
+  const int ncnt = nchunks * nb;
+  int* counts = counts_g;
+  if constexpr (STAGE) {
+    constexpr int U = 8;  // loads in flight per thread before the LDS stores
+    for (int i0 = tid; i0 < ncnt; i0 += 1024 * U) {
+      int v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = counts_g[min(i0 + u * 1024, ncnt - 1)];  // branch-free, in bounds
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (i0 + u * 1024 < ncnt) staged[i0 + u * 1024] = v[u];
+    }
+    __syncthreads();
+    counts = staged;
+  }
   const int G = max(1, min(1024 / nb, nchunks));
   const int cpg = (nchunks + G - 1) / G;
   const int g = tid / nb, b = tid - g * nb;
@@ -123,6 +142,10 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(
       counts[o] = base;
       base += x;
     }
+  }
+  if constexpr (STAGE) {
+    __syncthreads();
+    for (int i = tid; i < ncnt; i += 1024) counts_g[i] = staged[i];
   }
 }
 
@@ -275,15 +298,15 @@ __global__ __launch_bounds__(256) void dispatch_rows_kernel(
 // Quantise-and-dispatch in token order: the 1x128 e4m3 quantiser of quant_rows_kernel (same
 // group maximum, scale = amax / 448 or 1 when the group is all zeros, codes of v / scale) fused
 // with the row dispatch, so each token row is read once in its compute dtype and only its fp8
-// codes and scales are written, to the token's K sorted positions inv[n*K+k].  A 128-group
-// spans LPG = 128 / EPL lanes (16 for bf16, 32 for f32); each lane loads UNR groups' 16-byte
-// slices before any store.
+// codes and scales are written, to the token's K sorted positions inv[n*K+k].  Each lane holds
+// 16 elements of a 128-group (8 lanes per group), so every code store is 16 bytes; each lane
+// loads UNR groups' slices before any store.
 template <typename T, int UNR>
 __global__ __launch_bounds__(256) void dispatch_quant_rows_kernel(const T* __restrict__ x, int64_t N, int64_t D,
                                                                   const int32_t* __restrict__ inv, int K,
                                                                   uint8_t* __restrict__ outq,
                                                                   float* __restrict__ outs) {
-  constexpr int EPL = 16 / sizeof(T), LPG = 128 / EPL, GPW = 64 / LPG;
+  constexpr int EPL = 16, LPG = 8, GPW = 8, NLD = EPL * (int)sizeof(T) / 16;  // 16-byte loads per slice
   const int lane = threadIdx.x & 63;
   const int sub = lane / LPG, gl = lane % LPG;
   const int64_t ng = D / 128;
@@ -292,7 +315,7 @@ __global__ __launch_bounds__(256) void dispatch_quant_rows_kernel(const T* __res
   const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
   for (int64_t t0 = wid * GPW; t0 < total; t0 += nw * GPW * UNR) {
-    u32x4 raw[UNR];
+    u32x4 raw[UNR][NLD];
     int64_t tt[UNR];
     bool ok[UNR];
 #pragma unroll
@@ -301,19 +324,24 @@ __global__ __launch_bounds__(256) void dispatch_quant_rows_kernel(const T* __res
       ok[u] = t < total;
       tt[u] = ok[u] ? t : total - 1;
       const int64_t r = tt[u] / ng, g = tt[u] - r * ng;
-      raw[u] = *(const u32x4*)(x + r * D + g * 128 + gl * EPL);
+      const u32x4* src = (const u32x4*)(x + r * D + g * 128 + gl * EPL);
+#pragma unroll
+      for (int l = 0; l < NLD; ++l) raw[u][l] = src[l];
     }
 #pragma unroll
     for (int u = 0; u < UNR; ++u) {
       float v[EPL];
-      if constexpr (sizeof(T) == 4) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(raw[u][i]);
-      } else {
+      for (int l = 0; l < NLD; ++l) {
+        if constexpr (sizeof(T) == 4) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[2 * i] = __uint_as_float(raw[u][i] << 16);
-          v[2 * i + 1] = __uint_as_float(raw[u][i] & 0xffff0000u);
+          for (int i = 0; i < 4; ++i) v[4 * l + i] = __uint_as_float(raw[u][l][i]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v[8 * l + 2 * i] = __uint_as_float(raw[u][l][i] << 16);
+            v[8 * l + 2 * i + 1] = __uint_as_float(raw[u][l][i] & 0xffff0000u);
+          }
         }
       }
       float m = 0.0f;
@@ -323,18 +351,16 @@ __global__ __launch_bounds__(256) void dispatch_quant_rows_kernel(const T* __res
       for (int off = LPG / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
       float sc = m / 448.0f;
       if (sc == 0.0f) sc = 1.0f;
-      uint32_t q[EPL / 4];
+      u32x4 q;
 #pragma unroll
-      for (int i = 0; i < EPL / 4; ++i)
+      for (int i = 0; i < 4; ++i)
         q[i] = e4m3_pack4(v[4 * i] / sc, v[4 * i + 1] / sc, v[4 * i + 2] / sc, v[4 * i + 3] / sc);
       if (!ok[u]) continue;
       const int64_t r = tt[u] / ng, g = tt[u] - r * ng;
       for (int k = 0; k < K; ++k) {
         const int64_t j = inv[r * K + k];
         if (j < 0 || j >= M) continue;
-        uint8_t* dst = outq + j * D + g * 128 + gl * EPL;
-        if constexpr (EPL == 8) *(uint2*)dst = make_uint2(q[0], q[1]);
-        else *(uint32_t*)dst = q[0];
+        *(u32x4*)(outq + j * D + g * 128 + gl * EPL) = q;
         if (gl == 0) outs[j * ng + g] = sc;
       }
     }
@@ -561,7 +587,8 @@ __global__ __launch_bounds__(256) void unroute_rows_kernel(
     for (int k = 0; k < KMAX; ++k)
 #pragma unroll
       for (int s = 0; s < S; ++s)
-        if (jj[k] >= 0 && d0 + 512 * s < D) q[k][s] = *(const u32x4*)(Y + jj[k] * D + d0 + 512 * s);
+        if (jj[k] >= 0 && d0 + 512 * s < D)  // read once: non-temporal (C4 combine 136 -> 113 us)
+          q[k][s] = __builtin_nontemporal_load((const u32x4*)(Y + jj[k] * D + d0 + 512 * s));
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       const int64_t d = d0 + 512 * s;
@@ -662,14 +689,32 @@ extern "C" int64_t mtx_route_workspace_size(int64_t N, int64_t K, int64_t E) {
   return route_plan(N, K, E).ws_counts + round_up(N * K * 4, 256);
 }
 
+// LDS bytes a workgroup may use on the current device (static + dynamic), cached per device.
+static size_t max_lds_per_block() {
+  static size_t cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || n <= 0) return 0;
+    cache[dev] = (size_t)n;
+  }
+  return cache[dev];
+}
+
 // Stable counting sort of topk_idx: sort_indices, group_sizes and the inverse permutation.
 static int route_permutation(const RoutePlan& p, const int32_t* topk_idx, int64_t E, int32_t* counts,
                              int32_t* sort_indices, int32_t* group_sizes, int32_t* inverse, hipStream_t st) {
   const size_t hist_shm = (size_t)p.nb * sizeof(int);
   hipLaunchKernelGGL(route_count_kernel, dim3(p.nchunks), dim3(kRouteThreads), hist_shm, st,
                      topk_idx, p.M, (int)E, p.nb, p.chunk, counts);
-  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(1024), 0, st, counts, p.nchunks, p.nb, (int)E,
-                     group_sizes);
+  const size_t stage_bytes = (size_t)p.nchunks * p.nb * sizeof(int);
+  if (stage_bytes + 9 * 1024 <= max_lds_per_block())
+    hipLaunchKernelGGL(route_scan_kernel<true>, dim3(1), dim3(1024), stage_bytes, st, counts, p.nchunks, p.nb,
+                       (int)E, group_sizes);
+  else
+    hipLaunchKernelGGL(route_scan_kernel<false>, dim3(1), dim3(1024), 0, st, counts, p.nchunks, p.nb, (int)E,
+                       group_sizes);
   int nbits = 0;
   while ((1 << nbits) < p.nb) ++nbits;
   const size_t sc_shm = (size_t)5 * p.nb * sizeof(int);
@@ -741,7 +786,7 @@ extern "C" int mtx_route_quant_fp8(const void* tokens, int dtype, const int32_t*
   if (D % 128 != 0 || N * K > INT32_MAX) return MTX_ERR_ARG;
   if (!sort_indices || !group_sizes || !topk_idx) return MTX_ERR_ARG;
   if (N > 0 && D > 0 && (!tokens || !sorted_q || !sorted_scales)) return MTX_ERR_ARG;
-  if ((uintptr_t)tokens % 16 != 0 || (uintptr_t)sorted_q % 8 != 0 || (uintptr_t)sorted_scales % 4 != 0)
+  if ((uintptr_t)tokens % 16 != 0 || (uintptr_t)sorted_q % 16 != 0 || (uintptr_t)sorted_scales % 4 != 0)
     return MTX_ERR_ARG;
   const RoutePlan p = route_plan(N, K, E);
   if (!workspace || workspace_bytes < mtx_route_workspace_size(N, K, E)) return MTX_ERR_WORKSPACE;
@@ -753,8 +798,7 @@ extern "C" int mtx_route_quant_fp8(const void* tokens, int dtype, const int32_t*
   if (p.M == 0 || D == 0) return MTX_OK;
   constexpr int UNR = 4;
   const int64_t groups = N * (D / 128);
-  const int gpw = dtype == MTX_BF16 ? 4 : 2;  // 128-groups per wave and step
-  int64_t gb = ceil_div(groups, (int64_t)gpw * 4 * UNR);
+  int64_t gb = ceil_div(groups, (int64_t)8 * 4 * UNR);  // 8 groups per wave and step, 4 waves
   if (gb > 16384) gb = 16384;
   if (dtype == MTX_BF16)
     hipLaunchKernelGGL((dispatch_quant_rows_kernel<uint16_t, UNR>), dim3(gb), dim3(256), 0, st,
