@@ -858,16 +858,23 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
   auto rd_b = [&](int g_, int j) -> i32x8 {
     return ld32(lds + (g_ & (NSTAGE - 1)) * STAGE + A_BYTES, wn * WTN + j * 32 + frow);
   };
-  // scales of the k-block whose even stage sits in ring step g
-  float sa_c[TM], sb_c[2], sa_n[TM], sb_n[2];
+  // scales of the k-block whose even stage sits in ring step g.  Weight-block scales: SwiGLU
+  // tiles use both (gate columns j = 0, up columns j = 1); a plain tile's wave uses only the
+  // block holding its 64 columns, read once into sb[0] so that every index stays static.
+  constexpr int NSB = (EPI == EPI_SWIGLU_Q) ? 2 : 1;
+  float sa_c[TM], sb_c[NSB], sa_n[TM], sb_n[NSB];
   auto read_scales = [&](int g, float* sa, float* sb) {
     const float* sc = (const float*)(lds + (g & (NSTAGE - 1)) * STAGE + S_OFF);
 #pragma unroll
     for (int i = 0; i < TM; ++i) sa[i] = sc[wm * WTM + i * 32 + frow];
-    sb[0] = sc[256];
-    sb[1] = sc[257];
+    if (EPI == EPI_SWIGLU_Q) {
+      sb[0] = sc[256];
+      sb[NSB - 1] = sc[257];
+    } else {
+      sb[0] = sc[256 + (wn >> 1)];
+    }
   };
-  auto half_of = [&](int j) -> int { return (EPI == EPI_SWIGLU_Q) ? j : (wn >> 1); };
+  auto half_of = [&](int j) -> int { return (EPI == EPI_SWIGLU_Q) ? j : 0; };
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -893,7 +900,7 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
   // One stage of the rotating schedule: MFMAs of ring step g_ on fr_a / fr_b[cb], with the
   // fragments of step g_+1 read in between; at a k-block boundary each accumulator moves from
   // the previous block's scale units to this block's (f = s_prev / s_this) before its MFMA.
-  auto rot_stage = [&](int g_, int cb, bool rescale, const float (&f)[TM][2]) {
+  auto rot_stage = [&](int g_, int cb, bool rescale, const float (&f)[TM][NSB]) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) fr_b[cb ^ 1][j] = rd_b(g_ + 1, j);
     // accumulator q = i*TN + j is rescaled (block boundary only) one slot ahead of its MFMA,
@@ -922,16 +929,16 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
       const int kt = 2 * kb;
       // even stage kt (ring step g): B fragments in set 0
       issue(g + PD, kt + PD, false);
-      float f[TM][2] = {};
+      float f[TM][NSB] = {};
       if (kb > 0) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int h = 0; h < 2; ++h) f[i][h] = (sa_c[i] * sb_c[h]) * __builtin_amdgcn_rcpf(sa_n[i] * sb_n[h]);
+          for (int h = 0; h < NSB; ++h) f[i][h] = (sa_c[i] * sb_c[h]) * __builtin_amdgcn_rcpf(sa_n[i] * sb_n[h]);
 #pragma unroll
         for (int i = 0; i < TM; ++i) sa_c[i] = sa_n[i];
-        sb_c[0] = sb_n[0];
-        sb_c[1] = sb_n[1];
+#pragma unroll
+        for (int h = 0; h < NSB; ++h) sb_c[h] = sb_n[h];
         rot_stage(g, 0, true, f);
       } else {
         rot_stage(g, 0, false, f);
@@ -1058,8 +1065,8 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
     }
 #pragma unroll
     for (int i = 0; i < TM; ++i) sa_c[i] = sa_n[i];
-    sb_c[0] = sb_n[0];
-    sb_c[1] = sb_n[1];
+#pragma unroll
+    for (int h = 0; h < NSB; ++h) sb_c[h] = sb_n[h];
   }
   __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));  // filler loads of the last steps land before exit
 }
