@@ -943,14 +943,18 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
       } else {
         rot_stage(g, 0, false, f);
       }
-      __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS));  // step g+2 landed (g+3 may be in flight)
-      __syncthreads();
+      // Step g+2 landed (g+3 may be in flight), then a bare s_barrier: __syncthreads() would
+      // also wait for this wave's outstanding LDS reads, which are the fragments of the next
+      // step (visible since the previous barrier) and need not complete before it.  Slots are
+      // refilled only after every wave's MFMAs consumed the fragments read from them.
+      __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS));
+      __builtin_amdgcn_s_barrier();
       // odd stage kt+1 (ring step g+1): B fragments in set 1
       issue(g + 1 + PD, kt + 1 + PD, true);
       read_scales(g + 2, sa_n, sb_n);  // next block's scales (or the next tile's)
       rot_stage(g + 1, 1, false, f);
       __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));  // step g+3 landed (g+4 may be in flight)
-      __syncthreads();
+      __builtin_amdgcn_s_barrier();
       g += 2;
     }
 

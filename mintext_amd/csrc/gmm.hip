@@ -977,7 +977,7 @@ __global__ __launch_bounds__(WM* WN * 64, MTX_V3_WPE) void gmm_v3_kernel(Args p)
         }
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
-        __syncthreads();
+        __builtin_amdgcn_s_barrier();  // no LDS-read wait: see below
         continue;
       }
 #endif
@@ -1002,9 +1002,12 @@ __global__ __launch_bounds__(WM* WN * 64, MTX_V3_WPE) void gmm_v3_kernel(Args p)
         for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
       }
       // stage kt+2 must have landed before the barrier makes it visible to every wave (later
-      // stages, possibly re-reads past the end, may still be in flight)
+      // stages, possibly re-reads past the end, may still be in flight).  A bare s_barrier:
+      // __syncthreads() would also wait for this wave's outstanding LDS reads, which are
+      // fragments of stage kt+1 (visible since the previous barrier); the slot refilled next
+      // (stage kt's, by iteration kt+1) was read only by fragments this iteration's MFMAs used.
       __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
-      __syncthreads();
+      __builtin_amdgcn_s_barrier();
     }
   };
   // Both loop versions execute the same barriers, so waves of one workgroup may take either.
