@@ -368,6 +368,70 @@ def gemm_power_study(steps=10, warmup=3):
     return 0
 
 
+def fp8_vendor_study(steps=10, warmup=3):
+    """C4 fp8 grouped GEMMs (blockwise 1x128 / 128x128 scales; gate_up with the fused SwiGLU +
+    re-quantisation) beside hipBLASLt's dense fp8 GEMMs of the same shapes through
+    torch._scaled_mm with per-tensor and with rowwise scales (hipBLASLt has no blockwise fp8),
+    and hipBLASLt's bf16 GEMM.  Not a benchmark of the path: one JSON line of timings that
+    places the blockwise kernels against the vendor library on the same box and data."""
+    import torch
+
+    from mintext_amd import _lib
+    from mintext_amd.kernels.fp8 import (grouped_matmul_fp8, grouped_matmul_fp8_swiglu, quantize_fp8_rows,
+                                         quantize_fp8_weights)
+
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    T, D, E, K, I = 16384, 2048, 128, 8, 768
+    M = T * K
+    gs = torch.full((E,), M // E, dtype=torch.int32, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+
+    def t_ms(fn):
+        for _ in range(warmup):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            fn()
+        b.record()
+        b.synchronize()
+        return a.elapsed_time(b) / steps
+
+    out = {"study": "fp8-vendor", "shapes": "C4: gate_up [131072,2048]x[2048,1536], down [131072,768]x[768,2048]",
+           "steps": steps, "loads": "uniform (1024 rows per expert)"}
+    x = torch.randn(M, D, device=dev, generator=g).bfloat16()
+    h = torch.randn(M, I, device=dev, generator=g).bfloat16()
+    wgu = (torch.randn(E, D, 2 * I, device=dev, generator=g) * 0.02).bfloat16()
+    wdn = (torch.randn(E, I, D, device=dev, generator=g) * 0.02).bfloat16()
+    xq, xs = quantize_fp8_rows(x)
+    hq, hs = quantize_fp8_rows(h)
+    guq, gus = quantize_fp8_weights(wgu)
+    dnq, dns = quantize_fp8_weights(wdn)
+    one = torch.ones((), device=dev)
+    for name, (aq, a_s, wq, w_s, kin, kout, ours) in {
+        "gate_up": (xq, xs, guq, gus, D, 2 * I, lambda: grouped_matmul_fp8_swiglu(xq, xs, guq, gus, gs)),
+        "down": (hq, hs, dnq, dns, I, D, lambda: grouped_matmul_fp8(hq, hs, dnq, dns, gs)),
+    }.items():
+        flop = 2.0 * M * kin * kout
+        b = wq[0]  # [kout, kin] e4m3, k-contiguous: b.t() is the column-major right operand
+        row_a = torch.rand(M, 1, device=dev) + 0.5
+        row_b = torch.rand(1, kout, device=dev) + 0.5
+        ab = (x if name == "gate_up" else h)
+        bb = (wgu[0] if name == "gate_up" else wdn[0]).contiguous()
+        res = {"blockwise_grouped_ms": t_ms(ours),
+               "hipblaslt_fp8_pertensor_ms": t_ms(lambda: torch._scaled_mm(aq, b.t(), scale_a=one, scale_b=one,
+                                                                           out_dtype=torch.bfloat16)),
+               "hipblaslt_fp8_rowwise_ms": t_ms(lambda: torch._scaled_mm(aq, b.t(), scale_a=row_a, scale_b=row_b,
+                                                                         out_dtype=torch.bfloat16)),
+               "hipblaslt_bf16_ms": t_ms(lambda: torch.matmul(ab, bb))}
+        out[name] = {k: round(v, 4) for k, v in res.items()}
+        out[name].update({k.replace("_ms", "_tflops"): round(flop / v / 1e9, 1) for k, v in res.items()})
+    print(json.dumps(out))
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -381,11 +445,14 @@ def main(argv=None):
                     help="only run 3 plain 256 MiB device copies (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--graph", action="store_true",
                     help="also time the step captured in a HIP graph and replayed (reported as hip_graph)")
-    ap.add_argument("--study", choices=["gemm-power"], default=None,
-                    help="gemm-power: GEMM timings on normal vs all-zero data (clock / issue-efficiency study)")
+    ap.add_argument("--study", choices=["gemm-power", "fp8-vendor"], default=None,
+                    help="gemm-power: GEMM timings on normal vs all-zero data (clock / issue-efficiency study); "
+                         "fp8-vendor: C4 blockwise fp8 GEMMs beside hipBLASLt's per-tensor / rowwise fp8 GEMMs")
     a = ap.parse_args(argv)
     if a.study == "gemm-power":
         return gemm_power_study(a.steps if a.steps != 20 else 10, a.warmup)
+    if a.study == "fp8-vendor":
+        return fp8_vendor_study(a.steps if a.steps != 20 else 10, a.warmup)
     if a.copy_calibration:
         import torch
 
