@@ -145,6 +145,30 @@ def test_gmm_bf16_mfma(dev, M, E, Kin, Kout, kind):
     _close(dx.float().cpu().numpy(), O.gmm_dlhs(gr.float().cpu().numpy(), wr, gs), 2e-2)
 
 
+def test_gmm_short_last_tiles(dev):
+    """Groups of whole 256-row tiles plus a last tile of 1..128 rows (and single, empty and
+    one-row groups): every row computed once, for the forward, the fused SwiGLU and dlhs."""
+    from mintext_amd.kernels import grouped_matmul, grouped_matmul_swiglu
+    from mintext_amd.kernels.grouped_matmul import _gmm_dlhs
+
+    gs = np.array([257, 287, 544, 356, 383, 384, 200, 0, 1, 2049], np.int32)  # tails 1..127, 128, single
+    M, E, Kin, Kout = int(gs.sum()), len(gs), 128, 512
+    x = torch.randn(M, Kin, device=dev).bfloat16()
+    w = (torch.randn(E, Kin, Kout, device=dev) * 0.05).bfloat16()
+    xr, wr = x.float().cpu().numpy(), w.float().cpu().numpy()
+    ref = O.gmm(xr, wr, gs)
+    out = grouped_matmul(x, w, _t(gs, dev)).float().cpu().numpy()
+    _close(out, ref, 2e-2)
+    # per-row check: a dropped or doubly written row would show as a row-wise outlier
+    row_err = np.abs(out - ref).max(1) / (np.abs(ref).max(1) + 1e-6)
+    assert row_err.max() < 5e-2, int(np.argmax(row_err))
+    y = grouped_matmul_swiglu(x, w, _t(gs, dev)).float().cpu().numpy()
+    _close(y, O.swiglu(ref), 2e-2)
+    gr = torch.randn(M, Kout, device=dev).bfloat16()
+    dx = _gmm_dlhs(gr, w, _t(gs, dev))
+    _close(dx.float().cpu().numpy(), O.gmm_dlhs(gr.float().cpu().numpy(), wr, gs), 2e-2)
+
+
 @pytest.mark.parametrize("M,E,Kin,I,kind", [(2048, 4, 256, 256, "uniform"), (1000, 8, 128, 384, "ragged"),
                                             (300, 5, 64, 128, "skew")])
 def test_gmm_swiglu_fused(dev, M, E, Kin, I, kind):
