@@ -432,6 +432,53 @@ def fp8_vendor_study(steps=10, warmup=3):
     return 0
 
 
+def gate_study(steps=20, warmup=5):
+    """The router gate GEMM + top-k on the C2, C3 and C4 shapes: hipBLASLt's dense gate GEMM
+    (torch.matmul, [T,D] x [D,E]) followed by route_topk, against the fused gate_route_topk (the
+    gate weight already in the nn.Linear layout, a load-time transform).  One JSON line of
+    timings; not part of the layer bench, whose path starts from the logits."""
+    import torch
+
+    from mintext_amd import _lib
+    from mintext_amd.kernels import route_topk
+    from mintext_amd.kernels.router import gate_route_topk, gate_weight_linear_layout
+
+    _lib.lib()
+    dev = torch.device("cuda:0")
+
+    def t_ms(fn):
+        for _ in range(warmup):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            fn()
+        b.record()
+        b.synchronize()
+        return a.elapsed_time(b) / steps
+
+    out = {"study": "gate", "steps": steps}
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    for name in ("mixtral", "deepseek", "qwen3_fp8"):
+        cfg = CONFIGS[name]
+        T, D, E, K = cfg["T"], cfg["D"], cfg["E"], cfg["K"]
+        x = torch.randn(T, D, device=dev, generator=g).bfloat16()
+        wg = (torch.randn(D, E, device=dev, generator=g) * cfg["wstd"]).bfloat16()
+        wt = gate_weight_linear_layout(wg)
+        rkw = dict(scoring=cfg["scoring"], n_group=cfg.get("n_group", 1), topk_group=cfg.get("topk_group", 1),
+                   routed_scaling_factor=cfg.get("scale", 1.0))
+        unfused = t_ms(lambda: route_topk(torch.matmul(x, wg), K, **rkw))
+        gemm_only = t_ms(lambda: torch.matmul(x, wg))
+        fused = t_ms(lambda: gate_route_topk(x, wt, K, **rkw))
+        xbytes = T * D * 2
+        out[name] = {"T": T, "D": D, "E": E, "K": K, "hipblaslt_gate_plus_topk_us": round(unfused * 1e3, 1),
+                     "hipblaslt_gate_us": round(gemm_only * 1e3, 1), "fused_us": round(fused * 1e3, 1),
+                     "fused_x_read_GBs": round(xbytes / (fused * 1e-3) / 1e9, 1)}
+    print(json.dumps(out))
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -445,14 +492,17 @@ def main(argv=None):
                     help="only run 3 plain 256 MiB device copies (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--graph", action="store_true",
                     help="also time the step captured in a HIP graph and replayed (reported as hip_graph)")
-    ap.add_argument("--study", choices=["gemm-power", "fp8-vendor"], default=None,
+    ap.add_argument("--study", choices=["gemm-power", "fp8-vendor", "gate"], default=None,
                     help="gemm-power: GEMM timings on normal vs all-zero data (clock / issue-efficiency study); "
-                         "fp8-vendor: C4 blockwise fp8 GEMMs beside hipBLASLt's per-tensor / rowwise fp8 GEMMs")
+                         "fp8-vendor: C4 blockwise fp8 GEMMs beside hipBLASLt's per-tensor / rowwise fp8 GEMMs; "
+                         "gate: router gate GEMM + top-k, hipBLASLt + route_topk vs the fused kernel")
     a = ap.parse_args(argv)
     if a.study == "gemm-power":
         return gemm_power_study(a.steps if a.steps != 20 else 10, a.warmup)
     if a.study == "fp8-vendor":
         return fp8_vendor_study(a.steps if a.steps != 20 else 10, a.warmup)
+    if a.study == "gate":
+        return gate_study(a.steps, a.warmup)
     if a.copy_calibration:
         import torch
 

@@ -14,6 +14,8 @@
  *                             counterpart in the reference (Mixtral/Qwen3 router)
  *   mtx_router_topk_shared <- the same with MoEBlock's shared expert (moe.py:231-236,256-258)
  *                             folded in as an always-routed extra expert
+ *   mtx_gate_router_topk   <- the gate Linear.__call__ (mintext/modules/linear.py:123-147) +
+ *                             MoERouter (moe.py:41-103) in one kernel
  *   mtx_expert_bias_update <- update_expert_biases (mintext/trainer.py:371-410), one layer
  *   mtx_route              <- route (mintext/kernels/moe_dispatch.py:47-81)
  *   mtx_gather_rows        <- _sort_with_vjp forward (moe_dispatch.py:21-24)
@@ -95,6 +97,21 @@ int mtx_router_topk_shared(const void* logits, int logits_dtype, int64_t T, int6
                            int scoring, const float* bias, int64_t n_group, int64_t topk_group,
                            int norm_topk_prob, float routed_scaling_factor, int64_t shared_expert,
                            int32_t* topk_idx, float* topk_w, float* scores, void* stream);
+
+/* The router gate GEMM fused with mtx_router_topk: logits = x @ W_g (f32 accumulation, one
+ * rounding to bf16, as the gate Linear.__call__, mintext/modules/linear.py:123-147, computes
+ * them in the compute dtype) and the top-k on those logits, with no [T,E] round trip.
+ * x [T,D] bf16, gate_weight_t [E,D] bf16 (the gate kernel [D,E] of moe.py:30-35 transposed
+ * once: the nn.Linear layout), both 16-byte aligned; D % 64 == 0, E <= 256 (other shapes and
+ * dtypes: MTX_ERR_UNSUPPORTED, use the gate GEMM + mtx_router_topk).  shared_expert: -1, or an
+ * id >= E written as column K with weight 1 (as mtx_router_topk_shared; topk_* are then
+ * [T,K+1]).  logits_out [T,E] bf16 may be NULL.  Selection and weights are mtx_router_topk's
+ * on the rounded logits, bit for bit.                                                    */
+int mtx_gate_router_topk(const void* x, int dtype, const void* gate_weight_t, int64_t T, int64_t D,
+                         int64_t E, int64_t K, int scoring, const float* bias, int64_t n_group,
+                         int64_t topk_group, int norm_topk_prob, float routed_scaling_factor,
+                         int64_t shared_expert, int32_t* topk_idx, float* topk_w, void* logits_out,
+                         void* stream);
 
 /* Loss-free load balancing for one MoE layer (update_expert_biases, mintext/trainer.py:371-410):
  * bias[e] += rate * sign(float(sum(counts))/E - counts[e]).  expert_counts [E] int32 is the

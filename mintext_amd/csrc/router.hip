@@ -28,29 +28,23 @@ __device__ __forceinline__ bool cand_better(float av, int ai, float bv, int bi) 
   return av > bv || (av == bv && ai < bi);
 }
 
-template <int V>
-__global__ __launch_bounds__(256) void router_topk_kernel(
-    const void* __restrict__ logits, int ldt, int T, int E, int K, int L,
-    int scoring, const float* __restrict__ bias, int n_group, int topk_group, int norm,
-    float rscale, int32_t* __restrict__ idx_out, float* __restrict__ w_out,
-    float* __restrict__ scores_out, int ldo, int extra) {
-  extern __shared__ float smem[];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int tpw = 64 / L;
-  const int li = lane % L;
-  const int tok_local = wave * tpw + lane / L;
-  const int tpb = (blockDim.x >> 6) * tpw;
-  const int64_t t = (int64_t)blockIdx.x * tpb + tok_local;
-  const bool tok_ok = t < T;
-
+// Selection for one token t owned by lanes li = 0..L-1 of its lane group (tok_local: the
+// token's slot in the workgroup, for the group-limited scratch in smem).  load(e) returns the
+// token's logit of expert e as f32.  Every thread of the workgroup must call it (the
+// group-limited path synchronises the workgroup).
+template <int V, typename Load>
+__device__ __forceinline__ void router_select(Load load, int64_t t, bool tok_ok, int tok_local, int li, int L,
+                                              int E, int K, int scoring, const float* __restrict__ bias,
+                                              int n_group, int topk_group, int norm, float rscale,
+                                              int32_t* __restrict__ idx_out, float* __restrict__ w_out,
+                                              float* __restrict__ scores_out, int ldo, int extra, float* smem) {
   float sel[V], pay[V];
   bool ok[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     const int e = li + L * v;
     ok[v] = tok_ok && e < E;
-    float x = ok[v] ? load_as_f32(logits, t * E + e, ldt) : -INFINITY;
+    float x = ok[v] ? load(e) : -INFINITY;
     if (scoring == MTX_SCORING_SIGMOID_GROUP) {
       const float s = 1.0f / (1.0f + expf(-x));
       pay[v] = s;
@@ -179,9 +173,164 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   }
 }
 
+template <int V>
+__global__ __launch_bounds__(256) void router_topk_kernel(
+    const void* __restrict__ logits, int ldt, int T, int E, int K, int L,
+    int scoring, const float* __restrict__ bias, int n_group, int topk_group, int norm,
+    float rscale, int32_t* __restrict__ idx_out, float* __restrict__ w_out,
+    float* __restrict__ scores_out, int ldo, int extra) {
+  extern __shared__ float smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int tpw = 64 / L;
+  const int li = lane % L;
+  const int tok_local = wave * tpw + lane / L;
+  const int tpb = (blockDim.x >> 6) * tpw;
+  const int64_t t = (int64_t)blockIdx.x * tpb + tok_local;
+  const bool tok_ok = t < T;
+  router_select<V>([&](int e) { return load_as_f32(logits, t * E + e, ldt); }, t, tok_ok, tok_local, li, L, E, K,
+                   scoring, bias, n_group, topk_group, norm, rscale, idx_out, w_out, scores_out, ldo, extra, smem);
+}
+
+// ---- router gate GEMM fused with the top-k ---------------------------------------------------
+// logits = round_to_bf16(x @ Wg) (f32 accumulation), then router_select on those logits: the gate
+// Linear.__call__ (mintext/modules/linear.py:123-147, bf16 dot with one rounding) feeding
+// MoERouter (moe.py:41-103) without the [T,E] round trip.  A workgroup owns 32 tokens and all
+// (up to 256) experts; its 4 waves split the reduction over D in quarters, each with
+// v_mfma_f32_32x32x16_bf16 on operands loaded straight from memory (x rows and the gate weight
+// in the nn.Linear layout wt [E,D] are both k-contiguous: one 16-byte load per lane and
+// operand), and the quarters are added in wave order in LDS, so the sums are deterministic.
+typedef __attribute__((ext_vector_type(8))) __bf16 gate_bf16x8;
+typedef __attribute__((ext_vector_type(16))) float gate_f32x16;
+constexpr int kGateTokens = 32;
+
+template <int EB, int V>
+__global__ __launch_bounds__(256) void gate_topk_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wt, int T, int D, int E, int K, int L, int scoring,
+    const float* __restrict__ bias, int n_group, int topk_group, int norm, float rscale,
+    int32_t* __restrict__ idx_out, float* __restrict__ w_out, uint16_t* __restrict__ logits_out, int ldo,
+    int extra) {
+  constexpr int EP = EB * 32, LDP = EP + 1;  // logits tile row stride (+1: conflict-free)
+  extern __shared__ float smem[];
+  float* lg = smem;                              // [32][LDP] f32
+  float* scratch = smem + kGateTokens * LDP;     // group-limited scratch of router_select
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t t0 = (int64_t)blockIdx.x * kGateTokens;
+
+  // ---- logits: wave w reduces k in [w*D/4, (w+1)*D/4) ------------------------------------
+  gate_f32x16 acc[EB];
+#pragma unroll
+  for (int b = 0; b < EB; ++b)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[b][v] = 0.0f;
+  const int r = lane & 31, kh = lane >> 5;
+  const int64_t trow = min(t0 + r, (int64_t)T - 1);  // rows past T: computed, never stored
+  const uint16_t* xa = x + trow * D + kh * 8;
+  const uint16_t* wb[EB];
+#pragma unroll
+  for (int b = 0; b < EB; ++b) wb[b] = wt + (int64_t)min(b * 32 + r, E - 1) * D + kh * 8;
+  const int kq = D / 4, kbeg = wave * kq;
+#pragma unroll 4
+  for (int k = kbeg; k < kbeg + kq; k += 16) {
+    const gate_bf16x8 a = *(const gate_bf16x8*)(xa + k);
+#pragma unroll
+    for (int b = 0; b < EB; ++b) {
+      const gate_bf16x8 w = *(const gate_bf16x8*)(wb[b] + k);
+      acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w, a, acc[b], 0, 0, 0);
+    }
+  }
+  // lane l holds, for value 4g+q of block b, expert b*32 + 8g + 4(l/32) + q of token l%32
+  for (int w = 0; w < 4; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int b = 0; b < EB; ++b)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float* dst = lg + r * LDP + b * 32 + 8 * g + 4 * kh + q;
+            *dst = (w == 0) ? acc[b][4 * g + q] : *dst + acc[b][4 * g + q];
+          }
+    }
+    __syncthreads();
+  }
+  // the gate output in the compute dtype (one rounding, as the reference's bf16 dot)
+  for (int i = tid; i < kGateTokens * E; i += blockDim.x) {
+    const int tt = i / E, e = i - tt * E;
+    const uint16_t hb = f32_to_bf16(lg[tt * LDP + e]);
+    lg[tt * LDP + e] = bf16_to_f32(hb);
+    if (logits_out && t0 + tt < T) logits_out[(t0 + tt) * E + e] = hb;
+  }
+  __syncthreads();
+
+  // ---- top-k of the tile's tokens (passes of 4 * 64/L tokens) ------------------------------
+  const int tpw = 64 / L, li = lane % L, tpb = 4 * tpw;
+  for (int p0 = 0; p0 < kGateTokens; p0 += tpb) {
+    const int slot = wave * tpw + lane / L;
+    const int tl = p0 + slot;
+    const int64_t t = t0 + tl;
+    const bool tok_ok = tl < kGateTokens && t < T;
+    const float* row = lg + (tok_ok ? tl : 0) * LDP;
+    router_select<V>([&](int e) { return row[e]; }, t, tok_ok, slot, li, L, E, K, scoring, bias, n_group, topk_group,
+                     norm, rscale, idx_out, w_out, nullptr, ldo, extra, scratch);
+    __syncthreads();  // the scratch of the next pass
+  }
+}
+
 }  // namespace mtx
 
 using namespace mtx;
+
+static void router_lanes(int64_t E, int64_t K, int* L_out, int* V_out) {
+  int P = 1;
+  while (P < E) P <<= 1;
+  int L = P / 8 < 1 ? 1 : P / 8;
+  while (L < K) L <<= 1;  // lane li < K of a token holds the round-li winner (K <= 64)
+  if (L > 64) L = 64;
+  *L_out = L;
+  *V_out = (int)ceil_div(E, L);
+}
+
+extern "C" int mtx_gate_router_topk(const void* x, int dtype, const void* gate_weight_t, int64_t T, int64_t D,
+                                    int64_t E, int64_t K, int scoring, const float* bias, int64_t n_group,
+                                    int64_t topk_group, int norm_topk_prob, float routed_scaling_factor,
+                                    int64_t shared_expert, int32_t* topk_idx, float* topk_w, void* logits_out,
+                                    void* stream) {
+  if (T < 0 || D < 0 || E < 1 || K < 1 || K > E || K > 64) return MTX_ERR_ARG;
+  if (shared_expert >= 0 && (shared_expert < E || shared_expert > INT32_MAX)) return MTX_ERR_ARG;
+  if (scoring != MTX_SCORING_SOFTMAX && scoring != MTX_SCORING_SIGMOID_GROUP) return MTX_ERR_ARG;
+  if (n_group < 1) n_group = 1;
+  if (topk_group < 1) topk_group = 1;
+  if (scoring == MTX_SCORING_SIGMOID_GROUP && (E % n_group != 0 || topk_group > n_group)) return MTX_ERR_ARG;
+  if (dtype != MTX_BF16 || E > 256 || D % 64 != 0 || D == 0) return MTX_ERR_UNSUPPORTED;
+  if (T == 0) return MTX_OK;
+  if (!x || !gate_weight_t || !topk_idx || !topk_w) return MTX_ERR_ARG;
+  if ((uintptr_t)x % 16 != 0 || (uintptr_t)gate_weight_t % 16 != 0) return MTX_ERR_ARG;
+  int L, V;
+  router_lanes(E, K, &L, &V);
+  const int EB = (int)ceil_div(E, 32), EBp = EB <= 1 ? 1 : EB <= 2 ? 2 : EB <= 4 ? 4 : 8;
+  const int tpb = 4 * (64 / L);
+  const size_t shm = ((size_t)kGateTokens * (EBp * 32 + 1) + (size_t)tpb * (size_t)(E + 2 * n_group)) * sizeof(float);
+  const int grid = (int)ceil_div(T, kGateTokens);
+  hipStream_t st = (hipStream_t)stream;
+#define MTX_GATE(EBT, VV)                                                                                         \
+  hipLaunchKernelGGL((gate_topk_kernel<EBT, VV>), dim3(grid), dim3(256), shm, st, (const uint16_t*)x,             \
+                     (const uint16_t*)gate_weight_t, (int)T, (int)D, (int)E, (int)K, L, scoring, bias, (int)n_group, \
+                     (int)topk_group, norm_topk_prob, routed_scaling_factor, topk_idx, topk_w, (uint16_t*)logits_out, \
+                     (int)(shared_expert >= 0 ? K + 1 : K), (int)(shared_expert >= 0 ? shared_expert : -1))
+#define MTX_GATE_V(EBT)                      \
+  if (V <= 1) MTX_GATE(EBT, 1);              \
+  else if (V <= 2) MTX_GATE(EBT, 2);         \
+  else if (V <= 4) MTX_GATE(EBT, 4);         \
+  else MTX_GATE(EBT, 8);
+  if (EBp == 1) { MTX_GATE_V(1) }
+  else if (EBp == 2) { MTX_GATE_V(2) }
+  else if (EBp == 4) { MTX_GATE_V(4) }
+  else { MTX_GATE_V(8) }
+#undef MTX_GATE_V
+#undef MTX_GATE
+  return check_launch();
+}
 
 static int router_launch(const void* logits, int logits_dtype, int64_t T, int64_t E, int64_t K, int scoring,
                          const float* bias, int64_t n_group, int64_t topk_group, int norm_topk_prob,
@@ -197,12 +346,8 @@ static int router_launch(const void* logits, int logits_dtype, int64_t T, int64_
   if (!logits || !topk_idx || !topk_w) return MTX_ERR_ARG;
   // L lanes per token with up to 8 candidates each: few butterfly steps per round and several
   // tokens per wave (E = 8: one lane per token; E = 128: 16 lanes; E >= 512: 64 lanes)
-  int P = 1;
-  while (P < E) P <<= 1;
-  int L = P / 8 < 1 ? 1 : P / 8;
-  while (L < K) L <<= 1;  // lane li < K of a token holds the round-li winner (K <= 64)
-  if (L > 64) L = 64;
-  const int V = (int)ceil_div(E, L);
+  int L, V;
+  router_lanes(E, K, &L, &V);
   const int tpb = 4 * (64 / L);
   const int grid = (int)ceil_div(T, tpb);
   size_t shm = 0;

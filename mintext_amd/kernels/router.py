@@ -67,6 +67,76 @@ def route_topk(logits: torch.Tensor, k: int, *, scoring: str = "softmax", bias: 
     return idx, w
 
 
+def gate_weight_linear_layout(gate_weight: torch.Tensor) -> torch.Tensor:
+    """The router gate kernel [D, E] (the reference's ``kernel_axes=("embed", "mlp")`` layout,
+    moe.py:30-35) -> the nn.Linear layout [E, D] that ``gate_route_topk`` reads (each expert's
+    weights k-contiguous).  A load-time transform on the device (``mtx_transpose_batched``)."""
+    from .expert_layout import _transpose_into
+
+    dev = L.require_device(gate_weight)
+    w = gate_weight.contiguous()
+    D, E = w.shape
+    out = torch.empty((E, D), dtype=w.dtype, device=dev)
+    _transpose_into(w, out, 1, D, E, D * E, E, E * D, D)
+    return out
+
+
+def gate_supported(x: torch.Tensor, E: int) -> bool:
+    """Whether ``gate_route_topk`` covers this input (bf16 tokens, D % 64 == 0, E <= 256)."""
+    return x.dtype == torch.bfloat16 and x.dim() == 2 and x.shape[1] % 64 == 0 and x.shape[1] > 0 and 1 <= E <= 256
+
+
+# Each 32-token workgroup of the fused kernel reads the whole gate weight, so it beats a dense
+# gate GEMM + top-k only for few experts (measured: Mixtral E=8 19.6 vs 33.6 us; E=128 69 vs
+# 33 us, E=256 189 vs 57 us; bench.py --study gate).
+GATE_FUSED_MAX_E = 32
+
+
+def gate_fused_preferred(x: torch.Tensor, E: int) -> bool:
+    """Whether ``moe_block_forward`` should run the fused gate for this input."""
+    return gate_supported(x, E) and E <= GATE_FUSED_MAX_E
+
+
+def gate_route_topk(x: torch.Tensor, gate_weight_t: torch.Tensor, k: int, *, scoring: str = "softmax",
+                    bias: torch.Tensor | None = None, n_group: int = 1, topk_group: int = 1,
+                    norm_topk_prob: bool = True, routed_scaling_factor: float = 1.0,
+                    shared_expert: int | None = None, return_logits: bool = False):
+    """Router gate GEMM and top-k in one kernel (``mtx_gate_router_topk``): the gate
+    ``Linear.__call__`` (mintext/modules/linear.py:123-147) -- logits = x @ W_g with f32
+    accumulation and one rounding to bf16 -- followed by ``route_topk`` on those logits, with no
+    [T, E] round trip through memory.
+
+    Args:
+        x: [T, D] bfloat16 tokens (D % 64 == 0).
+        gate_weight_t: [E, D] bfloat16 gate weight in the nn.Linear layout
+            (``gate_weight_linear_layout`` of the reference's [D, E] kernel), E <= 256.
+        k, scoring, bias, n_group, topk_group, norm_topk_prob, routed_scaling_factor,
+        shared_expert: as ``route_topk``.
+
+    Returns:
+        (topk_indices, topk_weights) as ``route_topk`` on the bf16 logits, and the logits
+        [T, E] bfloat16 with ``return_logits``.
+    """
+    if scoring not in _SCORING:
+        raise ValueError(f"unknown scoring {scoring!r}")
+    dev = L.require_device(x, gate_weight_t)
+    xc = x.contiguous()
+    wt = gate_weight_t.contiguous()
+    T, D = xc.shape
+    E = wt.shape[0]
+    if wt.shape[1] != D:
+        raise ValueError(f"gate weight {tuple(wt.shape)} does not match tokens [T, {D}]")
+    kk = k if shared_expert is None else k + 1
+    idx = torch.empty((T, kk), dtype=torch.int32, device=dev)
+    w = torch.empty((T, kk), dtype=torch.float32, device=dev)
+    logits = torch.empty((T, E), dtype=torch.bfloat16, device=dev) if return_logits else None
+    b = None if bias is None else bias.to(device=dev, dtype=torch.float32).contiguous()
+    L.call("mtx_gate_router_topk", L.ptr(xc), L.dtype_code(xc.dtype), L.ptr(wt.to(xc.dtype)), T, D, E, k,
+           _SCORING[scoring], L.ptr(b), n_group, topk_group, int(bool(norm_topk_prob)), float(routed_scaling_factor),
+           -1 if shared_expert is None else int(shared_expert), L.ptr(idx), L.ptr(w), L.ptr(logits), L.stream(dev))
+    return (idx, w, logits) if return_logits else (idx, w)
+
+
 def update_expert_bias(bias: torch.Tensor, expert_counts: torch.Tensor, rate: float) -> torch.Tensor:
     """Loss-free load balancing of one MoE layer, in place (update_expert_biases,
     mintext/trainer.py:371-410): ``bias += rate * sign(mean(counts) - counts)``.

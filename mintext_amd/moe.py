@@ -22,7 +22,7 @@ import torch
 
 from .kernels.grouped_matmul import grouped_matmul_swiglu, grouped_matmul_vjp
 from .kernels.moe_dispatch import route, route_quantize_fp8, unroute, unroute_add
-from .kernels.router import route_topk
+from .kernels.router import gate_fused_preferred, gate_route_topk, gate_weight_linear_layout, route_topk
 from .kernels.swiglu import swiglu_autograd
 
 
@@ -79,30 +79,43 @@ def fold_shared_expert(gate_up: torch.Tensor, down: torch.Tensor, shared_gate_up
             torch.cat([down, sdn.to(down.dtype)], 0).contiguous())
 
 
-def moe_layer_forward(logits: torch.Tensor, x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, *,
+def moe_layer_forward(logits: torch.Tensor | None, x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, *,
                       k: int, scoring: str = "softmax", bias: torch.Tensor | None = None, n_group: int = 1,
                       topk_group: int = 1, norm_topk_prob: bool = True, routed_scaling_factor: float = 1.0,
                       shared_gate_up: torch.Tensor | None = None, shared_down: torch.Tensor | None = None,
-                      shared_folded: bool = False, return_expert_counts: bool = False):
+                      shared_folded: bool = False, return_expert_counts: bool = False,
+                      gate_weight_t: torch.Tensor | None = None):
     """Router top-k + routed experts (+ shared expert) -- MoEBlock.__call__ (moe.py:240-266) after
     the gate GEMM.  Returns (out [T,D] f32, topk_indices [T,k], topk_weights [T,k]) and, with
     ``return_expert_counts``, the [E] int32 per-expert token counts (trainer.py:297-308).
 
     ``shared_folded``: ``gate_up`` / ``down`` come from ``fold_shared_expert`` (E routed experts
     + the shared one as expert E, ``logits`` has E columns); the shared expert then runs inside
-    the routed grouped GEMMs.
+    the routed grouped GEMMs.  With ``gate_weight_t`` ([E, D], ``gate_weight_linear_layout``)
+    and ``logits=None`` the gate GEMM and the top-k run as one kernel (``gate_route_topk``).
     """
     rkw = dict(scoring=scoring, bias=bias, n_group=n_group, topk_group=topk_group, norm_topk_prob=norm_topk_prob,
                routed_scaling_factor=routed_scaling_factor)
-    E = logits.shape[1]
+    if logits is None:
+        if gate_weight_t is None:
+            raise ValueError("moe_layer_forward needs the logits or the gate weight")
+        E = gate_weight_t.shape[0]
+
+        def topk(shared_expert=None):
+            return gate_route_topk(x, gate_weight_t, k, shared_expert=shared_expert, **rkw)
+    else:
+        E = logits.shape[1]
+
+        def topk(shared_expert=None):
+            return route_topk(logits, k, shared_expert=shared_expert, **rkw)
     if shared_folded:
         if gate_up.shape[0] != E + 1:
             raise ValueError(f"folded weights need {E + 1} experts (E routed + shared), got {gate_up.shape[0]}")
-        idx, w = route_topk(logits, k, shared_expert=E, **rkw)
+        idx, w = topk(shared_expert=E)
         out, gs = moe_experts_forward(x, idx, w, gate_up, down, return_group_sizes=True)
         idx, w = idx[:, :k], w[:, :k]
     else:
-        idx, w = route_topk(logits, k, **rkw)
+        idx, w = topk()
         # the shared expert's output joins the combine's pass: routed_out + shared_out (moe.py:256-258)
         shared = None if shared_gate_up is None else shared_expert_forward(x, shared_gate_up, shared_down)
         out, gs = moe_experts_forward(x, idx, w, gate_up, down, return_group_sizes=True, addend=shared)
@@ -115,23 +128,36 @@ def moe_block_forward(x: torch.Tensor, gate_weight: torch.Tensor, gate_up: torch
                       k: int, scoring: str = "sigmoid_group", bias: torch.Tensor | None = None, n_group: int = 1,
                       topk_group: int = 1, norm_topk_prob: bool = True, routed_scaling_factor: float = 1.0,
                       shared_gate_up: torch.Tensor | None = None, shared_down: torch.Tensor | None = None,
-                      shared_folded: bool = False):
+                      shared_folded: bool = False, gate_weight_t: torch.Tensor | None = None):
     """``MoEBlock.__call__`` (mintext/modules/moe.py:240-266) on [B, S, D] or [N, D] tokens.
 
-    The router gate is ``Linear.__call__`` (mintext/modules/linear.py:123-147): a plain dense
-    GEMM ``x @ gate_weight`` ([D, E], the reference's kernel layout) in the compute dtype, f32
-    accumulation and one rounding to the compute dtype -- served by hipBLASLt through
-    ``torch.matmul``; everything after the logits runs on this package's kernels.  Returns
+    The router gate is ``Linear.__call__`` (mintext/modules/linear.py:123-147): a dense GEMM
+    ``x @ gate_weight`` ([D, E], the reference's kernel layout) with f32 accumulation and one
+    rounding to the compute dtype.  For bf16 tokens with D % 64 == 0 and few experts (E <= 32,
+    where it is faster; outside autograd) it runs fused with the top-k (``gate_route_topk``) on
+    the gate weight in the
+    nn.Linear layout -- pass ``gate_weight_t = gate_weight_linear_layout(gate_weight)``, a
+    load-time transform, to skip the per-call transpose; otherwise the GEMM is hipBLASLt's
+    (``torch.matmul``) and the top-k ``route_topk``.  Returns
     ``(output [.., D] float32, {"topk_indices", "topk_weights", "expert_counts"})``, the
     reference's aux data plus the counts of trainer.py:297-308.
     """
     shape = x.shape
     xf = x.reshape(-1, shape[-1])
-    logits = torch.matmul(xf, gate_weight.to(xf.dtype))
+    E = gate_weight.shape[-1]
+    needs_grad = torch.is_grad_enabled() and (x.requires_grad or gate_weight.requires_grad)
+    if not needs_grad and gate_fused_preferred(xf, E):
+        # gate GEMM + top-k in one kernel on the nn.Linear-layout gate weight
+        if gate_weight_t is None:
+            gate_weight_t = gate_weight_linear_layout(gate_weight.to(xf.dtype))
+        logits = None
+    else:
+        logits = torch.matmul(xf, gate_weight.to(xf.dtype))
+        gate_weight_t = None
     out, idx, w, counts = moe_layer_forward(
         logits, xf, gate_up, down, k=k, scoring=scoring, bias=bias, n_group=n_group, topk_group=topk_group,
         norm_topk_prob=norm_topk_prob, routed_scaling_factor=routed_scaling_factor, shared_gate_up=shared_gate_up,
-        shared_down=shared_down, shared_folded=shared_folded, return_expert_counts=True)
+        shared_down=shared_down, shared_folded=shared_folded, return_expert_counts=True, gate_weight_t=gate_weight_t)
     return out.reshape(*shape[:-1], out.shape[-1]), {"topk_indices": idx, "topk_weights": w, "expert_counts": counts}
 
 

@@ -95,3 +95,52 @@ def test_bias_steers_selection(dev):
                         bias=torch.tensor([10.0, 0, 0, 0]), n_group=2, topk_group=1)
     assert (idx[:, 0] == 0).all()
     assert ((idx >= 0) & (idx < 4)).all()
+
+
+# ---- router gate GEMM fused with the top-k -----------------------------------------------------
+GATE_CASES = [
+    # (T, D, E, K, scoring, n_group, topk_group, scale, with_bias, shared)
+    (300, 4096, 8, 2, "softmax", 1, 1, 1.0, False, False),         # Mixtral shape
+    (257, 2048, 128, 8, "softmax", 1, 1, 1.0, False, False),       # Qwen3 shape
+    (130, 7168, 256, 8, "sigmoid_group", 8, 4, 2.5, True, False),  # DeepSeek-V3 shape
+    (64, 64, 16, 4, "sigmoid_group", 4, 2, 2.5, True, True),       # folded shared expert column
+    (33, 128, 3, 1, "softmax", 1, 1, 1.0, False, False),           # odd E, T
+]
+
+
+@pytest.mark.parametrize("T,D,E,K,scoring,ng,tg,scale,with_bias,shared", GATE_CASES)
+def test_gate_route_topk_fused(dev, T, D, E, K, scoring, ng, tg, scale, with_bias, shared):
+    """gate_route_topk: logits within one bf16 rounding of the float64 product x @ Wg, and the
+    selection / weights of route_topk on those bf16 logits, bit for bit."""
+    from mintext_amd.kernels import route_topk
+    from mintext_amd.kernels.router import gate_route_topk, gate_weight_linear_layout
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(T + E)
+    x = torch.randn(T, D, device=dev, generator=g).bfloat16()
+    wg = (torch.randn(D, E, device=dev, generator=g) * 0.02).bfloat16()  # reference kernel layout [D, E]
+    bias = (torch.randn(E, device=dev, generator=g) * 1e-3) if with_bias else None
+    kw = dict(scoring=scoring, bias=bias, n_group=ng, topk_group=tg, routed_scaling_factor=scale)
+    se = E if shared else None
+    wt = gate_weight_linear_layout(wg)
+    assert torch.equal(wt, wg.t().contiguous())
+    idx, w, lg = gate_route_topk(x, wt, K, shared_expert=se, return_logits=True, **kw)
+    ref = x.double().cpu() @ wg.double().cpu()
+    got = lg.double().cpu()
+    assert ((got - ref).abs() <= 2.0 ** -8 * ref.abs() + 1e-4).all()
+    idx2, w2 = route_topk(lg, K, shared_expert=se, **kw)
+    assert torch.equal(idx, idx2) and torch.equal(w, w2)
+    idx3, w3 = gate_route_topk(x, wt, K, shared_expert=se, **kw)  # deterministic
+    assert torch.equal(idx, idx3) and torch.equal(w, w3)
+
+
+def test_gate_route_topk_unsupported_shapes_raise(dev):
+    from mintext_amd._lib import MtxError
+    from mintext_amd.kernels.router import gate_route_topk
+
+    x = torch.randn(8, 64, device=dev)
+    with pytest.raises(MtxError):
+        gate_route_topk(x, torch.randn(8, 64, device=dev), 2)  # f32 tokens
+    xb = x.bfloat16()
+    with pytest.raises(MtxError):
+        gate_route_topk(xb, torch.randn(300, 64, device=dev).bfloat16(), 2)  # E > 256
