@@ -52,6 +52,28 @@ def test_route_large_bit_exact(dev, N, K, E, D):
     assert torch.equal(st, x[torch.from_numpy(perm // K).to(dev)])
 
 
+@pytest.mark.parametrize("N,K,E", [(384, 3, 31), (900, 4, 9), (2048, 2, 8), (2049, 2, 8), (18432, 1, 1),
+                                   (18433, 1, 1), (5, 8, 2), (2500, 3, 31), (32768, 2, 32), (40000, 1, 17)])
+def test_route_few_experts_bit_exact(dev, N, K, E):
+    """E <= 32 and ids x (E+1) <= 36864 take the one-workgroup sort (bucket tables of 9, 17
+    and 33 entries; the cases at the limit and one id past it), larger products the chunked
+    sort.  Ragged sizes, about 1% out-of-range ids (sorted last, uncounted)."""
+    from mintext_amd.kernels.moe_dispatch import _route_impl
+
+    rng = np.random.default_rng(N * 7 + E)
+    idx = rng.integers(0, E, (N, K)).astype(np.int32)
+    bad = rng.random((N, K)) < 0.01
+    idx[bad] = rng.choice(np.array([-3, E, E + 5], np.int32), bad.sum())
+    x = torch.randn(N, 64, device=dev, dtype=torch.bfloat16)
+    st, si, gs, inv = _route_impl(x, _t(idx, dev), E)
+    key = np.where((idx >= 0) & (idx < E), idx, E).ravel()
+    perm = np.argsort(key, kind="stable")
+    np.testing.assert_array_equal(si.cpu().numpy(), perm)
+    np.testing.assert_array_equal(inv.cpu().numpy(), np.argsort(perm))
+    np.testing.assert_array_equal(gs.cpu().numpy(), np.bincount(key, minlength=E + 1)[:E])
+    assert torch.equal(st, x[torch.from_numpy(perm // K).to(dev)])
+
+
 def test_route_out_of_range_ids_sorted_last(dev):
     from mintext_amd.kernels import route
 
