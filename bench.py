@@ -432,6 +432,34 @@ def fp8_vendor_study(steps=10, warmup=3):
     return 0
 
 
+def copy_study(steps=20, warmup=3):
+    """The practical HBM ceiling for read+write streams on this box: a device-to-device copy
+    (torch copy_) of 64 MiB to 1 GiB, bytes read + bytes written per second.  Sizes up to about
+    128 MiB partly stay in the 256 MB MALL between repetitions; the larger ones are HBM.  The
+    dispatch and combine kernels move comparable volumes (C2: 201.5 / 268.6 MB)."""
+    import torch
+
+    out = {"study": "copy", "unit": "GB/s (read + write)", "sizes_MiB": {}}
+    for mib in (64, 128, 256, 512, 1024):
+        src = torch.empty(mib << 20, dtype=torch.uint8, device="cuda")
+        src.fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(warmup):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(steps):
+            dst.copy_(src)
+        e.record()
+        torch.cuda.synchronize()
+        t = s.elapsed_time(e) / steps * 1e-3
+        out["sizes_MiB"][mib] = {"us": round(t * 1e6, 1), "GBs": round(2 * (mib << 20) / t / 1e9, 1)}
+        del src, dst
+    print(json.dumps(out))
+    return 0
+
+
 def gate_study(steps=20, warmup=5):
     """The router gate GEMM + top-k on the C2, C3 and C4 shapes: hipBLASLt's dense gate GEMM
     (torch.matmul, [T,D] x [D,E]) followed by route_topk, against the fused gate_route_topk (the
@@ -492,10 +520,11 @@ def main(argv=None):
                     help="only run 3 plain 256 MiB device copies (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--graph", action="store_true",
                     help="also time the step captured in a HIP graph and replayed (reported as hip_graph)")
-    ap.add_argument("--study", choices=["gemm-power", "fp8-vendor", "gate"], default=None,
+    ap.add_argument("--study", choices=["gemm-power", "fp8-vendor", "gate", "copy"], default=None,
                     help="gemm-power: GEMM timings on normal vs all-zero data (clock / issue-efficiency study); "
                          "fp8-vendor: C4 blockwise fp8 GEMMs beside hipBLASLt's per-tensor / rowwise fp8 GEMMs; "
-                         "gate: router gate GEMM + top-k, hipBLASLt + route_topk vs the fused kernel")
+                         "gate: router gate GEMM + top-k, hipBLASLt + route_topk vs the fused kernel; "
+                         "copy: device-to-device copy bandwidth (the practical read+write HBM ceiling)")
     a = ap.parse_args(argv)
     if a.study == "gemm-power":
         return gemm_power_study(a.steps if a.steps != 20 else 10, a.warmup)
@@ -503,6 +532,8 @@ def main(argv=None):
         return fp8_vendor_study(a.steps if a.steps != 20 else 10, a.warmup)
     if a.study == "gate":
         return gate_study(a.steps, a.warmup)
+    if a.study == "copy":
+        return copy_study(a.steps, a.warmup)
     if a.copy_calibration:
         import torch
 

@@ -1177,11 +1177,21 @@ static int launch_v3(const mf::Args& a, int64_t grid, hipStream_t st) {
                      dim3(128 * MTX_V3_WN), 0, st, a);
   return check_launch();
 }
+#ifndef MTX_V3S_WM
+#define MTX_V3S_WM 2
+#endif
+#ifndef MTX_V3S_WN
+#define MTX_V3S_WN 2
+#endif
+#ifndef MTX_V3S_NST
+#define MTX_V3S_NST 3
+#endif
 template <int MODE, int EPI>
 static int launch_v3_small(const mf::Args& a, int64_t grid, hipStream_t st) {
   if (grid <= 0) return MTX_OK;
   grid = round_up(grid, 8);
-  hipLaunchKernelGGL((mf::gmm_v3_kernel<MODE, EPI, 2, 2, 128, 3>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((mf::gmm_v3_kernel<MODE, EPI, MTX_V3S_WM, MTX_V3S_WN, 128, MTX_V3S_NST>), dim3((unsigned)grid),
+                     dim3(64 * MTX_V3S_WM * MTX_V3S_WN), 0, st, a);
   return check_launch();
 }
 
