@@ -174,8 +174,9 @@ __global__ __launch_bounds__(256) void gmm_generic_kernel(const T* __restrict__ 
                                                           const MTile* __restrict__ tiles,
                                                           const int* __restrict__ count, int64_t Kred,
                                                           int64_t Nout, T* __restrict__ C) {
-  __shared__ float As[16][65];
-  __shared__ float Bs[16][65];
+  constexpr int KS = 32;  // reduction elements per step; the next step's operands load during this one
+  __shared__ float As[KS][65];
+  __shared__ float Bs[KS][65];
   if ((int)blockIdx.x >= count[0]) return;
   const MTile t = tiles[blockIdx.x];
   const int64_t I = Nout / 2;
@@ -196,11 +197,17 @@ __global__ __launch_bounds__(256) void gmm_generic_kernel(const T* __restrict__ 
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
-  for (int64_t k0 = 0; k0 < Kred; k0 += 16) {
-    for (int i = threadIdx.x; i < 16 * 64; i += 256) {
-      const int kk = i % 16, rr = i / 16;
+  // per thread and step: 8 elements of the 64 x KS A tile (k fastest: coalesced rows) and 8 of
+  // the KS x 64 W tile (n fastest), zero outside the group / matrix
+  constexpr int PT = KS * 64 / 256;
+  float ra[PT], rb[PT];
+  auto load = [&](int64_t k0) {
+#pragma unroll
+    for (int u = 0; u < PT; ++u) {
+      const int i = threadIdx.x + u * 256;
+      const int kk = i % KS, rr = i / KS;
       const int64_t r = t.r0 + rr, k = k0 + kk;
-      As[kk][rr] = (r < t.r1 && k < Kred) ? gld<T>(A, r * Kred + k) : 0.0f;
+      ra[u] = (r < t.r1 && k < Kred) ? gld<T>(A, r * Kred + k) : 0.0f;
       const int nn = i % 64, kb = i / 64;
       const int64_t k2 = k0 + kb;
       float b = 0.0f;
@@ -212,11 +219,21 @@ __global__ __launch_bounds__(256) void gmm_generic_kernel(const T* __restrict__ 
         const int64_t n = n0 + nn;
         if (n < Nout && k2 < Kred) b = (MODE == 0) ? gld<T>(We, k2 * Nout + n) : gld<T>(We, n * Kred + k2);
       }
-      Bs[kb][nn] = b;
+      rb[u] = b;
+    }
+  };
+  load(0);
+  for (int64_t k0 = 0; k0 < Kred; k0 += KS) {
+#pragma unroll
+    for (int u = 0; u < PT; ++u) {
+      const int i = threadIdx.x + u * 256;
+      As[i % KS][i / KS] = ra[u];
+      Bs[i / 64][i % 64] = rb[u];
     }
     __syncthreads();
+    if (k0 + KS < Kred) load(k0 + KS);
 #pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
+    for (int kk = 0; kk < KS; ++kk) {
       float a[4], b[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
