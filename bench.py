@@ -112,7 +112,7 @@ def _zipf_bias(E, s, rng, beta=0.55):
     return (-beta * s * np.log(rank)).astype(np.float32)
 
 
-def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_graph=False):
+def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_graph=False, gather=True):
     import torch
 
     from mintext_amd import _lib
@@ -157,18 +157,30 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
     flops_fwd = 2.0 * Mg * D * 2 * I + 2.0 * Mg * I * D
     fp8 = cfg["dtype"] == "fp8"
     if fp8:
-        from mintext_amd.kernels.fp8 import grouped_matmul_fp8, grouped_matmul_fp8_swiglu, quantize_fp8_weights
+        from mintext_amd.kernels.fp8 import (grouped_matmul_fp8, grouped_matmul_fp8_swiglu,
+                                             grouped_matmul_fp8_swiglu_gathered, quantize_fp8_rows,
+                                             quantize_fp8_weights)
         from mintext_amd.kernels.moe_dispatch import route_quantize_fp8
 
         guq, gus = quantize_fp8_weights(gate_up)
         dnq, dns = quantize_fp8_weights(down)
+    # the route's row gather inside the gate_up GEMM's operand loads (no sorted copy written)
+    from mintext_amd.kernels.grouped_matmul import gathered_swiglu_supported, grouped_matmul_swiglu_gathered
+    from mintext_amd.kernels.moe_dispatch import route_indices
+
+    gather = gather and cfg_name != "qwen3_bwd" and (D >= 256 if fp8 else gathered_swiglu_supported(x, gate_up))
 
     def step(timed):
         with torch.no_grad():
             idx, w = route_topk(logits, K, shared_expert=E if fold else None, **rkw)
             if timed:
                 t_disp.start()
-            if fp8:
+            if gather:
+                # permutation only; fp8: the tokens quantised in token order (1x128 groups)
+                if fp8:
+                    xq, xs = quantize_fp8_rows(x)
+                si, gs, _ = route_indices(idx, Eg)
+            elif fp8:
                 # 1x128 quantisation of the tokens fused into their dispatch
                 sq, ss, si, gs, _ = route_quantize_fp8(x, idx, E)
             else:
@@ -176,7 +188,12 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
             if timed:
                 t_disp.stop()
                 t_gu.start()
-            if fp8:
+            if gather:
+                if fp8:
+                    yq, ys = grouped_matmul_fp8_swiglu_gathered(xq, xs, si, Kc, guq, gus, gs)
+                else:
+                    y = grouped_matmul_swiglu_gathered(x, si, Kc, gate_up, gs)
+            elif fp8:
                 yq, ys = grouped_matmul_fp8_swiglu(sq, ss, guq, gus, gs)
             else:
                 y = grouped_matmul_swiglu(st, gate_up, gs)
@@ -271,12 +288,17 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
     tokens_per_s = T / (ms * 1e-3)
     gemm_ms = gu_ms + dn_ms
     # dispatch: token rows read once (bf16; fp8 runs quantise them in the same pass), sorted rows
-    # written (fp8 codes + 1x128 f32 scales for fp8), indices; combine: expert rows, weights,
+    # written (fp8 codes + 1x128 f32 scales for fp8), indices; with the gather in the gate_up
+    # GEMM only the indices (permutation + inverse written), plus for fp8 the token-order
+    # quantisation (bf16 rows read, codes + scales written).  combine: expert rows, weights,
     # permutation, f32 output (+ the bf16 shared-expert output when it is added in the pass)
     xb = 4 if cfg["dtype"] == "f32" else 2  # bytes per element of the token rows and expert outputs
-    disp_b = T * D * xb + Mg * D * (1 if fp8 else xb) + T * Kc * 4 + Mg * 4 + Eg * 4
-    if fp8:
-        disp_b += Mg * (D // 128) * 4
+    if gather:
+        disp_b = T * Kc * 4 + 2 * Mg * 4 + Eg * 4 + (T * D * 2 + T * D + T * (D // 128) * 4 if fp8 else 0)
+    else:
+        disp_b = T * D * xb + Mg * D * (1 if fp8 else xb) + T * Kc * 4 + Mg * 4 + Eg * 4
+        if fp8:
+            disp_b += Mg * (D // 128) * 4
     comb_b = Mg * D * xb + T * Kc * 4 + Mg * 4 + T * D * 4 + (T * D * xb if shared is not None and not fold else 0)
     res = {
         "metric": "MoE layer fwd tokens/s + grouped-GEMM TFLOP/s (% of peak), 1x MI355X",
@@ -300,7 +322,8 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
                                  flops_fwd / ((gu_ms + dn_ms) * 1e-3) / 1e12, 1),
                  "frac_of_peak": round((flops_fwd / (gemm_ms * 1e-3) / 1e12) / peak, 4),
                  "gate_up_ms": round(gu_ms, 4), "down_ms": round(dn_ms, 4)},
-        "dispatch_combine": {"dispatch_ms": round(t_disp.mean_ms(), 4), "combine_ms": round(t_comb.mean_ms(), 4),
+        "dispatch_combine": {"rows_gathered_in_gate_up": gather,
+                             "dispatch_ms": round(t_disp.mean_ms(), 4), "combine_ms": round(t_comb.mean_ms(), 4),
                              "dispatch_GBs": round(disp_b / (t_disp.mean_ms() * 1e-3) / 1e9, 1) if t_disp.pairs else None,
                              "combine_GBs": round(comb_b / (t_comb.mean_ms() * 1e-3) / 1e9, 1) if t_comb.pairs else None},
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 1), "peak": peak,
@@ -518,6 +541,9 @@ def main(argv=None):
                     help="deepseek: shared expert run as its own one-group GEMMs (default) or folded into the routed GEMMs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 plain 256 MiB device copies (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--no-gather", action="store_true",
+                    help="materialise the sorted tokens in the dispatch (route) instead of gathering the token "
+                         "rows inside the gate_up GEMM")
     ap.add_argument("--graph", action="store_true",
                     help="also time the step captured in a HIP graph and replayed (reported as hip_graph)")
     ap.add_argument("--study", choices=["gemm-power", "fp8-vendor", "gate", "copy"], default=None,
@@ -551,7 +577,7 @@ def main(argv=None):
               "collectives); run with --gpus 1", file=sys.stderr)
         return 2
     res = run(a.config, a.steps, a.warmup, cpu_baseline=not a.no_cpu_baseline, shared_mode=a.shared,
-              use_graph=a.graph)
+              use_graph=a.graph, gather=not a.no_gather)
     print(json.dumps(res))
     return 0
 

@@ -40,6 +40,9 @@
  *   mtx_quant_fp8_weights  <- no counterpart; 128x128 weight blocks
  *   mtx_gmm_fp8            <- no counterpart; blockwise-fp8 form of mtx_gmm
  *   mtx_gmm_fp8_swiglu     <- no counterpart; blockwise-fp8 form of mtx_gmm_swiglu
+ *   mtx_gmm_gathered       <- route's row gather (moe_dispatch.py:67,76) fused into the
+ *                             forward GEMMs of MoEExperts._forward_kernel (moe.py:161-196)
+ *   mtx_gmm_fp8_swiglu_gathered <- the same for the blockwise-fp8 gate_up GEMM
  *   mtx_transpose_batched  <- _import_expert_weights / _export_expert_weights
  *                             (mintext/checkpoint/conversion.py:80-166), on the device
  */
@@ -209,6 +212,17 @@ int mtx_tgmm(const void* x, const void* g, const int32_t* group_sizes, int dtype
 int mtx_gmm_tiled(int op, const void* x, const void* w, const int32_t* group_sizes, int dtype,
                   int64_t M, int64_t Kin, int64_t Kout, int64_t E, int64_t tile_m, int64_t tile_group,
                   void* out, void* workspace, int64_t workspace_bytes, void* stream);
+/* route (moe_dispatch.py:47-81, its row gather) fused into the A operand of the forward GEMMs
+ * (MoEExperts._forward_kernel, mintext/modules/moe.py:161-196): x [x_rows,Kin] in token order
+ * (BF16), row_index [M] = sort_indices of mtx_route (computed without tokens), index_div = K
+ * (top-k): sorted row r is x[row_index[r] / index_div] (indices clamped into x).  op
+ * MTX_GMM_OP_FWD or MTX_GMM_OP_SWIGLU as in mtx_gmm_tiled; results equal mtx_gmm /
+ * mtx_gmm_swiglu on the routed rows bit for bit.  Shapes outside the direct-to-LDS kernels
+ * (Kin % 32, 16-byte alignment, Kout % 256 / I % 128) return MTX_ERR_UNSUPPORTED.         */
+int mtx_gmm_gathered(int op, const void* x, int64_t x_rows, const int32_t* row_index,
+                     int64_t index_div, const void* w, const int32_t* group_sizes, int dtype,
+                     int64_t M, int64_t Kin, int64_t Kout, int64_t E, void* out,
+                     void* workspace, int64_t workspace_bytes, void* stream);
 /* out[r,j] = silu(h[r,j]) * h[r,I+j]   h [M,2I] -> out [M,I] (F32/BF16)                */
 int mtx_swiglu(const void* h, int dtype, int64_t M, int64_t I, void* out, void* stream);
 /* VJP of mtx_swiglu: dh [M,2I] from h [M,2I] and dy [M,I]                              */
@@ -247,6 +261,16 @@ int mtx_gmm_fp8_swiglu(const uint8_t* xq, const float* x_scale, const uint8_t* w
                        int64_t M, int64_t Kin, int64_t I, int64_t E,
                        uint8_t* out_q, float* out_scale, void* out_bf16,
                        void* workspace, int64_t workspace_bytes, void* stream);
+/* mtx_gmm_fp8_swiglu on gathered rows: xq [x_rows,Kin] + x_scale [x_rows,Kin/128] in token
+ * order (mtx_quant_fp8_rows of the tokens), sorted row r = token row row_index[r] / index_div
+ * (route fused into the A loads, as mtx_gmm_gathered).  Bit-identical to mtx_route_quant_fp8 +
+ * mtx_gmm_fp8_swiglu; Kin < 256 returns MTX_ERR_UNSUPPORTED.                               */
+int mtx_gmm_fp8_swiglu_gathered(const uint8_t* xq, const float* x_scale, int64_t x_rows,
+                                const int32_t* row_index, int64_t index_div, const uint8_t* w_q,
+                                const float* w_scale, const int32_t* group_sizes,
+                                int64_t M, int64_t Kin, int64_t I, int64_t E,
+                                uint8_t* out_q, float* out_scale, void* out_bf16,
+                                void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---- expert weight layouts -------------------------------------------------------------
  * Batched transpose-copy (the per-expert HF <-> fused conversions of

@@ -187,6 +187,10 @@ struct Args {
   const int* count;
   const MTileF8* tiles;
   int M, K, N, I, ldc;
+  // gathered rows (v4 kernel): sorted row r reads row gather[r] / gather_div of xq and xs
+  // (clamped to [0, gather_rows)); the dispatch copy of the quantised tokens is never written
+  const int32_t* gather;
+  int gather_div, gather_rows;
 };
 
 enum { EPI_STORE = 0, EPI_SWIGLU_Q = 1 };
@@ -796,24 +800,28 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
     const uint8_t* B;
     const float* sp;  // this lane's scale source for k-block 0 (stride 1 float per block)
   };
+  // row of xq / xs that holds sorted row r (the row itself unless the rows are gathered)
+  auto x_row = [&](int r) -> int {
+    return p.gather ? min(max(p.gather[r], 0) / p.gather_div, p.gather_rows - 1) : r;
+  };
   auto make_src = [&](const Tile& T) -> Src {
     Src S;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int seg = wave * 2 + i;
       const int r = seg * 16 + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
-      S.aoff[i] = (uint32_t)min(T.r0 + r, T.r1 - 1) * (uint32_t)p.K + (uint32_t)(c * 16);
+      S.aoff[i] = (uint32_t)x_row(min(T.r0 + r, T.r1 - 1)) * (uint32_t)p.K + (uint32_t)(c * 16);
       S.boff[i] = (uint32_t)b_row(T, r) * (uint32_t)p.K + (uint32_t)(c * 16);
     }
     S.B = p.wq + (int64_t)T.e * p.N * p.K;
     if (wave < 4) {
-      S.sp = p.xs + (int64_t)min(T.r0 + 64 * wave + lane, T.r1 - 1) * nkb;
+      S.sp = p.xs + (int64_t)x_row(min(T.r0 + 64 * wave + lane, T.r1 - 1)) * nkb;
     } else if (wave == 4) {
       const int h = lane & 1;
       const int nblk = (EPI == EPI_SWIGLU_Q) ? (h * (p.I / 128) + T.n_tile) : (T.n_tile * 2 + h);
       S.sp = p.ws + ((int64_t)T.e * (p.N / 128) + nblk) * nkb;
     } else {
-      S.sp = p.xs + (int64_t)T.r0 * nkb;  // filler load, keeps the per-wave load count uniform
+      S.sp = p.xs + (int64_t)x_row(T.r0) * nkb;  // filler load, keeps the per-wave load count uniform
     }
     return S;
   };
@@ -1083,7 +1091,9 @@ static inline int64_t f8_ws_bytes(int64_t M, int64_t E, int64_t BM) {
 
 template <int EPI>
 static int launch_fp8(const f8::Args& a, const int32_t* gs, int64_t E, int64_t nn, void* ws, hipStream_t st) {
-  const bool off32 = (int64_t)a.M * a.K < (int64_t(1) << 32) && (int64_t)a.N * a.K < (int64_t(1) << 32);
+  const int64_t a_rows = a.gather ? a.gather_rows : a.M;
+  const bool off32 = a_rows * a.K < (int64_t(1) << 32) && (int64_t)a.N * a.K < (int64_t(1) << 32);
+  if (a.gather && !(off32 && a.K >= 256)) return MTX_ERR_UNSUPPORTED;  // gathered rows: v4 kernel only
   if (off32 && a.K >= 256) {
     int* count = (int*)ws;
     MTileF8* tiles = (MTileF8*)((char*)ws + 256);
@@ -1190,16 +1200,21 @@ extern "C" int mtx_gmm_fp8(const uint8_t* xq, const float* x_scale, const uint8_
   return launch_fp8<f8::EPI_STORE>(a, group_sizes, E, Kout / 256, workspace, (hipStream_t)stream);
 }
 
-extern "C" int mtx_gmm_fp8_swiglu(const uint8_t* xq, const float* x_scale, const uint8_t* w_q, const float* w_scale,
-                                  const int32_t* group_sizes, int64_t M, int64_t Kin, int64_t I, int64_t E,
-                                  uint8_t* out_q, float* out_scale, void* out_bf16, void* workspace,
-                                  int64_t workspace_bytes, void* stream) {
+static int fp8_swiglu_entry(const uint8_t* xq, const float* x_scale, const uint8_t* w_q, const float* w_scale,
+                            const int32_t* group_sizes, int64_t M, int64_t Kin, int64_t I, int64_t E, uint8_t* out_q,
+                            float* out_scale, void* out_bf16, void* workspace, int64_t workspace_bytes, void* stream,
+                            const int32_t* gather, int64_t gather_div, int64_t gather_rows) {
   int rc = fp8_checks(xq, x_scale, w_q, w_scale, group_sizes, M, Kin, E, workspace, workspace_bytes);
   if (rc) return rc;
   if (I <= 0 || I % 128) return MTX_ERR_ARG;
+  if (gather && (gather_div < 1 || gather_div > INT32_MAX || gather_rows < 1 || gather_rows > INT32_MAX / 2))
+    return MTX_ERR_ARG;
   if (M == 0) return MTX_OK;
   if (!out_q || !out_scale) return MTX_ERR_ARG;
   f8::Args a{};
+  a.gather = gather;
+  a.gather_div = (int)gather_div;
+  a.gather_rows = (int)gather_rows;
   a.xq = xq;
   a.xs = x_scale;
   a.wq = w_q;
@@ -1213,4 +1228,22 @@ extern "C" int mtx_gmm_fp8_swiglu(const uint8_t* xq, const float* x_scale, const
   a.I = (int)I;
   a.ldc = (int)I;
   return launch_fp8<f8::EPI_SWIGLU_Q>(a, group_sizes, E, I / 128, workspace, (hipStream_t)stream);
+}
+
+extern "C" int mtx_gmm_fp8_swiglu(const uint8_t* xq, const float* x_scale, const uint8_t* w_q, const float* w_scale,
+                                  const int32_t* group_sizes, int64_t M, int64_t Kin, int64_t I, int64_t E,
+                                  uint8_t* out_q, float* out_scale, void* out_bf16, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  return fp8_swiglu_entry(xq, x_scale, w_q, w_scale, group_sizes, M, Kin, I, E, out_q, out_scale, out_bf16, workspace,
+                          workspace_bytes, stream, nullptr, 1, 0);
+}
+
+extern "C" int mtx_gmm_fp8_swiglu_gathered(const uint8_t* xq, const float* x_scale, int64_t x_rows,
+                                           const int32_t* row_index, int64_t index_div, const uint8_t* w_q,
+                                           const float* w_scale, const int32_t* group_sizes, int64_t M, int64_t Kin,
+                                           int64_t I, int64_t E, uint8_t* out_q, float* out_scale, void* out_bf16,
+                                           void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!row_index && M > 0) return MTX_ERR_ARG;
+  return fp8_swiglu_entry(xq, x_scale, w_q, w_scale, group_sizes, M, Kin, I, E, out_q, out_scale, out_bf16, workspace,
+                          workspace_bytes, stream, row_index, index_div, x_rows);
 }

@@ -407,6 +407,12 @@ struct Args {
   float* split_part = nullptr;  //   fp32 partials, kSplitItems slots of BM x BN per XCD
   int split_on = 0;             //   0: every tile runs whole
   int ncu_x = 32;               //   CUs per XCD (one resident 256-row workgroup per CU)
+  // FWD/SWIGLU with gathered A rows: sorted row r of the group layout reads row
+  // gather[r] / gather_div of A (clamped to [0, gather_rows)), i.e. the dispatch gather of
+  // token rows happens in the A loads and the sorted copy is never written.
+  const int32_t* gather = nullptr;
+  int gather_div = 1;
+  int gather_rows = 0;
 };
 
 // ---- tile loaders ------------------------------------------------------------------------------
@@ -830,6 +836,7 @@ __global__ __launch_bounds__(WM* WN * 64, MTX_V3_WPE) void gmm_v3_kernel(Args p)
       // rows past the tile's group repeat its last row: never used, and cache hits
       int gr = r0 + r;
       gr = gr < r1 ? gr : r1 - 1;
+      if (MODE == FWD && p.gather) gr = min(max(p.gather[gr], 0) / p.gather_div, p.gather_rows - 1);
       aoff[i] = ((uint32_t)gr * (uint32_t)p.Kred + (uint32_t)(c * 8)) * 2u;
     }
   }
@@ -1235,10 +1242,17 @@ static constexpr int kMinBM = 64;
 // FWD / DLHS / SWIGLU driver. mode: 0 fwd, 1 dlhs, 2 swiglu.  tile_m (0, 128 or 256 rows per
 // m-tile) and tile_group (0 or m-tiles per scheduling group) override the shape heuristics on the
 // bf16 MFMA path; every configuration computes each output element with the same MFMA sequence.
+// With gather (FWD / SWIGLU, bf16): A holds gather_rows rows and sorted row r reads A row
+// gather[r] / gather_div; only the direct-to-LDS kernels take it (MTX_ERR_UNSUPPORTED otherwise).
 static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs, int dtype, int64_t M, int64_t Kred,
                       int64_t Nout, int64_t I, int64_t E, void* out, void* ws, int64_t ws_bytes, hipStream_t st,
-                      int tile_m = 0, int tile_group = 0) {
+                      int tile_m = 0, int tile_group = 0, const int32_t* gather = nullptr, int64_t gather_div = 1,
+                      int64_t gather_rows = 0) {
   if (dtype != MTX_F32 && dtype != MTX_BF16) return MTX_ERR_ARG;
+  const bool gath = gather != nullptr;
+  if (gath && (mode == 1 || gather_div < 1 || gather_div > INT32_MAX || gather_rows < 1 ||
+               gather_rows > INT32_MAX / 2))
+    return MTX_ERR_ARG;
   int rc = common_checks(M, E, ws, ws_bytes, kMinBM);
   if (rc != MTX_OK) return rc;
   if (Kred < 0 || Nout < 0 || Kred > INT32_MAX / 2 || Nout > INT32_MAX / 2) return MTX_ERR_ARG;
@@ -1249,10 +1263,16 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
   if (mode == 2 && Nout != 2 * I) return MTX_ERR_ARG;
   // bf16 MFMA eligibility
   const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)w % 16 == 0);
+  if (gath && !(dtype == MTX_BF16 && aligned && Kred % mf::BK == 0 && Kred > 0)) return MTX_ERR_UNSUPPORTED;
   if (dtype == MTX_BF16 && aligned && Kred % mf::BK == 0 && Kred > 0) {
     mf::Args a;
     a.A = (const uint16_t*)x;
     a.B = (const uint16_t*)w;
+    if (gath) {
+      a.gather = gather;
+      a.gather_div = (int)gather_div;
+      a.gather_rows = (int)gather_rows;
+    }
     a.C = (uint16_t*)out;
     a.count = wsp.count;
     a.offsets = wsp.offsets;
@@ -1271,9 +1291,11 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
     // n-tiles run (C3 shapes: 6-7 % less time than 8).
     a.gm = tile_group > 0 ? tile_group : ((M / E) <= 256 ? MTX_GM_SMALL : 8);
     // tile shape: 256-row tiles when groups are large on average, else 128
-    const bool v3ok = Kred % mf::v3::BKS == 0 && M * Kred * 2 < (int64_t(1) << 32) &&
+    const bool v3ok = Kred % mf::v3::BKS == 0 && (gath ? gather_rows : M) * Kred * 2 < (int64_t(1) << 32) &&
                       Kred * Nout * 2 < (int64_t(1) << 32);
     const bool big_m = v3ok && (tile_m == 256 || (tile_m == 0 && (M / E) >= MTX_V3_SMALL_MEAN));
+    if (gath && (!v3ok || !((mode == 2 && I % 128 == 0) || (mode == 0 && Nout % 256 == 0))))
+      return MTX_ERR_UNSUPPORTED;
     if (mode == 2 && I % 128 == 0) {
       if (big_m) {
         rc = launch_build_tiles(gs, E, M, 256, wsp, st);
@@ -1321,6 +1343,7 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
     }
   }
   // generic path (exact fp32 FMA; also bf16 shapes the MFMA tiling does not cover)
+  if (gath) return MTX_ERR_UNSUPPORTED;
   rc = launch_build_tiles(gs, E, M, kMinBM, wsp, st);
   if (rc) return rc;
   const int64_t ntile_max = gmm_max_tiles(M, E, kMinBM);
@@ -1405,6 +1428,25 @@ extern "C" int mtx_gmm_tiled(int op, const void* x, const void* w, const int32_t
       if (Kout < 0) return MTX_ERR_ARG;
       return gmm_driver(2, x, w, group_sizes, dtype, M, Kin, 2 * Kout, Kout, E, out, workspace, workspace_bytes, st,
                         tm, tg);
+    default:
+      return MTX_ERR_ARG;
+  }
+}
+
+extern "C" int mtx_gmm_gathered(int op, const void* x, int64_t x_rows, const int32_t* row_index, int64_t index_div,
+                                const void* w, const int32_t* group_sizes, int dtype, int64_t M, int64_t Kin,
+                                int64_t Kout, int64_t E, void* out, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  if (!row_index && M > 0) return MTX_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  switch (op) {
+    case MTX_GMM_OP_FWD:
+      return gmm_driver(0, x, w, group_sizes, dtype, M, Kin, Kout, 0, E, out, workspace, workspace_bytes, st, 0, 0,
+                        row_index, index_div, x_rows);
+    case MTX_GMM_OP_SWIGLU:
+      if (Kout < 0) return MTX_ERR_ARG;
+      return gmm_driver(2, x, w, group_sizes, dtype, M, Kin, 2 * Kout, Kout, E, out, workspace, workspace_bytes, st,
+                        0, 0, row_index, index_div, x_rows);
     default:
       return MTX_ERR_ARG;
   }

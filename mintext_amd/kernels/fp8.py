@@ -79,3 +79,31 @@ def grouped_matmul_fp8_swiglu(xq, x_scale, w_q, w_scale, group_sizes, *, return_
     if return_bf16:
         return yq, ys, yb
     return yq, ys
+
+
+def grouped_matmul_fp8_swiglu_gathered(xq, x_scale, sort_indices, top_k: int, w_q, w_scale, group_sizes, *,
+                                       return_bf16: bool = False):
+    """``grouped_matmul_fp8_swiglu`` on the routed rows of token-order inputs: xq [T, Kin] and
+    x_scale [T, Kin/128] are ``quantize_fp8_rows(tokens)``; sorted row r is token row
+    ``sort_indices[r] // top_k``, read by the GEMM's operand loads (the dispatch copy is never
+    written).  Same bits as ``route_quantize_fp8`` + ``grouped_matmul_fp8_swiglu``.
+    """
+    gs = _gs(group_sizes)
+    dev = L.require_device(xq, x_scale, sort_indices, w_q, w_scale, gs)
+    si = sort_indices.to(torch.int32).contiguous()
+    T, Kin = xq.shape
+    E, two_i, Kin2 = w_q.shape
+    M = si.numel()
+    if Kin2 != Kin or two_i % 2 or top_k < 1:
+        raise ValueError("fp8 gathered gmm+swiglu shape mismatch")
+    I = two_i // 2
+    yq = torch.empty((M, I), dtype=torch.float8_e4m3fn, device=dev)
+    ys = torch.empty((M, I // 128), dtype=torch.float32, device=dev)
+    yb = torch.empty((M, I), dtype=torch.bfloat16, device=dev) if return_bf16 else None
+    ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
+    L.call("mtx_gmm_fp8_swiglu_gathered", L.ptr(xq.contiguous()), L.ptr(x_scale.contiguous()), T, L.ptr(si), top_k,
+           L.ptr(w_q.contiguous()), L.ptr(w_scale.contiguous()), L.ptr(gs), M, Kin, I, E, L.ptr(yq), L.ptr(ys),
+           L.ptr(yb), L.ptr(ws), ws.numel(), L.stream(dev))
+    if return_bf16:
+        return yq, ys, yb
+    return yq, ys

@@ -208,6 +208,45 @@ def grouped_matmul_swiglu(x: torch.Tensor, weights: torch.Tensor, group_sizes: t
     return out
 
 
+def gathered_swiglu_supported(tokens: torch.Tensor, weights: torch.Tensor) -> bool:
+    """Whether ``grouped_matmul_swiglu_gathered`` takes these operands: bf16, K_in a multiple of
+    64, I a multiple of 128, 16-byte aligned, 32-bit operand offsets (the direct-to-LDS kernels)."""
+    if tokens.dtype != torch.bfloat16 or weights.dtype != torch.bfloat16 or tokens.dim() != 2 or weights.dim() != 3:
+        return False
+    T, Kin = tokens.shape
+    two_i = weights.shape[2]
+    return (Kin > 0 and Kin % 64 == 0 and two_i % 256 == 0 and T * Kin * 2 < 2 ** 32 and Kin * two_i * 2 < 2 ** 32
+            and tokens.is_contiguous() and weights.is_contiguous()
+            and tokens.data_ptr() % 16 == 0 and weights.data_ptr() % 16 == 0)
+
+
+def grouped_matmul_swiglu_gathered(tokens: torch.Tensor, sort_indices: torch.Tensor, top_k: int,
+                                   weights: torch.Tensor, group_sizes: torch.Tensor) -> torch.Tensor:
+    """``grouped_matmul_swiglu(route(tokens, ...)[0], weights, group_sizes)`` with the route's row
+    gather done by the GEMM's operand loads: sorted row r is ``tokens[sort_indices[r] // top_k]``
+    (moe_dispatch.py:67,76), read straight from the token-order tensor, so the sorted copy is
+    never written.  Same bits as the two steps.  bf16 only; shapes outside the direct-to-LDS
+    kernels (K_in % 32, I % 128) raise MtxError with status MTX_ERR_UNSUPPORTED.  Forward only.
+    """
+    gs = _gs(group_sizes)
+    dev = L.require_device(tokens, sort_indices, weights, gs)
+    _check_float(tokens, weights)
+    x = tokens.contiguous()
+    w = weights.contiguous()
+    si = sort_indices.to(torch.int32).contiguous()
+    T, Kin = x.shape
+    E, Kin2, two_i = w.shape
+    M = si.numel()
+    if Kin2 != Kin or two_i % 2 or gs.numel() != E or top_k < 1:
+        raise ValueError("grouped_matmul_swiglu_gathered shape mismatch")
+    I = two_i // 2
+    out = torch.empty((M, I), dtype=x.dtype, device=dev)
+    ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
+    L.call("mtx_gmm_gathered", L.MTX_GMM_OP_SWIGLU, L.ptr(x), T, L.ptr(si), top_k, L.ptr(w), L.ptr(gs),
+           L.dtype_code(x.dtype), M, Kin, I, E, L.ptr(out), L.ptr(ws), ws.numel(), L.stream(dev))
+    return out
+
+
 def swiglu(h: torch.Tensor) -> torch.Tensor:
     """silu(h[:, :I]) * h[:, I:] (mintext/modules/moe.py:195-196) as one HIP kernel."""
     dev = L.require_device(h)

@@ -44,6 +44,29 @@ def _route_impl(tokens: torch.Tensor, topk_indices: torch.Tensor, num_experts: i
     return sorted_tokens, sort_indices, group_sizes, inverse
 
 
+def route_indices(topk_indices: torch.Tensor, num_experts: int):
+    """The permutation half of ``route`` (moe_dispatch.py:70-79) without moving any rows.
+
+    Returns (sort_indices [N*K] i32, group_sizes [E] i32, inverse [N*K] i32) equal to the ones
+    ``route`` returns.  For GEMMs that read the token rows through ``sort_indices`` themselves
+    (``grouped_matmul_swiglu_gathered``, ``grouped_matmul_fp8_swiglu_gathered``), so that the
+    sorted copy of the tokens is never written.  Forward only.
+    """
+    dev = L.require_device(topk_indices)
+    idx = _as_i32(topk_indices).contiguous()
+    N, K = idx.shape
+    M = N * K
+    sort_indices = torch.empty((M,), dtype=torch.int32, device=dev)
+    group_sizes = torch.empty((num_experts,), dtype=torch.int32, device=dev)
+    inverse = torch.empty((M,), dtype=torch.int32, device=dev)
+    ws = L.workspace(L.query("mtx_route_workspace_size", N, K, num_experts), dev)
+    L.call("mtx_route", None, L.dtype_code(torch.float32), L.ptr(idx), N, 0, K, num_experts, None,
+           L.ptr(sort_indices), L.ptr(group_sizes), L.ptr(inverse), None, None, L.ptr(ws), ws.numel(),
+           L.stream(dev))
+    sort_indices._mtx_inverse = inverse
+    return sort_indices, group_sizes, inverse
+
+
 def _inverse_of(sort_indices: torch.Tensor) -> torch.Tensor:
     """Inverse permutation; reuses the one route() computed when sort_indices is unchanged."""
     cached = getattr(sort_indices, "_mtx_inverse", None)

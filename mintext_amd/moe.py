@@ -12,16 +12,22 @@ and added, or -- after the load-time ``fold_shared_expert`` -- folded into the r
 as an always-routed extra expert with weight 1, whose output the combine adds after the
 routed sum (the same sum, in the same order, as routed_out + shared_out).
 
+Without autograd (and for the shapes the direct-to-LDS GEMM takes) the route's row gather runs
+inside the gate_up GEMM: ``route_indices`` computes the permutation only and the GEMM reads
+token row ``sort_indices[r] // K`` for sorted row r, so the sorted copy of the tokens is never
+written (the same bits as route + GEMM).
+
 ``moe_experts_forward_fp8`` is the blockwise-fp8 variant (no reference counterpart):
-activations quantised in 1x128 groups, routed with their scales, fp8 gate_up GEMM with the
-SwiGLU and the 1x128 re-quantisation fused, fp8 down GEMM to bf16, float32 combine.
+activations quantised in 1x128 groups in token order, fp8 gate_up GEMM on the gathered rows
+with the SwiGLU and the 1x128 re-quantisation fused, fp8 down GEMM to bf16, float32 combine.
 """
 from __future__ import annotations
 
 import torch
 
-from .kernels.grouped_matmul import grouped_matmul_swiglu, grouped_matmul_vjp
-from .kernels.moe_dispatch import route, route_quantize_fp8, unroute, unroute_add
+from .kernels.grouped_matmul import (gathered_swiglu_supported, grouped_matmul_swiglu, grouped_matmul_swiglu_gathered,
+                                     grouped_matmul_vjp)
+from .kernels.moe_dispatch import route, route_indices, route_quantize_fp8, unroute, unroute_add
 from .kernels.router import gate_fused_preferred, gate_route_topk, gate_weight_linear_layout, route_topk
 from .kernels.swiglu import swiglu_autograd
 
@@ -42,16 +48,21 @@ def moe_experts_forward(x: torch.Tensor, topk_indices: torch.Tensor, topk_weight
     gate_up = gate_up.to(x.dtype)
     down = down.to(x.dtype)
     E = gate_up.shape[0]
-    sorted_tokens, sort_indices, group_sizes = route(x, topk_indices, E)
     needs_grad = torch.is_grad_enabled() and (
         x.requires_grad or gate_up.requires_grad or down.requires_grad or topk_weights.requires_grad)
     if fuse_swiglu is None:
         fuse_swiglu = not needs_grad
-    if fuse_swiglu:
-        inter = grouped_matmul_swiglu(sorted_tokens, gate_up, group_sizes, tiling=gate_up_tiling)
+    if fuse_swiglu and not needs_grad and gate_up_tiling is None and gathered_swiglu_supported(x, gate_up):
+        # the route's row gather runs in the gate_up GEMM's operand loads: no sorted copy
+        sort_indices, group_sizes, _ = route_indices(topk_indices, E)
+        inter = grouped_matmul_swiglu_gathered(x, sort_indices, topk_indices.shape[1], gate_up, group_sizes)
     else:
-        h = grouped_matmul_vjp(sorted_tokens, gate_up, group_sizes, tiling=gate_up_tiling)
-        inter = swiglu_autograd(h)
+        sorted_tokens, sort_indices, group_sizes = route(x, topk_indices, E)
+        if fuse_swiglu:
+            inter = grouped_matmul_swiglu(sorted_tokens, gate_up, group_sizes, tiling=gate_up_tiling)
+        else:
+            h = grouped_matmul_vjp(sorted_tokens, gate_up, group_sizes, tiling=gate_up_tiling)
+            inter = swiglu_autograd(h)
     out = grouped_matmul_vjp(inter, down, group_sizes, tiling=down_tiling)
     if addend is None:
         res = unroute(out, sort_indices, topk_weights, topk_indices.shape[1])
@@ -175,12 +186,21 @@ def moe_experts_forward_fp8(x: torch.Tensor, topk_indices: torch.Tensor, topk_we
                             gate_up_q: torch.Tensor, gate_up_scale: torch.Tensor, down_q: torch.Tensor,
                             down_scale: torch.Tensor) -> torch.Tensor:
     """Blockwise-fp8 expert layer; weights from ``quantize_fp8_weights`` ([E, Kout, Kin] e4m3)."""
-    from .kernels.fp8 import grouped_matmul_fp8, grouped_matmul_fp8_swiglu
+    from .kernels.fp8 import (grouped_matmul_fp8, grouped_matmul_fp8_swiglu, grouped_matmul_fp8_swiglu_gathered,
+                              quantize_fp8_rows)
 
     E = gate_up_q.shape[0]
-    # 1x128 quantisation of the tokens fused into their dispatch (each row read once)
-    sq, ss, sort_indices, group_sizes, _ = route_quantize_fp8(x, topk_indices, E)
-    yq, ys = grouped_matmul_fp8_swiglu(sq, ss, gate_up_q, gate_up_scale, group_sizes)
+    T, D = x.shape
+    if D >= 256 and T * D < 2 ** 32 and gate_up_q.shape[1] * D < 2 ** 32:
+        # tokens quantised in token order; the gate_up GEMM gathers their rows (no sorted copy)
+        xq, xs = quantize_fp8_rows(x)
+        sort_indices, group_sizes, _ = route_indices(topk_indices, E)
+        yq, ys = grouped_matmul_fp8_swiglu_gathered(xq, xs, sort_indices, topk_indices.shape[1], gate_up_q,
+                                                    gate_up_scale, group_sizes)
+    else:
+        # 1x128 quantisation of the tokens fused into their dispatch (each row read once)
+        sq, ss, sort_indices, group_sizes, _ = route_quantize_fp8(x, topk_indices, E)
+        yq, ys = grouped_matmul_fp8_swiglu(sq, ss, gate_up_q, gate_up_scale, group_sizes)
     out = grouped_matmul_fp8(yq, ys, down_q, down_scale, group_sizes)
     return unroute(out, sort_indices, topk_weights, topk_indices.shape[1])
 

@@ -164,3 +164,39 @@ def test_gmm_fp8_more_zero_tiles_than_threads(dev):
     assert (out[500:] == 0).all()
     deq = O.gmm_fp8(_u8(xq)[:500], xs.cpu().numpy()[:500], _u8(wq), ws.cpu().numpy(), gs)
     assert rel_err(out.float().cpu().numpy()[:500], deq) < 1e-2
+
+
+@pytest.mark.parametrize("T,K,E,D,I", [(2048, 8, 128, 2048, 768), (1000, 2, 8, 256, 128), (333, 3, 5, 512, 256)])
+def test_gmm_fp8_swiglu_gathered_equals_route_quant(dev, T, K, E, D, I):
+    """Quantising the tokens in token order and gathering their rows inside the fp8 gate_up GEMM
+    gives the bits of the fused quantise-and-dispatch followed by the fp8 gate_up GEMM."""
+    from mintext_amd.kernels.fp8 import (grouped_matmul_fp8_swiglu, grouped_matmul_fp8_swiglu_gathered,
+                                         quantize_fp8_rows, quantize_fp8_weights)
+    from mintext_amd.kernels.moe_dispatch import route_indices, route_quantize_fp8
+
+    rng = np.random.default_rng(T + D)
+    idx = _t(rng.integers(0, E, (T, K)).astype(np.int32), dev)
+    x = torch.randn(T, D, device=dev).bfloat16()
+    wq, wsc = quantize_fp8_weights((torch.randn(E, D, 2 * I, device=dev) * 0.02).bfloat16())
+    sq, ss, si, gs, _ = route_quantize_fp8(x, idx, E)
+    yq1, ys1, yb1 = grouped_matmul_fp8_swiglu(sq, ss, wq, wsc, gs, return_bf16=True)
+    xq, xs = quantize_fp8_rows(x)
+    si2, gs2, _ = route_indices(idx, E)
+    yq2, ys2, yb2 = grouped_matmul_fp8_swiglu_gathered(xq, xs, si2, K, wq, wsc, gs2, return_bf16=True)
+    assert torch.equal(yq1.view(torch.uint8), yq2.view(torch.uint8))
+    assert torch.equal(ys1, ys2) and torch.equal(yb1, yb2)
+
+
+def test_gmm_fp8_swiglu_gathered_short_k_unsupported(dev):
+    from mintext_amd import _lib as L
+    from mintext_amd.kernels.fp8 import grouped_matmul_fp8_swiglu_gathered, quantize_fp8_rows, quantize_fp8_weights
+    from mintext_amd.kernels.moe_dispatch import route_indices
+
+    T, K, E, D, I = 200, 2, 4, 128, 128  # K_in = 128 < 256: only the non-persistent kernels take it
+    idx = _t(np.random.default_rng(0).integers(0, E, (T, K)).astype(np.int32), dev)
+    xq, xs = quantize_fp8_rows(torch.randn(T, D, device=dev).bfloat16())
+    wq, wsc = quantize_fp8_weights((torch.randn(E, D, 2 * I, device=dev) * 0.02).bfloat16())
+    si, gs, _ = route_indices(idx, E)
+    with pytest.raises(L.MtxError) as ei:
+        grouped_matmul_fp8_swiglu_gathered(xq, xs, si, K, wq, wsc, gs)
+    assert ei.value.status == L.MTX_ERR_UNSUPPORTED

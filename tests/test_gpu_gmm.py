@@ -384,3 +384,56 @@ def test_gmm_group_sizes_past_m_are_clipped(dev):
         w = (torch.randn(3, 64, 256, device=dev) * 0.1).to(cdt)
         out = grouped_matmul(x, w, _t(gs, dev))
         _close(out.float().cpu().numpy(), O.gmm(x.float().cpu().numpy(), w.float().cpu().numpy(), gs), tol)
+
+
+@pytest.mark.parametrize("T,K,E,D,I", [(512, 2, 8, 256, 256), (1000, 8, 64, 512, 128), (300, 3, 5, 128, 384)])
+def test_gmm_swiglu_gathered_equals_route_then_gmm(dev, T, K, E, D, I):
+    """The route's row gather inside the gate_up GEMM's operand loads gives the bits of
+    route + grouped_matmul_swiglu, and route_indices the route's permutation and sizes."""
+    from mintext_amd.kernels import route
+    from mintext_amd.kernels.grouped_matmul import grouped_matmul_swiglu, grouped_matmul_swiglu_gathered
+    from mintext_amd.kernels.moe_dispatch import route_indices
+
+    rng = np.random.default_rng(T + E)
+    idx = _t(rng.integers(0, E, (T, K)).astype(np.int32), dev)
+    x = torch.randn(T, D, device=dev).bfloat16()
+    w = (torch.randn(E, D, 2 * I, device=dev) * 0.05).bfloat16()
+    st, si, gs = route(x, idx, E)
+    si2, gs2, inv2 = route_indices(idx, E)
+    assert torch.equal(si, si2) and torch.equal(gs, gs2)
+    assert torch.equal(inv2.long(), torch.argsort(si2.long()))
+    ref = grouped_matmul_swiglu(st, w, gs)
+    out = grouped_matmul_swiglu_gathered(x, si2, K, w, gs2)
+    assert torch.equal(out, ref)
+
+
+def test_gmm_gathered_fwd_op_and_unsupported_shapes(dev):
+    """mtx_gmm_gathered's plain forward op equals grouped_matmul on the routed rows; shapes
+    outside the direct-to-LDS kernels are refused with MTX_ERR_UNSUPPORTED."""
+    from mintext_amd import _lib as L
+    from mintext_amd.kernels import grouped_matmul, route
+    from mintext_amd.kernels.grouped_matmul import grouped_matmul_swiglu_gathered
+    from mintext_amd.kernels.moe_dispatch import route_indices
+
+    T, K, E, D, N = 700, 2, 6, 256, 512
+    rng = np.random.default_rng(5)
+    idx = _t(rng.integers(0, E, (T, K)).astype(np.int32), dev)
+    x = torch.randn(T, D, device=dev).bfloat16()
+    w = (torch.randn(E, D, N, device=dev) * 0.05).bfloat16()
+    st, si, gs = route(x, idx, E)
+    ref = grouped_matmul(st, w, gs)
+    M = T * K
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
+    L.call("mtx_gmm_gathered", L.MTX_GMM_OP_FWD, L.ptr(x), T, L.ptr(si), K, L.ptr(w), L.ptr(gs),
+           L.dtype_code(torch.bfloat16), M, D, N, E, L.ptr(out), L.ptr(ws), ws.numel(), L.stream(dev))
+    assert torch.equal(out, ref)
+    si2, gs2, _ = route_indices(idx, E)
+    w_odd = (torch.randn(E, D, 2 * 64, device=dev) * 0.05).bfloat16()  # I = 64: not a 128 multiple
+    with pytest.raises(L.MtxError) as ei:
+        grouped_matmul_swiglu_gathered(x, si2, K, w_odd, gs2)
+    assert ei.value.status == L.MTX_ERR_UNSUPPORTED
+    xf = torch.randn(T, D, device=dev)  # f32 tokens: no gathered path
+    with pytest.raises(L.MtxError) as ei:
+        grouped_matmul_swiglu_gathered(xf, si2, K, w.float()[:, :, :256].contiguous(), gs2)
+    assert ei.value.status == L.MTX_ERR_UNSUPPORTED
