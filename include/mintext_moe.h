@@ -233,8 +233,8 @@ int mtx_swiglu_bwd(const void* h, const void* dy, int dtype, int64_t M, int64_t 
  * q = RNE(x / scale).  Weights: 128x128 blocks over (Kout, Kin), stored k-contiguous
  * w_q [E,Kout,Kin] with w_scale [E,Kout/128,Kin/128] (the per-expert nn.Linear layout).
  * Kin, Kout (and I) must be multiples of 128.  The block scales passed to the GEMMs must be
- * finite and nonzero (the quantisers never produce 0).  mtx_quant_fp8_rows needs x 16-byte
- * and xq 8-byte aligned (MTX_ERR_ARG otherwise).                                          */
+ * finite and nonzero (the quantisers never produce 0).  mtx_quant_fp8_rows needs x and xq
+ * 16-byte aligned (MTX_ERR_ARG otherwise).                                                 */
 int mtx_quant_fp8_rows(const void* x, int dtype, int64_t M, int64_t D,
                        uint8_t* xq, float* x_scale, void* stream);
 /* mtx_quant_fp8_rows followed by mtx_route of the codes and scales, in one row pass: tokens

@@ -33,50 +33,64 @@ constexpr int BK = 128;  // bytes of k per step == one scale block
 __device__ __forceinline__ int lds_off(int r, int c) { return r * 128 + ((c ^ (r & 7) ^ ((r >> 3) & 7)) << 4); }
 
 // ---- quantisers ------------------------------------------------------------------------------
-// 16 bytes per lane: a 128-group spans LPG = 128 / EPL lanes (16 for bf16, 32 for f32), so a
-// wave quantises 64 / LPG groups per step; the group maximum is a butterfly within those lanes.
-template <typename T>
+// 16 elements per lane: a 128-group spans 8 lanes, a wave quantises 8 groups per step, and each
+// lane issues the loads of UNR steps before their math so that UNR x 16-32 bytes are in flight
+// per lane; the group maximum is a butterfly within the 8 lanes.  Codes go out as one 16-byte
+// store per lane.
+template <typename T, int UNR>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const T* __restrict__ x, int64_t M, int64_t D,
                                                          uint8_t* __restrict__ xq, float* __restrict__ xs) {
-  constexpr int EPL = 16 / sizeof(T), LPG = 128 / EPL, GPW = 64 / LPG;
+  constexpr int EPL = 16, LPG = 8, GPW = 8, NLD = EPL * (int)sizeof(T) / 16;  // 16-byte loads per lane
   const int lane = threadIdx.x & 63;
   const int sub = lane / LPG, gl = lane % LPG;
   const int64_t ng = D / 128;
   const int64_t total = M * ng;
   const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
-  for (int64_t t0 = wid * GPW; t0 < total; t0 += nw * GPW) {
-    const int64_t t = t0 + sub;
-    const bool ok = t < total;
-    const int64_t tt = ok ? t : total - 1;
-    const int64_t r = tt / ng, g = tt % ng;
-    const int64_t base = r * D + g * 128 + gl * EPL;
-    float v[EPL];
-    const u32x4 raw = *(const u32x4*)(x + base);
-    if constexpr (sizeof(T) == 4) {
+  for (int64_t t0 = wid * GPW; t0 < total; t0 += nw * GPW * UNR) {
+    u32x4 raw[UNR][NLD];
+    int64_t tt[UNR];
+    bool ok[UNR];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(raw[i]);
-    } else {
+    for (int u = 0; u < UNR; ++u) {
+      const int64_t t = t0 + (int64_t)u * nw * GPW + sub;
+      ok[u] = t < total;
+      tt[u] = ok[u] ? t : total - 1;
+      const int64_t r = tt[u] / ng, g = tt[u] - r * ng;
+      const u32x4* src = (const u32x4*)(x + r * D + g * 128 + gl * EPL);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[2 * i] = __uint_as_float(raw[i] << 16);
-        v[2 * i + 1] = __uint_as_float(raw[i] & 0xffff0000u);
-      }
+      for (int l = 0; l < NLD; ++l) raw[u][l] = src[l];
     }
-    float m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) m = fmaxf(m, fabsf(v[i]));
+    for (int u = 0; u < UNR; ++u) {
+      float v[EPL];
 #pragma unroll
-    for (int off = LPG / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    float sc = m / 448.0f;
-    if (sc == 0.0f) sc = 1.0f;
-    uint32_t q[EPL / 4];
+      for (int l = 0; l < NLD; ++l) {
+        if constexpr (sizeof(T) == 4) {
 #pragma unroll
-    for (int i = 0; i < EPL / 4; ++i)
-      q[i] = e4m3_pack4(v[4 * i] / sc, v[4 * i + 1] / sc, v[4 * i + 2] / sc, v[4 * i + 3] / sc);
-    if (ok) {
-      if constexpr (EPL == 8) *(uint2*)(xq + base) = make_uint2(q[0], q[1]);
-      else *(uint32_t*)(xq + base) = q[0];
+          for (int i = 0; i < 4; ++i) v[4 * l + i] = __uint_as_float(raw[u][l][i]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v[8 * l + 2 * i] = __uint_as_float(raw[u][l][i] << 16);
+            v[8 * l + 2 * i + 1] = __uint_as_float(raw[u][l][i] & 0xffff0000u);
+          }
+        }
+      }
+      float m = 0.0f;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) m = fmaxf(m, fabsf(v[i]));
+#pragma unroll
+      for (int off = LPG / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+      float sc = m / 448.0f;
+      if (sc == 0.0f) sc = 1.0f;
+      u32x4 q;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        q[i] = e4m3_pack4(v[4 * i] / sc, v[4 * i + 1] / sc, v[4 * i + 2] / sc, v[4 * i + 3] / sc);
+      if (!ok[u]) continue;
+      const int64_t r = tt[u] / ng, g = tt[u] - r * ng;
+      *(u32x4*)(xq + r * D + g * 128 + gl * EPL) = q;
       if (gl == 0) xs[r * ng + g] = sc;
     }
   }
@@ -1139,16 +1153,17 @@ extern "C" int mtx_quant_fp8_rows(const void* x, int dtype, int64_t M, int64_t D
   if (M < 0 || D < 0 || D % 128 != 0 || (dtype != MTX_F32 && dtype != MTX_BF16)) return MTX_ERR_ARG;
   if (M == 0 || D == 0) return MTX_OK;
   if (!x || !xq || !x_scale) return MTX_ERR_ARG;
-  if (((uintptr_t)x % 16) || ((uintptr_t)xq % 8)) return MTX_ERR_ARG;
-  int64_t blocks = ceil_div(M * (D / 128), 16);
+  if (((uintptr_t)x % 16) || ((uintptr_t)xq % 16)) return MTX_ERR_ARG;
+  constexpr int UNR = 4;
+  int64_t blocks = ceil_div(M * (D / 128), (int64_t)8 * 4 * UNR);  // 8 groups per wave and step, 4 waves
   if (blocks > 16384) blocks = 16384;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MTX_F32)
-    hipLaunchKernelGGL(f8::quant_rows_kernel<float>, dim3(blocks), dim3(256), 0, st, (const float*)x, M, D, xq,
-                       x_scale);
-  else
-    hipLaunchKernelGGL(f8::quant_rows_kernel<uint16_t>, dim3(blocks), dim3(256), 0, st, (const uint16_t*)x, M, D,
+    hipLaunchKernelGGL((f8::quant_rows_kernel<float, UNR>), dim3(blocks), dim3(256), 0, st, (const float*)x, M, D,
                        xq, x_scale);
+  else
+    hipLaunchKernelGGL((f8::quant_rows_kernel<uint16_t, UNR>), dim3(blocks), dim3(256), 0, st, (const uint16_t*)x,
+                       M, D, xq, x_scale);
   return check_launch();
 }
 

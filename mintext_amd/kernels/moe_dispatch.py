@@ -64,6 +64,7 @@ def route_indices(topk_indices: torch.Tensor, num_experts: int):
            L.ptr(sort_indices), L.ptr(group_sizes), L.ptr(inverse), None, None, L.ptr(ws), ws.numel(),
            L.stream(dev))
     sort_indices._mtx_inverse = inverse
+    sort_indices._mtx_version = sort_indices._version
     return sort_indices, group_sizes, inverse
 
 

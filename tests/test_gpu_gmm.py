@@ -402,6 +402,9 @@ def test_gmm_swiglu_gathered_equals_route_then_gmm(dev, T, K, E, D, I):
     si2, gs2, inv2 = route_indices(idx, E)
     assert torch.equal(si, si2) and torch.equal(gs, gs2)
     assert torch.equal(inv2.long(), torch.argsort(si2.long()))
+    from mintext_amd.kernels.moe_dispatch import _inverse_of
+
+    assert _inverse_of(si2) is inv2  # the combine reuses the route's inverse
     ref = grouped_matmul_swiglu(st, w, gs)
     out = grouped_matmul_swiglu_gathered(x, si2, K, w, gs2)
     assert torch.equal(out, ref)
