@@ -28,6 +28,51 @@ __device__ __forceinline__ bool cand_better(float av, int ai, float bv, int bi) 
   return av > bv || (av == bv && ai < bi);
 }
 
+// Lane exchange of step S of an all-reduce over aligned groups of 2^(S+1) lanes.  Steps 0 and 1
+// are xor 1 and xor 2 (DPP quad permutes); steps 2 and 3 pair the two halves of each 8- and
+// 16-lane group by mirroring (DPP row_half_mirror, row_mirror), which after steps 0..S-1 hands
+// every lane the same partial as the xor-4 / xor-8 partner would; step 4 is xor 16 (ds_swizzle,
+// bitmask mode) and step 5 xor 32.  So the results equal an xor butterfly's bit for bit (the
+// combines are commutative), without the LDS round trip of ds_bpermute.
+template <int S>
+__device__ __forceinline__ int lane_xchg(int v) {
+  if constexpr (S == 0) return __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false);
+  else if constexpr (S == 1) return __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false);
+  else if constexpr (S == 2) return __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false);
+  else if constexpr (S == 3) return __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false);
+  else if constexpr (S == 4) return __builtin_amdgcn_ds_swizzle(v, 0x401F);
+  else return __shfl_xor(v, 32);
+}
+template <int S>
+__device__ __forceinline__ float lane_xchg(float v) {
+  return __int_as_float(lane_xchg<S>(__float_as_int(v)));
+}
+// Arg-max of (value, id, payload) over the token's L lanes (L a power of two <= 64).
+template <int S = 0>
+__device__ __forceinline__ void group_argmax(float& bv, int& bi, float& bs, int L) {
+  if constexpr (S < 6) {
+    if ((1 << S) < L) {
+      const float ov = lane_xchg<S>(bv);
+      const int oi = lane_xchg<S>(bi);
+      const float os = lane_xchg<S>(bs);
+      if (cand_better(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+        bs = os;
+      }
+      group_argmax<S + 1>(bv, bi, bs, L);
+    }
+  }
+}
+// Sum over the token's L lanes (the same additions as an xor butterfly).
+template <int S = 0>
+__device__ __forceinline__ float group_sum(float x, int L) {
+  if constexpr (S < 6) {
+    if ((1 << S) < L) return group_sum<S + 1>(x + lane_xchg<S>(x), L);
+  }
+  return x;
+}
+
 // Selection for one token t owned by lanes li = 0..L-1 of its lane group (tok_local: the
 // token's slot in the workgroup, for the group-limited scratch in smem).  load(e) returns the
 // token's logit of expert e as f32.  Every thread of the workgroup must call it (the
@@ -110,12 +155,7 @@ __device__ __forceinline__ void router_select(Load load, int64_t t, bool tok_ok,
       const int e = li + L * v;
       if (ok[v] && !taken[v] && cand_better(sel[v], e, bv, bi)) { bv = sel[v]; bi = e; bs = pay[v]; }
     }
-    for (int off = 1; off < L; off <<= 1) {
-      const float ov = __shfl_xor(bv, off);
-      const int oi = __shfl_xor(bi, off);
-      const float os = __shfl_xor(bs, off);
-      if (cand_better(ov, oi, bv, bi)) { bv = ov; bi = oi; bs = os; }
-    }
+    group_argmax(bv, bi, bs, L);
 #pragma unroll
     for (int v = 0; v < V; ++v)
       if (li + L * v == bi) taken[v] = true;
@@ -132,13 +172,12 @@ __device__ __forceinline__ void router_select(Load load, int64_t t, bool tok_ok,
 #pragma unroll
     for (int v = 0; v < V; ++v)
       if (ok[v]) part += expf(pay[v] - lmax);
-    for (int off = 1; off < L; off <<= 1) part += __shfl_xor(part, off);
+    part = group_sum(part, L);
     full_den = part;
     float ek = mine ? expf(my_s - lmax) : 0.0f;
     float den;
     if (norm) {
-      den = ek;
-      for (int off = 1; off < L; off <<= 1) den += __shfl_xor(den, off);
+      den = group_sum(ek, L);
     } else {
       den = full_den;
     }
@@ -146,8 +185,7 @@ __device__ __forceinline__ void router_select(Load load, int64_t t, bool tok_ok,
   } else {
     float wk = mine ? my_s : 0.0f;
     if (norm) {
-      float den = wk;
-      for (int off = 1; off < L; off <<= 1) den += __shfl_xor(den, off);
+      const float den = group_sum(wk, L);
       wk = wk / (den + 1e-20f);
     }
     w = wk;
