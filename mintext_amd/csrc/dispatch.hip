@@ -836,7 +836,8 @@ extern "C" int mtx_route(const void* tokens, int dtype, const int32_t* topk_idx,
   if ((token_scales == nullptr) != (sorted_scales == nullptr)) return MTX_ERR_ARG;
   if (token_scales && D % 128 != 0) return MTX_ERR_ARG;
   if (N * K > INT32_MAX) return MTX_ERR_ARG;
-  if (!sort_indices || !group_sizes) return MTX_ERR_ARG;
+  // no ids (N == 0): only the E zero group sizes are written; the other buffers may be empty
+  if (!group_sizes || (N * K > 0 && (!sort_indices || !topk_idx))) return MTX_ERR_ARG;
   const RoutePlan p = route_plan(N, K, E);
   if (!workspace || workspace_bytes < mtx_route_workspace_size(N, K, E)) return MTX_ERR_WORKSPACE;
   hipStream_t st = (hipStream_t)stream;
@@ -885,7 +886,7 @@ extern "C" int mtx_route_quant_fp8(const void* tokens, int dtype, const int32_t*
   if (N < 0 || D < 0 || K < 1 || E < 1 || E > 1023) return MTX_ERR_ARG;
   if (dtype != MTX_F32 && dtype != MTX_BF16) return MTX_ERR_ARG;
   if (D % 128 != 0 || N * K > INT32_MAX) return MTX_ERR_ARG;
-  if (!sort_indices || !group_sizes || !topk_idx) return MTX_ERR_ARG;
+  if (!group_sizes || (N > 0 && (!sort_indices || !topk_idx))) return MTX_ERR_ARG;
   if (N > 0 && D > 0 && (!tokens || !sorted_q || !sorted_scales)) return MTX_ERR_ARG;
   if ((uintptr_t)tokens % 16 != 0 || (uintptr_t)sorted_q % 16 != 0 || (uintptr_t)sorted_scales % 4 != 0)
     return MTX_ERR_ARG;

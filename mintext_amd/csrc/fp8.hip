@@ -1222,7 +1222,8 @@ static int fp8_swiglu_entry(const uint8_t* xq, const float* x_scale, const uint8
   int rc = fp8_checks(xq, x_scale, w_q, w_scale, group_sizes, M, Kin, E, workspace, workspace_bytes);
   if (rc) return rc;
   if (I <= 0 || I % 128) return MTX_ERR_ARG;
-  if (gather && (gather_div < 1 || gather_div > INT32_MAX || gather_rows < 1 || gather_rows > INT32_MAX / 2))
+  if (gather && (gather_div < 1 || gather_div > INT32_MAX || gather_rows < 0 || gather_rows > INT32_MAX / 2 ||
+                 (gather_rows == 0 && M > 0)))
     return MTX_ERR_ARG;
   if (M == 0) return MTX_OK;
   if (!out_q || !out_scale) return MTX_ERR_ARG;

@@ -1250,8 +1250,8 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
                       int64_t gather_rows = 0) {
   if (dtype != MTX_F32 && dtype != MTX_BF16) return MTX_ERR_ARG;
   const bool gath = gather != nullptr;
-  if (gath && (mode == 1 || gather_div < 1 || gather_div > INT32_MAX || gather_rows < 1 ||
-               gather_rows > INT32_MAX / 2))
+  if (gath && (mode == 1 || gather_div < 1 || gather_div > INT32_MAX || gather_rows < 0 ||
+               gather_rows > INT32_MAX / 2 || (gather_rows == 0 && M > 0)))
     return MTX_ERR_ARG;
   int rc = common_checks(M, E, ws, ws_bytes, kMinBM);
   if (rc != MTX_OK) return rc;

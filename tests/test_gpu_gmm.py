@@ -440,3 +440,31 @@ def test_gmm_gathered_fwd_op_and_unsupported_shapes(dev):
     with pytest.raises(L.MtxError) as ei:
         grouped_matmul_swiglu_gathered(xf, si2, K, w.float()[:, :, :256].contiguous(), gs2)
     assert ei.value.status == L.MTX_ERR_UNSUPPORTED
+
+
+def test_gathered_paths_on_empty_inputs(dev):
+    """No tokens: the permutation-only route and both gathered GEMMs return empty results."""
+    from mintext_amd.kernels.fp8 import grouped_matmul_fp8_swiglu_gathered, quantize_fp8_rows, quantize_fp8_weights
+    from mintext_amd.kernels.grouped_matmul import grouped_matmul_swiglu_gathered
+    from mintext_amd.kernels.moe_dispatch import route_indices
+
+    E, K, D, I = 4, 2, 256, 128
+    idx = torch.zeros(0, K, dtype=torch.int32, device=dev)
+    si, gs, inv = route_indices(idx, E)
+    assert si.numel() == 0 and inv.numel() == 0 and gs.cpu().tolist() == [0] * E
+    x = torch.zeros(0, D, device=dev).bfloat16()
+    w = torch.randn(E, D, 2 * I, device=dev).bfloat16()
+    assert grouped_matmul_swiglu_gathered(x, si, K, w, gs).shape == (0, I)
+    xq, xs = quantize_fp8_rows(x)
+    wq, wsc = quantize_fp8_weights(w)
+    yq, ys = grouped_matmul_fp8_swiglu_gathered(xq, xs, si, K, wq, wsc, gs)
+    assert yq.shape == (0, I) and ys.shape == (0, 1)
+    from mintext_amd.kernels import route
+    from mintext_amd.moe import moe_experts_forward
+
+    st, si0, gs0 = route(x, idx, E)
+    assert st.shape == (0, D) and si0.numel() == 0 and gs0.cpu().tolist() == [0] * E
+    down = torch.randn(E, I, D, device=dev).bfloat16()
+    out = moe_experts_forward(x, idx, torch.zeros(0, K, device=dev), w, down)
+    assert out.shape == (0, D)
+
