@@ -125,7 +125,8 @@ int mtx_expert_bias_update(const int32_t* expert_counts, int64_t E, float rate, 
  * tokens [N,D] (F32/BF16/FP8E4M3), topk_idx [N,K] -> sorted_tokens [N*K,D] (same dtype),
  * sort_indices [N*K] (stable argsort of ravel(topk_idx): value = flat position n*K+k),
  * group_sizes [E], and optionally inverse [N*K] (inverse[sort_indices[j]] = j; may be NULL).
- * tokens / sorted_tokens may both be NULL to compute only the permutation.
+ * tokens / sorted_tokens may both be NULL to compute only the permutation.  N == 0 writes
+ * only the E zero group sizes (the other buffers may then be NULL).
  * token_scales [N,D/128] f32 (may be NULL) are gathered alongside into sorted_scales.
  * Rows are moved in token order (each token row read once, written to its K positions);
  * with inverse == NULL the inverse permutation is kept in the workspace.
