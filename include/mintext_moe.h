@@ -217,13 +217,14 @@ int mtx_gmm_tiled(int op, const void* x, const void* w, const int32_t* group_siz
  * (MoEExperts._forward_kernel, mintext/modules/moe.py:161-196): x [x_rows,Kin] in token order
  * (BF16), row_index [M] = sort_indices of mtx_route (computed without tokens), index_div = K
  * (top-k): sorted row r is x[row_index[r] / index_div] (indices clamped into x).  op
- * MTX_GMM_OP_FWD or MTX_GMM_OP_SWIGLU as in mtx_gmm_tiled; results equal mtx_gmm /
- * mtx_gmm_swiglu on the routed rows bit for bit.  Shapes outside the direct-to-LDS kernels
- * (Kin % 32, 16-byte alignment, Kout % 256 / I % 128) return MTX_ERR_UNSUPPORTED.         */
+ * MTX_GMM_OP_FWD or MTX_GMM_OP_SWIGLU, tile_m / tile_group as in mtx_gmm_tiled; results equal
+ * mtx_gmm_tiled on the routed rows bit for bit.  Shapes outside the direct-to-LDS kernels
+ * (Kin % 64, 16-byte alignment, Kout % 256 / I % 128) return MTX_ERR_UNSUPPORTED.         */
 int mtx_gmm_gathered(int op, const void* x, int64_t x_rows, const int32_t* row_index,
                      int64_t index_div, const void* w, const int32_t* group_sizes, int dtype,
-                     int64_t M, int64_t Kin, int64_t Kout, int64_t E, void* out,
-                     void* workspace, int64_t workspace_bytes, void* stream);
+                     int64_t M, int64_t Kin, int64_t Kout, int64_t E, int64_t tile_m,
+                     int64_t tile_group, void* out, void* workspace, int64_t workspace_bytes,
+                     void* stream);
 /* out[r,j] = silu(h[r,j]) * h[r,I+j]   h [M,2I] -> out [M,I] (F32/BF16)                */
 int mtx_swiglu(const void* h, int dtype, int64_t M, int64_t I, void* out, void* stream);
 /* VJP of mtx_swiglu: dh [M,2I] from h [M,2I] and dy [M,I]                              */

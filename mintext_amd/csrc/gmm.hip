@@ -1435,18 +1435,21 @@ extern "C" int mtx_gmm_tiled(int op, const void* x, const void* w, const int32_t
 
 extern "C" int mtx_gmm_gathered(int op, const void* x, int64_t x_rows, const int32_t* row_index, int64_t index_div,
                                 const void* w, const int32_t* group_sizes, int dtype, int64_t M, int64_t Kin,
-                                int64_t Kout, int64_t E, void* out, void* workspace, int64_t workspace_bytes,
-                                void* stream) {
+                                int64_t Kout, int64_t E, int64_t tile_m, int64_t tile_group, void* out,
+                                void* workspace, int64_t workspace_bytes, void* stream) {
   if (!row_index && M > 0) return MTX_ERR_ARG;
+  if (tile_m != 0 && tile_m != 128 && tile_m != 256) return MTX_ERR_ARG;
+  if (tile_group < 0 || tile_group > 64) return MTX_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
+  const int tm = (int)tile_m, tg = (int)tile_group;
   switch (op) {
     case MTX_GMM_OP_FWD:
-      return gmm_driver(0, x, w, group_sizes, dtype, M, Kin, Kout, 0, E, out, workspace, workspace_bytes, st, 0, 0,
+      return gmm_driver(0, x, w, group_sizes, dtype, M, Kin, Kout, 0, E, out, workspace, workspace_bytes, st, tm, tg,
                         row_index, index_div, x_rows);
     case MTX_GMM_OP_SWIGLU:
       if (Kout < 0) return MTX_ERR_ARG;
       return gmm_driver(2, x, w, group_sizes, dtype, M, Kin, 2 * Kout, Kout, E, out, workspace, workspace_bytes, st,
-                        0, 0, row_index, index_div, x_rows);
+                        tm, tg, row_index, index_div, x_rows);
     default:
       return MTX_ERR_ARG;
   }

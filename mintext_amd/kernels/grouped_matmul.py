@@ -221,12 +221,13 @@ def gathered_swiglu_supported(tokens: torch.Tensor, weights: torch.Tensor) -> bo
 
 
 def grouped_matmul_swiglu_gathered(tokens: torch.Tensor, sort_indices: torch.Tensor, top_k: int,
-                                   weights: torch.Tensor, group_sizes: torch.Tensor) -> torch.Tensor:
+                                   weights: torch.Tensor, group_sizes: torch.Tensor, *, tiling=None) -> torch.Tensor:
     """``grouped_matmul_swiglu(route(tokens, ...)[0], weights, group_sizes)`` with the route's row
     gather done by the GEMM's operand loads: sorted row r is ``tokens[sort_indices[r] // top_k]``
     (moe_dispatch.py:67,76), read straight from the token-order tensor, so the sorted copy is
-    never written.  Same bits as the two steps.  bf16 only; shapes outside the direct-to-LDS
-    kernels (K_in % 32, I % 128) raise MtxError with status MTX_ERR_UNSUPPORTED.  Forward only.
+    never written.  Same bits as the two steps (with the same ``tiling``, as for
+    ``grouped_matmul_swiglu``).  bf16 only; shapes outside the direct-to-LDS kernels (K_in % 64,
+    I % 128) raise MtxError with status MTX_ERR_UNSUPPORTED.  Forward only.
     """
     gs = _gs(group_sizes)
     dev = L.require_device(tokens, sort_indices, weights, gs)
@@ -242,8 +243,9 @@ def grouped_matmul_swiglu_gathered(tokens: torch.Tensor, sort_indices: torch.Ten
     I = two_i // 2
     out = torch.empty((M, I), dtype=x.dtype, device=dev)
     ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
+    tm, tg = _tile_args(tiling)
     L.call("mtx_gmm_gathered", L.MTX_GMM_OP_SWIGLU, L.ptr(x), T, L.ptr(si), top_k, L.ptr(w), L.ptr(gs),
-           L.dtype_code(x.dtype), M, Kin, I, E, L.ptr(out), L.ptr(ws), ws.numel(), L.stream(dev))
+           L.dtype_code(x.dtype), M, Kin, I, E, tm, tg, L.ptr(out), L.ptr(ws), ws.numel(), L.stream(dev))
     return out
 
 

@@ -52,10 +52,11 @@ def moe_experts_forward(x: torch.Tensor, topk_indices: torch.Tensor, topk_weight
         x.requires_grad or gate_up.requires_grad or down.requires_grad or topk_weights.requires_grad)
     if fuse_swiglu is None:
         fuse_swiglu = not needs_grad
-    if fuse_swiglu and not needs_grad and gate_up_tiling is None and gathered_swiglu_supported(x, gate_up):
+    if fuse_swiglu and not needs_grad and gathered_swiglu_supported(x, gate_up):
         # the route's row gather runs in the gate_up GEMM's operand loads: no sorted copy
         sort_indices, group_sizes, _ = route_indices(topk_indices, E)
-        inter = grouped_matmul_swiglu_gathered(x, sort_indices, topk_indices.shape[1], gate_up, group_sizes)
+        inter = grouped_matmul_swiglu_gathered(x, sort_indices, topk_indices.shape[1], gate_up, group_sizes,
+                                               tiling=gate_up_tiling)
     else:
         sorted_tokens, sort_indices, group_sizes = route(x, topk_indices, E)
         if fuse_swiglu:

@@ -429,8 +429,15 @@ def test_gmm_gathered_fwd_op_and_unsupported_shapes(dev):
     out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
     ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
     L.call("mtx_gmm_gathered", L.MTX_GMM_OP_FWD, L.ptr(x), T, L.ptr(si), K, L.ptr(w), L.ptr(gs),
-           L.dtype_code(torch.bfloat16), M, D, N, E, L.ptr(out), L.ptr(ws), ws.numel(), L.stream(dev))
+           L.dtype_code(torch.bfloat16), M, D, N, E, 0, 0, L.ptr(out), L.ptr(ws), ws.numel(), L.stream(dev))
     assert torch.equal(out, ref)
+    for tiling in ((128, 2, 256), (256, 1, 256)):  # explicit tilings (the autotuner's space)
+        from mintext_amd.kernels.grouped_matmul import grouped_matmul_swiglu
+
+        wg = (torch.randn(E, D, 2 * 128, device=dev) * 0.05).bfloat16()
+        si3, gs3, _ = route_indices(idx, E)
+        got = grouped_matmul_swiglu_gathered(x, si3, K, wg, gs3, tiling=tiling)
+        assert torch.equal(got, grouped_matmul_swiglu(st, wg, gs, tiling=tiling)), tiling
     si2, gs2, _ = route_indices(idx, E)
     w_odd = (torch.randn(E, D, 2 * 64, device=dev) * 0.05).bfloat16()  # I = 64: not a 128 multiple
     with pytest.raises(L.MtxError) as ei:
