@@ -79,6 +79,29 @@ def test_host_validation_rejects_bad_args(built):
     assert built.mtx_quant_fp8_weights(P, 1, 2, 128, 100, P, P, P) == _lib.MTX_ERR_ARG
     assert built.mtx_unroute(P, 1, P, P, 0, 4, 0, 8, P, 0, P) == _lib.MTX_ERR_ARG  # K = 0
     assert built.mtx_swiglu(P, 3, 4, 4, P, P) == _lib.MTX_ERR_ARG
+    gw = ctypes.create_string_buffer(1 << 16)
+    g = ctypes.addressof(gw)
+    # gathered GEMMs: no row index, a bad index divisor, a bad tile shape, the dlhs op
+    assert built.mtx_gmm_gathered(1, g, 4, P, 2, g, g, 1, 8, 64, 128, 2, 0, 0, g, g, 1 << 16, P) == _lib.MTX_ERR_ARG
+    assert built.mtx_gmm_gathered(1, g, 4, g, 0, g, g, 1, 8, 64, 128, 2, 0, 0, g, g, 1 << 16, P) == _lib.MTX_ERR_ARG
+    assert built.mtx_gmm_gathered(1, g, 4, g, 2, g, g, 1, 8, 64, 128, 2, 64, 0, g, g, 1 << 16, P) == _lib.MTX_ERR_ARG
+    assert built.mtx_gmm_gathered(2, g, 4, g, 2, g, g, 1, 8, 64, 128, 2, 0, 0, g, g, 1 << 16, P) == _lib.MTX_ERR_ARG
+    assert built.mtx_gmm_fp8_swiglu_gathered(g, g, 4, P, 2, g, g, g, 8, 256, 128, 2, g, g, P, g, 1 << 16, P) == \
+        _lib.MTX_ERR_ARG
+
+
+def test_gathered_swiglu_supported_predicate():
+    """The host-side mirror of the gathered GEMM's shape conditions (bf16, K_in % 64, I % 128)."""
+    import torch
+
+    from mintext_amd.kernels.grouped_matmul import gathered_swiglu_supported
+
+    x = torch.zeros(16, 256, dtype=torch.bfloat16)
+    assert gathered_swiglu_supported(x, torch.zeros(4, 256, 256, dtype=torch.bfloat16))
+    assert not gathered_swiglu_supported(x.float(), torch.zeros(4, 256, 256))  # f32
+    assert not gathered_swiglu_supported(x, torch.zeros(4, 256, 128, dtype=torch.bfloat16))  # I = 64
+    assert not gathered_swiglu_supported(x[:, :96].contiguous(), torch.zeros(4, 96, 256, dtype=torch.bfloat16))
+    assert not gathered_swiglu_supported(x[:, :128], torch.zeros(4, 128, 256, dtype=torch.bfloat16))  # strided view
 
 
 def test_product_refuses_cpu_tensors():
