@@ -4,8 +4,10 @@
 
 A step is one MoE layer forward over one batch of synthetic tokens, inputs resident in HBM:
 router top-k on the gate logits -> route (dispatch) -> grouped GEMM gate_up with the fused
-SwiGLU -> grouped GEMM down -> weighted combine.  (The gate GEMM producing the logits is not
-part of the path; the logits are an input.)  For ``qwen3_bwd`` a step is the grouped-GEMM
+SwiGLU -> grouped GEMM down -> weighted combine.  By default the route computes only the
+permutation and the gate_up GEMM gathers the token rows itself (the same bits; ``--no-gather``
+copies the rows to sorted order first, as ``route`` does).  (The gate GEMM producing the logits
+is not part of the path; the logits are an input.)  For ``qwen3_bwd`` a step is the grouped-GEMM
 backward (dlhs + tgmm for both expert GEMMs) under Zipf-skewed routing.
 
 Prints ONE JSON line (rank 0).  ``roofline`` is measured live for the dominant kernel with HIP
