@@ -325,6 +325,8 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
                  "frac_of_peak": round((flops_fwd / (gemm_ms * 1e-3) / 1e12) / peak, 4),
                  "gate_up_ms": round(gu_ms, 4), "down_ms": round(dn_ms, 4)},
         "dispatch_combine": {"rows_gathered_in_gate_up": gather,
+                             **({"dispatch_note": "route computes the permutation only (index bytes); the token "
+                                                  "rows are read by the gate_up GEMM through it"} if gather else {}),
                              "dispatch_ms": round(t_disp.mean_ms(), 4), "combine_ms": round(t_comb.mean_ms(), 4),
                              "dispatch_GBs": round(disp_b / (t_disp.mean_ms() * 1e-3) / 1e9, 1) if t_disp.pairs else None,
                              "combine_GBs": round(comb_b / (t_comb.mean_ms() * 1e-3) / 1e9, 1) if t_comb.pairs else None},
