@@ -82,7 +82,7 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
   __shared__ int wsum[16];
   __shared__ long long wsum64[16];
   if (split_cnt && threadIdx.x < kSplitXcd * kSplitMaxRem) split_cnt[threadIdx.x] = 0;
-  __shared__ int s_gs[1024];
+  __shared__ __attribute__((aligned(16))) int s_gs[1024];
   __shared__ int s_total[2];
   const int e = threadIdx.x, lane = e & 63, w = e >> 6;
   const int g = (e < E) ? min(max(gs[e], 0), M) : 0;  // rows past M are dropped
@@ -122,14 +122,31 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
     s_total[1] = run;
   }
   __syncthreads();
-  const int tstart = incl - nt + wsum[w];
-  for (int i = 0; i < nt; ++i) {
+  // Tiles are written by all threads, tile j by thread j % 1024: its expert is the last one whose
+  // first tile is <= j (experts without tiles share their successor's start), so a skewed
+  // expert's tiles do not serialise on one thread.
+  __shared__ int s_tstart[1024], s_r0[1024], s_r1[1024];
+  if (e < E) {
+    s_tstart[e] = incl - nt + wsum[w];
+    s_r0[e] = r0;
+    s_r1[e] = r1;
+  }
+  __syncthreads();
+  const int ntiles = s_total[1];
+  for (int j = e; j < ntiles; j += blockDim.x) {
+    int lo = 0, hi = E - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_tstart[mid] <= j) lo = mid;
+      else hi = mid - 1;
+    }
+    const int i = j - s_tstart[lo];
     MTile t;
-    t.e = e;
-    t.r0 = r0 + i * BM;
-    t.r1 = min(r0 + (i + 1) * BM, r1);
+    t.e = lo;
+    t.r0 = s_r0[lo] + i * BM;
+    t.r1 = min(s_r0[lo] + (i + 1) * BM, s_r1[lo]);
     t.pad = 0;
-    tiles[tstart + i] = t;
+    tiles[j] = t;
   }
   // zero tiles for rows past sum(group_sizes)
   const int used = min(s_total[0], M);
@@ -148,10 +165,18 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
   }
   // expert order by descending group size (ties: lower id first), used by tgmm
   if (need_order && e < E) {
+    // four sizes per LDS read; entries past E hold 0 and never rank ahead (o > g fails for
+    // g >= 0, and o == g needs h < e < E)
     int rank = 0;
-    for (int h = 0; h < E; ++h) {
-      const int o = s_gs[h];
-      rank += (o > g || (o == g && h < e)) ? 1 : 0;
+    const int4* s4 = (const int4*)s_gs;
+#pragma unroll 4
+    for (int h4 = 0; h4 < (E + 3) / 4; ++h4) {
+      const int4 o = s4[h4];
+      const int h = 4 * h4;
+      rank += (o.x > g || (o.x == g && h < e)) ? 1 : 0;
+      rank += (o.y > g || (o.y == g && h + 1 < e)) ? 1 : 0;
+      rank += (o.z > g || (o.z == g && h + 2 < e)) ? 1 : 0;
+      rank += (o.w > g || (o.w == g && h + 3 < e)) ? 1 : 0;
     }
     order[rank] = e;
   }
