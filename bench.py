@@ -114,6 +114,41 @@ def _zipf_bias(E, s, rng, beta=0.55):
     return (-beta * s * np.log(rank)).astype(np.float32)
 
 
+def layer_inputs(cfg_name, dev, g=None):
+    """The synthetic inputs of a config, generated on the device from seed 2: tokens x [T,D],
+    gate logits [T,E] (x @ W_g in f32, rounded to the compute dtype; plus the Zipf popularity
+    bias for qwen3_bwd), expert weights gate_up [E,D,2I] / down [E,I,D] and, for deepseek, the
+    shared expert ([1,D,2I'], [1,I',D]).  Returns (x, logits, gate_up, down, shared, g) with g the
+    generator, positioned after the weights (the backward config draws its gradients from it)."""
+    import torch
+
+    cfg = CONFIGS[cfg_name]
+    T, D, E, I = cfg["T"], cfg["D"], cfg["E"], cfg["I"]
+    if g is None:
+        g = torch.Generator(device=dev)
+        g.manual_seed(2)
+    cdt = torch.float32 if cfg["dtype"] == "f32" else torch.bfloat16
+    x = torch.randn(T, D, device=dev, generator=g).to(cdt)
+    wg = torch.randn(D, E, device=dev, generator=g) * cfg["wstd"]
+    logits = (x.float() @ wg).to(cdt)  # the gate GEMM output: an input of the path
+    if cfg.get("zipf"):
+        bias = torch.from_numpy(_zipf_bias(E, cfg["zipf"], np.random.default_rng(5))).to(dev)
+        logits = (logits.float() + bias).to(cdt)
+    gate_up = (torch.randn(E, D, 2 * I, device=dev, generator=g) * cfg["wstd"]).to(cdt)
+    down = (torch.randn(E, I, D, device=dev, generator=g) * cfg["wstd"]).to(cdt)
+    shared = None
+    if cfg.get("shared"):
+        shared = ((torch.randn(1, D, 2 * I * cfg["shared"], device=dev, generator=g) * cfg["wstd"]).to(cdt),
+                  (torch.randn(1, I * cfg["shared"], D, device=dev, generator=g) * cfg["wstd"]).to(cdt))
+    return x, logits, gate_up, down, shared, g
+
+
+def router_kwargs(cfg_name):
+    cfg = CONFIGS[cfg_name]
+    return dict(scoring=cfg["scoring"], n_group=cfg.get("n_group", 1), topk_group=cfg.get("topk_group", 1),
+                routed_scaling_factor=cfg.get("scale", 1.0))
+
+
 def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_graph=False, gather=True):
     import torch
 
@@ -127,30 +162,17 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
     dev = torch.device("cuda:0")
     T, D, E, K, I = cfg["T"], cfg["D"], cfg["E"], cfg["K"], cfg["I"]
     M = T * K
-    g = torch.Generator(device=dev)
-    g.manual_seed(2)
     cdt = torch.float32 if cfg["dtype"] == "f32" else torch.bfloat16
-    x = torch.randn(T, D, device=dev, generator=g).to(cdt)
-    wg = torch.randn(D, E, device=dev, generator=g) * cfg["wstd"]
-    logits = (x.float() @ wg).to(cdt)  # the gate GEMM output: an input of the path
-    if cfg.get("zipf"):
-        bias = torch.from_numpy(_zipf_bias(E, cfg["zipf"], np.random.default_rng(5))).to(dev)
-        logits = (logits.float() + bias).to(cdt)
-    gate_up = (torch.randn(E, D, 2 * I, device=dev, generator=g) * cfg["wstd"]).to(cdt)
-    down = (torch.randn(E, I, D, device=dev, generator=g) * cfg["wstd"]).to(cdt)
-    shared = None
+    x, logits, gate_up, down, shared, g = layer_inputs(cfg_name, dev)
     fold = False
-    if cfg.get("shared"):
-        shared = ((torch.randn(1, D, 2 * I * cfg["shared"], device=dev, generator=g) * cfg["wstd"]).to(cdt),
-                  (torch.randn(1, I * cfg["shared"], D, device=dev, generator=g) * cfg["wstd"]).to(cdt))
+    if shared is not None:
         fold = shared_mode == "folded" and cfg["shared"] == 1
         if fold:
             # load-time transform: the shared expert becomes expert E of the routed weights
             from mintext_amd.moe import fold_shared_expert
 
             gate_up, down = fold_shared_expert(gate_up, down, shared[0], shared[1])
-    rkw = dict(scoring=cfg["scoring"], n_group=cfg.get("n_group", 1), topk_group=cfg.get("topk_group", 1),
-               routed_scaling_factor=cfg.get("scale", 1.0))
+    rkw = router_kwargs(cfg_name)
 
     t_gu, t_dn, t_disp, t_comb = EventTimer(torch), EventTimer(torch), EventTimer(torch), EventTimer(torch)
     Mg = M + T if fold else M  # rows through the expert GEMMs (the folded shared expert adds T)

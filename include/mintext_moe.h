@@ -16,6 +16,7 @@
  *                             folded in as an always-routed extra expert
  *   mtx_gate_router_topk   <- the gate Linear.__call__ (mintext/modules/linear.py:123-147) +
  *                             MoERouter (moe.py:41-103) in one kernel
+ *   mtx_router_topk_bwd    <- jax.grad through MoERouter.__call__ (moe.py:52-67,101)
  *   mtx_expert_bias_update <- update_expert_biases (mintext/trainer.py:371-410), one layer
  *   mtx_route              <- route (mintext/kernels/moe_dispatch.py:47-81)
  *   mtx_gather_rows        <- _sort_with_vjp forward (moe_dispatch.py:21-24)
@@ -108,13 +109,27 @@ int mtx_router_topk_shared(const void* logits, int logits_dtype, int64_t T, int6
  * once: the nn.Linear layout), both 16-byte aligned; D % 64 == 0, E <= 256 (other shapes and
  * dtypes: MTX_ERR_UNSUPPORTED, use the gate GEMM + mtx_router_topk).  shared_expert: -1, or an
  * id >= E written as column K with weight 1 (as mtx_router_topk_shared; topk_* are then
- * [T,K+1]).  logits_out [T,E] bf16 may be NULL.  Selection and weights are mtx_router_topk's
- * on the rounded logits, bit for bit.                                                    */
+ * [T,K+1]).  logits_out [T,E] bf16 and scores [T,E] f32 (the router's scores, as
+ * mtx_router_topk writes them) may be NULL.  Selection, weights and scores are
+ * mtx_router_topk's on the rounded logits, bit for bit.                                  */
 int mtx_gate_router_topk(const void* x, int dtype, const void* gate_weight_t, int64_t T, int64_t D,
                          int64_t E, int64_t K, int scoring, const float* bias, int64_t n_group,
                          int64_t topk_group, int norm_topk_prob, float routed_scaling_factor,
                          int64_t shared_expert, int32_t* topk_idx, float* topk_w, void* logits_out,
-                         void* stream);
+                         float* scores, void* stream);
+
+/* VJP of mtx_router_topk for fixed indices (what jax.grad takes through MoERouter.__call__,
+ * mintext/modules/moe.py:52-67,101: take_along_axis of the scores, the norm and the scaling;
+ * the top-k selection and the non-trainable bias carry no gradient).  logits [T,E] (F32/BF16)
+ * as passed to the forward, topk_idx [T,idx_ld] its indices (idx_ld = K, or K+1 for the
+ * _shared form, whose extra column has a constant weight), d_topk_w [T,K] f32 (may be NULL =
+ * zeros), d_scores [T,E] f32 (the gradient of the scores output; may be NULL) -> d_logits
+ * [T,E] (F32/BF16).  SOFTMAX with norm_topk_prob: unselected experts get zero gradient from
+ * the weights (the renormalised weights depend on the selected logits only).             */
+int mtx_router_topk_bwd(const void* logits, int logits_dtype, int64_t T, int64_t E, int64_t K,
+                        int scoring, int norm_topk_prob, float routed_scaling_factor,
+                        const int32_t* topk_idx, int64_t idx_ld, const float* d_topk_w,
+                        const float* d_scores, void* d_logits, int d_logits_dtype, void* stream);
 
 /* Loss-free load balancing for one MoE layer (update_expert_biases, mintext/trainer.py:371-410):
  * bias[e] += rate * sign(float(sum(counts))/E - counts[e]).  expert_counts [E] int32 is the

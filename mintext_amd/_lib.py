@@ -41,7 +41,8 @@ SIGNATURES = {
     "mtx_router_topk": (_I, [_P, _I, _I64, _I64, _I64, _I, _P, _I64, _I64, _I, _F, _P, _P, _P, _P]),
     "mtx_router_topk_shared": (_I, [_P, _I, _I64, _I64, _I64, _I, _P, _I64, _I64, _I, _F, _I64, _P, _P, _P, _P]),
     "mtx_gate_router_topk": (_I, [_P, _I, _P, _I64, _I64, _I64, _I64, _I, _P, _I64, _I64, _I, _F, _I64, _P, _P, _P,
-                                   _P]),
+                                   _P, _P]),
+    "mtx_router_topk_bwd": (_I, [_P, _I, _I64, _I64, _I64, _I, _I, _F, _P, _I64, _P, _P, _P, _I, _P]),
     "mtx_expert_bias_update": (_I, [_P, _I64, _F, _P, _P]),
     "mtx_route_workspace_size": (_I64, [_I64, _I64, _I64]),
     "mtx_route": (_I, [_P, _I, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P]),

@@ -246,8 +246,8 @@ template <int EB, int V>
 __global__ __launch_bounds__(256) void gate_topk_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wt, int T, int D, int E, int K, int L, int scoring,
     const float* __restrict__ bias, int n_group, int topk_group, int norm, float rscale,
-    int32_t* __restrict__ idx_out, float* __restrict__ w_out, uint16_t* __restrict__ logits_out, int ldo,
-    int extra) {
+    int32_t* __restrict__ idx_out, float* __restrict__ w_out, uint16_t* __restrict__ logits_out,
+    float* __restrict__ scores_out, int ldo, int extra) {
   constexpr int EP = EB * 32, LDP = EP + 1;  // logits tile row stride (+1: conflict-free)
   extern __shared__ float smem[];
   float* lg = smem;                              // [32][LDP] f32
@@ -310,8 +310,121 @@ __global__ __launch_bounds__(256) void gate_topk_kernel(
     const bool tok_ok = tl < kGateTokens && t < T;
     const float* row = lg + (tok_ok ? tl : 0) * LDP;
     router_select<V>([&](int e) { return row[e]; }, t, tok_ok, slot, li, L, E, K, scoring, bias, n_group, topk_group,
-                     norm, rscale, idx_out, w_out, nullptr, ldo, extra, scratch);
+                     norm, rscale, idx_out, w_out, scores_out, ldo, extra, scratch);
     __syncthreads();  // the scratch of the next pass
+  }
+}
+
+// ---- router VJP --------------------------------------------------------------------------
+// d logits of the weights (and optionally of the scores) the forward returned, for fixed
+// indices: the selection (top-k, group mask) carries no gradient and neither does the bias,
+// which MoERouter keeps as a non-trainable variable (moe.py:37-39).  One wave per token.
+//   SIGMOID_GROUP (moe.py:53,63-66,101): w_k = c * s_k / (S + 1e-20) with S = sum_j s_j
+//     (c = routed_scaling_factor; w_k = c * s_k without norm), s = sigmoid(l), so
+//     ds_k = c * (g_k - sum_j g_j s_j / (S + 1e-20)) / (S + 1e-20)  and  dl = ds * s * (1 - s).
+//   SOFTMAX, norm: w = c * softmax over the selected logits, dl_{i_k} = c * u_k (g_k - sum_j u_j g_j)
+//     with u = w / c; unselected logits get no gradient.  Without norm w_k = c * p_{i_k} of the
+//     full softmax p, dl_e = c * p_e (g'_e - sum_k g_k p_{i_k}) with g'_e = g_k where e = i_k.
+//   scores (sigmoid or full softmax) add dscores * s (1 - s), or p * (dscores - sum_j dscores_j p_j).
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+  return x;
+}
+
+__global__ __launch_bounds__(256) void router_topk_bwd_kernel(
+    const void* __restrict__ logits, int ldt, int T, int E, int K, int scoring, int norm, float rscale,
+    const int32_t* __restrict__ idx, int ldi, const float* __restrict__ dw, const float* __restrict__ dscores,
+    void* __restrict__ dlogits, int dldt) {
+  __shared__ int sel_e[4][64];
+  __shared__ float sel_d[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * 4 + wave;
+  if (t >= T) return;  // whole waves only: no workgroup barrier below
+  const int64_t row = t * E;
+  // the K selected experts and their upstream gradients, one per lane
+  const bool kl = lane < K;
+  const int ek = kl ? idx[t * ldi + lane] : -1;
+  const bool kv = kl && ek >= 0 && ek < E;
+  const float lk = kv ? load_as_f32(logits, row + ek, ldt) : 0.0f;
+  const float gk = (kv && dw) ? dw[t * K + lane] : 0.0f;
+  float dk = 0.0f;  // d logit of expert ek from the weights
+  float pmax = 0.0f, pden = 1.0f, pdot = 0.0f;  // full-softmax terms
+  if (scoring == MTX_SCORING_SIGMOID_GROUP) {
+    const float s = kv ? 1.0f / (1.0f + expf(-lk)) : 0.0f;
+    float ds;
+    if (norm) {
+      const float den = wave_sum(s) + 1e-20f;
+      const float gs = wave_sum(gk * s);
+      ds = rscale * (gk - gs / den) / den;
+    } else {
+      ds = rscale * gk;
+    }
+    dk = ds * s * (1.0f - s);
+  } else {
+    // the logit maximum over all experts (the top-1 logit) and the full softmax denominator
+    float m = -INFINITY;
+    for (int e = lane; e < E; e += 64) m = fmaxf(m, load_as_f32(logits, row + e, ldt));
+    pmax = wave_max(m);
+    const float ekx = kv ? expf(lk - pmax) : 0.0f;
+    if (norm) {
+      const float den = wave_sum(ekx);
+      const float u = ekx / den;
+      const float gu = wave_sum(gk * u);
+      dk = rscale * u * (gk - gu);
+    } else {
+      float part = 0.0f;
+      for (int e = lane; e < E; e += 64) part += expf(load_as_f32(logits, row + e, ldt) - pmax);
+      pden = wave_sum(part);
+      const float p = ekx / pden;
+      pdot = wave_sum(gk * p);
+      dk = rscale * p * gk;  // the -p_e * sum term is added per expert below
+    }
+  }
+  if (kl) {
+    sel_e[wave][lane] = kv ? ek : -1;
+    sel_d[wave][lane] = dk;
+  }
+  float sdot = 0.0f;  // sum_j dscores_j p_j of the full softmax
+  if (dscores && scoring == MTX_SCORING_SOFTMAX) {
+    if (norm) {  // the full-softmax terms were not needed for the weights
+      float m = -INFINITY;
+      for (int e = lane; e < E; e += 64) m = fmaxf(m, load_as_f32(logits, row + e, ldt));
+      pmax = wave_max(m);
+      float part = 0.0f;
+      for (int e = lane; e < E; e += 64) part += expf(load_as_f32(logits, row + e, ldt) - pmax);
+      pden = wave_sum(part);
+    }
+    float part = 0.0f;
+    for (int e = lane; e < E; e += 64)
+      part += dscores[row + e] * (expf(load_as_f32(logits, row + e, ldt) - pmax) / pden);
+    sdot = wave_sum(part);
+  }
+  __builtin_amdgcn_wave_barrier();
+  for (int e = lane; e < E; e += 64) {
+    float d = 0.0f;
+    for (int k = 0; k < K; ++k)
+      if (sel_e[wave][k] == e) d += sel_d[wave][k];
+    if (scoring == MTX_SCORING_SOFTMAX && !norm && dw) {
+      const float p = expf(load_as_f32(logits, row + e, ldt) - pmax) / pden;
+      d -= rscale * p * pdot;
+    }
+    if (dscores) {
+      const float l = load_as_f32(logits, row + e, ldt);
+      if (scoring == MTX_SCORING_SIGMOID_GROUP) {
+        const float s = 1.0f / (1.0f + expf(-l));
+        d += dscores[row + e] * s * (1.0f - s);
+      } else {
+        const float p = expf(l - pmax) / pden;
+        d += p * (dscores[row + e] - sdot);
+      }
+    }
+    store_from_f32(dlogits, row + e, dldt, d);
   }
 }
 
@@ -333,7 +446,7 @@ extern "C" int mtx_gate_router_topk(const void* x, int dtype, const void* gate_w
                                     int64_t E, int64_t K, int scoring, const float* bias, int64_t n_group,
                                     int64_t topk_group, int norm_topk_prob, float routed_scaling_factor,
                                     int64_t shared_expert, int32_t* topk_idx, float* topk_w, void* logits_out,
-                                    void* stream) {
+                                    float* scores, void* stream) {
   if (T < 0 || D < 0 || E < 1 || K < 1 || K > E || K > 64) return MTX_ERR_ARG;
   if (shared_expert >= 0 && (shared_expert < E || shared_expert > INT32_MAX)) return MTX_ERR_ARG;
   if (scoring != MTX_SCORING_SOFTMAX && scoring != MTX_SCORING_SIGMOID_GROUP) return MTX_ERR_ARG;
@@ -354,7 +467,7 @@ extern "C" int mtx_gate_router_topk(const void* x, int dtype, const void* gate_w
 #define MTX_GATE(EBT, VV)                                                                                         \
   hipLaunchKernelGGL((gate_topk_kernel<EBT, VV>), dim3(grid), dim3(256), shm, st, (const uint16_t*)x,             \
                      (const uint16_t*)gate_weight_t, (int)T, (int)D, (int)E, (int)K, L, scoring, bias, (int)n_group, \
-                     (int)topk_group, norm_topk_prob, routed_scaling_factor, topk_idx, topk_w, (uint16_t*)logits_out, \
+                     (int)topk_group, norm_topk_prob, routed_scaling_factor, topk_idx, topk_w, (uint16_t*)logits_out, scores, \
                      (int)(shared_expert >= 0 ? K + 1 : K), (int)(shared_expert >= 0 ? shared_expert : -1))
 #define MTX_GATE_V(EBT)                      \
   if (V <= 1) MTX_GATE(EBT, 1);              \
@@ -420,6 +533,23 @@ extern "C" int mtx_router_topk_shared(const void* logits, int logits_dtype, int6
   if (shared_expert < E || shared_expert > INT32_MAX) return MTX_ERR_ARG;
   return router_launch(logits, logits_dtype, T, E, K, scoring, bias, n_group, topk_group, norm_topk_prob,
                        routed_scaling_factor, topk_idx, topk_w, scores, K + 1, shared_expert, stream);
+}
+
+extern "C" int mtx_router_topk_bwd(const void* logits, int logits_dtype, int64_t T, int64_t E, int64_t K,
+                                   int scoring, int norm_topk_prob, float routed_scaling_factor,
+                                   const int32_t* topk_idx, int64_t idx_ld, const float* d_topk_w,
+                                   const float* d_scores, void* d_logits, int d_logits_dtype, void* stream) {
+  if (T < 0 || E < 1 || K < 1 || K > E || K > 64 || idx_ld < K) return MTX_ERR_ARG;
+  if (logits_dtype != MTX_F32 && logits_dtype != MTX_BF16) return MTX_ERR_ARG;
+  if (d_logits_dtype != MTX_F32 && d_logits_dtype != MTX_BF16) return MTX_ERR_ARG;
+  if (scoring != MTX_SCORING_SOFTMAX && scoring != MTX_SCORING_SIGMOID_GROUP) return MTX_ERR_ARG;
+  if (T == 0) return MTX_OK;
+  if (!logits || !topk_idx || !d_logits) return MTX_ERR_ARG;
+  if (T > INT32_MAX) return MTX_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(router_topk_bwd_kernel, dim3((unsigned)ceil_div(T, 4)), dim3(256), 0, (hipStream_t)stream,
+                     logits, logits_dtype, (int)T, (int)E, (int)K, scoring, norm_topk_prob, routed_scaling_factor,
+                     topk_idx, (int)idx_ld, d_topk_w, d_scores, d_logits, d_logits_dtype);
+  return check_launch();
 }
 
 // Loss-free load balancing (trainer.py:371-410 for one layer): bias[e] += rate * sign(mean - counts[e])

@@ -114,16 +114,40 @@ class _Route(torch.autograd.Function):
         return dx, None, None
 
 
+def _combine_add(Y: torch.Tensor, inv: torch.Tensor, w: torch.Tensor, N: int, K: int, addend: torch.Tensor,
+                 out_dtype: torch.dtype) -> torch.Tensor:
+    if addend.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"addend dtype {addend.dtype} not supported")
+    dev = L.require_device(Y, inv, w, addend)
+    Y = Y.contiguous()
+    D = Y.shape[1]
+    if tuple(addend.shape) != (N, D):
+        raise ValueError(f"addend shape {tuple(addend.shape)} != {(N, D)}")
+    a = addend.contiguous()
+    wc = w.contiguous()
+    out = torch.empty((N, D), dtype=out_dtype, device=dev)
+    L.call("mtx_unroute_add", L.ptr(Y), L.dtype_code(Y.dtype), L.ptr(inv), L.ptr(wc), L.dtype_code(wc.dtype), N, K, D,
+           L.ptr(a), L.dtype_code(a.dtype), L.ptr(out), L.dtype_code(out_dtype), L.stream(dev))
+    return out
+
+
 class _Unroute(torch.autograd.Function):
+    """unroute, and with an addend unroute + addend (one combine pass either way); the VJP is
+    ``mtx_unroute_bwd`` for the expert outputs and weights, the identity for the addend."""
+
     @staticmethod
-    def forward(ctx, sorted_output, sort_indices, topk_weights, K):
+    def forward(ctx, sorted_output, sort_indices, topk_weights, K, addend=None):
         N = topk_weights.shape[0]
         inv = _inverse_of(sort_indices)
         out_dtype = torch.result_type(sorted_output, topk_weights)
         if out_dtype not in (torch.float32, torch.bfloat16):
             raise TypeError(f"unroute output dtype {out_dtype} not supported")
         w = topk_weights.contiguous()
-        out = _combine(sorted_output, inv, w, N, K, out_dtype)
+        if addend is None:
+            out = _combine(sorted_output, inv, w, N, K, out_dtype)
+        else:
+            out = _combine_add(sorted_output, inv, w, N, K, addend, out_dtype)
+            ctx.add_dtype = addend.dtype
         ctx.save_for_backward(sorted_output, inv, w)
         ctx.K = K
         return out
@@ -138,12 +162,17 @@ class _Unroute(torch.autograd.Function):
         dout = dout.contiguous()
         if dout.dtype not in (torch.float32, torch.bfloat16):
             dout = dout.float()
-        dY = torch.empty_like(Y.contiguous())
-        dw = torch.empty_like(w) if ctx.needs_input_grad[2] else None
-        L.call("mtx_unroute_bwd", L.ptr(dout), L.dtype_code(dout.dtype), L.ptr(Y.contiguous()),
-               L.dtype_code(Y.dtype), L.ptr(inv), L.ptr(w), L.dtype_code(w.dtype), N, K, D,
-               L.ptr(dY), L.ptr(dw), L.stream(dev))
-        return dY, None, dw, None
+        dY = dw = None
+        if ctx.needs_input_grad[0] or ctx.needs_input_grad[2]:
+            dY = torch.empty_like(Y.contiguous())  # the kernel writes d sorted_output whenever it runs
+            dw = torch.empty_like(w) if ctx.needs_input_grad[2] else None
+            L.call("mtx_unroute_bwd", L.ptr(dout), L.dtype_code(dout.dtype), L.ptr(Y.contiguous()),
+                   L.dtype_code(Y.dtype), L.ptr(inv), L.ptr(w), L.dtype_code(w.dtype), N, K, D,
+                   L.ptr(dY), L.ptr(dw), L.stream(dev))
+        da = None
+        if len(ctx.needs_input_grad) > 4 and ctx.needs_input_grad[4]:
+            da = dout.to(ctx.add_dtype)
+        return dY, None, dw, None, da
 
 
 class _SortWithVjp(torch.autograd.Function):
@@ -211,31 +240,9 @@ def unroute_add(sorted_output: torch.Tensor, sort_indices: torch.Tensor, topk_we
     """``unroute(...) + addend`` -- the combine followed by ``output = routed_out + shared_out``
     of MoEBlock.__call__ (mintext/modules/moe.py:256-258) -- in one pass over the rows
     (``mtx_unroute_add``; the same f32 bits as the two steps).  ``addend`` is [N, D] float32 or
-    bfloat16.  With autograd active it is computed as the two differentiable steps.
+    bfloat16.  Differentiable in the expert outputs, the weights and the addend.
     """
-    needs_grad = torch.is_grad_enabled() and (
-        sorted_output.requires_grad or topk_weights.requires_grad or addend.requires_grad)
-    out_dtype = torch.result_type(sorted_output, topk_weights)
-    if needs_grad:
-        return unroute(sorted_output, sort_indices, topk_weights, num_experts_per_tok) + addend.to(out_dtype)
-    if out_dtype not in (torch.float32, torch.bfloat16):
-        raise TypeError(f"unroute output dtype {out_dtype} not supported")
-    if addend.dtype not in (torch.float32, torch.bfloat16):
-        raise TypeError(f"addend dtype {addend.dtype} not supported")
-    dev = L.require_device(sorted_output, sort_indices, topk_weights, addend)
-    K = int(num_experts_per_tok)
-    N = topk_weights.shape[0]
-    Y = sorted_output.contiguous()
-    D = Y.shape[1]
-    if tuple(addend.shape) != (N, D):
-        raise ValueError(f"addend shape {tuple(addend.shape)} != {(N, D)}")
-    inv = _inverse_of(sort_indices)
-    w = topk_weights.contiguous()
-    a = addend.contiguous()
-    out = torch.empty((N, D), dtype=out_dtype, device=dev)
-    L.call("mtx_unroute_add", L.ptr(Y), L.dtype_code(Y.dtype), L.ptr(inv), L.ptr(w), L.dtype_code(w.dtype), N, K, D,
-           L.ptr(a), L.dtype_code(a.dtype), L.ptr(out), L.dtype_code(out_dtype), L.stream(dev))
-    return out
+    return _Unroute.apply(sorted_output, sort_indices, topk_weights, int(num_experts_per_tok), addend)
 
 
 def route_quantize_fp8(tokens: torch.Tensor, topk_indices: torch.Tensor, num_experts: int):

@@ -96,10 +96,12 @@ def moe_layer_forward(logits: torch.Tensor | None, x: torch.Tensor, gate_up: tor
                       topk_group: int = 1, norm_topk_prob: bool = True, routed_scaling_factor: float = 1.0,
                       shared_gate_up: torch.Tensor | None = None, shared_down: torch.Tensor | None = None,
                       shared_folded: bool = False, return_expert_counts: bool = False,
-                      gate_weight_t: torch.Tensor | None = None):
+                      gate_weight_t: torch.Tensor | None = None, return_scores: bool = False):
     """Router top-k + routed experts (+ shared expert) -- MoEBlock.__call__ (moe.py:240-266) after
-    the gate GEMM.  Returns (out [T,D] f32, topk_indices [T,k], topk_weights [T,k]) and, with
-    ``return_expert_counts``, the [E] int32 per-expert token counts (trainer.py:297-308).
+    the gate GEMM.  Returns (out [T,D] f32, topk_indices [T,k], topk_weights [T,k]), then, with
+    ``return_expert_counts``, the [E] int32 per-expert token counts (trainer.py:297-308) and, with
+    ``return_scores``, the router's [T,E] f32 scores (sigmoid scores, or softmax probabilities).
+    Under autograd the weights (and scores) are differentiable in the logits (``route_topk``).
 
     ``shared_folded``: ``gate_up`` / ``down`` come from ``fold_shared_expert`` (E routed experts
     + the shared one as expert E, ``logits`` has E columns); the shared expert then runs inside
@@ -114,26 +116,31 @@ def moe_layer_forward(logits: torch.Tensor | None, x: torch.Tensor, gate_up: tor
         E = gate_weight_t.shape[0]
 
         def topk(shared_expert=None):
-            return gate_route_topk(x, gate_weight_t, k, shared_expert=shared_expert, **rkw)
+            return gate_route_topk(x, gate_weight_t, k, shared_expert=shared_expert, return_scores=return_scores,
+                                   **rkw)
     else:
         E = logits.shape[1]
 
         def topk(shared_expert=None):
-            return route_topk(logits, k, shared_expert=shared_expert, **rkw)
+            return route_topk(logits, k, shared_expert=shared_expert, return_scores=return_scores, **rkw)
     if shared_folded:
         if gate_up.shape[0] != E + 1:
             raise ValueError(f"folded weights need {E + 1} experts (E routed + shared), got {gate_up.shape[0]}")
-        idx, w = topk(shared_expert=E)
-        out, gs = moe_experts_forward(x, idx, w, gate_up, down, return_group_sizes=True)
-        idx, w = idx[:, :k], w[:, :k]
+        r = topk(shared_expert=E)
+        out, gs = moe_experts_forward(x, r[0], r[1], gate_up, down, return_group_sizes=True)
+        idx, w = r[0][:, :k], r[1][:, :k]
     else:
-        idx, w = topk()
+        r = topk()
+        idx, w = r[0], r[1]
         # the shared expert's output joins the combine's pass: routed_out + shared_out (moe.py:256-258)
         shared = None if shared_gate_up is None else shared_expert_forward(x, shared_gate_up, shared_down)
         out, gs = moe_experts_forward(x, idx, w, gate_up, down, return_group_sizes=True, addend=shared)
+    res = (out, idx, w)
     if return_expert_counts:
-        return out, idx, w, gs[:E]
-    return out, idx, w
+        res += (gs[:E],)
+    if return_scores:
+        res += (r[2],)
+    return res
 
 
 def moe_block_forward(x: torch.Tensor, gate_weight: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, *,
@@ -151,8 +158,11 @@ def moe_block_forward(x: torch.Tensor, gate_weight: torch.Tensor, gate_up: torch
     nn.Linear layout -- pass ``gate_weight_t = gate_weight_linear_layout(gate_weight)``, a
     load-time transform, to skip the per-call transpose; otherwise the GEMM is hipBLASLt's
     (``torch.matmul``) and the top-k ``route_topk``.  Returns
-    ``(output [.., D] float32, {"topk_indices", "topk_weights", "expert_counts"})``, the
-    reference's aux data plus the counts of trainer.py:297-308.
+    ``(output [.., D] float32, {"topk_indices", "scores", "topk_weights", "expert_counts"})``: the
+    reference's aux data (moe.py:262-266; ``scores`` [N, E] float32 are the sigmoid scores, or the
+    softmax probabilities in softmax mode) plus the weights and the counts of trainer.py:297-308.
+    Under autograd the gradient reaches ``gate_weight`` and ``x`` through the router's weights
+    (moe.py:53,101), as under jax.grad of the reference block.
     """
     shape = x.shape
     xf = x.reshape(-1, shape[-1])
@@ -166,27 +176,37 @@ def moe_block_forward(x: torch.Tensor, gate_weight: torch.Tensor, gate_up: torch
     else:
         logits = torch.matmul(xf, gate_weight.to(xf.dtype))
         gate_weight_t = None
-    out, idx, w, counts = moe_layer_forward(
+    out, idx, w, counts, scores = moe_layer_forward(
         logits, xf, gate_up, down, k=k, scoring=scoring, bias=bias, n_group=n_group, topk_group=topk_group,
         norm_topk_prob=norm_topk_prob, routed_scaling_factor=routed_scaling_factor, shared_gate_up=shared_gate_up,
-        shared_down=shared_down, shared_folded=shared_folded, return_expert_counts=True, gate_weight_t=gate_weight_t)
-    return out.reshape(*shape[:-1], out.shape[-1]), {"topk_indices": idx, "topk_weights": w, "expert_counts": counts}
+        shared_down=shared_down, shared_folded=shared_folded, return_expert_counts=True, gate_weight_t=gate_weight_t,
+        return_scores=True)
+    aux = {"topk_indices": idx, "scores": scores, "topk_weights": w, "expert_counts": counts}
+    return out.reshape(*shape[:-1], out.shape[-1]), aux
 
 
 def shared_expert_forward(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor) -> torch.Tensor:
     """Dense SwiGLU MLP (mintext/modules/linear.py:164-228 as used at moe.py:231-236) as a
-    one-group grouped GEMM: gate_up [D, 2I] or [1, D, 2I], down [I, D] or [1, I, D]."""
+    one-group grouped GEMM: gate_up [D, 2I] or [1, D, 2I], down [I, D] or [1, I, D].  Under
+    autograd the gate_up GEMM and the SwiGLU run as their differentiable steps."""
     gu = gate_up.reshape(1, *gate_up.shape[-2:]).to(x.dtype)
     dn = down.reshape(1, *down.shape[-2:]).to(x.dtype)
     gs = torch.full((1,), x.shape[0], dtype=torch.int32, device=x.device)
-    inter = grouped_matmul_swiglu(x, gu, gs)
+    if torch.is_grad_enabled() and (x.requires_grad or gu.requires_grad or dn.requires_grad):
+        inter = swiglu_autograd(grouped_matmul_vjp(x, gu, gs))
+    else:
+        inter = grouped_matmul_swiglu(x, gu, gs)
     return grouped_matmul_vjp(inter, dn, gs)
 
 
 def moe_experts_forward_fp8(x: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
                             gate_up_q: torch.Tensor, gate_up_scale: torch.Tensor, down_q: torch.Tensor,
                             down_scale: torch.Tensor) -> torch.Tensor:
-    """Blockwise-fp8 expert layer; weights from ``quantize_fp8_weights`` ([E, Kout, Kin] e4m3)."""
+    """Blockwise-fp8 expert layer; weights from ``quantize_fp8_weights`` ([E, Kout, Kin] e4m3).
+    Forward only: raises under autograd when an input requires grad."""
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (x, topk_weights, gate_up_q, down_q)):
+        raise RuntimeError("moe_experts_forward_fp8 is forward-only; run it under torch.no_grad() or train "
+                           "through moe_experts_forward")
     from .kernels.fp8 import (grouped_matmul_fp8, grouped_matmul_fp8_swiglu, grouped_matmul_fp8_swiglu_gathered,
                               quantize_fp8_rows)
 

@@ -179,6 +179,69 @@ def router_softmax(logits, k: int, norm_topk_prob: bool = True, routed_scaling_f
     return idx, w * routed_scaling_factor, probs
 
 
+def router_weights_given_idx(logits, topk_indices, scoring: str = "softmax", norm_topk_prob: bool = True,
+                             routed_scaling_factor: float = 1.0):
+    """The router's weights and scores as functions of the logits for FIXED indices, in float64:
+    sigmoid mode ``take_along_axis(sigmoid(l), idx)`` (moe.py:53,101), ``/ (sum + 1e-20)``
+    (moe.py:63-64), ``* scale`` (moe.py:66); softmax mode the renormalised top-k softmax or the
+    full-softmax probability (HF mixtral/modeling_mixtral.py:104-111, qwen3_moe:258-267).
+    Returns (weights [T,k], scores [T,E]).  The forward whose derivative ``router_vjp`` is."""
+    lg = np.asarray(logits, dtype=np.float64)
+    idx = np.asarray(topk_indices)
+    if scoring == "softmax":
+        ex = np.exp(lg - lg.max(-1, keepdims=True))
+        scores = ex / ex.sum(-1, keepdims=True)
+        top = np.take_along_axis(ex, idx, axis=1)
+        w = top / top.sum(-1, keepdims=True) if norm_topk_prob else np.take_along_axis(scores, idx, axis=1)
+    else:
+        scores = 1.0 / (1.0 + np.exp(-lg))
+        w = np.take_along_axis(scores, idx, axis=1)
+        if norm_topk_prob:
+            w = w / (w.sum(-1, keepdims=True) + 1e-20)
+    return w * routed_scaling_factor, scores
+
+
+def router_vjp(logits, topk_indices, d_weights, d_scores=None, scoring: str = "softmax",
+               norm_topk_prob: bool = True, routed_scaling_factor: float = 1.0) -> np.ndarray:
+    """d logits [T,E] float64 of <weights, d_weights> + <scores, d_scores> for fixed indices --
+    the gradient jax.grad takes through MoERouter.__call__ (moe.py:52-67,101); the top-k
+    selection and the bias carry none.  Chain rule through ``router_weights_given_idx``:
+    d w_k / d l_e = c * (dS_k/dl_e), with the selection's Jacobian written per mode below."""
+    lg = np.asarray(logits, dtype=np.float64)
+    idx = np.asarray(topk_indices)
+    T, E = lg.shape
+    c = float(routed_scaling_factor)
+    g = np.zeros((T, idx.shape[1])) if d_weights is None else np.asarray(d_weights, np.float64)
+    rows = np.arange(T)[:, None]
+    dl = np.zeros((T, E))
+    if scoring == "softmax":
+        ex = np.exp(lg - lg.max(-1, keepdims=True))
+        p = ex / ex.sum(-1, keepdims=True)
+        if norm_topk_prob:
+            top = np.take_along_axis(ex, idx, axis=1)
+            u = top / top.sum(-1, keepdims=True)               # softmax over the selected logits
+            np.add.at(dl, (rows, idx), c * u * (g - (g * u).sum(-1, keepdims=True)))
+        else:
+            pk = np.take_along_axis(p, idx, axis=1)            # w_k = c p_{i_k}
+            np.add.at(dl, (rows, idx), c * g * pk)
+            dl -= c * p * (g * pk).sum(-1, keepdims=True)
+        if d_scores is not None:
+            ds = np.asarray(d_scores, np.float64)
+            dl += p * (ds - (ds * p).sum(-1, keepdims=True))
+    else:
+        s = 1.0 / (1.0 + np.exp(-lg))
+        sk = np.take_along_axis(s, idx, axis=1)
+        if norm_topk_prob:
+            den = sk.sum(-1, keepdims=True) + 1e-20
+            dsk = c * (g - (g * sk).sum(-1, keepdims=True) / den) / den
+        else:
+            dsk = c * g
+        np.add.at(dl, (rows, idx), dsk * sk * (1.0 - sk))
+        if d_scores is not None:
+            dl += np.asarray(d_scores, np.float64) * s * (1.0 - s)
+    return dl
+
+
 # ---------------------------------------------------------------------------------------------
 # dispatch / combine   (mintext/kernels/moe_dispatch.py)
 # ---------------------------------------------------------------------------------------------
@@ -402,6 +465,73 @@ def moe_block(x, topk_indices, topk_weights, gate_up, down, shared_gate_up=None,
         x64 = np.asarray(x, np.float64)
         h = x64 @ np.asarray(shared_gate_up, np.float64).reshape(x64.shape[1], -1)
         out = out + swiglu(h) @ np.asarray(shared_down, np.float64).reshape(-1, x64.shape[1])
+    return out
+
+
+def moe_experts_vjp(x, topk_indices, topk_weights, gate_up, down, dout):
+    """VJP of ``moe_experts`` (MoEExperts._forward_kernel, moe.py:161-221, under jax.grad with
+    the custom VJPs of grouped_matmul.py:151-187 and moe_dispatch.py:33-38,102-111) in float64.
+    Returns (dx [N,D], d_topk_weights [N,K], d_gate_up [E,D,2I], d_down [E,I,D])."""
+    k = np.asarray(topk_indices).shape[1]
+    E = np.asarray(gate_up).shape[0]
+    x64 = np.asarray(x, np.float64)
+    N, D = x64.shape
+    xs, perm, gs = route(x64, topk_indices, E)
+    h = gmm(xs, gate_up, gs)
+    inter = swiglu(h)
+    y = gmm(inter, down, gs)
+    inv = invert_permutation(perm)
+    g = np.asarray(dout, np.float64)
+    w = np.asarray(topk_weights, np.float64)
+    yk = y[inv].reshape(N, k, -1)
+    d_w = np.einsum("nkd,nd->nk", yk, g)                    # einsum VJP (moe_dispatch.py:111)
+    dy = np.empty_like(y)
+    dy[inv] = (w[:, :, None] * g[:, None, :]).reshape(N * k, -1)  # gather VJP (:102-108)
+    d_inter = gmm_dlhs(dy, down, gs)
+    d_down = tgmm(inter, dy, gs)
+    dh = swiglu_bwd(h, d_inter)
+    dxs = gmm_dlhs(dh, gate_up, gs)
+    d_gate_up = tgmm(xs, dh, gs)
+    dx = np.zeros((N, D))
+    np.add.at(dx, perm // k, dxs)                           # sort + repeat VJP (:33-38, :67)
+    return dx, d_w, d_gate_up, d_down
+
+
+def moe_block_vjp(x, gate_weight, gate_up, down, dout, *, k: int, scoring: str = "sigmoid_group", bias=None,
+                  n_group: int = 1, topk_group: int = 1, norm_topk_prob: bool = True,
+                  routed_scaling_factor: float = 1.0, shared_gate_up=None, shared_down=None):
+    """VJP of MoEBlock.__call__ (moe.py:240-266) from the tokens, router included, in float64:
+    logits = x @ W_g (linear.py:123-147), router with its weights differentiated for fixed
+    indices (``router_vjp``), routed experts (``moe_experts_vjp``), shared expert MLP.  The
+    selection runs on the float32 logits (as the reference's f32 router does).
+    Returns a dict with dx, d_gate_weight [D,E], d_gate_up, d_down and, with a shared expert,
+    d_shared_gate_up [D,2I'], d_shared_down [I',D]."""
+    x64 = np.asarray(x, np.float64)
+    wg = np.asarray(gate_weight, np.float64)
+    logits = x64 @ wg
+    lg32 = logits.astype(np.float32)
+    if scoring == "softmax":
+        idx, w, _ = router_softmax(lg32, k, norm_topk_prob, routed_scaling_factor)
+    else:
+        idx, w, _ = router_sigmoid_group(lg32, k, bias, n_group, topk_group, norm_topk_prob, routed_scaling_factor)
+    w, _ = router_weights_given_idx(logits, idx, scoring, norm_topk_prob, routed_scaling_factor)
+    dx, d_w, d_gu, d_dn = moe_experts_vjp(x64, idx, w, gate_up, down, dout)
+    dl = router_vjp(logits, idx, d_w, None, scoring, norm_topk_prob, routed_scaling_factor)
+    out = {"d_gate_up": d_gu, "d_down": d_dn, "d_gate_weight": x64.T @ dl}
+    dx = dx + dl @ wg.T
+    if shared_gate_up is not None:
+        D = x64.shape[1]
+        sgu = np.asarray(shared_gate_up, np.float64).reshape(D, -1)
+        sdn = np.asarray(shared_down, np.float64).reshape(-1, D)
+        g = np.asarray(dout, np.float64)
+        h = x64 @ sgu
+        d_inter = g @ sdn.T
+        out["d_shared_down"] = swiglu(h).T @ g
+        dh = swiglu_bwd(h, d_inter)
+        out["d_shared_gate_up"] = x64.T @ dh
+        dx = dx + dh @ sgu.T
+    out["dx"] = dx
+    out["topk_indices"] = idx
     return out
 
 

@@ -109,6 +109,106 @@ def make_routers():
                         ds3_logits=l3, ds3_bias=b3, ds3_idx=d3i, ds3_w=d3w, ds3_scores=d3s)
 
 
+def _router_grad(router, logits: np.ndarray, G: np.ndarray):
+    """d/d logits of sum_k w[t,k] * G[t, idx[t,k]] through an HF router with an identity gate
+    (torch autograd of HF's own forward, which runs in float32)."""
+    x = torch.from_numpy(logits.astype(np.float32)).requires_grad_(True)
+    _, w, idx = router(x)
+    loss = (w.float() * torch.from_numpy(G).gather(1, idx.long())).sum()
+    loss.backward()
+    return idx.detach().numpy().astype(np.int32), x.grad.numpy().astype(np.float32)
+
+
+def make_router_grads():
+    """Router VJP fixtures: HF routers (softmax norm / no-norm, DeepSeek sigmoid + group-limited,
+    norm / no-norm) differentiated by torch autograd, plus the scores' VJPs from torch.sigmoid /
+    torch.softmax autograd (the reference differentiates jax.nn.sigmoid at moe.py:53)."""
+    from transformers import DeepseekV3Config, MixtralConfig, Qwen3MoeConfig
+    from transformers.models.deepseek_v3.modeling_deepseek_v3 import DeepseekV3TopkRouter
+    from transformers.models.mixtral.modeling_mixtral import MixtralTopKRouter
+    from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeTopKRouter
+
+    arrays = {}
+
+    def eye_(r, E):
+        with torch.no_grad():
+            r.weight.copy_(torch.eye(E))
+        return r
+
+    # Mixtral: E=8, k=2 (always renormalised)
+    lg = (_rng(111).standard_normal((64, 8)) * 1.3).astype(np.float32)
+    G = _rng(112).standard_normal((64, 8)).astype(np.float32)
+    r = eye_(MixtralTopKRouter(MixtralConfig(hidden_size=8, num_local_experts=8, num_experts_per_tok=2)), 8)
+    arrays["mixtral__idx"], arrays["mixtral__dl"] = _router_grad(r, lg, G)
+    arrays["mixtral__logits"], arrays["mixtral__G"] = lg, G
+    # Qwen3: E=128, k=8, norm and no-norm
+    lq = (_rng(113).standard_normal((32, 128)) * 0.9).astype(np.float32)
+    Gq = _rng(114).standard_normal((32, 128)).astype(np.float32)
+    for norm in (True, False):
+        cfg = Qwen3MoeConfig(hidden_size=128, num_experts=128, num_experts_per_tok=8, norm_topk_prob=norm)
+        r = eye_(Qwen3MoeTopKRouter(cfg), 128)
+        tag = "qwen_norm" if norm else "qwen_nonorm"
+        arrays[f"{tag}__idx"], arrays[f"{tag}__dl"] = _router_grad(r, lq, Gq)
+    arrays["qwen__logits"], arrays["qwen__G"] = lq, Gq
+    # DeepSeek-V3: E=64 in 8 groups, top-4 groups, k=8, bias, x2.5, norm and no-norm
+    ld = (_rng(115).standard_normal((32, 64)) * 1.5).astype(np.float32)
+    bd = (_rng(116).standard_normal(64) * 1e-3).astype(np.float32)
+    Gd = _rng(117).standard_normal((32, 64)).astype(np.float32)
+    for norm in (True, False):
+        cfg = DeepseekV3Config(hidden_size=64, n_routed_experts=64, num_experts_per_tok=8, n_group=8, topk_group=4,
+                               norm_topk_prob=norm, routed_scaling_factor=2.5)
+        r = eye_(DeepseekV3TopkRouter(cfg), 64)
+        with torch.no_grad():
+            r.e_score_correction_bias.copy_(torch.from_numpy(bd))
+        tag = "ds_norm" if norm else "ds_nonorm"
+        arrays[f"{tag}__idx"], arrays[f"{tag}__dl"] = _router_grad(r, ld, Gd)
+    arrays["ds__logits"], arrays["ds__bias"], arrays["ds__G"] = ld, bd, Gd
+    # scores: d/d logits of sum(scores * H), sigmoid and full softmax, float64
+    H = _rng(118).standard_normal((32, 64))
+    x = torch.from_numpy(ld.astype(np.float64)).requires_grad_(True)
+    (torch.sigmoid(x) * torch.from_numpy(H)).sum().backward()
+    arrays["scores__H"], arrays["scores__dl_sigmoid"] = H.astype(np.float32), x.grad.numpy()
+    x = torch.from_numpy(ld.astype(np.float64)).requires_grad_(True)
+    (torch.softmax(x, -1) * torch.from_numpy(H)).sum().backward()
+    arrays["scores__dl_softmax"] = x.grad.numpy()
+    np.savez_compressed(OUT / "router_grads.npz", **arrays)
+
+
+def make_moe_block_grads():
+    """HF DeepseekV3MoE (float64 experts, float32 router) differentiated by torch autograd:
+    d/d(x, gate weight, routed and shared expert weights) of sum(out * G) on the shared-expert
+    block fixture's inputs -- the gradients jax.grad takes through MoEBlock.__call__
+    (mintext/modules/moe.py:240-266), router included."""
+    from transformers import DeepseekV3Config
+    from transformers.models.deepseek_v3.modeling_deepseek_v3 import DeepseekV3MoE
+
+    p = moe_block_inputs()
+    D, E, K, I = p["D"], p["E"], p["K"], p["I"]
+    cfg = DeepseekV3Config(hidden_size=D, moe_intermediate_size=I, n_routed_experts=E, num_experts_per_tok=K,
+                           n_group=p["n_group"], topk_group=p["topk_group"], routed_scaling_factor=p["scale"],
+                           norm_topk_prob=True, n_shared_experts=1, hidden_act="silu")
+    blk = DeepseekV3MoE(cfg).double().train()
+    t64 = lambda a: torch.from_numpy(np.ascontiguousarray(a)).double()
+    with torch.no_grad():
+        blk.gate.weight.copy_(t64(p["wg"].T))
+        blk.gate.e_score_correction_bias.copy_(t64(p["bias"]))
+        blk.experts.gate_up_proj.copy_(t64(np.swapaxes(p["gate_up"], 1, 2)))
+        blk.experts.down_proj.copy_(t64(np.swapaxes(p["down"], 1, 2)))
+        blk.shared_experts.gate_proj.weight.copy_(t64(p["shared_gate_up"][:, :I].T))
+        blk.shared_experts.up_proj.weight.copy_(t64(p["shared_gate_up"][:, I:].T))
+        blk.shared_experts.down_proj.weight.copy_(t64(p["shared_down"].T))
+    G = _rng(22).standard_normal((p["T"], D))
+    xt = t64(p["x"]).requires_grad_(True)
+    out = blk(xt[None]).reshape(p["T"], D)
+    (out * torch.from_numpy(G)).sum().backward()
+    sg = torch.cat([blk.shared_experts.gate_proj.weight.grad.T, blk.shared_experts.up_proj.weight.grad.T], 1)
+    np.savez_compressed(OUT / "moe_block_grads.npz", G=G, dx=xt.grad.numpy(),
+                        dwg=blk.gate.weight.grad.T.numpy(),
+                        dgate_up=np.swapaxes(blk.experts.gate_up_proj.grad.numpy(), 1, 2),
+                        ddown=np.swapaxes(blk.experts.down_proj.grad.numpy(), 1, 2),
+                        dshared_gate_up=sg.numpy(), dshared_down=blk.shared_experts.down_proj.weight.grad.T.numpy())
+
+
 # --------------------------------------------------------------------------------- dispatch
 def _torch_route(idx: np.ndarray, E: int):
     flat = torch.from_numpy(idx.astype(np.int64)).reshape(-1)
@@ -283,6 +383,8 @@ def make_moe_block_shared():
 
 if __name__ == "__main__":
     torch.manual_seed(0)
+    make_router_grads()
+    make_moe_block_grads()
     make_routers()
     make_dispatch()
     make_gmm()

@@ -240,3 +240,93 @@ def test_moe_block_forward_with_gate(dev, dtype):
         ref = O.moe_block(f(t(p["x"])), idx, aux["topk_weights"].cpu().numpy(), f(t(p["gate_up"])), f(t(p["down"])),
                           f(t(p["shared_gate_up"])), f(t(p["shared_down"])))
         assert rel_err(out.reshape(p["T"], p["D"]).double().cpu().numpy(), ref) < 2e-2
+
+
+# ---- backward of the block, router included; the aux contract ----------------------------------
+
+def test_moe_block_backward_matches_hf_autograd(dev):
+    """MoEBlock.__call__ under autograd (fp32): gradients of sum(out * G) w.r.t. the tokens, the
+    gate weight (through the router's weights, moe.py:53,101), the routed and the shared expert
+    weights, against torch autograd through HF DeepseekV3MoE (float64 experts, float32 router)."""
+    from mintext_amd.moe import moe_block_forward
+
+    p = _block_inputs()
+    g = golden("moe_block_grads")
+    leaf = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev).requires_grad_(True)
+    x, wg, gu, dn = leaf(p["x"]), leaf(p["wg"]), leaf(p["gate_up"]), leaf(p["down"])
+    sgu, sdn = leaf(p["shared_gate_up"]), leaf(p["shared_down"])
+    out, aux = moe_block_forward(x.reshape(2, p["T"] // 2, p["D"]), wg, gu, dn, k=p["K"], scoring="sigmoid_group",
+                                 bias=torch.from_numpy(p["bias"]).to(dev), n_group=p["n_group"],
+                                 topk_group=p["topk_group"], routed_scaling_factor=p["scale"], shared_gate_up=sgu,
+                                 shared_down=sdn)
+    (out.reshape(p["T"], p["D"]) * torch.from_numpy(g["G"].astype(np.float32)).to(dev)).sum().backward()
+    for got, ref, name in ((x.grad, g["dx"], "x"), (wg.grad, g["dwg"], "gate_weight"),
+                           (gu.grad, g["dgate_up"], "gate_up"), (dn.grad, g["ddown"], "down"),
+                           (sgu.grad, g["dshared_gate_up"], "shared_gate_up"),
+                           (sdn.grad, g["dshared_down"], "shared_down")):
+        assert got is not None, name
+        assert rel_err(got.double().cpu().numpy(), ref) < 1e-5, name
+
+
+@pytest.mark.parametrize("scoring", ["sigmoid_group", "softmax"])
+@pytest.mark.parametrize("fused_gate", [False, True])
+def test_moe_block_aux_scores(dev, scoring, fused_gate):
+    """aux carries the reference's {"topk_indices", "scores"} (moe.py:262-266): [N, E] float32
+    sigmoid scores (softmax probabilities in softmax mode) of the gate logits."""
+    from mintext_amd.moe import moe_block_forward
+
+    rng = np.random.default_rng(11)
+    T, D, E, K, I = 256, 128, 16, 4, 128
+    cdt = torch.bfloat16 if fused_gate else torch.float32
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev).to(cdt)
+    x = t(rng.standard_normal((T, D)))
+    wg = t(rng.standard_normal((D, E)) * 0.2)
+    gu, dn = t(rng.standard_normal((E, D, 2 * I)) * 0.05), t(rng.standard_normal((E, I, D)) * 0.05)
+    kw = dict(k=K, scoring=scoring, n_group=4 if scoring != "softmax" else 1, topk_group=2 if scoring != "softmax" else 1)
+    with torch.no_grad():
+        out, aux = moe_block_forward(x, wg, gu, dn, **kw)
+    assert {"topk_indices", "scores"} <= set(aux)
+    s = aux["scores"]
+    assert s.shape == (T, E) and s.dtype == torch.float32
+    # the logits the router saw: the gate GEMM's output in the compute dtype
+    lg = (x.double() @ wg.double()).to(cdt).float().cpu().numpy()
+    if scoring == "softmax":
+        ex = np.exp(lg.astype(np.float64) - lg.max(-1, keepdims=True))
+        ref = ex / ex.sum(-1, keepdims=True)
+    else:
+        ref = O.sigmoid_f32(lg)
+    if fused_gate:  # the fused gate's logits are within one bf16 rounding of x @ Wg (checked elsewhere)
+        assert np.abs(s.cpu().numpy() - ref).max() < 2e-2
+    else:
+        np.testing.assert_allclose(s.cpu().numpy(), ref, rtol=1e-5, atol=1e-7)
+    # softmax mode: the selected experts hold the K largest of the scores returned beside them
+    if scoring == "softmax":
+        sn = s.cpu().numpy()
+        sel = np.zeros_like(sn, bool)
+        np.put_along_axis(sel, aux["topk_indices"].cpu().numpy().astype(np.int64), True, axis=1)
+        assert (np.where(sel, sn, np.inf).min(1) >= np.where(sel, -np.inf, sn).max(1)).all()
+
+
+@pytest.mark.parametrize("T,D,E,K,I", [(2048, 512, 8, 2, 512), (1024, 256, 32, 8, 256)])
+def test_bf16_layer_autograd_mfma_matches_oracle_vjp(dev, T, D, E, K, I):
+    """moe_experts_forward under autograd on the bf16 MFMA kernels (gmm fwd, dlhs, tgmm, SwiGLU
+    and its VJP, route / unroute VJPs) against the oracle's float64 VJP on the same inputs."""
+    from mintext_amd.kernels import route_topk
+    from mintext_amd.moe import moe_experts_forward
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(T + E)
+    x = torch.randn(T, D, device=dev, generator=gen).bfloat16().requires_grad_(True)
+    gu = (torch.randn(E, D, 2 * I, device=dev, generator=gen) * 0.05).bfloat16().requires_grad_(True)
+    dn = (torch.randn(E, I, D, device=dev, generator=gen) * 0.05).bfloat16().requires_grad_(True)
+    idx, w = route_topk(torch.randn(T, E, device=dev, generator=gen), K)
+    w = w.clone().requires_grad_(True)
+    G = torch.randn(T, D, device=dev, generator=gen)
+    out = moe_experts_forward(x, idx, w, gu, dn)
+    assert out.dtype == torch.float32
+    (out * G).sum().backward()
+    f = lambda a: a.detach().float().cpu().numpy()
+    dx, dw, dgu, ddn = O.moe_experts_vjp(f(x), idx.cpu().numpy(), f(w), f(gu), f(dn), f(G))
+    for got, ref, name in ((x.grad, dx, "x"), (w.grad, dw, "w"), (gu.grad, dgu, "gate_up"), (dn.grad, ddn, "down")):
+        assert got.dtype == (torch.float32 if name == "w" else torch.bfloat16), name
+        assert rel_err(f(got), ref) < 2e-2, name

@@ -128,10 +128,11 @@ def test_gate_route_topk_fused(dev, T, D, E, K, scoring, ng, tg, scale, with_bia
     ref = x.double().cpu() @ wg.double().cpu()
     got = lg.double().cpu()
     assert ((got - ref).abs() <= 2.0 ** -8 * ref.abs() + 1e-4).all()
-    idx2, w2 = route_topk(lg, K, shared_expert=se, **kw)
+    idx2, w2, s2 = route_topk(lg, K, shared_expert=se, return_scores=True, **kw)
     assert torch.equal(idx, idx2) and torch.equal(w, w2)
-    idx3, w3 = gate_route_topk(x, wt, K, shared_expert=se, **kw)  # deterministic
+    idx3, w3, s3 = gate_route_topk(x, wt, K, shared_expert=se, return_scores=True, **kw)  # deterministic
     assert torch.equal(idx, idx3) and torch.equal(w, w3)
+    assert torch.equal(s3, s2)  # the scores of route_topk on the same bf16 logits, bit for bit
 
 
 def test_gate_route_topk_unsupported_shapes_raise(dev):
@@ -144,3 +145,57 @@ def test_gate_route_topk_unsupported_shapes_raise(dev):
     xb = x.bfloat16()
     with pytest.raises(MtxError):
         gate_route_topk(xb, torch.randn(300, 64, device=dev).bfloat16(), 2)  # E > 256
+
+
+# ---- router VJP ---------------------------------------------------------------------------------
+VJP_FIXTURES = [("mixtral", "mixtral", "softmax", True, 1.0), ("qwen_norm", "qwen", "softmax", True, 1.0),
+                ("qwen_nonorm", "qwen", "softmax", False, 1.0), ("ds_norm", "ds", "sigmoid_group", True, 2.5),
+                ("ds_nonorm", "ds", "sigmoid_group", False, 2.5)]
+
+
+@pytest.mark.parametrize("tag,base,scoring,norm,scale", VJP_FIXTURES)
+def test_router_bwd_matches_hf_autograd(dev, tag, base, scoring, norm, scale):
+    """mtx_router_topk_bwd against torch autograd through the HF routers (float32)."""
+    from mintext_amd.kernels.router import router_topk_bwd
+
+    g = golden("router_grads")
+    lg, G, idx = g[f"{base}__logits"], g[f"{base}__G"], g[f"{tag}__idx"]
+    dw = np.take_along_axis(G, idx, axis=1)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    dl = router_topk_bwd(t(lg), t(idx), idx.shape[1], t(dw), None, scoring=scoring, norm_topk_prob=norm,
+                         routed_scaling_factor=scale)
+    assert dl.dtype == torch.float32
+    ref = g[f"{tag}__dl"]
+    err = np.linalg.norm(dl.cpu().numpy() - ref) / np.linalg.norm(ref)
+    assert err < 1e-5
+
+
+@pytest.mark.parametrize("scoring,T,E,K,ng,tg,norm,dt", [
+    ("sigmoid_group", 4096, 256, 8, 8, 4, True, torch.bfloat16),   # C3 router
+    ("softmax", 16384, 128, 8, 1, 1, True, torch.bfloat16),        # C4 / C5 router
+    ("softmax", 8192, 8, 2, 1, 1, True, torch.float32),            # C2 router
+    ("softmax", 1000, 64, 6, 1, 1, False, torch.float32),
+    ("sigmoid_group", 777, 64, 8, 8, 4, False, torch.float32),
+    ("softmax", 300, 1024, 8, 1, 1, True, torch.float32),
+])
+def test_router_bwd_matches_oracle(dev, scoring, T, E, K, ng, tg, norm, dt):
+    """The router VJP (weights and scores) through autograd of route_topk against the float64
+    oracle on the GPU's own indices; the logits' gradient comes back in the logits' dtype."""
+    from mintext_amd.kernels import route_topk
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(T + E)
+    logits = (torch.randn(T, E, device=dev, generator=gen) * 1.3).to(dt).requires_grad_(True)
+    bias = torch.randn(E, device=dev, generator=gen) * 1e-3 if scoring != "softmax" else None
+    idx, w, s = route_topk(logits, K, scoring=scoring, bias=bias, n_group=ng, topk_group=tg, norm_topk_prob=norm,
+                           routed_scaling_factor=2.5, return_scores=True)
+    assert w.requires_grad and s.requires_grad and not idx.requires_grad
+    gw = torch.randn(T, K, device=dev, generator=gen)
+    gs = torch.randn(T, E, device=dev, generator=gen)
+    ((w * gw).sum() + (s * gs).sum()).backward()
+    assert logits.grad.dtype == dt
+    ref = O.router_vjp(logits.detach().float().cpu().numpy(), idx.cpu().numpy(), gw.cpu().numpy(),
+                       gs.cpu().numpy(), scoring, norm, 2.5)
+    got = logits.grad.double().cpu().numpy()
+    err = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert err < (1e-5 if dt == torch.float32 else 2e-2 / 4)

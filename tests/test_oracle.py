@@ -111,6 +111,83 @@ def test_bias_steers_selection():
     assert (idx[:, 0] == 0).all()
 
 
+# ------------------------------------------------------------------------------ router VJP
+@pytest.mark.parametrize("case", [("mixtral", "mixtral", "softmax", True, 1.0), ("qwen_norm", "qwen", "softmax", True, 1.0),
+                                  ("qwen_nonorm", "qwen", "softmax", False, 1.0),
+                                  ("ds_norm", "ds", "sigmoid_group", True, 2.5),
+                                  ("ds_nonorm", "ds", "sigmoid_group", False, 2.5)])
+def test_router_vjp_matches_hf_autograd(case):
+    """d logits of sum_k w[t,k] G[t, idx[t,k]]: torch autograd through the HF routers (float32)."""
+    tag, base, scoring, norm, scale = case
+    g = golden("router_grads")
+    lg, G, idx = g[f"{base}__logits"], g[f"{base}__G"], g[f"{tag}__idx"]
+    if scoring == "softmax":
+        ours, _, _ = O.router_softmax(lg, idx.shape[1], norm, scale)
+    else:
+        ours, _, _ = O.router_sigmoid_group(lg, idx.shape[1], g["ds__bias"], 8, 4, norm, scale)
+    for t in range(lg.shape[0]):  # HF's DeepSeek top-k is unsorted: same sets
+        assert set(ours[t].tolist()) == set(idx[t].tolist())
+    dw = np.take_along_axis(G, idx, axis=1)
+    dl = O.router_vjp(lg, idx, dw, None, scoring, norm, scale)
+    assert rel_err(dl, g[f"{tag}__dl"]) < 2e-6
+    # the selection is not differentiated: unselected experts of a renormalised softmax get 0
+    if scoring == "softmax" and norm:
+        mask = np.ones_like(dl, bool)
+        np.put_along_axis(mask, idx, False, axis=1)
+        assert np.abs(dl[mask]).max() == 0.0 and np.abs(g[f"{tag}__dl"][mask]).max() < 1e-6
+
+
+@pytest.mark.parametrize("scoring", ["sigmoid_group", "softmax"])
+def test_router_vjp_scores_term_matches_torch_autograd(scoring):
+    g = golden("router_grads")
+    lg, H = g["ds__logits"].astype(np.float64), g["scores__H"].astype(np.float64)
+    idx = np.zeros((lg.shape[0], 1), np.int32)
+    dl = O.router_vjp(lg, idx, None, H, scoring, True, 1.0)
+    ref = g["scores__dl_sigmoid"] if scoring == "sigmoid_group" else g["scores__dl_softmax"]
+    assert rel_err(dl, ref) < 1e-7  # the fixture used H before its float32 storage rounding
+
+
+@pytest.mark.parametrize("scoring,norm", [("softmax", True), ("softmax", False), ("sigmoid_group", True),
+                                          ("sigmoid_group", False)])
+def test_router_vjp_central_differences(scoring, norm):
+    """The closed form against central differences of the weights/scores restatement."""
+    rng = np.random.default_rng(7)
+    T, E, k = 6, 12, 3
+    lg = rng.standard_normal((T, E))
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    dw, ds = rng.standard_normal((T, k)), rng.standard_normal((T, E))
+    f = lambda l: sum(float((a * b).sum()) for a, b in zip(O.router_weights_given_idx(l, idx, scoring, norm, 2.5),
+                                                             (dw, ds)))
+    num = np.zeros((T, E))
+    h = 1e-6
+    for t, e in itertools.product(range(T), range(E)):
+        p, m = lg.copy(), lg.copy()
+        p[t, e] += h
+        m[t, e] -= h
+        num[t, e] = (f(p) - f(m)) / (2 * h)
+    # scores enter with unit weight (no routed scaling), weights with the scaling factor
+    dl = O.router_vjp(lg, idx, dw, ds, scoring, norm, 2.5)
+    assert np.abs(dl - num).max() < 1e-7
+
+
+def test_moe_block_vjp_matches_hf_deepseek_autograd():
+    """Block backward, router included: HF DeepseekV3MoE (float64 experts, float32 router) under
+    torch autograd on the shared-expert fixture's inputs."""
+    p, g = _block_inputs(), golden("moe_block_grads")
+    r = O.moe_block_vjp(p["x"], p["wg"], p["gate_up"], p["down"], g["G"], k=p["K"], bias=p["bias"],
+                        n_group=p["n_group"], topk_group=p["topk_group"], routed_scaling_factor=p["scale"],
+                        shared_gate_up=p["shared_gate_up"], shared_down=p["shared_down"])
+    assert rel_err(r["dx"], g["dx"]) < 1e-6
+    assert rel_err(r["d_gate_weight"], g["dwg"]) < 1e-6
+    # HF's routed weights are float32: every routed term carries their 1e-7 rounding
+    assert rel_err(r["d_gate_up"], g["dgate_up"]) < 1e-6
+    assert rel_err(r["d_down"], g["ddown"]) < 1e-6
+    assert rel_err(r["d_shared_gate_up"], g["dshared_gate_up"]) < 1e-12
+    assert rel_err(r["d_shared_down"], g["dshared_down"]) < 1e-12
+    # the router's term is a real part of dx and the only source of the gate weight's gradient
+    assert np.abs(g["dwg"]).max() > 1e-2
+
+
 # -------------------------------------------------------------------------------- dispatch
 def _dispatch_cases():
     g = golden("dispatch")
