@@ -228,6 +228,18 @@ int mtx_tgmm(const void* x, const void* g, const int32_t* group_sizes, int dtype
 int mtx_gmm_tiled(int op, const void* x, const void* w, const int32_t* group_sizes, int dtype,
                   int64_t M, int64_t Kin, int64_t Kout, int64_t E, int64_t tile_m, int64_t tile_group,
                   void* out, void* workspace, int64_t workspace_bytes, void* stream);
+/* mtx_gmm_tiled without a workspace: no counterpart in the reference.  For callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The tile lists live in a device array of the library (about 280 KB per
+ * device, held until the process ends); every tile runs whole (no split tail), so the results
+ * equal mtx_gmm_tiled's with a workspace of only the tile lists, bit for bit.  Limits:
+ * M <= MTX_GMM_NOALLOC_MAX_ROWS and E <= MTX_GMM_NOALLOC_MAX_EXPERTS, else MTX_ERR_UNSUPPORTED.
+ * Calls that overlap on one device (other streams or threads) race on the array: serialise them. */
+#define MTX_GMM_NOALLOC_MAX_ROWS    1048576
+#define MTX_GMM_NOALLOC_MAX_EXPERTS 1024
+int mtx_gmm_tiled_noalloc(int op, const void* x, const void* w, const int32_t* group_sizes, int dtype,
+                          int64_t M, int64_t Kin, int64_t Kout, int64_t E, int64_t tile_m,
+                          int64_t tile_group, void* out, void* stream);
 /* route (moe_dispatch.py:47-81, its row gather) fused into the A operand of the forward GEMMs
  * (MoEExperts._forward_kernel, mintext/modules/moe.py:161-196): x [x_rows,Kin] in token order
  * (BF16), row_index [M] = sort_indices of mtx_route (computed without tokens), index_div = K

@@ -58,6 +58,7 @@ SIGNATURES = {
     "mtx_gmm_dlhs": (_I, [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "mtx_tgmm": (_I, [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "mtx_gmm_tiled": (_I, [_I, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
+    "mtx_gmm_tiled_noalloc": (_I, [_I, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P]),
     "mtx_gmm_gathered": (_I, [_I, _P, _I64, _P, _I64, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64,
                               _P]),
     "mtx_swiglu": (_I, [_P, _I, _I64, _I64, _P, _P]),

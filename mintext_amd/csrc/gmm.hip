@@ -26,6 +26,7 @@
 #include "lds_dma.h"
 #include <type_traits>
 #include <algorithm>
+#include <mutex>
 
 namespace mtx {
 
@@ -1550,4 +1551,62 @@ extern "C" int mtx_swiglu_bwd(const void* h, const void* dy, int dtype, int64_t 
     hipLaunchKernelGGL(swiglu_bwd_kernel<uint16_t>, dim3(blocks), dim3(256), 0, st, (const uint16_t*)h,
                        (const uint16_t*)dy, M, I, (uint16_t*)dh);
   return check_launch();
+}
+
+// ---- mtx_gmm_tiled without a caller workspace ---------------------------------------------------
+// For callers that cannot allocate device memory (code under HIP graph capture, serving loops):
+// the tile lists live in `scratch`, a file-scope device array of kNoAllocScratchBytes, one copy
+// per device, held until the process ends.  Its address on each device comes from
+// hipGetSymbolAddress on the first call with that device current and is passed to the kernels like
+// a workspace; the symbol itself is never handed to device code from the host.  The array holds
+// no split-tail partials, so every tile runs whole (the results equal mtx_gmm_tiled's with a
+// tile-list-only workspace, bit for bit).  The tile-list kernel of each call rewrites everything
+// the GEMM reads from the array, so no clearing is needed between calls; calls that overlap on
+// one device (concurrent streams or threads) race on the array.
+namespace mtx {
+constexpr int64_t kNoAllocMaxM = MTX_GMM_NOALLOC_MAX_ROWS;
+constexpr int64_t kNoAllocMaxE = MTX_GMM_NOALLOC_MAX_EXPERTS;
+constexpr int64_t kNoAllocScratchBytes =
+    ((48 + 2 * kNoAllocMaxE + 1) * 4 + 255) / 256 * 256 + (kNoAllocMaxM / kMinBM + kNoAllocMaxE + 1) * 16;
+static_assert(sizeof(MTile) == 16, "tile record size");
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+// The device address of `scratch` on the current device (looked up once per device).
+static int scratch_ptr_current(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    g_last_hip_error = (int)e;
+    return MTX_ERR_HIP;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return MTX_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      g_last_hip_error = (int)e;
+      return MTX_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MTX_OK;
+}
+}  // namespace mtx
+
+extern "C" int mtx_gmm_tiled_noalloc(int op, const void* x, const void* w, const int32_t* group_sizes, int dtype,
+                                     int64_t M, int64_t Kin, int64_t Kout, int64_t E, int64_t tile_m,
+                                     int64_t tile_group, void* out, void* stream) {
+  if (M < 0 || E < 1) return MTX_ERR_ARG;
+  if (M > kNoAllocMaxM || E > kNoAllocMaxE) return MTX_ERR_UNSUPPORTED;  // beyond the scratch array
+  void* ws = nullptr;
+  const int rc = scratch_ptr_current(&ws);
+  if (rc != MTX_OK) return rc;
+  return mtx_gmm_tiled(op, x, w, group_sizes, dtype, M, Kin, Kout, E, tile_m, tile_group, out, ws,
+                       kNoAllocScratchBytes, stream);
 }
