@@ -73,40 +73,36 @@ class EventTimer:
         return float(np.mean([a.elapsed_time(b) for a, b in self.pairs])) if self.pairs else 0.0
 
 
-def _cpu_baseline_layer(x, logits, gate_up, down, cfg, budget_s=12.0, shared=None):
-    """Oracle forward (float64) on the first Ts tokens; Ts doubles until the run takes >= budget/3."""
-    from oracle import moe_oracle as O
+def _cpu_baseline_layer(x, logits, gate_up, down, cfg, shared=None, target_s=4.0):
+    """The layer forward on the host CPU in the reference's arithmetic (oracle/cpu_port.py: torch,
+    bf16 operands, f32 routing and combine) on the first Ts tokens of the same inputs: one probe
+    run sizes Ts for about ``target_s`` per run, then 1 warm-up and the median of 3 timed runs."""
+    import torch
 
-    try:
-        from threadpoolctl import threadpool_info
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:
-        cores = len(os.sched_getaffinity(0))
-    gu = gate_up.astype(np.float64)
-    dn = down.astype(np.float64)
+    from oracle import cpu_port
+
+    torch.set_num_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    cores = torch.get_num_threads()
     T = x.shape[0]
-    ts, best = 16, None
-    while True:
+    kw = dict(k=cfg["K"], scoring=cfg["scoring"], shared=shared, n_group=cfg.get("n_group", 1),
+              topk_group=cfg.get("topk_group", 1), routed_scaling_factor=cfg.get("scale", 1.0))
+
+    def once(ts):
         t0 = time.perf_counter()
-        if cfg["scoring"] == "softmax":
-            idx, w, _ = O.router_softmax(logits[:ts], cfg["K"])
-        else:
-            idx, w, _ = O.router_sigmoid_group(logits[:ts], cfg["K"], n_group=cfg.get("n_group", 1),
-                                               topk_group=cfg.get("topk_group", 1),
-                                               routed_scaling_factor=cfg.get("scale", 1.0))
-        if shared is None:
-            O.moe_experts(x[:ts].astype(np.float64), idx, w, gu, dn)
-        else:
-            O.moe_block(x[:ts].astype(np.float64), idx, w, gu, dn, shared[0], shared[1])
-        dt = time.perf_counter() - t0
-        best = (ts, dt)
-        if dt >= budget_s / 3 or ts >= T:
-            break
-        ts = min(T, ts * 2)
-    ts, dt = best
-    return {"value": ts / dt, "unit": "tokens/s", "cores": int(cores), "kind": "port",
-            "sample": f"numpy float64 oracle (oracle/moe_oracle.py) of the full layer forward on the first {ts} "
-                      f"of {T} tokens of the same inputs, one run, {dt:.2f} s"}
+        cpu_port.moe_layer(x[:ts], logits[:ts], gate_up, down, **kw)
+        return time.perf_counter() - t0
+
+    ts = min(T, 256)
+    dt = once(ts)
+    ts = int(min(T, max(ts, ts * target_s / max(dt, 1e-3))))
+    once(ts)  # warm-up at the timed size
+    runs = sorted(once(ts) for _ in range(3))
+    med = runs[1]
+    dt_name = {torch.bfloat16: "bf16", torch.float32: "f32"}[x.dtype]
+    return {"value": ts / med, "unit": "tokens/s", "cores": int(cores), "kind": "port",
+            "sample": f"torch-CPU restatement of the reference layer (oracle/cpu_port.py; {dt_name} operands, "
+                      f"f32 routing and combine) on the first {ts} of {T} tokens of the same inputs; 1 warm-up, "
+                      f"median of 3 runs = {med:.2f} s"}
 
 
 def _zipf_bias(E, s, rng, beta=0.55):
@@ -309,6 +305,22 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
         kern_flops = 2.0 * Mg * D * 2 * I
         achieved = kern_flops / (gu_ms * 1e-3) / 1e12
         dominant = "gmm_fp8_swiglu (gate_up + SwiGLU + requant)" if fp8 else "gmm_swiglu (gate_up + fused SwiGLU)"
+    traffic = _traffic(cfg_name)
+    tsrc = {"traffic_source": f"profiles/traffic_{cfg_name}.json (rocprofv3 FETCH_SIZE/WRITE_SIZE of this kernel, "
+                              "scaled by a plain copy's counters)"} if traffic is not None else {}
+    if cfg_name == "deepseek":
+        # C3 streams its routed weights once per layer at ~128 rows per expert (arithmetic intensity
+        # ~128 FLOP/B < the bf16 ridge of ~315): HBM-bound.  Algorithmic bytes of the gate_up launch:
+        # the routed gate_up weights, the token rows (read once each) and the [M, I] bf16 output.
+        alg_b = Eg * D * 2 * I * 2 + T * D * 2 + Mg * I * 2
+        gbs = alg_b / (gu_ms * 1e-3) / 1e9
+        roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic, **tsrc,
+                    "bytes_per_launch": alg_b, "mfma": {"achieved": round(achieved, 1), "peak": peak,
+                                                        "unit": "TFLOP/s", "frac": round(achieved / peak, 4)}}
+    else:
+        roofline = {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 1), "peak": peak,
+                    "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic, **tsrc}
     tokens_per_s = T / (ms * 1e-3)
     gemm_ms = gu_ms + dn_ms
     # dispatch: token rows read once (bf16; fp8 runs quantise them in the same pass), sorted rows
@@ -352,8 +364,7 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
                              "dispatch_ms": round(t_disp.mean_ms(), 4), "combine_ms": round(t_comb.mean_ms(), 4),
                              "dispatch_GBs": round(disp_b / (t_disp.mean_ms() * 1e-3) / 1e9, 1) if t_disp.pairs else None,
                              "combine_GBs": round(comb_b / (t_comb.mean_ms() * 1e-3) / 1e9, 1) if t_comb.pairs else None},
-        "roofline": {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 1), "peak": peak,
-                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": _traffic(cfg_name)},
+        "roofline": roofline,
         "load": {"min": int(gs_host.min()), "max": int(gs_host.max()), "mean": float(gs_host.mean()),
                  "empty": int((gs_host == 0).sum())},
         "wall_s": round(wall, 3),
@@ -361,10 +372,12 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
     if graph_ms is not None:
         res["hip_graph"] = {"ms_per_step": round(graph_ms, 4), "tokens_per_s": round(T / (graph_ms * 1e-3), 1)}
     if cpu_baseline and cfg_name not in ("qwen3_bwd",):
-        sh = None if shared is None else (shared[0][0].float().cpu().numpy(), shared[1][0].float().cpu().numpy())
-        res["cpu_baseline"] = _cpu_baseline_layer(x.float().cpu().numpy(), logits.float().cpu().numpy(),
-                                                  gate_up[:E].float().cpu().numpy(), down[:E].float().cpu().numpy(),
-                                                  cfg, shared=sh)
+        # fp8 has no reference counterpart: the CPU leg runs the reference's bf16 layer on the same tokens
+        hdt = torch.float32 if cfg["dtype"] == "f32" else torch.bfloat16
+        h = lambda t: t.to(hdt).cpu()
+        sh = None if shared is None else (h(shared[0][0]), h(shared[1][0]))
+        res["cpu_baseline"] = _cpu_baseline_layer(h(x), logits.float().cpu(), h(gate_up[:E]), h(down[:E]), cfg,
+                                                  shared=sh)
     return res
 
 

@@ -21,6 +21,19 @@ inline int check_launch() {
   return MTX_OK;
 }
 
+// Compute units of the current device (cached per device; 0 if the query fails).
+inline int device_cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 inline int dtype_size(int dt) {
   switch (dt) {
     case MTX_F32: return 4;

@@ -1116,7 +1116,9 @@ static int launch_fp8(const f8::Args& a, const int32_t* gs, int64_t E, int64_t n
     b.count = count;
     b.tiles = tiles;
     int64_t grid = round_up((ceil_div(a.M, 256) + E + 1) * nn, 8);
-    if (grid > 256) grid = 256;  // persistent: one workgroup per CU
+    const int ncu = device_cu_count();
+    const int64_t cap = ncu > 0 ? round_up(ncu, 8) : 256;
+    if (grid > cap) grid = cap;  // persistent: one workgroup per CU (a multiple of the 8 XCDs)
     hipLaunchKernelGGL((f8::gmm_fp8_v4_kernel<EPI>), dim3((unsigned)grid), dim3(512), 0, st, b);
     return check_launch();
   }

@@ -13,14 +13,17 @@
 // into a compact list of (expert, row_begin, row_end) M-tiles plus group offsets; the GEMM
 // grid is sized to the upper bound ceil(M/BM) + E + 1 tiles and surplus workgroups exit.
 //
-// bf16 path: CDNA4 MFMA v_mfma_f32_32x32x16_bf16 with f32 accumulation.  A workgroup owns
-// a BM x BN output tile, its waves a (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks.
-// Operand tiles are staged through LDS in a k-contiguous layout (one 128-byte row = 64
-// bf16 of the reduction dim per M/N index) with the 16-byte chunks XOR-swizzled so that
-// both the 16-byte fragment reads and the tile writes avoid bank conflicts; two LDS
-// buffers alternate so the global loads of step k+1 overlap the MFMAs of step k.  Operands
-// whose reduction dim is not contiguous in HBM (W in the forward pass, both operands of
-// tgmm) are loaded as 8x8 blocks and transposed in registers with v_perm_b32.
+// bf16 path: CDNA4 MFMA v_mfma_f32_32x32x16_bf16 with f32 accumulation.  The main kernel
+// (gmm_v3_kernel, FWD / SWIGLU / DLHS / TGMM) computes 256x256 (or 128x256) output tiles with
+// 8 (4) waves; every operand load is a global_load_lds_dwordx4 straight into a 4-deep (3-deep) LDS
+// ring, three stages ahead of the MFMAs, with 16-byte chunks XOR-swizzled so that the DMA writes
+// and the fragment reads are bank-conflict-free.  Operands whose reduction dim is contiguous in
+// HBM are read as fragments with ds_read_b128; the others (W in the forward pass, both operands
+// of tgmm) keep their natural layout and are turned into MFMA operands by ds_read_b64_tr_b16
+// (gfx950 transpose read).  The epilogue (SwiGLU fused for gate_up) stages the tile through the
+// idle ring and writes whole 128-byte lines.  gmm_mfma_kernel, an earlier register-staged design
+// (two LDS buffers, 8x8 register transposes), runs only the shapes whose operands exceed 32-bit
+// byte offsets.
 // f32 path (and shapes the MFMA tiling does not cover): an LDS-tiled exact-fp32 FMA kernel.
 #include "common.h"
 #include "lds_dma.h"

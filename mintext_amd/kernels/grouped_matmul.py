@@ -14,7 +14,9 @@ width) -- ``tm`` rows per m-tile (128 or 256; other values round to the nearer),
 per XCD scheduling group (1..64).  ``None`` and any tuple with another ``tn`` (the reference's
 TPU tilings, such as its default (128, 128, 128)) keep the shape heuristics.  The
 9-tuple of ``grouped_matmul_vjp`` is padded from 3 like the reference (fwd, dlhs, tgmm; the
-tgmm entry is not used).  Tile configurations never change the output bits.  ``mosaic_fusion``
+tgmm entry is not used).  Every tile configuration computes the same f32 sums; the results are
+bit-identical unless the split tail splits different tiles, and then agree to a bf16 rounding
+(``mtx_gmm_workspace_size``).  ``mosaic_fusion``
 is accepted and ignored.  ``group_sizes`` never leaves the device.  Extra entry points beyond the reference: ``grouped_matmul_swiglu``
 (gate_up GEMM with the SwiGLU of moe.py:195-196 fused into the epilogue) and ``swiglu``.
 """

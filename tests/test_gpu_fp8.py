@@ -200,3 +200,27 @@ def test_gmm_fp8_swiglu_gathered_short_k_unsupported(dev):
     with pytest.raises(L.MtxError) as ei:
         grouped_matmul_fp8_swiglu_gathered(xq, xs, si, K, wq, wsc, gs)
     assert ei.value.status == L.MTX_ERR_UNSUPPORTED
+
+
+def test_gmm_fp8_operand_beyond_32bit_offsets(dev):
+    """fp8 codes of 4 GiB (2^21 rows x 2048): byte offsets past 32 bits take the register-staged
+    fp8 kernel; sampled rows against the dequantised float64 product."""
+    from mintext_amd.kernels.fp8 import grouped_matmul_fp8, quantize_fp8_weights
+
+    M, Kin, Kout, E = 1 << 21, 2048, 256, 2
+    gs = np.array([1234567, M - 1234567], np.int32)
+    codes = torch.randint(0, 127, (M, Kin), dtype=torch.uint8, device=dev)  # magnitudes 0..448, no NaN code
+    codes |= torch.randint(0, 2, (M, Kin), dtype=torch.uint8, device=dev) << 7
+    xq = codes.view(torch.float8_e4m3fn)
+    xs = torch.rand(M, Kin // 128, device=dev) * 0.1 + 0.01
+    wq, ws = quantize_fp8_weights((torch.randn(E, Kin, Kout, device=dev) * 0.03).bfloat16())
+    out = grouped_matmul_fp8(xq, xs, wq, ws, _t(gs, dev))
+    rng = np.random.default_rng(10)
+    rows = np.unique(np.concatenate([[0, 1234566, 1234567, M - 1], rng.integers(0, M, 40)]))
+    tr = torch.from_numpy(rows).to(dev)
+    xd = O.dequant_rows(_u8(xq[tr]), xs[tr].cpu().numpy())
+    wd = O.dequant_weights(_u8(wq), ws.cpu().numpy())
+    ref = np.stack([xd[i] @ wd[0 if r < 1234567 else 1] for i, r in enumerate(rows)])
+    assert rel_err(out[tr].float().cpu().numpy(), ref) < 1e-2
+    del xq, out
+    torch.cuda.empty_cache()

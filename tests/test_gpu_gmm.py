@@ -475,3 +475,27 @@ def test_gathered_paths_on_empty_inputs(dev):
     out = moe_experts_forward(x, idx, torch.zeros(0, K, device=dev), w, down)
     assert out.shape == (0, D)
 
+
+
+def test_gmm_bf16_operand_beyond_32bit_offsets(dev):
+    """An A operand of 4 GiB (2^21 rows x 1024 bf16): byte offsets past 32 bits take the
+    register-staged MFMA kernel; sampled rows of every group against float64."""
+    from mintext_amd.kernels import grouped_matmul
+
+    M, Kin, Kout, E = 1 << 21, 1024, 256, 3
+    gs = np.array([700001, 0, M - 700001], np.int32)
+    x = torch.empty(M, Kin, dtype=torch.bfloat16, device=dev)
+    x.normal_()
+    w = (torch.randn(E, Kin, Kout, device=dev) * 0.03).bfloat16()
+    out = grouped_matmul(x, w, _t(gs, dev))
+    rng = np.random.default_rng(9)
+    rows = np.unique(np.concatenate([[0, 700000, 700001, M - 1], rng.integers(0, M, 40)]))
+    off = np.concatenate([[0], np.cumsum(gs)])
+    tr = torch.from_numpy(rows).to(dev)
+    xs = x[tr].double().cpu().numpy()
+    got = out[tr].double().cpu().numpy()
+    ref = np.stack([xs[i] @ w[int(np.searchsorted(off, r, side="right") - 1)].double().cpu().numpy()
+                    for i, r in enumerate(rows)])
+    _close(got, ref, 2e-2)
+    del x, out
+    torch.cuda.empty_cache()
