@@ -44,6 +44,9 @@
  *   mtx_gmm_gathered       <- route's row gather (moe_dispatch.py:67,76) fused into the
  *                             forward GEMMs of MoEExperts._forward_kernel (moe.py:161-196)
  *   mtx_gmm_fp8_swiglu_gathered <- the same for the blockwise-fp8 gate_up GEMM
+ *   mtx_quant_fp8_weights_t, mtx_gmm_fp8_dlhs, mtx_quant_fp8_grouped_t, mtx_tgmm_fp8
+ *                          <- no counterpart; fp8 forms of the dlhs and tgmm backward
+ *                             (grouped_matmul.py:151-187, 197-235)
  *   mtx_transpose_batched  <- _import_expert_weights / _export_expert_weights
  *                             (mintext/checkpoint/conversion.py:80-166), on the device
  */
@@ -300,6 +303,35 @@ int mtx_gmm_fp8_swiglu_gathered(const uint8_t* xq, const float* x_scale, int64_t
                                 int64_t M, int64_t Kin, int64_t I, int64_t E,
                                 uint8_t* out_q, float* out_scale, void* out_bf16,
                                 void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---- fp8 e4m3fn blockwise backward (no reference counterpart; the bf16 forms are dlhs and tgmm,
+ * mintext/kernels/grouped_matmul.py:151-187 and :197-235, with the forward's fp8 conventions) ----
+ * dlhs: dX = dY @ W^T.  W's codes in its own layout, w_qt [E,Kin,Kout] with the same 128x128 block
+ * scales as mtx_quant_fp8_weights transposed, w_scale_t [E,Kin/128,Kout/128]:                     */
+int mtx_quant_fp8_weights_t(const void* w, int dtype, int64_t E, int64_t Kin, int64_t Kout,
+                            uint8_t* w_qt, float* w_scale_t, void* stream);
+/* dx [M,Kin] bf16 = sum_kb (gq*gs)(w_qt*ws_t)^T over 128-Kout blocks: gq [M,Kout] + g_scale
+ * [M,Kout/128] from mtx_quant_fp8_rows of dY; Kin % 256 == 0 (else MTX_ERR_UNSUPPORTED).
+ * Workspace: mtx_gmm_workspace_size(M,E).                                                         */
+int mtx_gmm_fp8_dlhs(const uint8_t* gq, const float* g_scale, const uint8_t* w_qt, const float* w_scale_t,
+                     const int32_t* group_sizes, int64_t M, int64_t Kin, int64_t Kout, int64_t E, void* dx,
+                     void* workspace, int64_t workspace_bytes, void* stream);
+/* tgmm: dW[e] = X_e^T G_e over the rows of group e.  Operands are quantised in expert-aligned
+ * chunks of 128 rows (chunk c of group e = its rows 128c..128c+127, zero-padded), transposed:
+ * xt [F, 128*C] e4m3fn with C = mtx_fp8_grouped_chunks(M,E) chunk slots, scales [F,C] (blocks = 0:
+ * one per feature and chunk) or [F/128,C] (blocks = 1: one per 128x128 block).  F % 128 == 0.
+ * Workspace: mtx_fp8_grouped_workspace_size(E).                                                   */
+int64_t mtx_fp8_grouped_chunks(int64_t M, int64_t E);
+int64_t mtx_fp8_grouped_workspace_size(int64_t E);
+int mtx_quant_fp8_grouped_t(const void* x, int dtype, const int32_t* group_sizes, int64_t M, int64_t F,
+                            int64_t E, int blocks, uint8_t* xt, float* xt_scale, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+/* dw [E,F,N] bf16, f32 accumulation: xt/xt_scale of X (blocks = 0), gt/gt_scale of G (blocks = 1),
+ * both from mtx_quant_fp8_grouped_t with the same group_sizes and M; an empty group gives zeros.
+ * F % 256 == 0 and N % 256 == 0 (else MTX_ERR_UNSUPPORTED).                                       */
+int mtx_tgmm_fp8(const uint8_t* xt, const float* xt_scale, const uint8_t* gt, const float* gt_scale,
+                 const int32_t* group_sizes, int64_t M, int64_t F, int64_t N, int64_t E, void* dw,
+                 void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---- expert weight layouts -------------------------------------------------------------
  * Batched transpose-copy (the per-expert HF <-> fused conversions of

@@ -1,0 +1,459 @@
+// Backward of the blockwise-fp8 grouped GEMM on gfx950 (no reference counterpart: the bf16 forms
+// are dlhs and tgmm of bzantium/mintext mintext/kernels/grouped_matmul.py:151-187 and :197-235;
+// the fp8 conventions are those of the forward, DeepSeek-V3 style blockwise e4m3fn with f32
+// scale = amax / 448).
+//
+// dlhs  dX = dY @ W^T: dY is quantised in 1x128 groups along its row (the reduction), and W in
+//       128x128 blocks exactly as for the forward but with its codes kept in W's own layout
+//       [E, Kin, Kout] (k-contiguous for this product) and the block-scale grid transposed; the
+//       product is then the forward fp8 grouped GEMM (mtx_gmm_fp8) on these operands.
+// tgmm  dW[e] = X_e^T @ G_e reduces over the rows of expert e.  Both operands are quantised in
+//       groups of 128 consecutive rows of the expert (expert-aligned chunks: chunk c of expert e
+//       covers its rows 128c .. 128c+127, the last chunk zero-padded), transposed so that the
+//       reduction is contiguous: XT [F, 128*C] with one scale per feature and chunk (1x128 along
+//       the transposed row), GT [N, 128*C] with one scale per 128 features and chunk (128x128
+//       blocks).  The GEMM is the forward kernel's tile loop with a per-expert k-range.
+#include "common.h"
+#include "lds_dma.h"
+
+namespace mtx {
+namespace f8b {
+
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(8))) int i32x8;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+
+__device__ __forceinline__ float ld_elem(const float* p, int64_t i) { return p[i]; }
+__device__ __forceinline__ float ld_elem(const uint16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
+
+// ---- weights in their own layout ---------------------------------------------------------------
+// The 128x128 block (Kin block y, Kout block x) of expert z: the scale of quant_weights_kernel
+// (amax / 448 of the same block) and the same codes, written in W's layout [E, Kin, Kout] with the
+// scale at [E, Kin/128, Kout/128].
+template <typename T>
+__global__ __launch_bounds__(256) void quant_weights_t_kernel(const T* __restrict__ w, int64_t Kin, int64_t Kout,
+                                                              uint8_t* __restrict__ wq, float* __restrict__ ws) {
+  __shared__ float wmax[4];
+  const int64_t e = blockIdx.z, k0 = (int64_t)blockIdx.y * 128, n0 = (int64_t)blockIdx.x * 128;
+  const T* src = w + e * Kin * Kout;
+  float m = 0.0f;
+  for (int i = threadIdx.x; i < 128 * 128; i += 256) m = fmaxf(m, fabsf(ld_elem(src, (k0 + i / 128) * Kout + n0 + i % 128)));
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  float s = m / 448.0f;
+  if (s == 0.0f) s = 1.0f;
+  uint8_t* dst = wq + e * Kin * Kout;
+  for (int i = threadIdx.x; i < 128 * 128; i += 256) {
+    const int64_t o = (k0 + i / 128) * Kout + n0 + i % 128;
+    dst[o] = f32_to_e4m3(ld_elem(src, o) / s);
+  }
+  if (threadIdx.x == 0) ws[(e * (Kin / 128) + blockIdx.y) * (Kout / 128) + blockIdx.x] = s;
+}
+
+// ---- expert chunks -----------------------------------------------------------------------------
+// One workgroup, E <= 1024: row offsets off[E+1] of the groups (clamped to M like the forward's
+// tile builder), chunk bases cb[E+1] (cb[e] = sum of ceil(rows/128) over the experts before e)
+// and the experts in descending size order (ties: lower id first), so the longest reductions
+// start first.
+__global__ __launch_bounds__(1024) void chunk_prologue_kernel(const int32_t* __restrict__ gs, int E, int M,
+                                                              int* __restrict__ cb, int* __restrict__ off,
+                                                              int* __restrict__ order) {
+  __shared__ long long wsum64[16];
+  __shared__ int wsum[16];
+  __shared__ int s_rows[1024];
+  const int e = threadIdx.x, lane = e & 63, w = e >> 6;
+  const int g = (e < E) ? min(max(gs[e], 0), M) : 0;
+  long long incl64 = g;
+  for (int o = 1; o < 64; o <<= 1) {
+    const long long v = __shfl_up(incl64, o);
+    if (lane >= o) incl64 += v;
+  }
+  if (lane == 63) wsum64[w] = incl64;
+  __syncthreads();
+  if (e == 0) {
+    long long run = 0;
+    for (int i = 0; i < 16; ++i) { const long long v = wsum64[i]; wsum64[i] = run; run += v; }
+  }
+  __syncthreads();
+  const long long start = incl64 - g + wsum64[w];
+  const int r0 = (int)min(start, (long long)M), r1 = (int)min(start + g, (long long)M);
+  const int rows = r1 - r0, nch = (rows + 127) / 128;
+  s_rows[e] = (e < E) ? rows : -1;
+  int incl = nch;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o);
+    if (lane >= o) incl += v;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  if (e == 0) {
+    int run = 0;
+    for (int i = 0; i < 16; ++i) { const int v = wsum[i]; wsum[i] = run; run += v; }
+  }
+  __syncthreads();
+  if (e < E) {
+    cb[e] = incl - nch + wsum[w];
+    off[e] = r0;
+    if (e == E - 1) {
+      cb[E] = incl + wsum[w];
+      off[E] = r1;
+    }
+    int rank = 0;
+    for (int h = 0; h < E; ++h) rank += (s_rows[h] > rows || (s_rows[h] == rows && h < e)) ? 1 : 0;
+    order[rank] = e;
+  }
+}
+
+// expert owning chunk c: the last e with cb[e] <= c (experts without chunks share their
+// successor's base)
+__device__ __forceinline__ int chunk_expert(const int* __restrict__ cb, int E, int c) {
+  int lo = 0, hi = E - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (cb[mid] <= c) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// ---- grouped transposing quantiser -------------------------------------------------------------
+// Workgroup (chunk c, 128-feature block fb): rows off[e] + 128(c - cb[e]) .. +127 of expert e
+// (rows past the expert are zero) x features fb*128 .. +127 of x [M, F] -> xt[f][128c + r]
+// (xt row stride ldt bytes).  ROW: scale per feature = amax over the chunk's rows / 448 at
+// xts[f * C + c]; BLOCK: one scale per 128x128 block at xts[fb * C + c].  Codes are
+// f32_to_e4m3(v / scale), scale 1 when the amax is 0.
+template <typename T, bool BLOCK>
+__global__ __launch_bounds__(256) void quant_grouped_t_kernel(const T* __restrict__ x, int F, const int* __restrict__ cb,
+                                                              const int* __restrict__ off, int E, int C, int64_t ldt,
+                                                              uint8_t* __restrict__ xt, float* __restrict__ xts) {
+  __shared__ float tile[128][129];
+  __shared__ float smax[2][128];
+  const int c = blockIdx.x, fb = blockIdx.y, tid = threadIdx.x;
+  if (c >= cb[E]) return;  // beyond the chunks of this call's groups
+  const int e = chunk_expert(cb, E, c);
+  const int rs = off[e] + 128 * (c - cb[e]);
+  const int nr = min(128, off[e + 1] - rs);
+  const int64_t f0 = (int64_t)fb * 128;
+  for (int i = tid; i < 128 * 128; i += 256) {
+    const int r = i / 128, f = i % 128;
+    tile[r][f] = (r < nr) ? ld_elem(x, (int64_t)(rs + r) * F + f0 + f) : 0.0f;
+  }
+  __syncthreads();
+  {
+    const int f = tid & 127, h = tid >> 7;
+    float m = 0.0f;
+    for (int r = h * 64; r < h * 64 + 64; ++r) m = fmaxf(m, fabsf(tile[r][f]));
+    smax[h][f] = m;
+  }
+  __syncthreads();
+  if (BLOCK) {
+    if (tid < 64) {
+      float m = fmaxf(fmaxf(smax[0][tid], smax[1][tid]), fmaxf(smax[0][tid + 64], smax[1][tid + 64]));
+      for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+      if (tid == 0) smax[0][0] = m;  // every lane has read its entries before this write
+    }
+    __syncthreads();
+  }
+  // 128 features x 8 runs of 16 rows: each item is one 16-byte store of codes
+  for (int it = tid; it < 128 * 8; it += 256) {
+    const int f = it >> 3, r0 = (it & 7) * 16;
+    float s = BLOCK ? smax[0][0] : fmaxf(smax[0][f], smax[1][f]);
+    s = s / 448.0f;
+    if (s == 0.0f) s = 1.0f;
+    uint32_t q[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      q[k] = (uint32_t)f32_to_e4m3(tile[r0 + 4 * k][f] / s) | ((uint32_t)f32_to_e4m3(tile[r0 + 4 * k + 1][f] / s) << 8) |
+             ((uint32_t)f32_to_e4m3(tile[r0 + 4 * k + 2][f] / s) << 16) |
+             ((uint32_t)f32_to_e4m3(tile[r0 + 4 * k + 3][f] / s) << 24);
+    *(u32x4*)(xt + (f0 + f) * ldt + (int64_t)c * 128 + r0) = u32x4{q[0], q[1], q[2], q[3]};
+    if (r0 == 0 && (!BLOCK || f == 0)) xts[(BLOCK ? (int64_t)fb : f0 + f) * C + c] = s;
+  }
+}
+
+// ---- tgmm: dW[e] = XT_e GT_e^T over the expert's chunks ---------------------------------------------
+// 256x256 output tiles of dW[e] [F, N], 8 waves (2 x 4, 128x64 wave tiles of 32x32 blocks), 64-k
+// stages of 256 XT rows and 256 GT rows (32 KB) loaded with global_load_lds_dwordx4 into a 4-deep
+// LDS ring three stages ahead; one v_mfma_scale_f32_32x32x64_f8f6f4 (unit scales) per block and
+// stage, operands swapped so that each lane owns four consecutive output columns.  Per 128-k
+// chunk the accumulators are kept in units of the chunk's scale product and moved to the next
+// chunk's units by (sa_c / sa_n) * (sb_c / sb_n) (no product of two small scales is formed), the
+// last chunk's scales applied at the end.  An expert without rows gives a zero tile.
+constexpr int TBM = 256, TBN = 256, TBK = 64, TNST = 4, TPD = 3;
+constexpr int TA_BYTES = TBM * TBK, TSTAGE = 2 * TA_BYTES;
+__device__ __forceinline__ int t_off(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
+
+struct TArgs {
+  const uint8_t* xt;  // [F, ldt]
+  const float* xts;   // [F, C]
+  const uint8_t* gt;  // [N, ldt]
+  const float* gts;   // [N/128, C]
+  uint16_t* dw;       // [E, F, N] bf16
+  const int* cb;      // [E+1]
+  const int* order;   // [E]
+  int E, F, N, C;
+  int64_t ldt;
+};
+
+__global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
+  constexpr int WN = 4, WTM = 128, WTN = 64, TM = 4, TN = 2, LPS = 4;
+  __shared__ __attribute__((aligned(1024))) char lds[TNST * TSTAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int nf = p.F / TBM, nn = p.N / TBN, per_e = nf * nn;
+  const int total = p.E * per_e;
+  const int pid = blockIdx.x;
+  const int total8 = (total + 7) & ~7;
+  if (pid >= total8) return;
+  const int lid = (pid & 7) * (total8 >> 3) + (pid >> 3);  // each XCD sweeps a contiguous range
+  if (lid >= total) return;
+  const int e = p.order[lid / per_e];
+  const int rem = lid % per_e;
+  const int fb = rem / nn, nb = rem % nn;
+  const int c0 = p.cb[e], nch = p.cb[e + 1] - c0;
+  uint16_t* out = p.dw + (int64_t)e * p.F * p.N + (int64_t)fb * TBM * p.N + nb * TBN;
+  if (nch <= 0) {  // empty group: dW[e] tile = 0
+    for (int i = tid; i < TBM * TBN / 8; i += 512) {
+      const int r = i / (TBN / 8), cc = (i % (TBN / 8)) * 8;
+      *(u32x4*)(out + (int64_t)r * p.N + cc) = u32x4{0u, 0u, 0u, 0u};
+    }
+    return;
+  }
+  const int nk = 2 * nch;  // 64-byte stages
+  const uint32_t kbase = (uint32_t)c0 * 128u;
+
+  // per-lane sources: lane l of segment s fills tile row 16s + l/4, chunk slot l%4
+  uint32_t aoff[2], boff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int seg = wave * 2 + i;
+    const int r = seg * 16 + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
+    aoff[i] = (uint32_t)(fb * TBM + r) * (uint32_t)p.ldt + kbase + (uint32_t)(c * 16);
+    boff[i] = (uint32_t)(nb * TBN + r) * (uint32_t)p.ldt + kbase + (uint32_t)(c * 16);
+  }
+  const uint32_t lds_base = lds_addr(lds);
+  const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+  // stages past the end re-read the last one (in bounds) into a slot that is no longer read
+  auto issue_stage = [&](int kt) {
+    const uint32_t st = lds_base + (uint32_t)((kt & (TNST - 1)) * TSTAGE);
+    const uint32_t kofs = (uint32_t)min(kt, nk - 1) * TBK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) gload_lds16(p.xt + aoff[i] + kofs, st + (wave_u * 2 + i) * 1024u);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) gload_lds16(p.gt + boff[i] + kofs, st + (uint32_t)TA_BYTES + (wave_u * 2 + i) * 1024u);
+  };
+  i32x8 fa[2][TM], fbr[2][TN];
+  const int frow = lane & 31, fhalf = lane >> 5;
+  auto ld32 = [&](const char* base, int r) -> i32x8 {
+    const u32x4 lo = *(const u32x4*)(base + t_off(r, 2 * fhalf));
+    const u32x4 hi = *(const u32x4*)(base + t_off(r, 2 * fhalf + 1));
+    return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  };
+  auto read_frags = [&](int kt, int buf) {
+    const char* st = lds + (kt & (TNST - 1)) * TSTAGE;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[buf][i] = ld32(st, wm * WTM + i * 32 + frow);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fbr[buf][j] = ld32(st + TA_BYTES, wn * WTN + j * 32 + frow);
+  };
+  // scales of chunk c0 + kb: this lane's four XT rows, and the GT block of this wave's columns
+  const float* sa_src = p.xts + (int64_t)(fb * TBM + wm * WTM + frow) * p.C + c0;
+  const float* sb_src = p.gts + (int64_t)(nb * 2 + (wn >> 1)) * p.C + c0;
+  float sa_c[TM], sa_n[TM], sb_c, sb_n;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) sa_c[i] = sa_src[(int64_t)i * 32 * p.C];
+  sb_c = sb_src[0];
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+#pragma unroll
+  for (int s = 0; s < TPD; ++s) issue_stage(s);  // nk >= 2: stages past the end re-read the last
+  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (TPD - 2)));
+  __syncthreads();  // stages 0 and 1 visible
+  read_frags(0, 0);
+  auto mfmas = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fbr[buf][j], fa[buf][i], acc[i][j], 0, 0, 0, 127, 0,
+                                                                    127);
+  };
+  auto finish_stage = [&]() {
+    // stage kt+2 landed before the barrier makes it visible (kt+3 may still be in flight)
+    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (TPD - 2)));
+    __syncthreads();
+  };
+  for (int kb = 0; kb < nch; ++kb) {
+    const int kt = 2 * kb;
+    const bool more = kb + 1 < nch;
+    if (more) {  // next chunk's scales, in flight during this chunk's MFMAs
+#pragma unroll
+      for (int i = 0; i < TM; ++i) sa_n[i] = sa_src[(int64_t)i * 32 * p.C + kb + 1];
+      sb_n = sb_src[kb + 1];
+    }
+    issue_stage(kt + TPD);
+    read_frags(kt + 1, 1);
+    mfmas(0);
+    finish_stage();
+    issue_stage(kt + 1 + TPD);
+    read_frags(kt + 2, 0);  // the last step reads an unused ring slot (in bounds)
+    mfmas(1);
+    if (more) {
+      const float rb = sb_c * __builtin_amdgcn_rcpf(sb_n);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const float f = (sa_c[i] * __builtin_amdgcn_rcpf(sa_n[i])) * rb;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[i][j][v] *= f;
+        sa_c[i] = sa_n[i];
+      }
+      sb_c = sb_n;
+    }
+    finish_stage();
+  }
+  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));  // no ring load lands after the workgroup ends
+
+  // epilogue: acc[i][j][4g+q] of lane l is dW[row i*32 + l%32][col j*32 + 8g + 4(l/32) + q]
+  const int ecol = wn * WTN + 4 * fhalf;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int row = wm * WTM + i * 32 + frow;
+    uint16_t* orow = out + (int64_t)row * p.N + ecol;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *(bf16x4*)(orow + j * 32 + 8 * g) =
+            bf16x4{(__bf16)((acc[i][j][4 * g] * sa_c[i]) * sb_c), (__bf16)((acc[i][j][4 * g + 1] * sa_c[i]) * sb_c),
+                   (__bf16)((acc[i][j][4 * g + 2] * sa_c[i]) * sb_c), (__bf16)((acc[i][j][4 * g + 3] * sa_c[i]) * sb_c)};
+  }
+}
+
+}  // namespace f8b
+
+static inline int64_t fp8_grouped_chunks(int64_t M, int64_t E) { return ceil_div(M, 128) + E; }
+
+}  // namespace mtx
+
+using namespace mtx;
+
+extern "C" int mtx_quant_fp8_weights_t(const void* w, int dtype, int64_t E, int64_t Kin, int64_t Kout, uint8_t* w_qt,
+                                       float* w_scale_t, void* stream) {
+  if (E < 0 || Kin < 0 || Kout < 0 || Kin % 128 || Kout % 128 || (dtype != MTX_F32 && dtype != MTX_BF16))
+    return MTX_ERR_ARG;
+  if (E == 0 || Kin == 0 || Kout == 0) return MTX_OK;
+  if (!w || !w_qt || !w_scale_t) return MTX_ERR_ARG;
+  if (E > 65535 || Kin / 128 > 65535) return MTX_ERR_UNSUPPORTED;
+  dim3 grid((unsigned)(Kout / 128), (unsigned)(Kin / 128), (unsigned)E);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == MTX_F32)
+    hipLaunchKernelGGL(f8b::quant_weights_t_kernel<float>, grid, dim3(256), 0, st, (const float*)w, Kin, Kout, w_qt,
+                       w_scale_t);
+  else
+    hipLaunchKernelGGL(f8b::quant_weights_t_kernel<uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)w, Kin, Kout,
+                       w_qt, w_scale_t);
+  return check_launch();
+}
+
+extern "C" int64_t mtx_fp8_grouped_chunks(int64_t M, int64_t E) {
+  if (M < 0 || E < 1) return -1;
+  return fp8_grouped_chunks(M, E);
+}
+
+extern "C" int64_t mtx_fp8_grouped_workspace_size(int64_t E) {
+  if (E < 1) return -1;
+  return round_up((3 * E + 2) * 4, 256);
+}
+
+// workspace: cb [E+1], off [E+1], order [E] (ints)
+static int grouped_prologue(const int32_t* gs, int64_t E, int64_t M, void* ws, hipStream_t st, int** cb, int** off,
+                            int** order) {
+  int* b = (int*)ws;
+  *cb = b;
+  *off = b + E + 1;
+  *order = b + 2 * E + 2;
+  hipLaunchKernelGGL(f8b::chunk_prologue_kernel, dim3(1), dim3(1024), 0, st, gs, (int)E, (int)M, *cb, *off, *order);
+  return check_launch();
+}
+
+extern "C" int mtx_quant_fp8_grouped_t(const void* x, int dtype, const int32_t* group_sizes, int64_t M, int64_t F,
+                                       int64_t E, int blocks, uint8_t* xt, float* xt_scale, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
+  if (M < 0 || M > INT32_MAX / 2 || F <= 0 || F % 128 || E < 1 || E > 1024) return MTX_ERR_ARG;
+  if (dtype != MTX_F32 && dtype != MTX_BF16) return MTX_ERR_ARG;
+  if (!workspace || workspace_bytes < mtx_fp8_grouped_workspace_size(E)) return MTX_ERR_WORKSPACE;
+  if (!group_sizes || !xt || !xt_scale || (M > 0 && !x)) return MTX_ERR_ARG;
+  if ((uintptr_t)xt % 16) return MTX_ERR_ARG;
+  const int64_t C = fp8_grouped_chunks(M, E);
+  if (C > 2147483647 / 128 || F / 128 > 65535) return MTX_ERR_UNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  int *cb, *off, *order;
+  int rc = grouped_prologue(group_sizes, E, M, workspace, st, &cb, &off, &order);
+  if (rc) return rc;
+  dim3 grid((unsigned)C, (unsigned)(F / 128));
+  const int64_t ldt = C * 128;
+#define MTX_QG(T, B)                                                                                              \
+  hipLaunchKernelGGL((f8b::quant_grouped_t_kernel<T, B>), grid, dim3(256), 0, st, (const T*)x, (int)F, cb, off, \
+                     (int)E, (int)C, ldt, xt, xt_scale)
+  if (dtype == MTX_F32) {
+    if (blocks) MTX_QG(float, true); else MTX_QG(float, false);
+  } else {
+    if (blocks) MTX_QG(uint16_t, true); else MTX_QG(uint16_t, false);
+  }
+#undef MTX_QG
+  return check_launch();
+}
+
+extern "C" int mtx_tgmm_fp8(const uint8_t* xt, const float* xt_scale, const uint8_t* gt, const float* gt_scale,
+                            const int32_t* group_sizes, int64_t M, int64_t F, int64_t N, int64_t E, void* dw,
+                            void* workspace, int64_t workspace_bytes, void* stream) {
+  if (M < 0 || M > INT32_MAX / 2 || F <= 0 || N <= 0 || E < 1 || E > 1024) return MTX_ERR_ARG;
+  if (F % 128 || N % 128) return MTX_ERR_ARG;
+  if (F % 256 || N % 256) return MTX_ERR_UNSUPPORTED;
+  if (!workspace || workspace_bytes < mtx_fp8_grouped_workspace_size(E)) return MTX_ERR_WORKSPACE;
+  if (!xt || !xt_scale || !gt || !gt_scale || !group_sizes || !dw) return MTX_ERR_ARG;
+  if (((uintptr_t)xt | (uintptr_t)gt) % 16) return MTX_ERR_ARG;
+  const int64_t C = fp8_grouped_chunks(M, E), ldt = C * 128;
+  if ((F > N ? F : N) * ldt >= (int64_t(1) << 32)) return MTX_ERR_UNSUPPORTED;  // 32-bit byte offsets
+  hipStream_t st = (hipStream_t)stream;
+  int *cb, *off, *order;
+  int rc = grouped_prologue(group_sizes, E, M, workspace, st, &cb, &off, &order);
+  if (rc) return rc;
+  f8b::TArgs a;
+  a.xt = xt;
+  a.xts = xt_scale;
+  a.gt = gt;
+  a.gts = gt_scale;
+  a.dw = (uint16_t*)dw;
+  a.cb = cb;
+  a.order = order;
+  a.E = (int)E;
+  a.F = (int)F;
+  a.N = (int)N;
+  a.C = (int)C;
+  a.ldt = ldt;
+  const int64_t grid = round_up(E * (F / 256) * (N / 256), 8);
+  hipLaunchKernelGGL(f8b::tgmm_fp8_kernel, dim3((unsigned)grid), dim3(512), 0, st, a);
+  return check_launch();
+}
+
+extern "C" int mtx_gmm_fp8_dlhs(const uint8_t* gq, const float* g_scale, const uint8_t* w_qt, const float* w_scale_t,
+                                const int32_t* group_sizes, int64_t M, int64_t Kin, int64_t Kout, int64_t E, void* dx,
+                                void* workspace, int64_t workspace_bytes, void* stream) {
+  // dX [M, Kin] = dY [M, Kout] @ W[e]^T: the forward product with the weight codes in W's own
+  // layout [E, Kin, Kout] (rows = output columns, k-contiguous over the reduction Kout)
+  return mtx_gmm_fp8(gq, g_scale, w_qt, w_scale_t, group_sizes, M, Kout, Kin, E, dx, workspace, workspace_bytes,
+                     stream);
+}

@@ -107,3 +107,72 @@ def grouped_matmul_fp8_swiglu_gathered(xq, x_scale, sort_indices, top_k: int, w_
     if return_bf16:
         return yq, ys, yb
     return yq, ys
+
+
+# ---- backward: dlhs and tgmm with fp8 operands ----------------------------------------------------
+# The bf16 forms are grouped_matmul.py:151-187 (dlhs) and :197-235 (tgmm); the fp8 ones keep the
+# forward's conventions (e4m3fn codes, f32 scale = amax / 448 per group).
+
+def quantize_fp8_weights_t(w: torch.Tensor):
+    """w [E, Kin, Kout] -> (w_qt [E, Kin, Kout] e4m3fn, w_scale_t [E, Kin/128, Kout/128]): the 128x128
+    blocks and codes of ``quantize_fp8_weights`` kept in w's own layout, the operand of
+    ``grouped_matmul_fp8_dlhs`` (a load-time transform beside the forward one)."""
+    dev = L.require_device(w)
+    w = w.contiguous()
+    E, Kin, Kout = w.shape
+    wq = torch.empty((E, Kin, Kout), dtype=torch.float8_e4m3fn, device=dev)
+    ws = torch.empty((E, Kin // 128, Kout // 128), dtype=torch.float32, device=dev)
+    L.call("mtx_quant_fp8_weights_t", L.ptr(w), L.dtype_code(w.dtype), E, Kin, Kout, L.ptr(wq), L.ptr(ws),
+           L.stream(dev))
+    return wq, ws
+
+
+def grouped_matmul_fp8_dlhs(gq, g_scale, w_qt, w_scale_t, group_sizes) -> torch.Tensor:
+    """dX [M, Kin] bf16 = dequant(gq) @ dequant(W[g])^T per group, f32 accumulation: the fp8 dlhs
+    (``mtx_gmm_fp8_dlhs``).  gq [M, Kout] / g_scale [M, Kout/128] from ``quantize_fp8_rows`` of the
+    upstream gradient; w_qt / w_scale_t from ``quantize_fp8_weights_t``."""
+    gs = _gs(group_sizes)
+    dev = L.require_device(gq, g_scale, w_qt, w_scale_t, gs)
+    M, Kout = gq.shape
+    E, Kin, Kout2 = w_qt.shape
+    if Kout2 != Kout:
+        raise ValueError("fp8 dlhs shape mismatch")
+    dx = torch.empty((M, Kin), dtype=torch.bfloat16, device=dev)
+    ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
+    L.call("mtx_gmm_fp8_dlhs", L.ptr(gq.contiguous()), L.ptr(g_scale.contiguous()), L.ptr(w_qt.contiguous()),
+           L.ptr(w_scale_t.contiguous()), L.ptr(gs), M, Kin, Kout, E, L.ptr(dx), L.ptr(ws), ws.numel(), L.stream(dev))
+    return dx
+
+
+def quantize_fp8_grouped_t(x: torch.Tensor, group_sizes: torch.Tensor, *, blocks: bool = False):
+    """Operand of ``tgmm_fp8``: x [M, F] (f32/bf16, rows grouped by expert) quantised in chunks of
+    128 consecutive rows of each expert and transposed: codes [F, 128*C] (C = ceil(M/128) + E chunk
+    slots; chunk c of expert e holds its rows 128c' .. 128c'+127, zero-padded) and scales [F, C] --
+    one per feature and chunk -- or, with ``blocks``, [F/128, C] -- one per 128x128 block."""
+    gs = _gs(group_sizes)
+    dev = L.require_device(x, gs)
+    x = x.contiguous()
+    M, F = x.shape
+    E = gs.numel()
+    C = L.query("mtx_fp8_grouped_chunks", M, E)
+    xt = torch.empty((F, 128 * C), dtype=torch.float8_e4m3fn, device=dev)
+    xs = torch.empty((F // 128, C) if blocks else (F, C), dtype=torch.float32, device=dev)
+    ws = L.workspace(L.query("mtx_fp8_grouped_workspace_size", E), dev)
+    L.call("mtx_quant_fp8_grouped_t", L.ptr(x), L.dtype_code(x.dtype), L.ptr(gs), M, F, E, int(bool(blocks)),
+           L.ptr(xt), L.ptr(xs), L.ptr(ws), ws.numel(), L.stream(dev))
+    return xt, xs
+
+
+def tgmm_fp8(xt, xt_scale, gt, gt_scale, group_sizes, M: int) -> torch.Tensor:
+    """dW [E, F, N] bf16 = per group dequant(x)^T @ dequant(g) with f32 accumulation (``mtx_tgmm_fp8``):
+    x from ``quantize_fp8_grouped_t(x, gs)`` (per-feature chunk scales), g from
+    ``quantize_fp8_grouped_t(g, gs, blocks=True)``; M = rows of x and g.  Empty groups give zeros.
+    F and N must be multiples of 256."""
+    gs = _gs(group_sizes)
+    dev = L.require_device(xt, xt_scale, gt, gt_scale, gs)
+    F, N, E = xt.shape[0], gt.shape[0], gs.numel()
+    dw = torch.empty((E, F, N), dtype=torch.bfloat16, device=dev)
+    ws = L.workspace(L.query("mtx_fp8_grouped_workspace_size", E), dev)
+    L.call("mtx_tgmm_fp8", L.ptr(xt.contiguous()), L.ptr(xt_scale.contiguous()), L.ptr(gt.contiguous()),
+           L.ptr(gt_scale.contiguous()), L.ptr(gs), M, F, N, E, L.ptr(dw), L.ptr(ws), ws.numel(), L.stream(dev))
+    return dw

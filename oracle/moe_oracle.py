@@ -425,6 +425,85 @@ def gmm_fp8(xq, xs, wq, ws, group_sizes) -> np.ndarray:
     return gmm(dequant_rows(xq, xs), dequant_weights(wq, ws), group_sizes)
 
 
+def quant_fp8_weights_t(w, block: int = 128):
+    """The 128 x 128 blocks of ``quant_fp8_weights`` with the codes kept in w's own layout:
+    (wq [E,Kin,Kout], ws [E,Kin/128,Kout/128]) -- the weight operand of the fp8 dlhs, whose
+    reduction is Kout (grouped_matmul.py:162-176 with swapaxes(W,1,2) in fp8)."""
+    q, sc = quant_fp8_weights(w, block)
+    return np.ascontiguousarray(np.swapaxes(q, 1, 2)), np.ascontiguousarray(np.swapaxes(sc, 1, 2))
+
+
+def gmm_fp8_dlhs(gq, gs_, wq_t, ws_t, group_sizes) -> np.ndarray:
+    """fp8 dlhs dX = dY @ W^T per group: dequantise dY (1x128 rows) and W (codes in W's layout),
+    then float64 (grouped_matmul.py:162-176)."""
+    g = dequant_rows(gq, gs_)
+    # wq_t [E,Kin,Kout] with scales [E,Kin/128,Kout/128] is the forward format of W^T
+    w_t = dequant_weights(wq_t, ws_t)  # [E, Kout, Kin]  (= (W^T)^T in the reference layout)
+    return gmm(g, w_t, group_sizes)
+
+
+def fp8_group_chunks(group_sizes, M: int, block: int = 128):
+    """Expert-aligned 128-row chunks: (row offsets [E+1] clamped to M, chunk bases [E+1])."""
+    off = group_offsets(group_sizes, M)
+    nch = (np.diff(off) + block - 1) // block
+    cb = np.concatenate([[0], np.cumsum(nch)]).astype(np.int64)
+    return off, cb
+
+
+def quant_fp8_grouped_t(x, group_sizes, blocks: bool, C: int | None = None, block: int = 128):
+    """The tgmm operands: x [M,F] -> codes xt [F, 128*C] (row f = feature f, column 128c + r = row r
+    of the expert's chunk c, zero past the expert) and scales: one per feature and chunk [F, C]
+    (``blocks`` False, 1 x 128 along xt's row) or one per 128 features and chunk [F/128, C]
+    (``blocks`` True, 128 x 128), scale = amax/448 (1 if 0), q = RNE(x / scale).  C defaults to
+    ceil(M/128) + E (the allocation of the kernels); chunks past the groups are left 0."""
+    x = np.asarray(x, dtype=np.float32)
+    M, F = x.shape
+    E = len(group_sizes)
+    off, cb = fp8_group_chunks(group_sizes, M, block)
+    C = int(-(-M // block) + E) if C is None else C
+    xt = np.zeros((F, C * block), np.uint8)
+    xs = np.zeros((F // block, C) if blocks else (F, C), np.float32)
+    for e in range(E):
+        for j, c in enumerate(range(int(cb[e]), int(cb[e + 1]))):
+            r0 = int(off[e]) + block * j
+            rows = x[r0:min(r0 + block, int(off[e + 1]))]
+            chunk = np.zeros((block, F), np.float32)
+            chunk[: rows.shape[0]] = rows
+            t = chunk.T  # [F, 128]
+            if blocks:
+                amax = np.abs(t.reshape(F // block, block * block)).max(-1)
+            else:
+                amax = np.abs(t).max(-1)
+            sc = (amax / np.float32(E4M3_MAX)).astype(np.float32)
+            sc = np.where(sc == 0, np.float32(1.0), sc).astype(np.float32)
+            sfull = np.repeat(sc, block) if blocks else sc
+            xt[:, c * block:(c + 1) * block] = e4m3_encode((t / sfull[:, None]).astype(np.float32))
+            xs[:, c] = sc
+    return xt, xs
+
+
+def dequant_grouped_t(xt, xs, group_sizes, M: int, blocks: bool, block: int = 128):
+    """Inverse of ``quant_fp8_grouped_t``: the [M, F] float64 rows (zero-padding dropped)."""
+    F = xt.shape[0]
+    off, cb = fp8_group_chunks(group_sizes, M, block)
+    q = e4m3_decode(xt).astype(np.float64)
+    out = np.zeros((M, F))
+    for e in range(len(group_sizes)):
+        for j, c in enumerate(range(int(cb[e]), int(cb[e + 1]))):
+            r0 = int(off[e]) + block * j
+            n = min(block, int(off[e + 1]) - r0)
+            sc = np.repeat(np.asarray(xs[:, c], np.float64), block) if blocks else np.asarray(xs[:, c], np.float64)
+            out[r0:r0 + n] = (q[:, c * block:c * block + n] * sc[:, None]).T
+    return out
+
+
+def tgmm_fp8(xt, xts, gt, gts, group_sizes, M: int) -> np.ndarray:
+    """fp8 tgmm: dequantise both transposed operands (x with per-feature chunk scales, g with
+    128 x 128 block scales), then the float64 per-group x^T g (grouped_matmul.py:197-235)."""
+    return tgmm(dequant_grouped_t(xt, xts, group_sizes, M, False), dequant_grouped_t(gt, gts, group_sizes, M, True),
+                group_sizes)
+
+
 # ---------------------------------------------------------------------------------------------
 # composition  (MoEExperts._forward_kernel, mintext/modules/moe.py:161-221)
 # ---------------------------------------------------------------------------------------------

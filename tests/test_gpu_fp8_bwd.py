@@ -1,0 +1,151 @@
+"""GPU parity of the blockwise-fp8 backward (dlhs and tgmm with e4m3 operands; the bf16 forms are
+grouped_matmul.py:151-187 and :197-235): quantisers bit-exact against the oracle, the GEMMs within
+1e-2 of the dequantised float64 oracle and 6e-2 of the unquantised product, empty and skewed groups,
+the C5 backward shapes at full size."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_err
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _u8(t):
+    return t.view(torch.uint8).cpu().numpy()
+
+
+def _zipf_groups(rng, M, E, empty=(1,)):
+    p = 1.0 / np.arange(1, E + 1) ** 1.2
+    gs = rng.multinomial(M, p[rng.permutation(E)] / p.sum()).astype(np.int32)
+    for e in empty:
+        gs[(e + 1) % E] += gs[e]
+        gs[e] = 0
+    return gs
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_quant_weights_t_bit_exact(dev, dt):
+    from mintext_amd.kernels.fp8 import quantize_fp8_weights, quantize_fp8_weights_t
+
+    w = (torch.randn(3, 256, 384, device=dev) * 0.02).to(dt)
+    w[1, :128, :128] = 0  # an all-zero block -> scale 1
+    q, s = quantize_fp8_weights_t(w)
+    oq, os_ = O.quant_fp8_weights_t(w.float().cpu().numpy())
+    assert np.array_equal(_u8(q), oq) and np.array_equal(s.cpu().numpy(), os_)
+    # the same blocks as the forward's prepack
+    qf, sf = quantize_fp8_weights(w)
+    assert torch.equal(q.view(torch.uint8), qf.view(torch.uint8).transpose(1, 2)) and torch.equal(s, sf.transpose(1, 2))
+
+
+@pytest.mark.parametrize("blocks", [False, True])
+@pytest.mark.parametrize("M,F,E", [(1000, 256, 6), (4095, 512, 16), (129, 128, 3), (5000, 768, 64)])
+def test_quant_grouped_t_bit_exact(dev, blocks, M, F, E):
+    from mintext_amd.kernels.fp8 import quantize_fp8_grouped_t
+
+    rng = np.random.default_rng(M + F)
+    gs = _zipf_groups(rng, M - 7, E)  # 7 rows past sum(group_sizes): not quantised
+    x = (torch.randn(M, F, device=dev) * torch.rand(1, F, device=dev) * 5).bfloat16()
+    xt, xs = quantize_fp8_grouped_t(x, _t(gs, dev), blocks=blocks)
+    oq, os_ = O.quant_fp8_grouped_t(x.float().cpu().numpy(), gs, blocks)
+    _, cb = O.fp8_group_chunks(gs, M)
+    used = 128 * int(cb[-1])
+    assert np.array_equal(_u8(xt)[:, :used], oq[:, :used])
+    assert np.array_equal(xs.cpu().numpy()[:, :int(cb[-1])], os_[:, :int(cb[-1])])
+
+
+@pytest.mark.parametrize("M,Kin,Kout,E", [(2000, 256, 384, 6), (3000, 768, 2048, 16), (700, 2048, 1536, 4)])
+def test_gmm_fp8_dlhs(dev, M, Kin, Kout, E):
+    from mintext_amd.kernels.fp8 import grouped_matmul_fp8_dlhs, quantize_fp8_rows, quantize_fp8_weights_t
+
+    rng = np.random.default_rng(M)
+    gs = _zipf_groups(rng, M, E)
+    g = torch.randn(M, Kout, device=dev).bfloat16()
+    w = (torch.randn(E, Kin, Kout, device=dev) * 0.02).bfloat16()
+    gq, gsc = quantize_fp8_rows(g)
+    wq, ws = quantize_fp8_weights_t(w)
+    dx = grouped_matmul_fp8_dlhs(gq, gsc, wq, ws, _t(gs, dev))
+    assert dx.dtype == torch.bfloat16 and dx.shape == (M, Kin)
+    got = dx.float().cpu().numpy()
+    ref_q = O.gmm_fp8_dlhs(_u8(gq), gsc.cpu().numpy(), _u8(wq), ws.cpu().numpy(), gs)
+    assert rel_err(got, ref_q) < 1e-2
+    ref = O.gmm_dlhs(g.float().cpu().numpy(), w.float().cpu().numpy(), gs)
+    assert rel_err(got, ref) < 6e-2
+
+
+@pytest.mark.parametrize("M,F,N,E", [(2000, 256, 256, 6), (5000, 768, 2048, 16), (3000, 2048, 1536, 8),
+                                     (300, 256, 512, 40)])
+def test_tgmm_fp8(dev, M, F, N, E):
+    from mintext_amd.kernels.fp8 import quantize_fp8_grouped_t, tgmm_fp8
+
+    rng = np.random.default_rng(M + E)
+    gs = _zipf_groups(rng, M, E, empty=(0, E // 2))
+    x = torch.randn(M, F, device=dev).bfloat16()
+    g = torch.randn(M, N, device=dev).bfloat16()
+    tg = _t(gs, dev)
+    xt, xs = quantize_fp8_grouped_t(x, tg)
+    gt, gsc = quantize_fp8_grouped_t(g, tg, blocks=True)
+    dw = tgmm_fp8(xt, xs, gt, gsc, tg, M)
+    assert dw.dtype == torch.bfloat16 and dw.shape == (E, F, N)
+    got = dw.float().cpu().numpy()
+    for e in np.flatnonzero(gs == 0):
+        assert not got[e].any()
+    ref_q = O.tgmm_fp8(_u8(xt), xs.cpu().numpy(), _u8(gt), gsc.cpu().numpy(), gs, M)
+    assert rel_err(got, ref_q) < 1e-2
+    ref = O.tgmm(x.float().cpu().numpy(), g.float().cpu().numpy(), gs)
+    assert rel_err(got, ref) < 6e-2
+
+
+@pytest.mark.timeout(600)
+def test_fp8_backward_c5_full_size(dev):
+    """The C5 backward shapes (M=131072, D=2048, I=768, E=128, the bench's Zipf(1.2) routing) with
+    fp8 operands: dlhs of both expert GEMMs on sampled rows, tgmm of both on sampled blocks."""
+    import bench
+    from mintext_amd.kernels import route, route_topk
+    from mintext_amd.kernels.fp8 import (grouped_matmul_fp8_dlhs, quantize_fp8_grouped_t, quantize_fp8_rows,
+                                         quantize_fp8_weights_t, tgmm_fp8)
+
+    cfg = bench.CONFIGS["qwen3_bwd"]
+    T, D, E, K, I = cfg["T"], cfg["D"], cfg["E"], cfg["K"], cfg["I"]
+    M = T * K
+    with torch.no_grad():
+        x, logits, gate_up, down, _, g = bench.layer_inputs("qwen3_bwd", dev)
+        idx, _ = route_topk(logits, K)
+        st, _, gs = route(x, idx, E)
+        gy = torch.randn(M, D, device=dev, generator=g).bfloat16()    # d out of the down GEMM
+        gh = torch.randn(M, 2 * I, device=dev, generator=g).bfloat16()  # d out of the gate_up GEMM
+        y = torch.randn(M, I, device=dev, generator=g).bfloat16()      # the down GEMM's input
+        dnq, dns = quantize_fp8_weights_t(down)
+        guq, gus = quantize_fp8_weights_t(gate_up)
+        a = grouped_matmul_fp8_dlhs(*quantize_fp8_rows(gy), dnq, dns, gs)   # [M, I]
+        b = grouped_matmul_fp8_dlhs(*quantize_fp8_rows(gh), guq, gus, gs)   # [M, D]
+        c = tgmm_fp8(*quantize_fp8_grouped_t(y, gs), *quantize_fp8_grouped_t(gy, gs, blocks=True), gs, M)   # [E, I, D]
+        d = tgmm_fp8(*quantize_fp8_grouped_t(st, gs), *quantize_fp8_grouped_t(gh, gs, blocks=True), gs, M)  # [E, D, 2I]
+    gsh = gs.cpu().numpy()
+    off = np.concatenate([[0], np.cumsum(gsh)])
+    rng = np.random.default_rng(61)
+    nz = np.flatnonzero(gsh)
+    experts = np.unique(np.concatenate([[int(np.argmax(gsh)), int(nz[np.argmin(gsh[nz])])],
+                                        rng.choice(nz, 6, replace=False)]))
+    h = lambda t: t.float().cpu().numpy().astype(np.float64)
+    for e in experts:
+        r0, r1 = int(off[e]), int(off[e + 1])
+        rows = np.unique(np.concatenate([[r0, r1 - 1], rng.integers(r0, r1, 6)]))
+        tr = torch.from_numpy(rows).to(dev)
+        assert rel_err(h(a[tr]), h(gy[tr]) @ h(down[e]).T) < 6e-2, f"dlhs down, expert {e}"
+        assert rel_err(h(b[tr]), h(gh[tr]) @ h(gate_up[e]).T) < 6e-2, f"dlhs gate_up, expert {e}"
+        ks, ns = np.sort(rng.choice(I, 16, replace=False)), np.sort(rng.choice(D, 16, replace=False))
+        ref_c = h(y[r0:r1][:, torch.from_numpy(ks).to(dev)]).T @ h(gy[r0:r1][:, torch.from_numpy(ns).to(dev)])
+        got_c = h(c[int(e)][torch.from_numpy(ks).to(dev)][:, torch.from_numpy(ns).to(dev)])
+        assert rel_err(got_c, ref_c) < 6e-2, f"tgmm down, expert {e}"
+        kd, nd = np.sort(rng.choice(D, 16, replace=False)), np.sort(rng.choice(2 * I, 16, replace=False))
+        ref_d = h(st[r0:r1][:, torch.from_numpy(kd).to(dev)]).T @ h(gh[r0:r1][:, torch.from_numpy(nd).to(dev)])
+        got_d = h(d[int(e)][torch.from_numpy(kd).to(dev)][:, torch.from_numpy(nd).to(dev)])
+        assert rel_err(got_d, ref_d) < 6e-2, f"tgmm gate_up, expert {e}"

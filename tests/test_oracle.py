@@ -434,3 +434,76 @@ def test_planted_mistake_is_caught():
     gs, x, w = g["uniform_e4__gs"], g["uniform_e4__x"], g["uniform_e4__w"]
     wrong = O.gmm(x, w[::-1], gs)  # experts in reversed order
     assert rel_err(wrong, g["uniform_e4__out"]) > 0.5
+
+
+# ------------------------------------------------------------------------ fp8 backward operands
+def test_quant_weights_t_is_the_forward_blocks_in_w_layout():
+    """The dlhs weight operand: the forward's 128x128 blocks (pinned through quant_fp8_weights
+    against torch's e4m3 cast) with codes in w's own layout; dequantised it is within half an e4m3
+    step of w everywhere."""
+    w = (np.random.default_rng(3).standard_normal((2, 256, 384)) * 0.05).astype(np.float32)
+    q, s = O.quant_fp8_weights_t(w)
+    qf, sf = O.quant_fp8_weights(w)
+    assert q.shape == (2, 256, 384) and s.shape == (2, 2, 3)
+    assert np.array_equal(q, np.swapaxes(qf, 1, 2)) and np.array_equal(s, np.swapaxes(sf, 1, 2))
+    deq = O.e4m3_decode(q).astype(np.float64) * np.repeat(np.repeat(s, 128, 1), 128, 2)
+    assert np.all(np.abs(deq - w) <= np.abs(w) * 2.0 ** -4 + np.repeat(np.repeat(s, 128, 1), 128, 2) * 2.0 ** -9)
+
+
+def test_gmm_fp8_dlhs_equals_dequantised_dlhs():
+    rng = np.random.default_rng(4)
+    gs = np.array([100, 0, 37, 123], np.int32)
+    M, Kin, Kout = int(gs.sum()) + 4, 256, 384
+    g = rng.standard_normal((M, Kout)).astype(np.float32)
+    w = (rng.standard_normal((4, Kin, Kout)) * 0.05).astype(np.float32)
+    gq, gsc = O.quant_fp8_rows(g)
+    wq, ws = O.quant_fp8_weights_t(w)
+    got = O.gmm_fp8_dlhs(gq, gsc, wq, ws, gs)
+    wd = O.e4m3_decode(wq).astype(np.float64) * np.repeat(np.repeat(ws, 128, 1), 128, 2)  # [E,Kin,Kout]
+    ref = O.gmm_dlhs(O.dequant_rows(gq, gsc), wd, gs)  # g @ W^T per group (torch-pinned)
+    assert rel_err(got, ref) < 1e-12
+    # against the unquantised product: two e4m3 quantisations
+    assert rel_err(got, O.gmm_dlhs(g, w, gs)) < 6e-2
+
+
+@pytest.mark.parametrize("blocks", [False, True])
+def test_quant_grouped_t_chunks_equal_row_and_block_quantisers(blocks):
+    """Each expert-aligned chunk of the transposed operand is quant_fp8_rows (1x128 along the
+    transposed row) or, with blocks, quant_fp8_weights (128x128) of that zero-padded chunk."""
+    rng = np.random.default_rng(5)
+    gs = np.array([130, 0, 5, 256, 0, 77], np.int32)
+    M, F = int(gs.sum()) + 9, 256
+    x = (rng.standard_normal((M, F)) * rng.uniform(0.01, 10, (1, F))).astype(np.float32)
+    xt, xs = O.quant_fp8_grouped_t(x, gs, blocks)
+    off, cb = O.fp8_group_chunks(gs, M)
+    assert int(cb[-1]) == sum(-(-int(g) // 128) for g in gs)
+    for e in range(len(gs)):
+        for j, c in enumerate(range(int(cb[e]), int(cb[e + 1]))):
+            r0 = int(off[e]) + 128 * j
+            chunk = np.zeros((128, F), np.float32)
+            rows = x[r0:min(r0 + 128, int(off[e + 1]))]
+            chunk[: len(rows)] = rows
+            if blocks:
+                q, s = O.quant_fp8_weights(chunk[None])  # [1, F, 128] codes, [1, F/128, 1] scales
+                assert np.array_equal(xt[:, 128 * c:128 * (c + 1)], q[0]) and np.array_equal(xs[:, c], s[0, :, 0])
+            else:
+                q, s = O.quant_fp8_rows(np.ascontiguousarray(chunk.T))
+                assert np.array_equal(xt[:, 128 * c:128 * (c + 1)], q) and np.array_equal(xs[:, c], s[:, 0])
+    # round trip within the e4m3 bound, padding dropped
+    d = O.dequant_grouped_t(xt, xs, gs, M, blocks)
+    used = int(gs.sum())
+    assert rel_err(d[:used], x[:used]) < 4e-2 and not d[used:].any()
+
+
+def test_tgmm_fp8_equals_dequantised_tgmm_and_empty_groups_are_zero():
+    rng = np.random.default_rng(6)
+    gs = np.array([300, 0, 1, 200], np.int32)
+    M, F, N = int(gs.sum()), 256, 256
+    x, g = rng.standard_normal((M, F)).astype(np.float32), rng.standard_normal((M, N)).astype(np.float32)
+    xt, xs = O.quant_fp8_grouped_t(x, gs, False)
+    gt, gsc = O.quant_fp8_grouped_t(g, gs, True)
+    got = O.tgmm_fp8(xt, xs, gt, gsc, gs, M)
+    ref = O.tgmm(O.dequant_grouped_t(xt, xs, gs, M, False), O.dequant_grouped_t(gt, gsc, gs, M, True), gs)
+    assert rel_err(got, ref) < 1e-12
+    assert not got[1].any()
+    assert rel_err(got, O.tgmm(x, g, gs)) < 6e-2
