@@ -1,6 +1,6 @@
 """Benchmark of the MoE layer forward on one MI355X (default: the Mixtral-8x7B shape, bf16).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config mixtral|tiny|deepseek|qwen3_fp8|qwen3_bwd]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config mixtral|tiny|deepseek|qwen3_fp8|qwen3_bwd|qwen3_bwd_fp8]
 
 A step is one MoE layer forward over one batch of synthetic tokens, inputs resident in HBM:
 router top-k on the gate logits -> route (dispatch) -> grouped GEMM gate_up with the fused
@@ -39,6 +39,8 @@ CONFIGS = {
                      n_group=8, topk_group=4, scale=2.5, shared=1),
     "qwen3_fp8": dict(T=16384, D=2048, E=128, K=8, I=768, dtype="fp8", scoring="softmax", wstd=0.02),
     "qwen3_bwd": dict(T=16384, D=2048, E=128, K=8, I=768, dtype="bf16", scoring="softmax", wstd=0.02, zipf=1.2),
+    # the C5 backward with fp8 operands (not a BASELINE config: the same shapes and routing)
+    "qwen3_bwd_fp8": dict(T=16384, D=2048, E=128, K=8, I=768, dtype="fp8", scoring="softmax", wstd=0.02, zipf=1.2),
 }
 
 
@@ -188,7 +190,8 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
     from mintext_amd.kernels.grouped_matmul import gathered_swiglu_supported, grouped_matmul_swiglu_gathered
     from mintext_amd.kernels.moe_dispatch import route_indices
 
-    gather = gather and cfg_name != "qwen3_bwd" and (D >= 256 if fp8 else gathered_swiglu_supported(x, gate_up))
+    bwd = cfg_name in ("qwen3_bwd", "qwen3_bwd_fp8")
+    gather = gather and not bwd and (D >= 256 if fp8 else gathered_swiglu_supported(x, gate_up))
 
     def step(timed):
         with torch.no_grad():
@@ -236,7 +239,7 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
                 t_comb.stop()
             return out
 
-    if cfg_name == "qwen3_bwd":
+    if bwd:
         with torch.no_grad():
             idx, w = route_topk(logits, K)
             st, si, gs = route(x, idx, E)
@@ -258,6 +261,38 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
                     t_tg.start()
                 c = tgmm(y, gy, gs)              # d down   [E, I, D]
                 d = tgmm(st, gh, gs)             # d gate_up [E, D, 2I]
+                if timed:
+                    t_tg.stop()
+                return a, b, c, d
+
+    if cfg_name == "qwen3_bwd_fp8":
+        # operands quantised once outside the timed region, as a training step quantises each
+        # operand once and may reuse it: upstream gradients in 1x128 rows for the dlhs, both tgmm
+        # operands in expert-aligned 128-row chunks; weights prepacked in their own layout
+        from mintext_amd.kernels.fp8 import (grouped_matmul_fp8_dlhs, quantize_fp8_grouped_t, quantize_fp8_rows,
+                                             quantize_fp8_weights_t, tgmm_fp8)
+
+        with torch.no_grad():
+            dnq, dns = quantize_fp8_weights_t(down)
+            guq, gus = quantize_fp8_weights_t(gate_up)
+            gyq, gys = quantize_fp8_rows(gy)
+            ghq, ghs = quantize_fp8_rows(gh)
+            yt = quantize_fp8_grouped_t(y, gs)
+            gyt = quantize_fp8_grouped_t(gy, gs, blocks=True)
+            stt = quantize_fp8_grouped_t(st, gs)
+            ght = quantize_fp8_grouped_t(gh, gs, blocks=True)
+
+        def step(timed):  # noqa: F811
+            with torch.no_grad():
+                if timed:
+                    t_dl.start()
+                a = grouped_matmul_fp8_dlhs(gyq, gys, dnq, dns, gs)   # d inter [M, I]
+                b = grouped_matmul_fp8_dlhs(ghq, ghs, guq, gus, gs)   # d x     [M, D]
+                if timed:
+                    t_dl.stop()
+                    t_tg.start()
+                c = tgmm_fp8(*yt, *gyt, gs, M)                        # d down    [E, I, D]
+                d = tgmm_fp8(*stt, *ght, gs, M)                       # d gate_up [E, D, 2I]
                 if timed:
                     t_tg.stop()
                 return a, b, c, d
@@ -297,7 +332,7 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
 
     gu_ms, dn_ms = t_gu.mean_ms(), t_dn.mean_ms()
     peak = PEAK_FP8_TFLOPS if fp8 else PEAK_BF16_TFLOPS
-    if cfg_name == "qwen3_bwd":
+    if bwd:
         kern_flops = 2.0 * M * D * I + 2.0 * M * 2 * I * D  # both dlhs GEMMs
         achieved = kern_flops / (gu_ms * 1e-3) / 1e12
         dominant = "gmm_dlhs (both expert GEMMs)"
@@ -349,13 +384,12 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
         "vs_baseline": None,
         "dtype": {"bf16": "bf16", "f32": "f32", "fp8": "fp8e4m3"}[cfg["dtype"]],
         "data": "synthetic (seeded N(0,1) activations, N(0,%g) weights, random-init experts)" % cfg["wstd"],
-        "config": {"workload": f"{cfg_name} MoE layer forward" if cfg_name != "qwen3_bwd" else
-                   "qwen3 grouped-GEMM backward (dlhs+tgmm), Zipf(1.2) skew",
+        "config": {"workload": f"{cfg_name} MoE layer forward" if not bwd else
+                   f"qwen3 grouped-GEMM backward (dlhs+tgmm){', fp8 operands' if fp8 else ''}, Zipf(1.2) skew",
                    "T": T, "d_model": D, "experts": E, "top_k": K, "d_ff": I, "routing": cfg["scoring"],
                    "parallelism": "single GPU",
                    **({"shared_expert": shared_mode if fold else "separate"} if shared is not None else {})},
-        "gemm": {"tflops": round(flops_fwd / (gemm_ms * 1e-3) / 1e12 if cfg_name != "qwen3_bwd" else
-                                 flops_fwd / ((gu_ms + dn_ms) * 1e-3) / 1e12, 1),
+        "gemm": {"tflops": round(flops_fwd / (gemm_ms * 1e-3) / 1e12, 1),
                  "frac_of_peak": round((flops_fwd / (gemm_ms * 1e-3) / 1e12) / peak, 4),
                  "gate_up_ms": round(gu_ms, 4), "down_ms": round(dn_ms, 4)},
         "dispatch_combine": {"rows_gathered_in_gate_up": gather,
@@ -371,7 +405,7 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
     }
     if graph_ms is not None:
         res["hip_graph"] = {"ms_per_step": round(graph_ms, 4), "tokens_per_s": round(T / (graph_ms * 1e-3), 1)}
-    if cpu_baseline and cfg_name not in ("qwen3_bwd",):
+    if cpu_baseline and not bwd:
         # fp8 has no reference counterpart: the CPU leg runs the reference's bf16 layer on the same tokens
         hdt = torch.float32 if cfg["dtype"] == "f32" else torch.bfloat16
         h = lambda t: t.to(hdt).cpu()

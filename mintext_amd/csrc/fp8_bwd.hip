@@ -8,11 +8,15 @@
 //       [E, Kin, Kout] (k-contiguous for this product) and the block-scale grid transposed; the
 //       product is then the forward fp8 grouped GEMM (mtx_gmm_fp8) on these operands.
 // tgmm  dW[e] = X_e^T @ G_e reduces over the rows of expert e.  Both operands are quantised in
-//       groups of 128 consecutive rows of the expert (expert-aligned chunks: chunk c of expert e
-//       covers its rows 128c .. 128c+127, the last chunk zero-padded), transposed so that the
-//       reduction is contiguous: XT [F, 128*C] with one scale per feature and chunk (1x128 along
-//       the transposed row), GT [N, 128*C] with one scale per 128 features and chunk (128x128
-//       blocks).  The GEMM is the forward kernel's tile loop with a per-expert k-range.
+//       groups of 128 consecutive rows of the expert (expert-aligned chunks: chunk j of expert e
+//       covers its rows 128j .. 128j+127, the last chunk zero-padded) and transposed per expert so
+//       that the reduction is contiguous: expert e's block XT_e [F, 128*n_e] (n_e chunks) starts
+//       at byte 128*F*cb[e] (cb[e] = chunks of the experts before e), with one scale per feature
+//       and chunk ([F, n_e] at float cb[e]*F; 1x128 along the transposed row), and GT_e [N, 128*n_e]
+//       likewise with one scale per 128 features and chunk ([N/128, n_e] at float cb[e]*N/128;
+//       128x128 blocks).  Expert-major blocks keep each tile's 256 rows within a few hundred KB
+//       (a row-major [F, 128*C] layout put them 128*C bytes apart, one page per row).  The GEMM is
+//       the forward kernel's tile loop with a per-expert k-range.
 #include "common.h"
 #include "lds_dma.h"
 
@@ -120,23 +124,26 @@ __device__ __forceinline__ int chunk_expert(const int* __restrict__ cb, int E, i
 }
 
 // ---- grouped transposing quantiser -------------------------------------------------------------
-// Workgroup (chunk c, 128-feature block fb): rows off[e] + 128(c - cb[e]) .. +127 of expert e
-// (rows past the expert are zero) x features fb*128 .. +127 of x [M, F] -> xt[f][128c + r]
-// (xt row stride ldt bytes).  ROW: scale per feature = amax over the chunk's rows / 448 at
-// xts[f * C + c]; BLOCK: one scale per 128x128 block at xts[fb * C + c].  Codes are
-// f32_to_e4m3(v / scale), scale 1 when the amax is 0.
+// Workgroup (chunk c, 128-feature block fb): chunk j = c - cb[e] of expert e, its rows off[e] + 128j
+// .. +127 (rows past the expert are zero) x features fb*128 .. +127 of x [M, F] -> codes at
+// xt[128*F*cb[e] + f*128*n_e + 128j + r] (n_e = chunks of expert e).  ROW: scale per feature =
+// amax over the chunk's rows / 448 at xts[F*cb[e] + f*n_e + j]; BLOCK: one scale per 128x128 block
+// at xts[(F/128)*cb[e] + fb*n_e + j].  Codes are f32_to_e4m3(v / scale), scale 1 when the amax is 0.
 template <typename T, bool BLOCK>
 __global__ __launch_bounds__(256) void quant_grouped_t_kernel(const T* __restrict__ x, int F, const int* __restrict__ cb,
-                                                              const int* __restrict__ off, int E, int C, int64_t ldt,
+                                                              const int* __restrict__ off, int E,
                                                               uint8_t* __restrict__ xt, float* __restrict__ xts) {
   __shared__ float tile[128][129];
   __shared__ float smax[2][128];
   const int c = blockIdx.x, fb = blockIdx.y, tid = threadIdx.x;
   if (c >= cb[E]) return;  // beyond the chunks of this call's groups
   const int e = chunk_expert(cb, E, c);
-  const int rs = off[e] + 128 * (c - cb[e]);
+  const int j = c - cb[e], ne = cb[e + 1] - cb[e];
+  const int rs = off[e] + 128 * j;
   const int nr = min(128, off[e + 1] - rs);
   const int64_t f0 = (int64_t)fb * 128;
+  uint8_t* xe = xt + (int64_t)128 * F * cb[e] + (int64_t)128 * j;  // + f * 128 * ne
+  const int64_t lde = (int64_t)128 * ne;
   for (int i = tid; i < 128 * 128; i += 256) {
     const int r = i / 128, f = i % 128;
     tile[r][f] = (r < nr) ? ld_elem(x, (int64_t)(rs + r) * F + f0 + f) : 0.0f;
@@ -169,8 +176,9 @@ __global__ __launch_bounds__(256) void quant_grouped_t_kernel(const T* __restric
       q[k] = (uint32_t)f32_to_e4m3(tile[r0 + 4 * k][f] / s) | ((uint32_t)f32_to_e4m3(tile[r0 + 4 * k + 1][f] / s) << 8) |
              ((uint32_t)f32_to_e4m3(tile[r0 + 4 * k + 2][f] / s) << 16) |
              ((uint32_t)f32_to_e4m3(tile[r0 + 4 * k + 3][f] / s) << 24);
-    *(u32x4*)(xt + (f0 + f) * ldt + (int64_t)c * 128 + r0) = u32x4{q[0], q[1], q[2], q[3]};
-    if (r0 == 0 && (!BLOCK || f == 0)) xts[(BLOCK ? (int64_t)fb : f0 + f) * C + c] = s;
+    *(u32x4*)(xe + (f0 + f) * lde + r0) = u32x4{q[0], q[1], q[2], q[3]};
+    if (r0 == 0 && (!BLOCK || f == 0))
+      xts[(int64_t)(BLOCK ? F / 128 : F) * cb[e] + (BLOCK ? (int64_t)fb : f0 + f) * ne + j] = s;
   }
 }
 
@@ -178,37 +186,38 @@ __global__ __launch_bounds__(256) void quant_grouped_t_kernel(const T* __restric
 // 256x256 output tiles of dW[e] [F, N], 8 waves (2 x 4, 128x64 wave tiles of 32x32 blocks), 64-k
 // stages of 256 XT rows and 256 GT rows (32 KB) loaded with global_load_lds_dwordx4 into a 4-deep
 // LDS ring three stages ahead; one v_mfma_scale_f32_32x32x64_f8f6f4 (unit scales) per block and
-// stage, operands swapped so that each lane owns four consecutive output columns.  Per 128-k
-// chunk the accumulators are kept in units of the chunk's scale product and moved to the next
-// chunk's units by (sa_c / sa_n) * (sb_c / sb_n) (no product of two small scales is formed), the
-// last chunk's scales applied at the end.  An expert without rows gives a zero tile.
+// stage, operands swapped so that each lane owns four consecutive output columns.  The scales of
+// chunk j travel with its even stage 2j (global_load_lds_dword: waves 0-3 the 256 XT-row scales,
+// wave 4 the two GT-block scales, waves 5-7 a filler load so that every wave issues the same
+// number of loads), so no wait on memory is added for them.  Per chunk the accumulators are kept
+// in units of the chunk's scale product and moved to the next chunk's units by
+// (sa_c / sa_n) * (sb_c / sb_n) (no product of two small scales is formed), the last chunk's
+// scales applied at the end.  An expert without rows gives a zero tile.
 constexpr int TBM = 256, TBN = 256, TBK = 64, TNST = 4, TPD = 3;
-constexpr int TA_BYTES = TBM * TBK, TSTAGE = 2 * TA_BYTES;
+constexpr int TA_BYTES = TBM * TBK, TS_OFF = 2 * TA_BYTES, TSTAGE = TS_OFF + 2048;
 __device__ __forceinline__ int t_off(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
 
 struct TArgs {
-  const uint8_t* xt;  // [F, ldt]
-  const float* xts;   // [F, C]
-  const uint8_t* gt;  // [N, ldt]
-  const float* gts;   // [N/128, C]
+  const uint8_t* xt;  // expert-major blocks [F, 128 n_e]
+  const float* xts;   // expert-major [F, n_e]
+  const uint8_t* gt;  // expert-major blocks [N, 128 n_e]
+  const float* gts;   // expert-major [N/128, n_e]
   uint16_t* dw;       // [E, F, N] bf16
   const int* cb;      // [E+1]
   const int* order;   // [E]
-  int E, F, N, C;
-  int64_t ldt;
+  int E, F, N;
 };
 
 __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
-  constexpr int WN = 4, WTM = 128, WTN = 64, TM = 4, TN = 2, LPS = 4;
+  constexpr int WN = 4, WTM = 128, WTN = 64, TM = 4, TN = 2, LPS = 4;  // data loads per wave and stage
   __shared__ __attribute__((aligned(1024))) char lds[TNST * TSTAGE];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int nf = p.F / TBM, nn = p.N / TBN, per_e = nf * nn;
   const int total = p.E * per_e;
-  const int pid = blockIdx.x;
-  const int total8 = (total + 7) & ~7;
-  if (pid >= total8) return;
-  const int lid = (pid & 7) * (total8 >> 3) + (pid >> 3);  // each XCD sweeps a contiguous range
+  // consecutive workgroups (which the dispatcher places on consecutive XCDs) take consecutive tiles,
+  // so the tiles of the large experts, which come first, spread over all XCDs
+  const int lid = blockIdx.x;
   if (lid >= total) return;
   const int e = p.order[lid / per_e];
   const int rem = lid % per_e;
@@ -223,7 +232,9 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
     return;
   }
   const int nk = 2 * nch;  // 64-byte stages
-  const uint32_t kbase = (uint32_t)c0 * 128u;
+  const uint32_t lde = (uint32_t)nch * 128u;  // bytes per row of this expert's blocks
+  const uint8_t* xe = p.xt + (int64_t)128 * p.F * c0;
+  const uint8_t* ge = p.gt + (int64_t)128 * p.N * c0;
 
   // per-lane sources: lane l of segment s fills tile row 16s + l/4, chunk slot l%4
   uint32_t aoff[2], boff[2];
@@ -231,19 +242,28 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
   for (int i = 0; i < 2; ++i) {
     const int seg = wave * 2 + i;
     const int r = seg * 16 + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
-    aoff[i] = (uint32_t)(fb * TBM + r) * (uint32_t)p.ldt + kbase + (uint32_t)(c * 16);
-    boff[i] = (uint32_t)(nb * TBN + r) * (uint32_t)p.ldt + kbase + (uint32_t)(c * 16);
+    aoff[i] = (uint32_t)(fb * TBM + r) * lde + (uint32_t)(c * 16);
+    boff[i] = (uint32_t)(nb * TBN + r) * lde + (uint32_t)(c * 16);
   }
+  // this lane's scale source for chunk 0 (one float per chunk after it): waves 0-3 XT row
+  // fb*256 + 64*wave + lane, wave 4 the GT block nb*2 + (lane & 1), the others a filler
+  const float* sp;
+  if (wave < 4) sp = p.xts + (int64_t)p.F * c0 + (int64_t)(fb * TBM + 64 * wave + lane) * nch;
+  else if (wave == 4) sp = p.gts + (int64_t)(p.N / 128) * c0 + (int64_t)(nb * 2 + (lane & 1)) * nch;
+  else sp = p.xts + (int64_t)p.F * c0;
   const uint32_t lds_base = lds_addr(lds);
   const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
-  // stages past the end re-read the last one (in bounds) into a slot that is no longer read
+  // stages past the end re-read the last one (in bounds) into a slot that is no longer read;
+  // even stages also carry their chunk's scales (LPS + 1 loads per wave)
   auto issue_stage = [&](int kt) {
     const uint32_t st = lds_base + (uint32_t)((kt & (TNST - 1)) * TSTAGE);
-    const uint32_t kofs = (uint32_t)min(kt, nk - 1) * TBK;
+    const int k = min(kt, nk - 1);
+    const uint32_t kofs = (uint32_t)k * TBK;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) gload_lds16(p.xt + aoff[i] + kofs, st + (wave_u * 2 + i) * 1024u);
+    for (int i = 0; i < 2; ++i) gload_lds16(xe + aoff[i] + kofs, st + (wave_u * 2 + i) * 1024u);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) gload_lds16(p.gt + boff[i] + kofs, st + (uint32_t)TA_BYTES + (wave_u * 2 + i) * 1024u);
+    for (int i = 0; i < 2; ++i) gload_lds16(ge + boff[i] + kofs, st + (uint32_t)TA_BYTES + (wave_u * 2 + i) * 1024u);
+    if ((kt & 1) == 0) gload_lds4(sp + (k >> 1), st + (uint32_t)TS_OFF + wave_u * 256u);
   };
   i32x8 fa[2][TM], fbr[2][TN];
   const int frow = lane & 31, fhalf = lane >> 5;
@@ -259,13 +279,14 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) fbr[buf][j] = ld32(st + TA_BYTES, wn * WTN + j * 32 + frow);
   };
-  // scales of chunk c0 + kb: this lane's four XT rows, and the GT block of this wave's columns
-  const float* sa_src = p.xts + (int64_t)(fb * TBM + wm * WTM + frow) * p.C + c0;
-  const float* sb_src = p.gts + (int64_t)(nb * 2 + (wn >> 1)) * p.C + c0;
+  // scales of the chunk whose even stage is kt: this lane's four XT rows and this wave's GT block
   float sa_c[TM], sa_n[TM], sb_c, sb_n;
+  auto read_scales = [&](int kt, float* sa, float& sb) {
+    const float* sc = (const float*)(lds + (kt & (TNST - 1)) * TSTAGE + TS_OFF);
 #pragma unroll
-  for (int i = 0; i < TM; ++i) sa_c[i] = sa_src[(int64_t)i * 32 * p.C];
-  sb_c = sb_src[0];
+    for (int i = 0; i < TM; ++i) sa[i] = sc[wm * WTM + i * 32 + frow];
+    sb = sc[256 + (wn >> 1)];
+  };
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -275,10 +296,12 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
+  // prologue: stages 0 (+ scales), 1, 2 (+ scales); 0 and 1 landed (2's LPS + 1 loads may fly)
 #pragma unroll
   for (int s = 0; s < TPD; ++s) issue_stage(s);  // nk >= 2: stages past the end re-read the last
-  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (TPD - 2)));
-  __syncthreads();  // stages 0 and 1 visible
+  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));
+  __syncthreads();
+  read_scales(0, sa_c, sb_c);
   read_frags(0, 0);
   auto mfmas = [&](int buf) {
 #pragma unroll
@@ -288,24 +311,17 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fbr[buf][j], fa[buf][i], acc[i][j], 0, 0, 0, 127, 0,
                                                                     127);
   };
-  auto finish_stage = [&]() {
-    // stage kt+2 landed before the barrier makes it visible (kt+3 may still be in flight)
-    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (TPD - 2)));
-    __syncthreads();
-  };
   for (int kb = 0; kb < nch; ++kb) {
     const int kt = 2 * kb;
     const bool more = kb + 1 < nch;
-    if (more) {  // next chunk's scales, in flight during this chunk's MFMAs
-#pragma unroll
-      for (int i = 0; i < TM; ++i) sa_n[i] = sa_src[(int64_t)i * 32 * p.C + kb + 1];
-      sb_n = sb_src[kb + 1];
-    }
-    issue_stage(kt + TPD);
+    issue_stage(kt + TPD);  // odd stage: LPS loads
     read_frags(kt + 1, 1);
     mfmas(0);
-    finish_stage();
-    issue_stage(kt + 1 + TPD);
+    // stage kt+2 (LPS + 1 loads, issued before stage kt+3) landed; kt+3 may still be in flight
+    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS));
+    __syncthreads();
+    if (more) read_scales(kt + 2, sa_n, sb_n);  // the next chunk's scales, now visible
+    issue_stage(kt + 1 + TPD);  // even stage: LPS + 1 loads
     read_frags(kt + 2, 0);  // the last step reads an unused ring slot (in bounds)
     mfmas(1);
     if (more) {
@@ -321,7 +337,9 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
       }
       sb_c = sb_n;
     }
-    finish_stage();
+    // stage kt+3 (LPS loads) landed; kt+4 (LPS + 1) may still be in flight
+    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));
+    __syncthreads();
   }
   __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));  // no ring load lands after the workgroup ends
 
@@ -403,10 +421,9 @@ extern "C" int mtx_quant_fp8_grouped_t(const void* x, int dtype, const int32_t* 
   int rc = grouped_prologue(group_sizes, E, M, workspace, st, &cb, &off, &order);
   if (rc) return rc;
   dim3 grid((unsigned)C, (unsigned)(F / 128));
-  const int64_t ldt = C * 128;
 #define MTX_QG(T, B)                                                                                              \
   hipLaunchKernelGGL((f8b::quant_grouped_t_kernel<T, B>), grid, dim3(256), 0, st, (const T*)x, (int)F, cb, off, \
-                     (int)E, (int)C, ldt, xt, xt_scale)
+                     (int)E, xt, xt_scale)
   if (dtype == MTX_F32) {
     if (blocks) MTX_QG(float, true); else MTX_QG(float, false);
   } else {
@@ -425,8 +442,8 @@ extern "C" int mtx_tgmm_fp8(const uint8_t* xt, const float* xt_scale, const uint
   if (!workspace || workspace_bytes < mtx_fp8_grouped_workspace_size(E)) return MTX_ERR_WORKSPACE;
   if (!xt || !xt_scale || !gt || !gt_scale || !group_sizes || !dw) return MTX_ERR_ARG;
   if (((uintptr_t)xt | (uintptr_t)gt) % 16) return MTX_ERR_ARG;
-  const int64_t C = fp8_grouped_chunks(M, E), ldt = C * 128;
-  if ((F > N ? F : N) * ldt >= (int64_t(1) << 32)) return MTX_ERR_UNSUPPORTED;  // 32-bit byte offsets
+  const int64_t C = fp8_grouped_chunks(M, E);
+  if ((F > N ? F : N) * C * 128 >= (int64_t(1) << 32)) return MTX_ERR_UNSUPPORTED;  // 32-bit byte offsets
   hipStream_t st = (hipStream_t)stream;
   int *cb, *off, *order;
   int rc = grouped_prologue(group_sizes, E, M, workspace, st, &cb, &off, &order);
@@ -442,8 +459,6 @@ extern "C" int mtx_tgmm_fp8(const uint8_t* xt, const float* xt_scale, const uint
   a.E = (int)E;
   a.F = (int)F;
   a.N = (int)N;
-  a.C = (int)C;
-  a.ldt = ldt;
   const int64_t grid = round_up(E * (F / 256) * (N / 256), 8);
   hipLaunchKernelGGL(f8b::tgmm_fp8_kernel, dim3((unsigned)grid), dim3(512), 0, st, a);
   return check_launch();

@@ -146,31 +146,45 @@ def grouped_matmul_fp8_dlhs(gq, g_scale, w_qt, w_scale_t, group_sizes) -> torch.
 
 def quantize_fp8_grouped_t(x: torch.Tensor, group_sizes: torch.Tensor, *, blocks: bool = False):
     """Operand of ``tgmm_fp8``: x [M, F] (f32/bf16, rows grouped by expert) quantised in chunks of
-    128 consecutive rows of each expert and transposed: codes [F, 128*C] (C = ceil(M/128) + E chunk
-    slots; chunk c of expert e holds its rows 128c' .. 128c'+127, zero-padded) and scales [F, C] --
-    one per feature and chunk -- or, with ``blocks``, [F/128, C] -- one per 128x128 block."""
+    128 consecutive rows of each expert (chunk j of expert e = its rows 128j .. 128j+127,
+    zero-padded) and transposed per expert into expert-major blocks: flat codes of F*128*C bytes
+    (C = ceil(M/128) + E chunk slots; expert e's block [F, 128 n_e] at byte 128*F*cb[e], cb[e] =
+    chunks of the experts before it) and flat scales -- one per feature and chunk (expert e's
+    [F, n_e] at F*cb[e]) or, with ``blocks``, one per 128x128 block ([F/128, n_e] at
+    (F/128)*cb[e])."""
     gs = _gs(group_sizes)
     dev = L.require_device(x, gs)
     x = x.contiguous()
     M, F = x.shape
     E = gs.numel()
     C = L.query("mtx_fp8_grouped_chunks", M, E)
-    xt = torch.empty((F, 128 * C), dtype=torch.float8_e4m3fn, device=dev)
-    xs = torch.empty((F // 128, C) if blocks else (F, C), dtype=torch.float32, device=dev)
+    xt = torch.empty((F * 128 * C,), dtype=torch.float8_e4m3fn, device=dev)
+    xs = torch.empty(((F // 128) * C if blocks else F * C,), dtype=torch.float32, device=dev)
+    xt._mtx_features = F
+    xs._mtx_features = F
     ws = L.workspace(L.query("mtx_fp8_grouped_workspace_size", E), dev)
     L.call("mtx_quant_fp8_grouped_t", L.ptr(x), L.dtype_code(x.dtype), L.ptr(gs), M, F, E, int(bool(blocks)),
            L.ptr(xt), L.ptr(xs), L.ptr(ws), ws.numel(), L.stream(dev))
     return xt, xs
 
 
-def tgmm_fp8(xt, xt_scale, gt, gt_scale, group_sizes, M: int) -> torch.Tensor:
+def tgmm_fp8(xt, xt_scale, gt, gt_scale, group_sizes, M: int, F: int | None = None,
+             N: int | None = None) -> torch.Tensor:
     """dW [E, F, N] bf16 = per group dequant(x)^T @ dequant(g) with f32 accumulation (``mtx_tgmm_fp8``):
     x from ``quantize_fp8_grouped_t(x, gs)`` (per-feature chunk scales), g from
-    ``quantize_fp8_grouped_t(g, gs, blocks=True)``; M = rows of x and g.  Empty groups give zeros.
-    F and N must be multiples of 256."""
+    ``quantize_fp8_grouped_t(g, gs, blocks=True)``; M = rows of x and g, F / N their columns (taken
+    from the quantiser's outputs when omitted).  Empty groups give zeros.  F and N must be multiples
+    of 256."""
     gs = _gs(group_sizes)
     dev = L.require_device(xt, xt_scale, gt, gt_scale, gs)
-    F, N, E = xt.shape[0], gt.shape[0], gs.numel()
+    E = gs.numel()
+    F = getattr(xt, "_mtx_features", None) if F is None else F
+    N = getattr(gt, "_mtx_features", None) if N is None else N
+    if F is None or N is None:
+        raise ValueError("tgmm_fp8 needs F and N (the feature counts of x and g)")
+    C = L.query("mtx_fp8_grouped_chunks", M, E)
+    if xt.numel() != F * 128 * C or gt.numel() != N * 128 * C:
+        raise ValueError("tgmm_fp8: operands were not quantised with these M, F, N and group count")
     dw = torch.empty((E, F, N), dtype=torch.bfloat16, device=dev)
     ws = L.workspace(L.query("mtx_fp8_grouped_workspace_size", E), dev)
     L.call("mtx_tgmm_fp8", L.ptr(xt.contiguous()), L.ptr(xt_scale.contiguous()), L.ptr(gt.contiguous()),

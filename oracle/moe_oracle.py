@@ -451,57 +451,64 @@ def fp8_group_chunks(group_sizes, M: int, block: int = 128):
 
 
 def quant_fp8_grouped_t(x, group_sizes, blocks: bool, C: int | None = None, block: int = 128):
-    """The tgmm operands: x [M,F] -> codes xt [F, 128*C] (row f = feature f, column 128c + r = row r
-    of the expert's chunk c, zero past the expert) and scales: one per feature and chunk [F, C]
-    (``blocks`` False, 1 x 128 along xt's row) or one per 128 features and chunk [F/128, C]
-    (``blocks`` True, 128 x 128), scale = amax/448 (1 if 0), q = RNE(x / scale).  C defaults to
-    ceil(M/128) + E (the allocation of the kernels); chunks past the groups are left 0."""
+    """The tgmm operands: x [M,F] quantised in expert-aligned chunks of 128 rows (chunk j of expert
+    e = its rows 128j .. 128j+127, zero past the expert) and transposed per expert, in expert-major
+    blocks: returns flat codes (expert e's block [F, 128 n_e] at offset 128*F*cb[e], n_e = its
+    chunks) and flat scales -- one per feature and chunk ([F, n_e] at F*cb[e], ``blocks`` False,
+    1 x 128 along the transposed row) or one per 128 features and chunk ([F/128, n_e] at
+    (F/128)*cb[e], ``blocks`` True, 128 x 128).  scale = amax/448 (1 if 0), q = RNE(x / scale).
+    C (chunk slots allocated) defaults to ceil(M/128) + E; slots past the groups stay 0."""
     x = np.asarray(x, dtype=np.float32)
     M, F = x.shape
     E = len(group_sizes)
     off, cb = fp8_group_chunks(group_sizes, M, block)
     C = int(-(-M // block) + E) if C is None else C
-    xt = np.zeros((F, C * block), np.uint8)
-    xs = np.zeros((F // block, C) if blocks else (F, C), np.float32)
+    nf = F // block if blocks else F
+    xt = np.zeros(F * block * C, np.uint8)
+    xs = np.zeros(nf * C, np.float32)
     for e in range(E):
-        for j, c in enumerate(range(int(cb[e]), int(cb[e + 1]))):
-            r0 = int(off[e]) + block * j
-            rows = x[r0:min(r0 + block, int(off[e + 1]))]
-            chunk = np.zeros((block, F), np.float32)
-            chunk[: rows.shape[0]] = rows
-            t = chunk.T  # [F, 128]
-            if blocks:
-                amax = np.abs(t.reshape(F // block, block * block)).max(-1)
-            else:
-                amax = np.abs(t).max(-1)
-            sc = (amax / np.float32(E4M3_MAX)).astype(np.float32)
-            sc = np.where(sc == 0, np.float32(1.0), sc).astype(np.float32)
-            sfull = np.repeat(sc, block) if blocks else sc
-            xt[:, c * block:(c + 1) * block] = e4m3_encode((t / sfull[:, None]).astype(np.float32))
-            xs[:, c] = sc
+        ne = int(cb[e + 1] - cb[e])
+        if ne == 0:
+            continue
+        rows = np.zeros((ne * block, F), np.float32)
+        rows[: int(off[e + 1] - off[e])] = x[int(off[e]):int(off[e + 1])]
+        t = rows.T.reshape(F, ne, block)  # [F, chunk, row]
+        if blocks:
+            amax = np.abs(t.reshape(F // block, block, ne, block)).max(axis=(1, 3))  # [F/128, ne]
+        else:
+            amax = np.abs(t).max(-1)  # [F, ne]
+        sc = (amax / np.float32(E4M3_MAX)).astype(np.float32)
+        sc = np.where(sc == 0, np.float32(1.0), sc).astype(np.float32)
+        sfull = np.repeat(sc, block, axis=0) if blocks else sc  # [F, ne]
+        q = e4m3_encode((t / sfull[:, :, None]).astype(np.float32))
+        xt[block * F * int(cb[e]):block * F * int(cb[e + 1])] = q.reshape(-1)
+        xs[nf * int(cb[e]):nf * int(cb[e + 1])] = sc.reshape(-1)
     return xt, xs
 
 
-def dequant_grouped_t(xt, xs, group_sizes, M: int, blocks: bool, block: int = 128):
+def dequant_grouped_t(xt, xs, group_sizes, M: int, F: int, blocks: bool, block: int = 128):
     """Inverse of ``quant_fp8_grouped_t``: the [M, F] float64 rows (zero-padding dropped)."""
-    F = xt.shape[0]
     off, cb = fp8_group_chunks(group_sizes, M, block)
-    q = e4m3_decode(xt).astype(np.float64)
+    nf = F // block if blocks else F
+    q = e4m3_decode(np.asarray(xt)).astype(np.float64)
     out = np.zeros((M, F))
     for e in range(len(group_sizes)):
-        for j, c in enumerate(range(int(cb[e]), int(cb[e + 1]))):
-            r0 = int(off[e]) + block * j
-            n = min(block, int(off[e + 1]) - r0)
-            sc = np.repeat(np.asarray(xs[:, c], np.float64), block) if blocks else np.asarray(xs[:, c], np.float64)
-            out[r0:r0 + n] = (q[:, c * block:c * block + n] * sc[:, None]).T
+        ne = int(cb[e + 1] - cb[e])
+        if ne == 0:
+            continue
+        t = q[block * F * int(cb[e]):block * F * int(cb[e + 1])].reshape(F, ne * block)
+        sc = np.asarray(xs[nf * int(cb[e]):nf * int(cb[e + 1])], np.float64).reshape(nf, ne)
+        sfull = np.repeat(np.repeat(sc, block, axis=0) if blocks else sc, block, axis=1)  # [F, ne*128]
+        n = int(off[e + 1] - off[e])
+        out[int(off[e]):int(off[e + 1])] = (t * sfull)[:, :n].T
     return out
 
 
-def tgmm_fp8(xt, xts, gt, gts, group_sizes, M: int) -> np.ndarray:
+def tgmm_fp8(xt, xts, gt, gts, group_sizes, M: int, F: int, N: int) -> np.ndarray:
     """fp8 tgmm: dequantise both transposed operands (x with per-feature chunk scales, g with
     128 x 128 block scales), then the float64 per-group x^T g (grouped_matmul.py:197-235)."""
-    return tgmm(dequant_grouped_t(xt, xts, group_sizes, M, False), dequant_grouped_t(gt, gts, group_sizes, M, True),
-                group_sizes)
+    return tgmm(dequant_grouped_t(xt, xts, group_sizes, M, F, False),
+                dequant_grouped_t(gt, gts, group_sizes, M, N, True), group_sizes)
 
 
 # ---------------------------------------------------------------------------------------------

@@ -56,9 +56,10 @@ def test_quant_grouped_t_bit_exact(dev, blocks, M, F, E):
     xt, xs = quantize_fp8_grouped_t(x, _t(gs, dev), blocks=blocks)
     oq, os_ = O.quant_fp8_grouped_t(x.float().cpu().numpy(), gs, blocks)
     _, cb = O.fp8_group_chunks(gs, M)
-    used = 128 * int(cb[-1])
-    assert np.array_equal(_u8(xt)[:, :used], oq[:, :used])
-    assert np.array_equal(xs.cpu().numpy()[:, :int(cb[-1])], os_[:, :int(cb[-1])])
+    used = int(cb[-1])
+    assert np.array_equal(_u8(xt)[:128 * F * used], oq[:128 * F * used])
+    nf = F // 128 if blocks else F
+    assert np.array_equal(xs.cpu().numpy()[:nf * used], os_[:nf * used])
 
 
 @pytest.mark.parametrize("M,Kin,Kout,E", [(2000, 256, 384, 6), (3000, 768, 2048, 16), (700, 2048, 1536, 4)])
@@ -97,7 +98,7 @@ def test_tgmm_fp8(dev, M, F, N, E):
     got = dw.float().cpu().numpy()
     for e in np.flatnonzero(gs == 0):
         assert not got[e].any()
-    ref_q = O.tgmm_fp8(_u8(xt), xs.cpu().numpy(), _u8(gt), gsc.cpu().numpy(), gs, M)
+    ref_q = O.tgmm_fp8(_u8(xt), xs.cpu().numpy(), _u8(gt), gsc.cpu().numpy(), gs, M, F, N)
     assert rel_err(got, ref_q) < 1e-2
     ref = O.tgmm(x.float().cpu().numpy(), g.float().cpu().numpy(), gs)
     assert rel_err(got, ref) < 6e-2

@@ -469,7 +469,8 @@ def test_gmm_fp8_dlhs_equals_dequantised_dlhs():
 @pytest.mark.parametrize("blocks", [False, True])
 def test_quant_grouped_t_chunks_equal_row_and_block_quantisers(blocks):
     """Each expert-aligned chunk of the transposed operand is quant_fp8_rows (1x128 along the
-    transposed row) or, with blocks, quant_fp8_weights (128x128) of that zero-padded chunk."""
+    transposed row) or, with blocks, quant_fp8_weights (128x128) of that zero-padded chunk, stored
+    in expert-major blocks."""
     rng = np.random.default_rng(5)
     gs = np.array([130, 0, 5, 256, 0, 77], np.int32)
     M, F = int(gs.sum()) + 9, 256
@@ -477,20 +478,24 @@ def test_quant_grouped_t_chunks_equal_row_and_block_quantisers(blocks):
     xt, xs = O.quant_fp8_grouped_t(x, gs, blocks)
     off, cb = O.fp8_group_chunks(gs, M)
     assert int(cb[-1]) == sum(-(-int(g) // 128) for g in gs)
+    nf = F // 128 if blocks else F
     for e in range(len(gs)):
-        for j, c in enumerate(range(int(cb[e]), int(cb[e + 1]))):
+        ne = int(cb[e + 1] - cb[e])
+        blk = xt[128 * F * int(cb[e]):128 * F * int(cb[e + 1])].reshape(F, 128 * ne)
+        sce = xs[nf * int(cb[e]):nf * int(cb[e + 1])].reshape(nf, ne)
+        for j in range(ne):
             r0 = int(off[e]) + 128 * j
             chunk = np.zeros((128, F), np.float32)
             rows = x[r0:min(r0 + 128, int(off[e + 1]))]
             chunk[: len(rows)] = rows
             if blocks:
                 q, s = O.quant_fp8_weights(chunk[None])  # [1, F, 128] codes, [1, F/128, 1] scales
-                assert np.array_equal(xt[:, 128 * c:128 * (c + 1)], q[0]) and np.array_equal(xs[:, c], s[0, :, 0])
+                assert np.array_equal(blk[:, 128 * j:128 * (j + 1)], q[0]) and np.array_equal(sce[:, j], s[0, :, 0])
             else:
                 q, s = O.quant_fp8_rows(np.ascontiguousarray(chunk.T))
-                assert np.array_equal(xt[:, 128 * c:128 * (c + 1)], q) and np.array_equal(xs[:, c], s[:, 0])
+                assert np.array_equal(blk[:, 128 * j:128 * (j + 1)], q) and np.array_equal(sce[:, j], s[:, 0])
     # round trip within the e4m3 bound, padding dropped
-    d = O.dequant_grouped_t(xt, xs, gs, M, blocks)
+    d = O.dequant_grouped_t(xt, xs, gs, M, F, blocks)
     used = int(gs.sum())
     assert rel_err(d[:used], x[:used]) < 4e-2 and not d[used:].any()
 
@@ -502,8 +507,8 @@ def test_tgmm_fp8_equals_dequantised_tgmm_and_empty_groups_are_zero():
     x, g = rng.standard_normal((M, F)).astype(np.float32), rng.standard_normal((M, N)).astype(np.float32)
     xt, xs = O.quant_fp8_grouped_t(x, gs, False)
     gt, gsc = O.quant_fp8_grouped_t(g, gs, True)
-    got = O.tgmm_fp8(xt, xs, gt, gsc, gs, M)
-    ref = O.tgmm(O.dequant_grouped_t(xt, xs, gs, M, False), O.dequant_grouped_t(gt, gsc, gs, M, True), gs)
+    got = O.tgmm_fp8(xt, xs, gt, gsc, gs, M, F, N)
+    ref = O.tgmm(O.dequant_grouped_t(xt, xs, gs, M, F, False), O.dequant_grouped_t(gt, gsc, gs, M, N, True), gs)
     assert rel_err(got, ref) < 1e-12
     assert not got[1].any()
     assert rel_err(got, O.tgmm(x, g, gs)) < 6e-2
