@@ -13,6 +13,7 @@
 // a 1x128 re-quantisation of its output fused into the epilogue.
 #include "common.h"
 #include "lds_dma.h"
+#include "fp8_tile.h"
 #include <type_traits>
 
 namespace mtx {
@@ -96,36 +97,27 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const T* __restrict__ x
   }
 }
 
-// One workgroup per 128x128 (Kin x Kout) block of one expert; writes the transposed block.
+// One workgroup per 128x128 (Kin x Kout) block of one expert: one scale for the block, codes
+// written transposed ([E, Kout, Kin], k contiguous) through LDS.
 template <typename T>
 __global__ __launch_bounds__(256) void quant_weights_kernel(const T* __restrict__ w, int64_t Kin, int64_t Kout,
                                                             uint8_t* __restrict__ wq, float* __restrict__ ws) {
-  __shared__ float tile[128][129];
-  __shared__ float wmax[4];
-  const int e = blockIdx.z;
-  const int64_t k0 = (int64_t)blockIdx.y * 128, n0 = (int64_t)blockIdx.x * 128;
-  const T* src = w + (int64_t)e * Kin * Kout;
-  float m = 0.0f;
-  for (int i = threadIdx.x; i < 128 * 128; i += 256) {
-    const int kr = i / 128, nc = i % 128;
-    float v;
-    if constexpr (sizeof(T) == 4) v = ((const float*)src)[(k0 + kr) * Kout + n0 + nc];
-    else v = bf16_to_f32(((const uint16_t*)src)[(k0 + kr) * Kout + n0 + nc]);
-    tile[kr][nc] = v;
-    m = fmaxf(m, fabsf(v));
-  }
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+  __shared__ __attribute__((aligned(16))) uint8_t tt[128 * q8::TSTRIDE];
+  __shared__ float red[4];
+  using S = q8::TileShape<T>;
+  const int64_t e = blockIdx.z, k0 = (int64_t)blockIdx.y * 128, n0 = (int64_t)blockIdx.x * 128;
+  q8::Tile<T> t;
+  t.load(w + (e * Kin + k0) * Kout + n0, Kout, 128);
+  float m[S::VE];
+  t.col_amax(m);
+  float a = 0.0f;
+#pragma unroll
+  for (int j = 0; j < S::VE; ++j) a = fmaxf(a, m[j]);
+  const float s = q8::block_scale(a, red);
+  q8::codes_to_lds_t(t, [&](int) { return s; }, tt);
   __syncthreads();
-  m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  float s = m / 448.0f;
-  if (s == 0.0f) s = 1.0f;
-  uint8_t* dst = wq + (int64_t)e * Kout * Kin;
-  for (int i = threadIdx.x; i < 128 * 128; i += 256) {
-    const int nr = i / 128, kc = i % 128;
-    dst[(n0 + nr) * Kin + k0 + kc] = f32_to_e4m3(tile[kc][nr] / s);
-  }
-  if (threadIdx.x == 0) ws[((int64_t)e * (Kout / 128) + blockIdx.x) * (Kin / 128) + blockIdx.y] = s;
+  q8::lds_t_to_global(tt, wq + (e * Kout + n0) * Kin + k0, Kin);
+  if (threadIdx.x == 0) ws[(e * (Kout / 128) + blockIdx.x) * (Kin / 128) + blockIdx.y] = s;
 }
 
 // ---- tile scheduler (same contract as the bf16 path) ---------------------------------------------
@@ -1175,6 +1167,8 @@ extern "C" int mtx_quant_fp8_weights(const void* w, int dtype, int64_t E, int64_
     return MTX_ERR_ARG;
   if (E == 0 || Kin == 0 || Kout == 0) return MTX_OK;
   if (!w || !w_q || !w_scale) return MTX_ERR_ARG;
+  if (((uintptr_t)w | (uintptr_t)w_q) % 16) return MTX_ERR_ARG;  // 16-byte loads and stores
+  if (E > 65535 || Kin / 128 > 65535) return MTX_ERR_UNSUPPORTED;
   dim3 grid((unsigned)(Kout / 128), (unsigned)(Kin / 128), (unsigned)E);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MTX_F32)

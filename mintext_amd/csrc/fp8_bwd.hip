@@ -19,6 +19,7 @@
 //       the forward kernel's tile loop with a per-expert k-range.
 #include "common.h"
 #include "lds_dma.h"
+#include "fp8_tile.h"
 
 namespace mtx {
 namespace f8b {
@@ -28,8 +29,6 @@ typedef __attribute__((ext_vector_type(8))) int i32x8;
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
 typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
 
-__device__ __forceinline__ float ld_elem(const float* p, int64_t i) { return p[i]; }
-__device__ __forceinline__ float ld_elem(const uint16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
 
 // ---- weights in their own layout ---------------------------------------------------------------
 // The 128x128 block (Kin block y, Kout block x) of expert z: the scale of quant_weights_kernel
@@ -38,22 +37,19 @@ __device__ __forceinline__ float ld_elem(const uint16_t* p, int64_t i) { return 
 template <typename T>
 __global__ __launch_bounds__(256) void quant_weights_t_kernel(const T* __restrict__ w, int64_t Kin, int64_t Kout,
                                                               uint8_t* __restrict__ wq, float* __restrict__ ws) {
-  __shared__ float wmax[4];
+  __shared__ float red[4];
+  using S = q8::TileShape<T>;
   const int64_t e = blockIdx.z, k0 = (int64_t)blockIdx.y * 128, n0 = (int64_t)blockIdx.x * 128;
-  const T* src = w + e * Kin * Kout;
-  float m = 0.0f;
-  for (int i = threadIdx.x; i < 128 * 128; i += 256) m = fmaxf(m, fabsf(ld_elem(src, (k0 + i / 128) * Kout + n0 + i % 128)));
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
-  __syncthreads();
-  m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  float s = m / 448.0f;
-  if (s == 0.0f) s = 1.0f;
-  uint8_t* dst = wq + e * Kin * Kout;
-  for (int i = threadIdx.x; i < 128 * 128; i += 256) {
-    const int64_t o = (k0 + i / 128) * Kout + n0 + i % 128;
-    dst[o] = f32_to_e4m3(ld_elem(src, o) / s);
-  }
+  const int64_t base = (e * Kin + k0) * Kout + n0;
+  q8::Tile<T> t;
+  t.load(w + base, Kout, 128);
+  float m[S::VE];
+  t.col_amax(m);
+  float a = 0.0f;
+#pragma unroll
+  for (int j = 0; j < S::VE; ++j) a = fmaxf(a, m[j]);
+  const float s = q8::block_scale(a, red);
+  q8::codes_to_global(t, s, wq + base, Kout);
   if (threadIdx.x == 0) ws[(e * (Kin / 128) + blockIdx.y) * (Kout / 128) + blockIdx.x] = s;
 }
 
@@ -128,13 +124,15 @@ __device__ __forceinline__ int chunk_expert(const int* __restrict__ cb, int E, i
 // .. +127 (rows past the expert are zero) x features fb*128 .. +127 of x [M, F] -> codes at
 // xt[128*F*cb[e] + f*128*n_e + 128j + r] (n_e = chunks of expert e).  ROW: scale per feature =
 // amax over the chunk's rows / 448 at xts[F*cb[e] + f*n_e + j]; BLOCK: one scale per 128x128 block
-// at xts[(F/128)*cb[e] + fb*n_e + j].  Codes are f32_to_e4m3(v / scale), scale 1 when the amax is 0.
+// at xts[(F/128)*cb[e] + fb*n_e + j].  Codes are e4m3 of v / scale, scale 1 when the amax is 0.
 template <typename T, bool BLOCK>
 __global__ __launch_bounds__(256) void quant_grouped_t_kernel(const T* __restrict__ x, int F, const int* __restrict__ cb,
                                                               const int* __restrict__ off, int E,
                                                               uint8_t* __restrict__ xt, float* __restrict__ xts) {
-  __shared__ float tile[128][129];
-  __shared__ float smax[2][128];
+  using S = q8::TileShape<T>;
+  __shared__ __attribute__((aligned(16))) uint8_t tt[128 * q8::TSTRIDE];
+  __shared__ float red[S::TR][128];
+  __shared__ float scs[128];
   const int c = blockIdx.x, fb = blockIdx.y, tid = threadIdx.x;
   if (c >= cb[E]) return;  // beyond the chunks of this call's groups
   const int e = chunk_expert(cb, E, c);
@@ -142,44 +140,35 @@ __global__ __launch_bounds__(256) void quant_grouped_t_kernel(const T* __restric
   const int rs = off[e] + 128 * j;
   const int nr = min(128, off[e + 1] - rs);
   const int64_t f0 = (int64_t)fb * 128;
-  uint8_t* xe = xt + (int64_t)128 * F * cb[e] + (int64_t)128 * j;  // + f * 128 * ne
-  const int64_t lde = (int64_t)128 * ne;
-  for (int i = tid; i < 128 * 128; i += 256) {
-    const int r = i / 128, f = i % 128;
-    tile[r][f] = (r < nr) ? ld_elem(x, (int64_t)(rs + r) * F + f0 + f) : 0.0f;
-  }
-  __syncthreads();
-  {
-    const int f = tid & 127, h = tid >> 7;
-    float m = 0.0f;
-    for (int r = h * 64; r < h * 64 + 64; ++r) m = fmaxf(m, fabsf(tile[r][f]));
-    smax[h][f] = m;
-  }
-  __syncthreads();
+  q8::Tile<T> t;
+  t.load(x + (int64_t)rs * F + f0, F, nr);
+  float m[S::VE];
+  t.col_amax(m);
   if (BLOCK) {
-    if (tid < 64) {
-      float m = fmaxf(fmaxf(smax[0][tid], smax[1][tid]), fmaxf(smax[0][tid + 64], smax[1][tid + 64]));
-      for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-      if (tid == 0) smax[0][0] = m;  // every lane has read its entries before this write
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < S::VE; ++i) a = fmaxf(a, m[i]);
+    const float s = q8::block_scale(a, &red[0][0]);
+    q8::codes_to_lds_t(t, [&](int) { return s; }, tt);
+    if (tid == 0) xts[(int64_t)(F / 128) * cb[e] + (int64_t)fb * ne + j] = s;
+  } else {
+#pragma unroll
+    for (int i = 0; i < S::VE; ++i) red[t.rl][t.cl * S::VE + i] = m[i];
+    __syncthreads();
+    if (tid < 128) {
+      float a = 0.0f;
+#pragma unroll
+      for (int r = 0; r < S::TR; ++r) a = fmaxf(a, red[r][tid]);
+      const float s = q8::scale_of(a);
+      scs[tid] = s;
+      xts[(int64_t)F * cb[e] + (f0 + tid) * ne + j] = s;
     }
     __syncthreads();
+    q8::codes_to_lds_t(t, [&](int i) { return scs[t.cl * S::VE + i]; }, tt);
   }
-  // 128 features x 8 runs of 16 rows: each item is one 16-byte store of codes
-  for (int it = tid; it < 128 * 8; it += 256) {
-    const int f = it >> 3, r0 = (it & 7) * 16;
-    float s = BLOCK ? smax[0][0] : fmaxf(smax[0][f], smax[1][f]);
-    s = s / 448.0f;
-    if (s == 0.0f) s = 1.0f;
-    uint32_t q[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      q[k] = (uint32_t)f32_to_e4m3(tile[r0 + 4 * k][f] / s) | ((uint32_t)f32_to_e4m3(tile[r0 + 4 * k + 1][f] / s) << 8) |
-             ((uint32_t)f32_to_e4m3(tile[r0 + 4 * k + 2][f] / s) << 16) |
-             ((uint32_t)f32_to_e4m3(tile[r0 + 4 * k + 3][f] / s) << 24);
-    *(u32x4*)(xe + (f0 + f) * lde + r0) = u32x4{q[0], q[1], q[2], q[3]};
-    if (r0 == 0 && (!BLOCK || f == 0))
-      xts[(int64_t)(BLOCK ? F / 128 : F) * cb[e] + (BLOCK ? (int64_t)fb : f0 + f) * ne + j] = s;
-  }
+  __syncthreads();
+  const int64_t lde = (int64_t)128 * ne;
+  q8::lds_t_to_global(tt, xt + (int64_t)128 * F * cb[e] + (int64_t)128 * j + f0 * lde, lde);
 }
 
 // ---- tgmm: dW[e] = XT_e GT_e^T over the expert's chunks ---------------------------------------------
@@ -373,6 +362,7 @@ extern "C" int mtx_quant_fp8_weights_t(const void* w, int dtype, int64_t E, int6
     return MTX_ERR_ARG;
   if (E == 0 || Kin == 0 || Kout == 0) return MTX_OK;
   if (!w || !w_qt || !w_scale_t) return MTX_ERR_ARG;
+  if (((uintptr_t)w | (uintptr_t)w_qt) % 16) return MTX_ERR_ARG;  // 16-byte loads, 8-byte stores
   if (E > 65535 || Kin / 128 > 65535) return MTX_ERR_UNSUPPORTED;
   dim3 grid((unsigned)(Kout / 128), (unsigned)(Kin / 128), (unsigned)E);
   hipStream_t st = (hipStream_t)stream;
@@ -413,7 +403,7 @@ extern "C" int mtx_quant_fp8_grouped_t(const void* x, int dtype, const int32_t* 
   if (dtype != MTX_F32 && dtype != MTX_BF16) return MTX_ERR_ARG;
   if (!workspace || workspace_bytes < mtx_fp8_grouped_workspace_size(E)) return MTX_ERR_WORKSPACE;
   if (!group_sizes || !xt || !xt_scale || (M > 0 && !x)) return MTX_ERR_ARG;
-  if ((uintptr_t)xt % 16) return MTX_ERR_ARG;
+  if (((uintptr_t)xt | (uintptr_t)x) % 16) return MTX_ERR_ARG;  // 16-byte loads and stores
   const int64_t C = fp8_grouped_chunks(M, E);
   if (C > 2147483647 / 128 || F / 128 > 65535) return MTX_ERR_UNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
