@@ -195,6 +195,7 @@ struct TArgs {
   const int* cb;      // [E+1]
   const int* order;   // [E]
   int E, F, N;
+  int xa, xb;         // XCD rectangles: 0 = row-major tiles, else an xa x xb grid of the tile grid
 };
 
 __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
@@ -204,13 +205,23 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
   const int wm = wave / WN, wn = wave % WN;
   const int nf = p.F / TBM, nn = p.N / TBN, per_e = nf * nn;
   const int total = p.E * per_e;
-  // consecutive workgroups (which the dispatcher places on consecutive XCDs) take consecutive tiles,
-  // so the tiles of the large experts, which come first, spread over all XCDs
+  // consecutive workgroups (which the dispatcher places on consecutive XCDs, x = lid % 8) take
+  // consecutive tiles, so the tiles of the large experts, which come first, spread over all XCDs.
+  // With xa > 0 (per_e a multiple of 8) XCD x takes the tiles of one (nf/xa) x (nn/xb) rectangle
+  // of the expert's tile grid, so that it reads few XT and GT blocks of the expert into its L2.
   const int lid = blockIdx.x;
   if (lid >= total) return;
   const int e = p.order[lid / per_e];
   const int rem = lid % per_e;
-  const int fb = rem / nn, nb = rem % nn;
+  int fb, nb;
+  if (p.xa > 0) {
+    const int x = rem & 7, q = rem >> 3, rh = nf / p.xa, rw = nn / p.xb;
+    fb = (x % p.xa) * rh + q / rw;
+    nb = (x / p.xa) * rw + q % rw;
+  } else {
+    fb = rem / nn;
+    nb = rem % nn;
+  }
   const int c0 = p.cb[e], nch = p.cb[e + 1] - c0;
   uint16_t* out = p.dw + (int64_t)e * p.F * p.N + (int64_t)fb * TBM * p.N + nb * TBN;
   if (nch <= 0) {  // empty group: dW[e] tile = 0
@@ -254,19 +265,19 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
     for (int i = 0; i < 2; ++i) gload_lds16(ge + boff[i] + kofs, st + (uint32_t)TA_BYTES + (wave_u * 2 + i) * 1024u);
     if ((kt & 1) == 0) gload_lds4(sp + (k >> 1), st + (uint32_t)TS_OFF + wave_u * 256u);
   };
-  i32x8 fa[2][TM], fbr[2][TN];
   const int frow = lane & 31, fhalf = lane >> 5;
   auto ld32 = [&](const char* base, int r) -> i32x8 {
     const u32x4 lo = *(const u32x4*)(base + t_off(r, 2 * fhalf));
     const u32x4 hi = *(const u32x4*)(base + t_off(r, 2 * fhalf + 1));
     return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
   };
-  auto read_frags = [&](int kt, int buf) {
-    const char* st = lds + (kt & (TNST - 1)) * TSTAGE;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) fa[buf][i] = ld32(st, wm * WTM + i * 32 + frow);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) fbr[buf][j] = ld32(st + TA_BYTES, wn * WTN + j * 32 + frow);
+  // rotating fragments: one A set and two B sets; A of row block i is reloaded from the next stage
+  // right after its last MFMA, the next stage's B fragments go to the other set, so that the live
+  // fragments fit beside the 128 accumulators without serialising every LDS read before its MFMA
+  i32x8 fr_a[TM], fr_b[2][TN];
+  auto rd_a = [&](int kt, int i) -> i32x8 { return ld32(lds + (kt & (TNST - 1)) * TSTAGE, wm * WTM + i * 32 + frow); };
+  auto rd_b = [&](int kt, int j) -> i32x8 {
+    return ld32(lds + (kt & (TNST - 1)) * TSTAGE + TA_BYTES, wn * WTN + j * 32 + frow);
   };
   // scales of the chunk whose even stage is kt: this lane's four XT rows and this wave's GT block
   float sa_c[TM], sa_n[TM], sb_c, sb_n;
@@ -285,66 +296,101 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
+  // One stage: MFMAs of stage kt on fr_a / fr_b[cb] with the fragments of stage kt+1 read in
+  // between; at a chunk boundary each accumulator is moved to the new chunk's units one slot ahead
+  // of its MFMA, while the previous MFMA runs.
+  auto rot_stage = [&](int kt, int cb, bool rescale, const float (&f)[TM]) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fr_b[cb ^ 1][j] = rd_b(kt + 1, j);
+    auto rescale_acc = [&](int q) {
+      const int i = q / TN, j = q % TN;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] *= f[i];
+    };
+    if (rescale) rescale_acc(0);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr_b[cb][j], fr_a[i], acc[i][j], 0, 0, 0, 127, 0,
+                                                                    127);
+        if (rescale && i * TN + j + 1 < TM * TN) rescale_acc(i * TN + j + 1);
+      }
+      fr_a[i] = rd_a(kt + 1, i);
+    }
+  };
+
   // prologue: stages 0 (+ scales), 1, 2 (+ scales); 0 and 1 landed (2's LPS + 1 loads may fly)
 #pragma unroll
   for (int s = 0; s < TPD; ++s) issue_stage(s);  // nk >= 2: stages past the end re-read the last
   __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));
   __syncthreads();
   read_scales(0, sa_c, sb_c);
-  read_frags(0, 0);
-  auto mfmas = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < TM; ++i) fr_a[i] = rd_a(0, i);
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fbr[buf][j], fa[buf][i], acc[i][j], 0, 0, 0, 127, 0,
-                                                                    127);
-  };
+  for (int j = 0; j < TN; ++j) fr_b[0][j] = rd_b(0, j);
   for (int kb = 0; kb < nch; ++kb) {
     const int kt = 2 * kb;
-    const bool more = kb + 1 < nch;
     issue_stage(kt + TPD);  // odd stage: LPS loads
-    read_frags(kt + 1, 1);
-    mfmas(0);
-    // stage kt+2 (LPS + 1 loads, issued before stage kt+3) landed; kt+3 may still be in flight
-    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS));
-    __syncthreads();
-    if (more) read_scales(kt + 2, sa_n, sb_n);  // the next chunk's scales, now visible
-    issue_stage(kt + 1 + TPD);  // even stage: LPS + 1 loads
-    read_frags(kt + 2, 0);  // the last step reads an unused ring slot (in bounds)
-    mfmas(1);
-    if (more) {
+    float f[TM];
+    if (kb > 0) {
+      // (sa_c / sa_n) * (sb_c / sb_n): no product of two small scales is formed
       const float rb = sb_c * __builtin_amdgcn_rcpf(sb_n);
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
-        const float f = (sa_c[i] * __builtin_amdgcn_rcpf(sa_n[i])) * rb;
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) acc[i][j][v] *= f;
+        f[i] = (sa_c[i] * __builtin_amdgcn_rcpf(sa_n[i])) * rb;
         sa_c[i] = sa_n[i];
       }
       sb_c = sb_n;
+      rot_stage(kt, 0, true, f);
+    } else {
+      rot_stage(kt, 0, false, f);
     }
-    // stage kt+3 (LPS loads) landed; kt+4 (LPS + 1) may still be in flight
-    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));
-    __syncthreads();
+    // stage kt+2 (LPS + 1 loads, issued before stage kt+3) landed; kt+3 may still be in flight.
+    // Bare s_barrier: this wave's outstanding LDS reads are the next stage's fragments (visible
+    // since the previous barrier) and need not complete before it; a slot is refilled only after
+    // every wave's MFMAs consumed the fragments read from it.
+    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS));
+    __builtin_amdgcn_s_barrier();
+    issue_stage(kt + 1 + TPD);  // even stage: LPS + 1 loads
+    read_scales(kt + 2, sa_n, sb_n);  // the next chunk's scales (past the last: an unused slot)
+    rot_stage(kt + 1, 1, false, f);  // its fragment reads of stage kt+2 past the end are unused
+    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));  // stage kt+3 landed; kt+4 may still be in flight
+    __builtin_amdgcn_s_barrier();
   }
-  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));  // no ring load lands after the workgroup ends
+  // every ring load (the ones past the end included) has landed before the ring is reused
+  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));
+  __syncthreads();
 
-  // epilogue: acc[i][j][4g+q] of lane l is dW[row i*32 + l%32][col j*32 + 8g + 4(l/32) + q]
-  const int ecol = wn * WTN + 4 * fhalf;
+  // epilogue: acc[i][j][4g+q] of lane l is dW[row i*32 + l%32][col j*32 + 8g + 4(l/32) + q]; staged
+  // through the ring (32 rows x 64 bf16 columns per wave at a time, 16-byte chunk c of row r at
+  // chunk c ^ (r & 7)) so that each store writes whole 128-byte row segments
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int row = wm * WTM + i * 32 + frow;
-    uint16_t* orow = out + (int64_t)row * p.N + ecol;
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *(bf16x4*)(orow + j * 32 + 8 * g) =
-            bf16x4{(__bf16)((acc[i][j][4 * g] * sa_c[i]) * sb_c), (__bf16)((acc[i][j][4 * g + 1] * sa_c[i]) * sb_c),
-                   (__bf16)((acc[i][j][4 * g + 2] * sa_c[i]) * sb_c), (__bf16)((acc[i][j][4 * g + 3] * sa_c[i]) * sb_c)};
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = (acc[i][j][v] * sa_c[i]) * sb_c;
+  char* wst = lds + wave * 4096;
+  const uint32_t lo = (uint32_t)(wm * WTM + (lane >> 3)) * (uint32_t)p.N + (uint32_t)(wn * WTN + (lane & 7) * 8);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+        *(bf16x4*)(wst + frow * 128 + (((4 * j + gq) ^ (frow & 7)) << 4) + 8 * fhalf) =
+            bf16x4{(__bf16)acc[i][j][4 * gq], (__bf16)acc[i][j][4 * gq + 1], (__bf16)acc[i][j][4 * gq + 2],
+                   (__bf16)acc[i][j][4 * gq + 3]};
+    __builtin_amdgcn_s_waitcnt(MTX_LGKMCNT0);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int rloc = rr * 8 + (lane >> 3);
+      const u32x4 v = *(const u32x4*)(wst + rloc * 128 + (((lane & 7) ^ (rloc & 7)) << 4));
+      *(u32x4*)(out + lo + (uint32_t)(i * 32 + rr * 8) * (uint32_t)p.N) = v;
+    }
+    __builtin_amdgcn_s_waitcnt(MTX_LGKMCNT0);  // reads done before the next block overwrites
   }
 }
 
@@ -449,6 +495,20 @@ extern "C" int mtx_tgmm_fp8(const uint8_t* xt, const float* xt_scale, const uint
   a.E = (int)E;
   a.F = (int)F;
   a.N = (int)N;
+  // XCD rectangles of the tile grid: xa x xb = 8 with xa | nf, xb | nn, fewest blocks per XCD
+  const int nf = (int)(F / 256), nn = (int)(N / 256);
+  a.xa = a.xb = 0;
+  int best = 1 << 30;
+  for (int xa = 1; xa <= 8; xa *= 2) {
+    const int xb = 8 / xa;
+    if (nf % xa || nn % xb) continue;
+    const int blocks = nf / xa + nn / xb;
+    if (blocks < best) {
+      best = blocks;
+      a.xa = xa;
+      a.xb = xb;
+    }
+  }
   const int64_t grid = round_up(E * (F / 256) * (N / 256), 8);
   hipLaunchKernelGGL(f8b::tgmm_fp8_kernel, dim3((unsigned)grid), dim3(512), 0, st, a);
   return check_launch();
