@@ -529,28 +529,51 @@ def fp8_vendor_study(steps=10, warmup=3):
 
 
 def copy_study(steps=20, warmup=3):
-    """The practical HBM ceiling for read+write streams on this box: a device-to-device copy
-    (torch copy_) of 64 MiB to 1 GiB, bytes read + bytes written per second.  Sizes up to about
-    128 MiB partly stay in the 256 MB MALL between repetitions; the larger ones are HBM.  The
-    dispatch and combine kernels move comparable volumes (C2: 201.5 / 268.6 MB)."""
+    """The practical HBM ceiling for read+write streams on this box: device-to-device copies of
+    64 MiB to 1 GiB (bytes read + bytes written per second) by torch's copy_ and by the library's
+    streaming copy (mtx_stream_copy: 16-byte loads and stores, 2-16 loads in flight per lane,
+    plain or non-temporal, a grid-stride loop over 2-8 workgroups per CU), every variant timed
+    and the best one reported per size.  Sizes up to about 128 MiB partly stay in the 256 MB MALL
+    between repetitions; the larger ones are HBM.  The dispatch and combine kernels move
+    comparable volumes (C2: 201.5 / 268.6 MB)."""
     import torch
 
-    out = {"study": "copy", "unit": "GB/s (read + write)", "sizes_MiB": {}}
-    for mib in (64, 128, 256, 512, 1024):
-        src = torch.empty(mib << 20, dtype=torch.uint8, device="cuda")
-        src.fill_(1)
-        dst = torch.empty_like(src)
+    from mintext_amd import _lib as L
+
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    variants = [(nt, u, k) for nt in (0, 1) for u in (4, 8, 16) for k in (2, 4, 8)]
+    out = {"study": "copy", "unit": "GB/s (read + write)", "cus": ncu, "sizes_MiB": {}}
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn):
         for _ in range(warmup):
-            dst.copy_(src)
+            fn()
         torch.cuda.synchronize()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
         for _ in range(steps):
-            dst.copy_(src)
+            fn()
         e.record()
         torch.cuda.synchronize()
-        t = s.elapsed_time(e) / steps * 1e-3
-        out["sizes_MiB"][mib] = {"us": round(t * 1e6, 1), "GBs": round(2 * (mib << 20) / t / 1e9, 1)}
+        return s.elapsed_time(e) / steps * 1e-3
+
+    for mib in (64, 128, 256, 512, 1024):
+        nbytes = mib << 20
+        src = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        src.fill_(1)
+        dst = torch.empty_like(src)
+        stream = L.stream(src.device)
+        row = {"torch_copy_GBs": round(2 * nbytes / timed(lambda: dst.copy_(src)) / 1e9, 1)}
+        best = None
+        for nt, u, k in variants:
+            var = nt | (u << 4 if u < 16 else 15 << 4)
+            t = timed(lambda: L.call("mtx_stream_copy", L.ptr(src), L.ptr(dst), nbytes, var, k * ncu, stream))
+            gbs = 2 * nbytes / t / 1e9
+            if best is None or gbs > best[0]:
+                best = (gbs, {"nontemporal": bool(nt), "loads_in_flight": u, "wg_per_cu": k})
+        assert torch.equal(dst, src), "streaming copy mismatch"
+        row["stream_copy_GBs"] = round(best[0], 1)
+        row["stream_copy_best"] = best[1]
+        out["sizes_MiB"][mib] = row
         del src, dst
     print(json.dumps(out))
     return 0

@@ -345,6 +345,15 @@ int mtx_transpose_batched(const void* in, int dtype, int64_t B, int64_t R, int64
                           int64_t in_batch_stride, int64_t in_ld, void* out,
                           int64_t out_batch_stride, int64_t out_ld, void* stream);
 
+/* ---- measurement ------------------------------------------------------------------------
+ * No counterpart in the reference: the read+write streaming kernel that measures this device's
+ * practical HBM ceiling for the dispatch and combine kernels (bench.py --study copy).
+ * dst[i] = src[i] for nbytes bytes (nbytes % 16 == 0, both pointers 16-byte aligned, no
+ * overlap).  variant: bit 0 = non-temporal loads and stores, bits 4..7 = 16-byte loads in
+ * flight per lane (rounded up to 2, 4, 8 or 16; 0 = 8); grid = workgroups of 256 threads
+ * (0 = 4 per CU).                                                                            */
+int mtx_stream_copy(const void* src, void* dst, int64_t nbytes, int variant, int64_t grid, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

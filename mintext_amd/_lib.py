@@ -77,6 +77,7 @@ SIGNATURES = {
     "mtx_quant_fp8_grouped_t": (_I, [_P, _I, _P, _I64, _I64, _I64, _I, _P, _P, _P, _I64, _P]),
     "mtx_tgmm_fp8": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "mtx_transpose_batched": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P]),
+    "mtx_stream_copy": (_I, [_P, _P, _I64, _I, _I64, _P]),
 }
 
 

@@ -3,16 +3,18 @@
 // route (bzantium/mintext mintext/kernels/moe_dispatch.py:47-81) is a stable argsort of
 // ravel(topk_indices) by expert id, a row gather x[p // K] in that order and a bincount.
 // Here the argsort is a stable counting sort, with no comparison sort and no atomics in
-// the ranking:
+// the ranking, in two launches:
 //   1. route_count   : one workgroup per chunk of the flat index array builds an LDS
-//                      histogram over E+1 buckets (bucket E = ids outside [0,E)).
-//   2. route_scan    : one workgroup turns the [chunk][bucket] counts into exclusive
-//                      offsets (bucket-major, then chunk) and writes group_sizes.
-//   3. route_scatter : each chunk ranks its elements in flat order; within a wave the
-//                      rank is a ballot "multisplit" (log2(E+1) ballots build the mask of
-//                      lanes with an equal key, rank = popcount of the lower lanes), across
-//                      waves per-wave counts in LDS, across sub-tiles a running LDS base.
-//   4. gather_rows   : one wave per output row, 16-byte vector copies.
+//                      histogram over E+1 buckets (bucket E = ids outside [0,E)), stored
+//                      bucket-major [bucket][chunk].
+//   2. route_scatter : each chunk first derives its own offsets from the whole count table
+//                      (bucket b's offset = all ids of buckets < b + ids of bucket b in
+//                      earlier chunks: row sums, a scan over the buckets, a partial row
+//                      sum), then ranks its elements in flat order; within a wave the rank
+//                      is a ballot "multisplit" (log2(E+1) ballots build the mask of lanes
+//                      with an equal key, rank = popcount of the lower lanes), across waves
+//                      per-wave counts in LDS, across sub-tiles a running LDS base.
+//   3. gather_rows   : one wave per output row, 16-byte vector copies.
 // unroute (moe_dispatch.py:84-111) inverts the permutation (scatter of j to perm[j]) and
 // combines out[n] = sum_k w[n,k] * Y[inv[n*K+k]] in f32 with k ascending, one wave per token.
 #include <type_traits>
@@ -29,20 +31,26 @@ struct RoutePlan {
   int64_t M;
   int nb;      // number of buckets = E + 1
   int nchunks;
+  int cstride;  // count-table row length: nchunks rounded up to 4 (the pad columns hold 0)
   int64_t chunk;
   int64_t ws_counts;  // bytes
 };
 
+// About 1024 ids per chunk, at most 256 chunks, and at most 16384 entries in the count table,
+// which every scatter workgroup reads whole.
 static RoutePlan route_plan(int64_t N, int64_t K, int64_t E) {
   RoutePlan p;
   p.M = N * K;
   p.nb = (int)E + 1;
   int64_t nch = ceil_div(p.M, 1024);
-  if (nch < 1) nch = 1;
+  const int64_t cap = 16384 / p.nb;
+  if (nch > cap) nch = cap;
   if (nch > 256) nch = 256;
-  p.nchunks = (int)nch;
+  if (nch < 1) nch = 1;
   p.chunk = round_up(ceil_div(p.M > 0 ? p.M : 1, nch), kRouteThreads);
-  p.ws_counts = round_up((int64_t)p.nchunks * p.nb * 4, 256);
+  p.nchunks = (int)ceil_div(p.M > 0 ? p.M : 1, p.chunk);
+  p.cstride = (int)round_up(p.nchunks, 4);
+  p.ws_counts = round_up((int64_t)p.cstride * p.nb * 4, 256);
   return p;
 }
 
@@ -51,19 +59,33 @@ __device__ __forceinline__ int route_key(const int32_t* idx, int64_t p, int E) {
   return (v < 0 || v >= E) ? E : v;
 }
 
+// counts[b * cstride + c] = ids of chunk c in bucket b; workgroup 0 also zeroes the pad columns.
 __global__ __launch_bounds__(kRouteThreads) void route_count_kernel(
-    const int32_t* __restrict__ idx, int64_t M, int E, int nb, int64_t chunk,
+    const int32_t* __restrict__ idx, int64_t M, int E, int nb, int64_t chunk, int nchunks, int cstride,
     int32_t* __restrict__ counts) {
   extern __shared__ int hist[];
   for (int b = threadIdx.x; b < nb; b += blockDim.x) hist[b] = 0;
   __syncthreads();
   const int64_t start = (int64_t)blockIdx.x * chunk;
   const int64_t end = min(start + chunk, M);
-  for (int64_t p = start + threadIdx.x; p < end; p += blockDim.x)
-    atomicAdd(&hist[route_key(idx, p, E)], 1);
+  constexpr int U = 8;  // ids loaded per lane before their atomics
+  for (int64_t p0 = start + threadIdx.x; p0 < end; p0 += (int64_t)U * kRouteThreads) {
+    int k[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t p = p0 + (int64_t)u * kRouteThreads;
+      k[u] = p < end ? route_key(idx, p, E) : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (k[u] >= 0) atomicAdd(&hist[k[u]], 1);
+  }
   __syncthreads();
   for (int b = threadIdx.x; b < nb; b += blockDim.x)
-    counts[(int64_t)blockIdx.x * nb + b] = hist[b];
+    counts[(int64_t)b * cstride + blockIdx.x] = hist[b];
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i < nb * (cstride - nchunks); i += blockDim.x)
+      counts[(int64_t)(i / (cstride - nchunks)) * cstride + nchunks + i % (cstride - nchunks)] = 0;
 }
 
 // Few experts and few ids: the whole stable counting sort in one workgroup of 1024 threads
@@ -153,106 +175,114 @@ __global__ __launch_bounds__(1024) void route_small_kernel(const int32_t* __rest
   }
 }
 
-// Single workgroup of 1024 threads; nb <= 1024.  counts[c][b] (per-chunk bucket counts) become
-// the exclusive offsets of chunk c's keys b in the stable order.  Thread (g, b) owns bucket b
-// for chunk group g (G = 1024 / nb groups of consecutive chunks), so the serial part is one
-// group's chunks.
-// With STAGE the [nchunks][nb] counts are first copied to LDS (coalesced), scanned there and
-// written back coalesced, so the serial per-thread walks run at LDS rather than memory latency.
-template <bool STAGE>
-__global__ __launch_bounds__(1024) void route_scan_kernel(
-    int32_t* __restrict__ counts_g, int nchunks, int nb, int E, int32_t* __restrict__ group_sizes) {
-  __shared__ int part[1024];  // [g][b] group sums, then group bases
-  __shared__ int wsum[16];
-  __shared__ int bucket_base[1024];
-  extern __shared__ int staged[];  // [nchunks][nb] when STAGE
-  const int tid = threadIdx.x;
-  const int ncnt = nchunks * nb;
-  int* counts = counts_g;
-  if constexpr (STAGE) {
-    constexpr int U = 8;  // loads in flight per thread before the LDS stores
-    for (int i0 = tid; i0 < ncnt; i0 += 1024 * U) {
-      int v[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) v[u] = counts_g[min(i0 + u * 1024, ncnt - 1)];  // branch-free, in bounds
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (i0 + u * 1024 < ncnt) staged[i0 + u * 1024] = v[u];
-    }
-    __syncthreads();
-    counts = staged;
-  }
-  const int G = max(1, min(1024 / nb, nchunks));
-  const int cpg = (nchunks + G - 1) / G;
-  const int g = tid / nb, b = tid - g * nb;
-  const bool act = g < G;
-  const int c0 = g * cpg, c1 = min(c0 + cpg, nchunks);
-  int sum = 0;
-  if (act)
-    for (int c = c0; c < c1; ++c) sum += counts[(int64_t)c * nb + b];
-  if (act) part[g * nb + b] = sum;
-  __syncthreads();
-  // per bucket: exclusive scan over groups, and the bucket total
-  int total = 0;
-  if (tid < nb) {
-    for (int q = 0; q < G; ++q) {
-      const int x = part[q * nb + tid];
-      part[q * nb + tid] = total;
-      total += x;
-    }
-  }
-  // exclusive scan of bucket totals over b (wave scan + scan of wave totals)
-  const int lane = tid & 63, w = tid >> 6;
-  const int v = (tid < nb) ? total : 0;
-  int incl = v;
-  for (int off = 1; off < 64; off <<= 1) {
-    const int o = __shfl_up(incl, off);
-    if (lane >= off) incl += o;
-  }
-  if (lane == 63) wsum[w] = incl;
-  __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int i = 0; i < 16; ++i) { const int x = wsum[i]; wsum[i] = run; run += x; }
-  }
-  __syncthreads();
-  if (tid < nb) {
-    bucket_base[tid] = incl - v + wsum[w];
-    if (tid < E) group_sizes[tid] = total;
-  }
-  __syncthreads();
-  if (act) {
-    int base = bucket_base[b] + part[g * nb + b];
-    for (int c = c0; c < c1; ++c) {
-      const int64_t o = (int64_t)c * nb + b;
-      const int x = counts[o];
-      counts[o] = base;
-      base += x;
-    }
-  }
-  if constexpr (STAGE) {
-    __syncthreads();
-    for (int i = tid; i < ncnt; i += 1024) counts_g[i] = staged[i];
-  }
-}
-
+// Chunk c's offsets from the bucket-major count table (every workgroup reads the whole table,
+// at most 16384 entries, as 16-byte units): row sums R[b] and the sums P[b] over the chunks
+// before c, an exclusive scan of R over the buckets (thread t scans rows 4t..4t+3), run[b] =
+// scan[b] + P[b]; workgroup 0 writes group_sizes = R.  Then the elements are ranked in flat
+// order and scattered.
 __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
-    const int32_t* __restrict__ idx, int64_t M, int E, int nb, int nbits, int64_t chunk,
-    const int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ inv) {
+    const int32_t* __restrict__ idx, int64_t M, int E, int nb, int nbits, int64_t chunk, int cstride,
+    const int32_t* __restrict__ counts, int32_t* __restrict__ perm, int32_t* __restrict__ inv,
+    int32_t* __restrict__ group_sizes) {
   extern __shared__ int sh[];
-  int* run = sh;            // [nb]
-  int* wcnt = sh + nb;      // [4][nb]
+  const int nu = nb * (cstride >> 2);  // 16-byte units of the count table (<= 4096)
+  int* run = sh;               // [nb]
+  int* wcnt = sh + nb;         // [4][nb]
+  int* rsum = sh + 5 * nb;     // [nb]
+  int* ur = sh + 6 * nb;       // [nu] unit sums
+  int* up = sh + 6 * nb + nu;  // [nu] unit sums over the chunks before this one
+  __shared__ int wtot[4];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  for (int b = tid; b < nb; b += blockDim.x) run[b] = offsets[(int64_t)blockIdx.x * nb + b];
-  const int64_t start = (int64_t)blockIdx.x * chunk;
+  const int c = blockIdx.x;
+  // row sums and partial row sums: unit sums first (eight loads in flight per lane), then one
+  // thread per row adds its units
+  {
+    const u32x4* tab = (const u32x4*)counts;
+    const int upr = cstride >> 2;
+    constexpr int U = 8;
+    for (int i0 = tid; i0 < nu; i0 += kRouteThreads * U) {
+      u32x4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = tab[min(i0 + u * kRouteThreads, nu - 1)];  // in bounds
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + u * kRouteThreads;
+        if (i < nu) {
+          const int c0 = 4 * (i % upr);
+          int r = 0, pre = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            r += (int)v[u][k];
+            pre += (c0 + k < c) ? (int)v[u][k] : 0;
+          }
+          ur[i] = r;
+          up[i] = pre;
+        }
+      }
+    }
+    __syncthreads();
+    for (int b = tid; b < nb; b += kRouteThreads) {
+      int r = 0, pre = 0;
+      for (int q = 0; q < upr; ++q) {
+        r += ur[b * upr + q];
+        pre += up[b * upr + q];
+      }
+      rsum[b] = r;
+      run[b] = pre;
+    }
+  }
+  __syncthreads();
+  // exclusive scan of rsum over the buckets (nb <= 1024: four rows per thread)
+  int loc[4], tsum = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int b = 4 * tid + k;
+    loc[k] = (b < nb) ? rsum[b] : 0;
+    tsum += loc[k];
+  }
+  int incl = tsum;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o);
+    if (lane >= o) incl += v;
+  }
+  if (lane == 63) wtot[w] = incl;
+  __syncthreads();
+  int base = incl - tsum;
+  for (int ww = 0; ww < w; ++ww) base += wtot[ww];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int b = 4 * tid + k;
+    if (b < nb) {
+      run[b] += base;
+      if (c == 0 && b < E) group_sizes[b] = loc[k];
+    }
+    base += loc[k];
+  }
+  // Ranking in flat order, 256 ids per step: within a wave a ballot multisplit, across the four
+  // waves per-wave counts in LDS, across steps the running bases run[]; the ids of U steps are
+  // loaded before their ranking.
+  const int64_t start = (int64_t)c * chunk;
   const int64_t end = min(start + chunk, M);
   const unsigned long long lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
-  for (int64_t base = start; base < end; base += kRouteThreads) {
+  constexpr int U = 8;
+  int kreg[U];
+  for (int64_t sb = start; sb < end; sb += kRouteThreads) {
+    const int u = (int)(((sb - start) / kRouteThreads) % U);
+    if (u == 0) {
+#pragma unroll
+      for (int v = 0; v < U; ++v) {
+        const int64_t p = sb + (int64_t)v * kRouteThreads + tid;
+        kreg[v] = p < end ? route_key(idx, p, E) : 0;
+      }
+    }
     for (int b = tid; b < 4 * nb; b += blockDim.x) wcnt[b] = 0;
     __syncthreads();
-    const int64_t p = base + tid;
+    const int64_t p = sb + tid;
     const bool valid = p < end;
-    const int key = valid ? route_key(idx, p, E) : 0;
+    int key = 0;
+#pragma unroll
+    for (int v = 0; v < U; ++v)
+      if (v == u) key = kreg[v];
     unsigned long long m = __ballot(valid);
     for (int bit = 0; bit < nbits; ++bit) {
       const bool on = (key >> bit) & 1;
@@ -769,24 +799,64 @@ extern "C" const char* mtx_status_string(int s) {
 extern "C" int mtx_last_hip_error(void) { return g_last_hip_error; }
 extern "C" int mtx_version(void) { return 1; }
 
+// ---- streaming copy (HBM ceiling measurement) --------------------------------------------------
+// Grid-stride over blocks of 256 x U 16-byte units: each lane issues its U loads, then its U
+// stores; NT: non-temporal loads and stores (streamed past the caches).
+template <int U, bool NT>
+__global__ __launch_bounds__(256) void stream_copy_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                          int64_t n) {
+  const int64_t step = (int64_t)gridDim.x * 256 * U;
+  for (int64_t b = (int64_t)blockIdx.x * 256 * U + threadIdx.x; b < n; b += step) {
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = min(b + (int64_t)u * 256, n - 1);  // in bounds; the store below is guarded
+      v[u] = NT ? __builtin_nontemporal_load(src + i) : src[i];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = b + (int64_t)u * 256;
+      if (i < n) {
+        if (NT) __builtin_nontemporal_store(v[u], dst + i);
+        else dst[i] = v[u];
+      }
+    }
+  }
+}
+
+extern "C" int mtx_stream_copy(const void* src, void* dst, int64_t nbytes, int variant, int64_t grid, void* stream) {
+  if (nbytes < 0 || nbytes % 16 || grid < 0 || grid > 65535 * 16) return MTX_ERR_ARG;
+  if (nbytes == 0) return MTX_OK;
+  if (!src || !dst || ((uintptr_t)src | (uintptr_t)dst) % 16) return MTX_ERR_ARG;
+  int u = (variant >> 4) & 15;
+  if (u == 0) u = 8;
+  const bool nt = variant & 1;
+  if (grid == 0) {
+    const int ncu = device_cu_count();
+    grid = 4 * (ncu > 0 ? ncu : 256);
+  }
+  const int64_t n = nbytes / 16;
+  hipStream_t st = (hipStream_t)stream;
+  const u32x4* s = (const u32x4*)src;
+  u32x4* d = (u32x4*)dst;
+#define MTX_SC(U)                                                                                          \
+  do {                                                                                                     \
+    if (nt) hipLaunchKernelGGL((stream_copy_kernel<U, true>), dim3((unsigned)grid), dim3(256), 0, st, s, d, n); \
+    else hipLaunchKernelGGL((stream_copy_kernel<U, false>), dim3((unsigned)grid), dim3(256), 0, st, s, d, n); \
+  } while (0)
+  if (u <= 2) MTX_SC(2);
+  else if (u <= 4) MTX_SC(4);
+  else if (u <= 8) MTX_SC(8);
+  else MTX_SC(16);
+#undef MTX_SC
+  return check_launch();
+}
+
 // Workspace: per-chunk bucket counts, then room for the inverse permutation (used when the
 // caller passes inverse == NULL, since the row dispatch runs in token order).
 extern "C" int64_t mtx_route_workspace_size(int64_t N, int64_t K, int64_t E) {
   if (N < 0 || K < 1 || E < 1) return -1;
   return route_plan(N, K, E).ws_counts + round_up(N * K * 4, 256);
-}
-
-// LDS bytes a workgroup may use on the current device (static + dynamic), cached per device.
-static size_t max_lds_per_block() {
-  static size_t cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cache[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || n <= 0) return 0;
-    cache[dev] = (size_t)n;
-  }
-  return cache[dev];
 }
 
 // Stable counting sort of topk_idx: sort_indices, group_sizes and the inverse permutation.
@@ -808,20 +878,13 @@ static int route_permutation(const RoutePlan& p, const int32_t* topk_idx, int64_
   }
   const size_t hist_shm = (size_t)p.nb * sizeof(int);
   hipLaunchKernelGGL(route_count_kernel, dim3(p.nchunks), dim3(kRouteThreads), hist_shm, st,
-                     topk_idx, p.M, (int)E, p.nb, p.chunk, counts);
-  const size_t stage_bytes = (size_t)p.nchunks * p.nb * sizeof(int);
-  if (stage_bytes + 9 * 1024 <= max_lds_per_block())
-    hipLaunchKernelGGL(route_scan_kernel<true>, dim3(1), dim3(1024), stage_bytes, st, counts, p.nchunks, p.nb,
-                       (int)E, group_sizes);
-  else
-    hipLaunchKernelGGL(route_scan_kernel<false>, dim3(1), dim3(1024), 0, st, counts, p.nchunks, p.nb, (int)E,
-                       group_sizes);
+                     topk_idx, p.M, (int)E, p.nb, p.chunk, p.nchunks, p.cstride, counts);
   int nbits = 0;
   while ((1 << nbits) < p.nb) ++nbits;
-  const size_t sc_shm = (size_t)5 * p.nb * sizeof(int);
-  if (p.M > 0)
-    hipLaunchKernelGGL(route_scatter_kernel, dim3(p.nchunks), dim3(kRouteThreads), sc_shm, st, topk_idx,
-                       p.M, (int)E, p.nb, nbits, p.chunk, counts, sort_indices, inverse);
+  const size_t sc_shm = ((size_t)6 * p.nb + 2 * (size_t)p.nb * (p.cstride / 4)) * sizeof(int);
+  // M == 0: one chunk with no ids still writes the zero group sizes
+  hipLaunchKernelGGL(route_scatter_kernel, dim3(p.nchunks), dim3(kRouteThreads), sc_shm, st, topk_idx,
+                     p.M, (int)E, p.nb, nbits, p.chunk, p.cstride, counts, sort_indices, inverse, group_sizes);
   return check_launch();
 }
 

@@ -74,6 +74,39 @@ def test_route_few_experts_bit_exact(dev, N, K, E):
     assert torch.equal(st, x[torch.from_numpy(perm // K).to(dev)])
 
 
+@pytest.mark.parametrize("N,K,E", [(70000, 2, 1023), (5000, 8, 600), (300000, 1, 64), (1, 1, 1023), (777, 5, 200),
+                                   (0, 8, 128)])
+def test_route_chunked_bit_exact(dev, N, K, E):
+    """The two-launch counting sort with its count-table cap (at most 16384 entries: 16 chunks at
+    E = 1023, chunks of many ids), ragged chunk counts (the table's zero pad columns), one id, no
+    ids (group sizes still written as zeros), about 1% out-of-range ids (sorted last)."""
+    from mintext_amd.kernels.moe_dispatch import _route_impl
+
+    rng = np.random.default_rng(N * 3 + E)
+    idx = rng.integers(0, E, (N, K)).astype(np.int32)
+    bad = rng.random((N, K)) < 0.01
+    idx[bad] = rng.choice(np.array([-1, E, E + 9], np.int32), bad.sum())
+    x = torch.randn(N, 64, device=dev, dtype=torch.bfloat16)
+    st, si, gs, inv = _route_impl(x, _t(idx, dev), E)
+    key = np.where((idx >= 0) & (idx < E), idx, E).ravel()
+    perm = np.argsort(key, kind="stable")
+    np.testing.assert_array_equal(si.cpu().numpy(), perm)
+    np.testing.assert_array_equal(inv.cpu().numpy(), np.argsort(perm))
+    np.testing.assert_array_equal(gs.cpu().numpy(), np.bincount(key, minlength=E + 1)[:E])
+    assert torch.equal(st, x[torch.from_numpy(perm // K).to(dev)])
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096 * 16 + 48, 37 << 20])
+@pytest.mark.parametrize("variant", [0x00, 0x41, 0x81, 0xF0, 0x21])
+def test_stream_copy(dev, nbytes, variant):
+    from mintext_amd import _lib as L
+
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=dev)
+    dst = torch.zeros_like(src)
+    L.call("mtx_stream_copy", L.ptr(src), L.ptr(dst), nbytes, variant, 0 if variant & 0x40 else 7, L.stream(dev))
+    assert torch.equal(dst, src)
+
+
 def test_route_out_of_range_ids_sorted_last(dev):
     from mintext_amd.kernels import route
 
