@@ -442,6 +442,9 @@ struct Args {
   const int32_t* gather = nullptr;
   int gather_div = 1;
   int gather_rows = 0;
+  // TGMM (256-row tiles): xa > 0 gives XCD x = rem % 8 the tiles of one (nrt/xa) x (ntiles/xb)
+  // rectangle of each expert's tile grid (few x and g blocks per XCD L2); 0: row-major tiles
+  int xa = 0, xb = 0;
 };
 
 // ---- tile loaders ------------------------------------------------------------------------------
@@ -768,8 +771,14 @@ __global__ __launch_bounds__(WM* WN * 64, MTX_V3_WPE) void gmm_v3_kernel(Args p)
     if (lid >= p.E * per_e) return;
     e = p.order[lid / per_e];
     const int rem = lid % per_e;
-    row0 = (rem / ntiles) * BM;
-    n_tile = rem % ntiles;
+    if (p.xa > 0) {  // consecutive workgroups land on consecutive XCDs: x = rem % 8 (per_e % 8 == 0)
+      const int x = rem & 7, qq = rem >> 3, rh = (p.Kd / BM) / p.xa, rw = ntiles / p.xb;
+      row0 = ((x % p.xa) * rh + qq / rw) * BM;
+      n_tile = (x / p.xa) * rw + qq % rw;
+    } else {
+      row0 = (rem / ntiles) * BM;
+      n_tile = rem % ntiles;
+    }
     col0 = n_tile * BN;
     r0 = p.offsets[e];
     r1 = p.offsets[e + 1];
@@ -1521,8 +1530,20 @@ extern "C" int mtx_tgmm(const void* x, const void* g, const int32_t* group_sizes
     a.I = 0;
     a.E = (int)E;
     a.gm = 8;
-    if (K % 256 == 0 && N % 256 == 0 && M * K * 2 < (int64_t(1) << 32) && M * N * 2 < (int64_t(1) << 32))
+    if (K % 256 == 0 && N % 256 == 0 && M * K * 2 < (int64_t(1) << 32) && M * N * 2 < (int64_t(1) << 32)) {
+      // XCD rectangles of each expert's tile grid: xa x xb = 8, xa | K/256, xb | N/256, fewest
+      // blocks per XCD
+      const int nr = (int)(K / 256), nc = (int)(N / 256);
+      int best = 1 << 30;
+      for (int xa = 1; xa <= 8; xa *= 2) {
+        const int xb = 8 / xa;
+        if (nr % xa || nc % xb || nr / xa + nc / xb >= best) continue;
+        best = nr / xa + nc / xb;
+        a.xa = xa;
+        a.xb = xb;
+      }
       return launch_v3<mf::TGMM, mf::EPI_STORE>(a, E * (K / 256) * (N / 256), st);
+    }
     if (K % 256 == 0 && N % 256 == 0) {
       const int64_t grid = round_up(E * (K / 256) * (N / 256), 8);
       return launch_mfma<256, 256, 2, 2, mf::TGMM, mf::EPI_STORE>(a, grid, st);
