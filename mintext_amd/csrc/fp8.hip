@@ -595,9 +595,10 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v3_kernel(Args p) {
 
   // weight-scale half of accumulator column block j
   auto half_of = [&](int j) -> int { return (EPI == EPI_SWIGLU_Q) ? j : (wn >> 1); };
-  auto scale_of = [&](int i, int j, int kb) -> float {
-    return s_sa[kb * BM + wm * WTM + i * 32 + frow] * s_sb[half_of(j) * MAX_KB + kb];
-  };
+  // the two factors of an accumulator's scale in block kb (never multiplied together, so that two
+  // small scales cannot underflow)
+  auto sa_of = [&](int i, int kb) -> float { return s_sa[kb * BM + wm * WTM + i * 32 + frow]; };
+  auto sb_of = [&](int j, int kb) -> float { return s_sb[half_of(j) * MAX_KB + kb]; };
 
   // 32-row blocks of this wave that hold rows of the group
   const int nbi = min(max((r1 - r0 - wm * WTM + 31) / 32, 0), TM);
@@ -640,7 +641,9 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v3_kernel(Args p) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int j = 0; j < TN; ++j) f[i][j] = scale_of(i, j, kb) * __builtin_amdgcn_rcpf(scale_of(i, j, kb + 1));
+          for (int j = 0; j < TN; ++j)
+            f[i][j] = (sa_of(i, kb) * __builtin_amdgcn_rcpf(sa_of(i, kb + 1))) *
+                      (sb_of(j, kb) * __builtin_amdgcn_rcpf(sb_of(j, kb + 1)));
       }
       issue_stage(kt + PD);
       read_frags(kt + 1, 1, nb);
@@ -671,9 +674,9 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v3_kernel(Args p) {
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const float f = scale_of(i, j, nkb - 1);
+      const float fa = sa_of(i, nkb - 1), fb_ = sb_of(j, nkb - 1);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] *= f;
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = (acc[i][j][v] * fa) * fb_;
     }
   const int erow = wm * WTM + frow;
   if (EPI == EPI_STORE) {
@@ -948,7 +951,8 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int h = 0; h < NSB; ++h) f[i][h] = (sa_c[i] * sb_c[h]) * __builtin_amdgcn_rcpf(sa_n[i] * sb_n[h]);
+          for (int h = 0; h < NSB; ++h)  // (sa_c / sa_n) * (sb_c / sb_n): no product of two small scales
+            f[i][h] = (sa_c[i] * __builtin_amdgcn_rcpf(sa_n[i])) * (sb_c[h] * __builtin_amdgcn_rcpf(sb_n[h]));
 #pragma unroll
         for (int i = 0; i < TM; ++i) sa_c[i] = sa_n[i];
 #pragma unroll
@@ -977,9 +981,10 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        const float f = sa_c[i] * sb_c[half_of(j)];
+        const float fa = sa_c[i], fb_ = sb_c[half_of(j)];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][j][v] = cur.zero ? 0.0f : acc[i][j][v] * f;  // (not 0 * x: x may be NaN)
+        for (int v = 0; v < 16; ++v)
+          acc[i][j][v] = cur.zero ? 0.0f : (acc[i][j][v] * fa) * fb_;  // (not 0 * x: x may be NaN)
       }
     // Outputs are staged through ring slot g-1 (the tile's last stage, consumed; the next DMA
     // into it is issued after the closing barrier) so that every global store writes 16

@@ -101,6 +101,38 @@ def test_gmm_fp8(dev, M, E, Kin, Kout):
     assert (out[tot:] == 0).all()
 
 
+@pytest.mark.parametrize("swiglu", [False, True])
+def test_gmm_fp8_tiny_block_scales(dev, swiglu):
+    """Every other row scaled by 1e-33 (1x128 scales near 2e-36, block-to-block ratios of order 1):
+    the product of such a scale and a weight-block scale (~2e-4) is below the f32 normal range, so
+    the kernels never form it (block-to-block factor (sa_c/sa_n)*(sb_c/sb_n), final scale applied
+    factor by factor).  The outputs stay finite and match the dequantised oracle."""
+    from mintext_amd.kernels.fp8 import (grouped_matmul_fp8, grouped_matmul_fp8_swiglu, quantize_fp8_rows,
+                                         quantize_fp8_weights)
+
+    rng = np.random.default_rng(11)
+    M, E, Kin, Kout = 1024, 4, 512, 512
+    gs = _groups(rng, M, E)
+    blk = np.ones((M, Kin // 128))
+    blk[::2] = 1e-33
+    x = (torch.randn(M, Kin, device=dev) * torch.from_numpy(blk).float().to(dev).repeat_interleave(128, 1)).bfloat16()
+    w = (torch.randn(E, Kin, Kout, device=dev) * 0.02).bfloat16()
+    xq, xs = quantize_fp8_rows(x)
+    assert float(xs.min()) < 1e-35  # the tiny blocks really have tiny scales
+    wq, ws = quantize_fp8_weights(w)
+    tg = _t(gs, dev)
+    deq = O.gmm_fp8(_u8(xq), xs.cpu().numpy(), _u8(wq), ws.cpu().numpy(), gs)
+    if swiglu:
+        yq, ys, yb = grouped_matmul_fp8_swiglu(xq, xs, wq, ws, tg, return_bf16=True)
+        tot = int(gs.sum())
+        got = yb.float().cpu().numpy()[:tot]
+        ref = O.swiglu(deq)[:tot]
+        assert np.isfinite(got).all() and np.isfinite(ys.cpu().numpy()).all() and rel_err(got, ref) < 1e-2
+    else:
+        out = grouped_matmul_fp8(xq, xs, wq, ws, tg).float().cpu().numpy()
+        assert np.isfinite(out).all() and rel_err(out, deq) < 1e-2
+
+
 @pytest.mark.parametrize("M,E,Kin,I", [(1024, 4, 256, 256), (900, 8, 512, 384), (2048, 8, 2048, 768),
                                        (12000, 8, 1024, 768)])
 def test_gmm_fp8_swiglu_requant(dev, M, E, Kin, I):
