@@ -787,7 +787,15 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
     const int first_m = grp * GM;
     const int gsz = min(GM, cnt - first_m);
     const int local = l - grp * GM * nn;
-    const MTileF8 t = p.tiles[first_m + local % gsz];
+    // the tile list is read-only here: read through the scalar cache (constant address space,
+    // uniform index), so that the tile switch waits on lgkmcnt, not on the ring's vmcnt
+    typedef const __attribute__((address_space(4))) int cint_t;
+    const int ti = __builtin_amdgcn_readfirstlane(first_m + local % gsz);
+    const cint_t* tp = (const cint_t*)(uintptr_t)(p.tiles + ti);
+    MTileF8 t;
+    t.e = tp[0];
+    t.r0 = tp[1];
+    t.r1 = tp[2];
     Tile T;
     T.zero = t.e < 0;
     T.e = t.e < 0 ? 0 : t.e;  // rows past sum(group_sizes): computed with expert 0, stored as 0
