@@ -770,6 +770,7 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
   __shared__ float red[BM * 4];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
   const int wm = wave / WN, wn = wave % WN;
   const int nn = (EPI == EPI_SWIGLU_Q) ? (p.I / 128) : (p.N / BN);
   const int cnt = p.count[0];
@@ -815,7 +816,8 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
   struct Src {
     uint32_t aoff[2], boff[2];
     const uint8_t* B;
-    const float* sp;  // this lane's scale source for k-block 0 (stride 1 float per block)
+    const float* sb;  // this wave's scale base (uniform) ...
+    uint32_t so;      // ... + this lane's byte offset: its scale for k-block 0 (one float per block after it)
   };
   // row of xq / xs that holds sorted row r (the row itself unless the rows are gathered)
   auto x_row = [&](int r) -> int {
@@ -831,14 +833,17 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
       S.boff[i] = (uint32_t)b_row(T, r) * (uint32_t)p.K + (uint32_t)(c * 16);
     }
     S.B = p.wq + (int64_t)T.e * p.N * p.K;
-    if (wave < 4) {
-      S.sp = p.xs + (int64_t)x_row(min(T.r0 + 64 * wave + lane, T.r1 - 1)) * nkb;
-    } else if (wave == 4) {
+    if (wave_u < 4) {
+      S.sb = p.xs;
+      S.so = (uint32_t)x_row(min(T.r0 + 64 * wave + lane, T.r1 - 1)) * (uint32_t)nkb * 4u;
+    } else if (wave_u == 4) {
       const int h = lane & 1;
       const int nblk = (EPI == EPI_SWIGLU_Q) ? (h * (p.I / 128) + T.n_tile) : (T.n_tile * 2 + h);
-      S.sp = p.ws + ((int64_t)T.e * (p.N / 128) + nblk) * nkb;
+      S.sb = p.ws + (int64_t)T.e * (p.N / 128) * nkb;
+      S.so = (uint32_t)nblk * (uint32_t)nkb * 4u;
     } else {
-      S.sp = p.xs + (int64_t)x_row(T.r0) * nkb;  // filler load, keeps the per-wave load count uniform
+      S.sb = p.xs;  // filler load, keeps the per-wave load count uniform
+      S.so = (uint32_t)x_row(T.r0) * (uint32_t)nkb * 4u;
     }
     return S;
   };
@@ -849,21 +854,21 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
   Src scur = make_src(cur), snxt = make_src(nxt);
 
   const uint32_t lds_base = lds_addr(lds);
-  const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
   // issue ring step g = stage kt of the current tile, or of the next one when kt >= nk
+  // (uniform bases in SGPRs, per-lane 32-bit offsets)
   auto issue = [&](int g, int kt, bool even) {
     const bool in = kt < nk;
     const int k = in ? kt : kt - nk;
     const uint32_t st = lds_base + (uint32_t)((g & (NSTAGE - 1)) * STAGE);
     const uint32_t kofs = (uint32_t)k * BKB;
+    const uint8_t* A = p.xq + kofs;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) gload_lds16_s(A, in ? scur.aoff[i] : snxt.aoff[i], st + (wave_u * 2 + i) * 1024u);
+    const uint8_t* B = (in ? scur.B : snxt.B) + kofs;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-      gload_lds16(p.xq + (in ? scur.aoff[i] : snxt.aoff[i]) + kofs, st + (wave_u * 2 + i) * 1024u);
-    const uint8_t* B = in ? scur.B : snxt.B;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      gload_lds16(B + (in ? scur.boff[i] : snxt.boff[i]) + kofs, st + (uint32_t)A_BYTES + (wave_u * 2 + i) * 1024u);
-    if (even) gload_lds4((in ? scur.sp : snxt.sp) + (k >> 1), st + (uint32_t)S_OFF + wave_u * 256u);
+      gload_lds16_s(B, in ? scur.boff[i] : snxt.boff[i], st + (uint32_t)A_BYTES + (wave_u * 2 + i) * 1024u);
+    if (even) gload_lds4_s((in ? scur.sb : snxt.sb) + (k >> 1), in ? scur.so : snxt.so, st + (uint32_t)S_OFF + wave_u * 256u);
   };
 
   const int frow = lane & 31, fhalf = lane >> 5;

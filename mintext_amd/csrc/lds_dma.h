@@ -21,6 +21,17 @@ __device__ __forceinline__ void gload_lds4(const void* gptr, uint32_t lds_base) 
                : "memory", "m0");
 }
 
+// The same two loads with a uniform 64-bit base in SGPRs and a per-lane 32-bit byte offset, so
+// that advancing the base (a k step, another tile) costs scalar instead of per-lane 64-bit adds.
+__device__ __forceinline__ void gload_lds16_s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void gload_lds4_s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base)
+               : "memory", "m0");
+}
+
 // LDS byte address of a __shared__ array (for M0).
 template <typename T>
 __device__ __forceinline__ uint32_t lds_addr(T* p) {
