@@ -1002,6 +1002,11 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
     // Outputs are staged through ring slot g-1 (the tile's last stage, consumed; the next DMA
     // into it is issued after the closing barrier) so that every global store writes 16
     // contiguous bytes per lane and whole 128-byte lines per group of 8 lanes (32 KB used).
+    // The bare barriers of the k-loop do not order LDS reads (the compiler may place a stage's
+    // last fragment reads and their waits after them), so every wave's reads complete before
+    // the staging writes: an LDS-only release fence, then a barrier.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
     char* stg = lds + ((g - 1) & (NSTAGE - 1)) * STAGE;
     const int erow = wm * WTM + frow;
     if (EPI == EPI_STORE) {
