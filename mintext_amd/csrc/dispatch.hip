@@ -674,17 +674,21 @@ __global__ __launch_bounds__(256) void unroute_kernel(
   }
 }
 
-// Row-wise combine for bf16 expert outputs: one wave per token; the K rows of the token are
-// requested whole (S consecutive 1 KB slices of a row back to back, kept packed in registers),
-// so each gathered row reaches HBM as one contiguous burst rather than as slices a latency
-// apart.  Then the slices are summed in k order with the same fmaf chain as unroute_kernel.
-template <typename WT, typename OT, int KMAX, int S>
+// Row-wise combine for bf16 expert outputs: SPLIT waves per token, each owning a contiguous
+// 1/SPLIT of the row (more waves in flight than one per token: C2 combine 52 -> 49 us with 4,
+// C4 114 -> 110 us with 2); the K row pieces of the token are requested whole (S consecutive
+// 1 KB slices back to back, kept packed in registers), so each gathered piece reaches HBM as one
+// contiguous burst rather than as slices a latency apart.  Then the slices are summed in k
+// order with the same fmaf chain as unroute_kernel.  Needs D % (8 * SPLIT) == 0.
+template <typename WT, typename OT, int KMAX, int S, int SPLIT>
 __global__ __launch_bounds__(256) void unroute_rows_kernel(
     const uint16_t* __restrict__ Y, const int32_t* __restrict__ inv, const WT* __restrict__ w,
     int64_t N, int K, int64_t D, OT* __restrict__ out, Addend add) {
   const int lane = threadIdx.x & 63;
-  const int64_t n = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t gw = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t n = gw / SPLIT;
   if (n >= N) return;
+  const int64_t dbeg = (gw % SPLIT) * (D / SPLIT), dend = dbeg + D / SPLIT;
   const int64_t M = N * (int64_t)K;
   int64_t jj[KMAX];
   float ww[KMAX];
@@ -698,18 +702,18 @@ __global__ __launch_bounds__(256) void unroute_rows_kernel(
       ww[k] = w ? ldf<WT>(w, n * K + k) : 1.0f;
     }
   }
-  for (int64_t d0 = (int64_t)lane * 8; d0 < D; d0 += 512 * S) {
+  for (int64_t d0 = dbeg + (int64_t)lane * 8; d0 < dend; d0 += 512 * S) {
     u32x4 q[KMAX][S];
 #pragma unroll
     for (int k = 0; k < KMAX; ++k)
 #pragma unroll
       for (int s = 0; s < S; ++s)
-        if (jj[k] >= 0 && d0 + 512 * s < D)  // read once: non-temporal (C4 combine 136 -> 113 us)
+        if (jj[k] >= 0 && d0 + 512 * s < dend)  // read once: non-temporal (C4 combine 136 -> 113 us)
           q[k][s] = __builtin_nontemporal_load((const u32x4*)(Y + jj[k] * D + d0 + 512 * s));
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       const int64_t d = d0 + 512 * s;
-      if (d >= D) break;
+      if (d >= dend) break;
       float acc[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
@@ -738,13 +742,17 @@ static void launch_unroute_t(const void* Y, const int32_t* inv, const void* w, i
   hipLaunchKernelGGL((unroute_kernel<YT, WT, OT, V, KM>), dim3(blocks), dim3(256), 0, st, (const YT*)Y, inv, \
                      (const WT*)w, N, K, D, (OT*)out, add)
   if (std::is_same<YT, uint16_t>::value && v8 && K <= 8) {
-    const int64_t blocks_ = ceil_div(N, 4);
-#define MTX_UNROUTE_ROWS_L(KM, SS)                                                                           \
-  hipLaunchKernelGGL((unroute_rows_kernel<WT, OT, KM, SS>), dim3(blocks_), dim3(256), 0, st, (const uint16_t*)Y, \
-                     inv, (const WT*)w, N, K, D, (OT*)out, add)
-    if (K <= 2) MTX_UNROUTE_ROWS_L(2, 4);  // 2 x 4 KB per step: C2 combine 56 -> 52 us (S = 8: 2 x 8 KB; S = 1: 67 us)
-    else if (K <= 4) MTX_UNROUTE_ROWS_L(4, 8);
-    else MTX_UNROUTE_ROWS_L(8, 4);
+#define MTX_UNROUTE_ROWS_L(KM, SS, SP)                                                                        \
+  hipLaunchKernelGGL((unroute_rows_kernel<WT, OT, KM, SS, SP>), dim3(ceil_div(N * SP, 4)), dim3(256), 0, st,   \
+                     (const uint16_t*)Y, inv, (const WT*)w, N, K, D, (OT*)out, add)
+    // per token: K <= 2, four waves of 2 x 2 KB steps (one wave of 2 x 4 KB: 52 us on C2, of 2 x 8 KB
+    // or 2 x 1 KB slower still; eight waves of 1 KB: 51 us); K <= 8, two waves of 8 x 2 KB
+    // (one wave of 8 x 4 KB: C4 114 us, C3 120 us; four waves: 122-126 us)
+    if (K <= 2 && D % 32 == 0) MTX_UNROUTE_ROWS_L(2, 2, 4);
+    else if (K <= 2) MTX_UNROUTE_ROWS_L(2, 4, 1);
+    else if (K <= 4) MTX_UNROUTE_ROWS_L(4, 8, 1);
+    else if (D % 16 == 0) MTX_UNROUTE_ROWS_L(8, 2, 2);
+    else MTX_UNROUTE_ROWS_L(8, 4, 1);
 #undef MTX_UNROUTE_ROWS_L
   } else if (v8 && K <= 2) MTX_UNROUTE(true, 2);
   else if (v8 && K <= 4) MTX_UNROUTE(true, 4);
