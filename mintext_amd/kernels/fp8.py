@@ -190,3 +190,52 @@ def tgmm_fp8(xt, xt_scale, gt, gt_scale, group_sizes, M: int, F: int | None = No
     L.call("mtx_tgmm_fp8", L.ptr(xt.contiguous()), L.ptr(xt_scale.contiguous()), L.ptr(gt.contiguous()),
            L.ptr(gt_scale.contiguous()), L.ptr(gs), M, F, N, E, L.ptr(dw), L.ptr(ws), ws.numel(), L.stream(dev))
     return dw
+
+
+# ---- differentiable form: fp8 operands in the forward and in both backward GEMMs -------------------
+
+class _GMMFP8(torch.autograd.Function):
+    """Forward: 1x128 row groups of x and 128x128 blocks of W, fp8 grouped GEMM.  Backward: the fp8
+    dlhs (1x128 groups of the gradient rows against W's blocks in its own layout) and the fp8 tgmm
+    (x and the gradient quantised in 128-row chunks of each expert).  The quantisations follow
+    the forward's conventions (scale = amax / 448, e4m3fn codes), and the backward treats each
+    quantise/dequantise pair as the identity (straight-through), as fp8 training recipes do; the
+    reference's only fp8 product (the per-tensor matmul of mintext/modules/linear.py:37-57) has no
+    grouped form to pin this against."""
+
+    @staticmethod
+    def forward(ctx, x, weights, group_sizes):
+        gs = _gs(group_sizes)
+        xq, xs = quantize_fp8_rows(x)
+        wq, wsc = quantize_fp8_weights(weights)
+        out = grouped_matmul_fp8(xq, xs, wq, wsc, gs)
+        ctx.save_for_backward(x, weights, gs)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        x, w, gs = ctx.saved_tensors
+        grad = grad.contiguous()
+        dx = dw = None
+        if ctx.needs_input_grad[0]:
+            gq, g_s = quantize_fp8_rows(grad)
+            wqt, wst = quantize_fp8_weights_t(w)
+            dx = grouped_matmul_fp8_dlhs(gq, g_s, wqt, wst, gs).to(x.dtype)
+        if ctx.needs_input_grad[1]:
+            M = x.shape[0]
+            xt, xts = quantize_fp8_grouped_t(x, gs)
+            gt, gts = quantize_fp8_grouped_t(grad, gs, blocks=True)
+            dw = tgmm_fp8(xt, xts, gt, gts, gs, M, x.shape[1], grad.shape[1]).to(w.dtype)
+        return dx, dw, None
+
+
+def grouped_matmul_fp8_vjp(x: torch.Tensor, weights: torch.Tensor, group_sizes: torch.Tensor) -> torch.Tensor:
+    """Blockwise-fp8 counterpart of ``grouped_matmul_vjp`` (grouped_matmul.py:83-190): x [M, Kin]
+    and weights [E, Kin, Kout] (bf16 / f32 master values, the reference layout) are quantised on
+    each call; the output is bf16 [M, Kout] and differentiable in (x, weights), both backward GEMMs
+    on fp8 operands.  Kin and Kout must be multiples of 256 (the tgmm tiles)."""
+    if x.dim() != 2 or weights.dim() != 3 or weights.shape[1] != x.shape[1]:
+        raise ValueError(f"grouped_matmul_fp8_vjp: x {tuple(x.shape)} and weights {tuple(weights.shape)} do not match")
+    if x.shape[1] % 256 or weights.shape[2] % 256:
+        raise ValueError("grouped_matmul_fp8_vjp needs Kin and Kout multiples of 256")
+    return _GMMFP8.apply(x, weights, group_sizes)

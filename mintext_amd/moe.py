@@ -205,8 +205,8 @@ def moe_experts_forward_fp8(x: torch.Tensor, topk_indices: torch.Tensor, topk_we
     """Blockwise-fp8 expert layer; weights from ``quantize_fp8_weights`` ([E, Kout, Kin] e4m3).
     Forward only: raises under autograd when an input requires grad."""
     if torch.is_grad_enabled() and any(t.requires_grad for t in (x, topk_weights, gate_up_q, down_q)):
-        raise RuntimeError("moe_experts_forward_fp8 is forward-only; run it under torch.no_grad() or train "
-                           "through moe_experts_forward")
+        raise RuntimeError("moe_experts_forward_fp8 is forward-only; run it under torch.no_grad(), or train "
+                           "through moe_experts_forward or moe_experts_forward_fp8_train")
     from .kernels.fp8 import (grouped_matmul_fp8, grouped_matmul_fp8_swiglu, grouped_matmul_fp8_swiglu_gathered,
                               quantize_fp8_rows)
 
@@ -223,6 +223,24 @@ def moe_experts_forward_fp8(x: torch.Tensor, topk_indices: torch.Tensor, topk_we
         sq, ss, sort_indices, group_sizes, _ = route_quantize_fp8(x, topk_indices, E)
         yq, ys = grouped_matmul_fp8_swiglu(sq, ss, gate_up_q, gate_up_scale, group_sizes)
     out = grouped_matmul_fp8(yq, ys, down_q, down_scale, group_sizes)
+    return unroute(out, sort_indices, topk_weights, topk_indices.shape[1])
+
+
+def moe_experts_forward_fp8_train(x: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
+                                  gate_up: torch.Tensor, down: torch.Tensor) -> torch.Tensor:
+    """Differentiable blockwise-fp8 expert layer: the composition of ``moe_experts_forward``
+    (route, gate_up GEMM, SwiGLU, down GEMM, combine; moe.py:161-221) with both grouped GEMMs as
+    ``grouped_matmul_fp8_vjp``, so that all six GEMMs of a training step (the two forward
+    products, the two dlhs and the two tgmm) run on fp8 operands.  gate_up [E, D, 2I] and down
+    [E, I, D] are the master weights (reference layout), quantised on each call; x [N, D] bf16.
+    Gradients reach x, topk_weights, gate_up and down."""
+    from .kernels.fp8 import grouped_matmul_fp8_vjp
+
+    E = gate_up.shape[0]
+    sorted_tokens, sort_indices, group_sizes = route(x, topk_indices, E)
+    h = grouped_matmul_fp8_vjp(sorted_tokens, gate_up, group_sizes)
+    inter = swiglu_autograd(h)
+    out = grouped_matmul_fp8_vjp(inter, down, group_sizes)
     return unroute(out, sort_indices, topk_weights, topk_indices.shape[1])
 
 

@@ -150,3 +150,65 @@ def test_fp8_backward_c5_full_size(dev):
         ref_d = h(st[r0:r1][:, torch.from_numpy(kd).to(dev)]).T @ h(gh[r0:r1][:, torch.from_numpy(nd).to(dev)])
         got_d = h(d[int(e)][torch.from_numpy(kd).to(dev)][:, torch.from_numpy(nd).to(dev)])
         assert rel_err(got_d, ref_d) < 6e-2, f"tgmm gate_up, expert {e}"
+
+
+def test_gmm_fp8_vjp_matches_kernels_and_oracle(dev):
+    """grouped_matmul_fp8_vjp: the forward and both gradients are bit for bit the fp8 kernels on the
+    quantised operands (rows / 128x128 blocks / 128-row chunks), and within 6e-2 of the float64
+    product and VJP of the unquantised operands; an empty group gets a zero weight gradient."""
+    from mintext_amd.kernels.fp8 import (grouped_matmul_fp8, grouped_matmul_fp8_dlhs, grouped_matmul_fp8_vjp,
+                                         quantize_fp8_grouped_t, quantize_fp8_rows, quantize_fp8_weights,
+                                         quantize_fp8_weights_t, tgmm_fp8)
+
+    rng = np.random.default_rng(5)
+    M, Kin, Kout, E = 3000, 512, 768, 12
+    gs = _zipf_groups(rng, M, E)
+    tg = _t(gs, dev)
+    x = torch.randn(M, Kin, device=dev).bfloat16().requires_grad_(True)
+    w = (torch.randn(E, Kin, Kout, device=dev) * 0.02).bfloat16().requires_grad_(True)
+    G = torch.randn(M, Kout, device=dev).bfloat16()
+    out = grouped_matmul_fp8_vjp(x, w, tg)
+    out.backward(G)
+    assert out.dtype == torch.bfloat16 and x.grad.dtype == torch.bfloat16 and w.grad.dtype == torch.bfloat16
+    with torch.no_grad():
+        ref_out = grouped_matmul_fp8(*quantize_fp8_rows(x), *quantize_fp8_weights(w), tg)
+        ref_dx = grouped_matmul_fp8_dlhs(*quantize_fp8_rows(G), *quantize_fp8_weights_t(w), tg)
+        ref_dw = tgmm_fp8(*quantize_fp8_grouped_t(x, tg), *quantize_fp8_grouped_t(G, tg, blocks=True), tg, M)
+    assert torch.equal(out, ref_out) and torch.equal(x.grad, ref_dx) and torch.equal(w.grad, ref_dw)
+    f = lambda t: t.detach().float().cpu().numpy()
+    assert rel_err(f(out), O.gmm(f(x), f(w), gs)) < 6e-2
+    assert rel_err(f(x.grad), O.gmm_dlhs(f(G), f(w), gs)) < 6e-2
+    assert rel_err(f(w.grad), O.tgmm(f(x), f(G), gs)) < 6e-2
+    for e in np.flatnonzero(gs == 0):
+        assert not w.grad[e].any()
+
+
+@pytest.mark.parametrize("T,D,E,K,I", [(1024, 512, 16, 4, 256), (2048, 256, 8, 2, 512)])
+def test_fp8_layer_training_matches_oracle_vjp(dev, T, D, E, K, I):
+    """moe_experts_forward_fp8_train (all six GEMMs on fp8 operands) against the float64 forward
+    and VJP of the unquantised layer.  Each fp8 GEMM is within 6e-2 of its unquantised product
+    (test above); the layer and its gradients pass through two of them in series (the output:
+    x, then the SwiGLU output quantised; dx: the down and gate_up dlhs), so the bound is 1e-1, as
+    for the fp8 inference layer (test_gpu_moe.py)."""
+    from mintext_amd.kernels import route_topk
+    from mintext_amd.moe import moe_experts_forward_fp8_train
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(T + E)
+    x = torch.randn(T, D, device=dev, generator=gen).bfloat16().requires_grad_(True)
+    gu = (torch.randn(E, D, 2 * I, device=dev, generator=gen) * 0.05).bfloat16().requires_grad_(True)
+    dn = (torch.randn(E, I, D, device=dev, generator=gen) * 0.05).bfloat16().requires_grad_(True)
+    idx, w = route_topk(torch.randn(T, E, device=dev, generator=gen), K)
+    w = w.clone().requires_grad_(True)
+    G = torch.randn(T, D, device=dev, generator=gen)
+    out = moe_experts_forward_fp8_train(x, idx, w, gu, dn)
+    assert out.dtype == torch.float32
+    (out * G).sum().backward()
+    f = lambda a: a.detach().float().cpu().numpy()
+    ref = O.moe_experts(f(x), idx.cpu().numpy(), f(w), f(gu), f(dn))
+    errs = {"out": rel_err(f(out), ref)}
+    dx, dw, dgu, ddn = O.moe_experts_vjp(f(x), idx.cpu().numpy(), f(w), f(gu), f(dn), f(G))
+    for got, r, name in ((x.grad, dx, "x"), (w.grad, dw, "w"), (gu.grad, dgu, "gate_up"), (dn.grad, ddn, "down")):
+        errs[name] = rel_err(f(got), r)
+    print("fp8 training layer rel errors", {k: round(v, 4) for k, v in errs.items()})
+    assert all(v < 1e-1 for v in errs.values()), errs
