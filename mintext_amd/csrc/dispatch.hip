@@ -732,6 +732,9 @@ __global__ __launch_bounds__(256) void unroute_rows_kernel(
   }
 }
 
+#ifndef MTX_K8_WPB
+#define MTX_K8_WPB 4
+#endif
 template <typename YT, typename WT, typename OT>
 static void launch_unroute_t(const void* Y, const int32_t* inv, const void* w, int64_t N, int K,
                              int64_t D, void* out, Addend add, hipStream_t st) {
@@ -742,17 +745,18 @@ static void launch_unroute_t(const void* Y, const int32_t* inv, const void* w, i
   hipLaunchKernelGGL((unroute_kernel<YT, WT, OT, V, KM>), dim3(blocks), dim3(256), 0, st, (const YT*)Y, inv, \
                      (const WT*)w, N, K, D, (OT*)out, add)
   if (std::is_same<YT, uint16_t>::value && v8 && K <= 8) {
-#define MTX_UNROUTE_ROWS_L(KM, SS, SP)                                                                        \
-  hipLaunchKernelGGL((unroute_rows_kernel<WT, OT, KM, SS, SP>), dim3(ceil_div(N * SP, 4)), dim3(256), 0, st,   \
-                     (const uint16_t*)Y, inv, (const WT*)w, N, K, D, (OT*)out, add)
-    // per token: K <= 2, four waves of 2 x 2 KB steps (one wave of 2 x 4 KB: 52 us on C2, of 2 x 8 KB
-    // or 2 x 1 KB slower still; eight waves of 1 KB: 51 us); K <= 8, two waves of 8 x 2 KB
-    // (one wave of 8 x 4 KB: C4 114 us, C3 120 us; four waves: 122-126 us)
-    if (K <= 2 && D % 32 == 0) MTX_UNROUTE_ROWS_L(2, 2, 4);
-    else if (K <= 2) MTX_UNROUTE_ROWS_L(2, 4, 1);
-    else if (K <= 4) MTX_UNROUTE_ROWS_L(4, 8, 1);
-    else if (D % 16 == 0) MTX_UNROUTE_ROWS_L(8, 2, 2);
-    else MTX_UNROUTE_ROWS_L(8, 4, 1);
+#define MTX_UNROUTE_ROWS_L(KM, SS, SP, WPB)                                                                   \
+  hipLaunchKernelGGL((unroute_rows_kernel<WT, OT, KM, SS, SP>), dim3(ceil_div(N * SP, WPB)), dim3(64 * WPB), 0, \
+                     st, (const uint16_t*)Y, inv, (const WT*)w, N, K, D, (OT*)out, add)
+    // per token: K <= 2, four waves of 2 x 2 KB steps, one wave per workgroup (one wave of
+    // 2 x 4 KB: 52 us on C2, of 2 x 8 KB or 2 x 1 KB slower still; eight waves of 1 KB: 51 us;
+    // four waves per workgroup: 2 % slower); K <= 8, two waves of 8 x 2 KB (one wave of 8 x 4 KB:
+    // C4 114 us, C3 120 us; four waves: 122-126 us)
+    if (K <= 2 && D % 32 == 0) MTX_UNROUTE_ROWS_L(2, 2, 4, 1);
+    else if (K <= 2) MTX_UNROUTE_ROWS_L(2, 4, 1, 4);
+    else if (K <= 4) MTX_UNROUTE_ROWS_L(4, 8, 1, 4);
+    else if (D % 16 == 0) MTX_UNROUTE_ROWS_L(8, 2, 2, MTX_K8_WPB);
+    else MTX_UNROUTE_ROWS_L(8, 4, 1, 4);
 #undef MTX_UNROUTE_ROWS_L
   } else if (v8 && K <= 2) MTX_UNROUTE(true, 2);
   else if (v8 && K <= 4) MTX_UNROUTE(true, 4);
