@@ -626,6 +626,81 @@ def gate_study(steps=20, warmup=5):
     return 0
 
 
+KERNEL_STUDY_CONFIGS = {  # benchmarks/benchmark_moe_kernels.py:21-28 (the reference's own kernel benchmark)
+    "tiny": {"E": 4, "D": 64, "I": 128, "K": 2, "tokens": 128},
+    "small": {"E": 4, "D": 128, "I": 256, "K": 2, "tokens": 256},
+    "medium": {"E": 8, "D": 256, "I": 512, "K": 2, "tokens": 1024},
+    "dsv3_small": {"E": 64, "D": 512, "I": 1024, "K": 8, "tokens": 2048},
+    "dsv3": {"E": 256, "D": 7168, "I": 2048, "K": 8, "tokens": 4096},
+    "llama_moe": {"E": 8, "D": 4096, "I": 14336, "K": 2, "tokens": 4096},
+}
+
+
+def kernels_study(steps=20, warmup=5, configs=None):
+    """The reference's kernel benchmark (benchmarks/benchmark_moe_kernels.py) on this build: the
+    gate_up grouped GEMM [M=tokens*K, D] x [E, D, N=2I] with N(0,1) bf16 operands and uniform groups
+    (:31-39), forward, backward (d/dx and d/dw of out.sum(), :68-96) and forward + backward (:99-125),
+    for grouped_matmul / grouped_matmul_vjp and, where D and N allow, the blockwise-fp8 VJP.  Times
+    are HIP-event means over ``steps`` calls; TFLOP/s counts the GEMMs actually run (forward 2MDN,
+    backward 4MDN: dlhs + tgmm, forward + backward 6MDN), not the reference's 3x / 4x approximations."""
+    import torch
+    from mintext_amd.kernels import grouped_matmul, grouped_matmul_vjp
+    from mintext_amd.kernels.fp8 import grouped_matmul_fp8_vjp
+
+    dev = torch.device("cuda:0")
+
+    def t_ms(fn):
+        for _ in range(warmup):
+            fn()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            fn()
+        b.record()
+        b.synchronize()
+        return a.elapsed_time(b) / steps
+
+    out = {"study": "kernels", "reference": "benchmarks/benchmark_moe_kernels.py", "steps": steps, "rows": []}
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    for name in configs or list(KERNEL_STUDY_CONFIGS):
+        c = KERNEL_STUDY_CONFIGS[name]
+        E, D, N, M = c["E"], c["D"], 2 * c["I"], c["tokens"] * c["K"]
+        x = torch.randn(M, D, device=dev, generator=g).bfloat16()
+        w = torch.randn(E, D, N, device=dev, generator=g).bfloat16()
+        gs = torch.tensor([M // E + (1 if i < M % E else 0) for i in range(E)], dtype=torch.int32, device=dev)
+        fl = 2.0 * M * D * N
+        backends = {"grouped_matmul": grouped_matmul, "grouped_matmul_vjp": grouped_matmul_vjp}
+        if D % 256 == 0 and N % 256 == 0:
+            backends["fp8_vjp"] = grouped_matmul_fp8_vjp
+        row = {"config": name, "M": M, "D": D, "N": N, "E": E}
+        for bname, fn in backends.items():
+            xr = x.clone().requires_grad_(True)
+            wr = w.clone().requires_grad_(True)
+
+            def fwd():
+                with torch.no_grad():
+                    fn(x, w, gs)
+
+            def bwd():
+                o = fn(xr, wr, gs)
+                dx, dw = torch.autograd.grad(o.sum(), (xr, wr))
+                return dx, dw
+
+            f_ms = t_ms(fwd)
+            fb_ms = t_ms(bwd)
+            # backward alone: the forward of the same call subtracted
+            row[bname] = {"forward_ms": round(f_ms, 4), "forward_TFLOPs": round(fl / f_ms / 1e9, 1),
+                          "backward_ms": round(fb_ms - f_ms, 4),
+                          "backward_TFLOPs": round(2 * fl / max(fb_ms - f_ms, 1e-6) / 1e9, 1),
+                          "fwd_bwd_ms": round(fb_ms, 4), "fwd_bwd_TFLOPs": round(3 * fl / fb_ms / 1e9, 1)}
+        out["rows"].append(row)
+        del x, w
+    print(json.dumps(out))
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -642,11 +717,15 @@ def main(argv=None):
                          "rows inside the gate_up GEMM")
     ap.add_argument("--graph", action="store_true",
                     help="also time the step captured in a HIP graph and replayed (reported as hip_graph)")
-    ap.add_argument("--study", choices=["gemm-power", "fp8-vendor", "gate", "copy"], default=None,
+    ap.add_argument("--study", choices=["gemm-power", "fp8-vendor", "gate", "copy", "kernels"], default=None,
                     help="gemm-power: GEMM timings on normal vs all-zero data (clock / issue-efficiency study); "
                          "fp8-vendor: C4 blockwise fp8 GEMMs beside hipBLASLt's per-tensor / rowwise fp8 GEMMs; "
                          "gate: router gate GEMM + top-k, hipBLASLt + route_topk vs the fused kernel; "
-                         "copy: device-to-device copy bandwidth (the practical read+write HBM ceiling)")
+                         "copy: device-to-device copy bandwidth (the practical read+write HBM ceiling); "
+                         "kernels: the reference's benchmarks/benchmark_moe_kernels.py (gate_up grouped GEMM "
+                         "forward / backward / fwd+bwd per config)")
+    ap.add_argument("--configs", nargs="+", default=None, choices=sorted(KERNEL_STUDY_CONFIGS),
+                    help="--study kernels: configs to run (default: all)")
     a = ap.parse_args(argv)
     if a.study == "gemm-power":
         return gemm_power_study(a.steps if a.steps != 20 else 10, a.warmup)
@@ -656,6 +735,8 @@ def main(argv=None):
         return gate_study(a.steps, a.warmup)
     if a.study == "copy":
         return copy_study(a.steps, a.warmup)
+    if a.study == "kernels":
+        return kernels_study(a.steps, a.warmup, a.configs)
     if a.copy_calibration:
         import torch
 
