@@ -82,7 +82,7 @@ static inline GmmWs gmm_ws(void* ws, int64_t M, int64_t E) {
 __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __restrict__ gs, int E, int M, int BM,
                                                            int* __restrict__ count, int* __restrict__ offsets,
                                                            int* __restrict__ order, MTile* __restrict__ tiles,
-                                                           int need_order, int* __restrict__ split_cnt) {
+                                                           int need_order, int* __restrict__ split_cnt, int spread) {
   __shared__ int wsum[16];
   __shared__ long long wsum64[16];
   if (split_cnt && threadIdx.x < kSplitXcd * kSplitMaxRem) split_cnt[threadIdx.x] = 0;
@@ -135,16 +135,54 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
     s_r0[e] = r0;
     s_r1[e] = r1;
   }
+  // Spread order (spread > 0, for schedules of one m-tile per group): the m-tiles of experts with
+  // at least `spread` tiles (a folded shared expert) go to evenly spaced positions of the list --
+  // big tile b at floor((2b+1) N / 2B) of N -- and the other tiles fill the rest in expert order,
+  // so that every XCD's contiguous range holds its share of them.
+  __shared__ int s_bstart[1024], s_sstart[1024], s_nbig[1];
+  if (spread > 0) {
+    const int nbig = (e < E && nt >= spread) ? nt : 0;
+    int bincl = nbig;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(bincl, off);
+      if (lane >= off) bincl += o;
+    }
+    __syncthreads();  // wsum is reused
+    if (lane == 63) wsum[w] = bincl;
+    __syncthreads();
+    if (e == 0) {
+      int run = 0;
+      for (int i = 0; i < 16; ++i) { const int x = wsum[i]; wsum[i] = run; run += x; }
+      s_nbig[0] = run;
+    }
+    __syncthreads();
+    if (e < E) {
+      s_bstart[e] = bincl - nbig + wsum[w];
+      s_sstart[e] = s_tstart[e] - s_bstart[e];  // tiles of the non-big experts before e
+    }
+  }
   __syncthreads();
   const int ntiles = s_total[1];
+  const int nbig_total = (spread > 0) ? s_nbig[0] : 0;
   for (int j = e; j < ntiles; j += blockDim.x) {
+    // position j -> list (start array) and index in it
+    const int* starts = s_tstart;
+    int idx = j;
+    if (nbig_total > 0) {
+      const int64_t B = nbig_total, N = ntiles;
+      const int64_t num = 2 * B * (j + 1) - N;  // big slots <= j: b with (2b+1) N < 2B (j+1)
+      const int cnt = num <= 0 ? 0 : (int)min(B, (num + 2 * N - 1) / (2 * N));
+      const bool isbig = cnt > 0 && ((2 * (int64_t)(cnt - 1) + 1) * N) / (2 * B) == j;
+      starts = isbig ? s_bstart : s_sstart;
+      idx = isbig ? cnt - 1 : j - cnt;
+    }
     int lo = 0, hi = E - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if (s_tstart[mid] <= j) lo = mid;
+      if (starts[mid] <= idx) lo = mid;
       else hi = mid - 1;
     }
-    const int i = j - s_tstart[lo];
+    const int i = idx - starts[lo];
     MTile t;
     t.e = lo;
     t.r0 = s_r0[lo] + i * BM;
@@ -1195,9 +1233,9 @@ struct MfmaCfg {
 };
 
 static int launch_build_tiles(const int32_t* gs, int64_t E, int64_t M, int BM, const GmmWs& w, hipStream_t st,
-                              bool need_order = false, bool reset_split = false) {
+                              bool need_order = false, bool reset_split = false, int spread = 0) {
   hipLaunchKernelGGL(build_tiles_kernel, dim3(1), dim3(1024), 0, st, gs, (int)E, (int)M, BM, w.count, w.offsets,
-                     w.order, w.tiles, need_order ? 1 : 0, reset_split ? w.split_cnt : (int*)nullptr);
+                     w.order, w.tiles, need_order ? 1 : 0, reset_split ? w.split_cnt : (int*)nullptr, spread);
   return check_launch();
 }
 
@@ -1221,6 +1259,10 @@ static int cus_per_xcd() {
 // whose empty 32-row blocks skip their MFMAs, so each expert's weights stream once).
 #ifndef MTX_GM_SMALL
 #define MTX_GM_SMALL 1
+#endif
+// m-tiles an expert needs to be spread through the tile order (0: never)
+#ifndef MTX_SPREAD_MIN
+#define MTX_SPREAD_MIN 4
 #endif
 #ifndef MTX_V3_NSTAGE
 #define MTX_V3_NSTAGE 4
@@ -1334,9 +1376,11 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
     const bool big_m = v3ok && (tile_m == 256 || (tile_m == 0 && (M / E) >= MTX_V3_SMALL_MEAN));
     if (gath && (!v3ok || !((mode == 2 && I % 128 == 0) || (mode == 0 && Nout % 256 == 0))))
       return MTX_ERR_UNSUPPORTED;
+    // one m-tile per scheduling group: spread the m-tiles of experts with several of them
+    const int spread = (a.gm == 1) ? MTX_SPREAD_MIN : 0;
     if (mode == 2 && I % 128 == 0) {
       if (big_m) {
-        rc = launch_build_tiles(gs, E, M, 256, wsp, st);
+        rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, false, spread);
         if (rc) return rc;
         return launch_v3<mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 256) * (I / 128), st);
       }
@@ -1357,7 +1401,7 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
           a.split_part = wsp.split_part;
           a.ncu_x = ncu;
         }
-        rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, split);
+        rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, split, spread);
         if (rc) return rc;
         // split pieces add at most ncu - rem < ncu workgroups per XCD
         const int64_t grid = round_up(gmm_max_tiles(M, E, 256) * (Nout / 256), 8) + (split ? 8 * (int64_t)ncu : 0);
