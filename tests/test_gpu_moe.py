@@ -184,14 +184,17 @@ def test_expert_bias_update_matches_oracle(dev, E):
 
 
 @pytest.mark.gpu
-def test_folded_shared_expert_mfma_shapes(dev):
+@pytest.mark.parametrize("T,E,K", [(512, 32, 8), (2048, 128, 4)])
+def test_folded_shared_expert_mfma_shapes(dev, T, E, K):
     # shapes on the bf16 MFMA kernels (D, I multiples of 256 / 128): folded == separate up to the
     # f32 summation order of split-K tail tiles (the two layouts split different tiles), i.e.
-    # within a bf16 rounding of each expert output
+    # within a bf16 rounding of each expert output.  T = 2048, E = 128: about 80 rows per expert
+    # (one m-tile per scheduling group) and a shared group of 8 m-tiles, spread through the
+    # tile order by the tile builder
     from mintext_amd.moe import fold_shared_expert, moe_layer_forward
 
     rng = np.random.default_rng(3)
-    T, D, E, K, I = 512, 512, 32, 8, 256
+    D, I = 512, 256
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev).bfloat16()
     x = t(rng.standard_normal((T, D)))
     gu, dn = t(rng.standard_normal((E, D, 2 * I)) * 0.03), t(rng.standard_normal((E, I, D)) * 0.03)
