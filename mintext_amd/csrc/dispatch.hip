@@ -732,9 +732,6 @@ __global__ __launch_bounds__(256) void unroute_rows_kernel(
   }
 }
 
-#ifndef MTX_K8_WPB
-#define MTX_K8_WPB 4
-#endif
 template <typename YT, typename WT, typename OT>
 static void launch_unroute_t(const void* Y, const int32_t* inv, const void* w, int64_t N, int K,
                              int64_t D, void* out, Addend add, hipStream_t st) {
@@ -755,7 +752,7 @@ static void launch_unroute_t(const void* Y, const int32_t* inv, const void* w, i
     if (K <= 2 && D % 32 == 0) MTX_UNROUTE_ROWS_L(2, 2, 4, 1);
     else if (K <= 2) MTX_UNROUTE_ROWS_L(2, 4, 1, 4);
     else if (K <= 4) MTX_UNROUTE_ROWS_L(4, 8, 1, 4);
-    else if (D % 16 == 0) MTX_UNROUTE_ROWS_L(8, 2, 2, MTX_K8_WPB);
+    else if (D % 16 == 0) MTX_UNROUTE_ROWS_L(8, 2, 2, 4);
     else MTX_UNROUTE_ROWS_L(8, 4, 1, 4);
 #undef MTX_UNROUTE_ROWS_L
   } else if (v8 && K <= 2) MTX_UNROUTE(true, 2);
