@@ -99,12 +99,55 @@ __device__ __forceinline__ uint32_t e4m3_pack4(float a, float b, float c, float 
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(cl(a), cl(b), 0, false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(cl(c), cl(d), w, true);
   uint32_t q = (uint32_t)w;
-  const float v[4] = {a, b, c, d};
+  // one branch per four values (the clamp turns NaN into -448; NaN is rare)
+  if (__builtin_expect((a != a) | (b != b) | (c != c) | (d != d), 0)) {
+    const float v[4] = {a, b, c, d};
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    if (__builtin_expect(v[i] != v[i], 0))
-      q = (q & ~(0xffu << (8 * i))) | ((uint32_t)(f32_to_e4m3(v[i])) << (8 * i));
+    for (int i = 0; i < 4; ++i)
+      if (v[i] != v[i]) q = (q & ~(0xffu << (8 * i))) | ((uint32_t)(f32_to_e4m3(v[i])) << (8 * i));
+  }
   return q;
+}
+
+// Lane exchange of step S of an all-reduce over aligned groups of 2^(S+1) lanes.  Steps 0 and 1
+// are xor 1 and xor 2 (DPP quad permutes); steps 2 and 3 pair the two halves of each 8- and
+// 16-lane group by mirroring (DPP row_half_mirror, row_mirror), which after steps 0..S-1 hands
+// every lane the same partial as the xor-4 / xor-8 partner would; step 4 is xor 16 (ds_swizzle,
+// bitmask mode) and step 5 xor 32.  So the results equal an xor butterfly's bit for bit (the
+// combines are commutative), without the LDS round trip of ds_bpermute.
+template <int S>
+__device__ __forceinline__ int lane_xchg(int v) {
+  if constexpr (S == 0) return __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false);
+  else if constexpr (S == 1) return __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false);
+  else if constexpr (S == 2) return __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false);
+  else if constexpr (S == 3) return __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false);
+  else if constexpr (S == 4) return __builtin_amdgcn_ds_swizzle(v, 0x401F);
+  else return __shfl_xor(v, 32);
+}
+template <int S>
+__device__ __forceinline__ float lane_xchg(float v) {
+  return __int_as_float(lane_xchg<S>(__float_as_int(v)));
+}
+// maximum over each aligned group of 8 lanes (every lane gets it)
+__device__ __forceinline__ float max8_lanes(float m) {
+  m = fmaxf(m, lane_xchg<0>(m));
+  m = fmaxf(m, lane_xchg<1>(m));
+  return fmaxf(m, lane_xchg<2>(m));
+}
+
+// Division by a quantisation scale b shared by a group of values, in four VALU instructions
+// instead of the ten of the full IEEE division: with rb = 1.0f / b (correctly rounded) and
+// q = RN(a * rb), RN(q + (a - b*q) * rb) is RN(a / b), the residual a - b*q being exact in one
+// FMA (Markstein's correction, IBM J. Res. Develop. 34(1), 1990).  Valid for b in
+// [2^-64, 2^100] (div_rn_ok): the result is the IEEE quotient bit for bit whenever |a| >= 2^-100
+// or a == 0, and the quotient has a's sign (copysign, for a == -0).  Smaller nonzero |a| can put
+// the residual in the subnormal range and the quotient one ulp off, but such quotients are below
+// 2^-36 and their e4m3 code (+-0) is the same.  Callers take the IEEE division when
+// div_rn_ok(b) fails.
+__device__ __forceinline__ bool div_rn_ok(float b) { return b >= 0x1p-64f && b <= 0x1p100f; }
+__device__ __forceinline__ float div_rn(float a, float b, float rb) {
+  const float q = a * rb;
+  return __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q, b, a), rb, q), a);
 }
 
 __device__ __forceinline__ float e4m3_to_f32(uint8_t v) {

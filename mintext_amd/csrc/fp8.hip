@@ -81,14 +81,22 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const T* __restrict__ x
       float m = 0.0f;
 #pragma unroll
       for (int i = 0; i < EPL; ++i) m = fmaxf(m, fabsf(v[i]));
-#pragma unroll
-      for (int off = LPG / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+      static_assert(LPG == 8, "one 128-group per 8 lanes");
+      m = max8_lanes(m);  // DPP lane exchanges, no LDS round trip
       float sc = m / 448.0f;
       if (sc == 0.0f) sc = 1.0f;
       u32x4 q;
+      if (__builtin_expect(div_rn_ok(sc), 1)) {
+        const float rsc = 1.0f / sc;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        q[i] = e4m3_pack4(v[4 * i] / sc, v[4 * i + 1] / sc, v[4 * i + 2] / sc, v[4 * i + 3] / sc);
+        for (int i = 0; i < 4; ++i)
+          q[i] = e4m3_pack4(div_rn(v[4 * i], sc, rsc), div_rn(v[4 * i + 1], sc, rsc), div_rn(v[4 * i + 2], sc, rsc),
+                            div_rn(v[4 * i + 3], sc, rsc));
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          q[i] = e4m3_pack4(v[4 * i] / sc, v[4 * i + 1] / sc, v[4 * i + 2] / sc, v[4 * i + 3] / sc);
+      }
       if (!ok[u]) continue;
       const int64_t r = tt[u] / ng, g = tt[u] - r * ng;
       *(u32x4*)(xq + r * D + g * 128 + gl * EPL) = q;

@@ -6,7 +6,7 @@
 // holds rows 4 (rl + TR h) + q (q = 0..3), so that it owns four consecutive rows of each of its
 // columns and can pack their four codes into one 32-bit word for the transposed layout.
 // Scales are amax / 448 (1 when the amax is 0) over the whole tile or per column; codes are
-// e4m3 of value / scale (IEEE division), by e4m3_pack4.
+// e4m3 of value / scale (the IEEE quotient's code, through div_rn), by e4m3_pack4.
 #pragma once
 #include "common.h"
 
@@ -86,14 +86,27 @@ constexpr int TSTRIDE = 132;  // bytes per transposed row: 4-byte aligned, 2-way
 template <typename T, typename SC>
 __device__ __forceinline__ void codes_to_lds_t(const Tile<T>& t, SC sc, uint8_t* tt) {
   using S = TileShape<T>;
+  auto put = [&](auto quot) {
 #pragma unroll
-  for (int h = 0; h < S::G4; ++h)
+    for (int h = 0; h < S::G4; ++h)
 #pragma unroll
-    for (int j = 0; j < S::VE; ++j) {
-      const float s = sc(j);
-      const uint32_t w = e4m3_pack4(t.at(h, 0, j) / s, t.at(h, 1, j) / s, t.at(h, 2, j) / s, t.at(h, 3, j) / s);
-      *(uint32_t*)(tt + (t.cl * S::VE + j) * TSTRIDE + 4 * (t.rl + S::TR * h)) = w;
-    }
+      for (int j = 0; j < S::VE; ++j) {
+        const uint32_t w = e4m3_pack4(quot(t.at(h, 0, j), j), quot(t.at(h, 1, j), j), quot(t.at(h, 2, j), j),
+                                      quot(t.at(h, 3, j), j));
+        *(uint32_t*)(tt + (t.cl * S::VE + j) * TSTRIDE + 4 * (t.rl + S::TR * h)) = w;
+      }
+  };
+  // one branch per lane: the four-instruction quotient when every scale of the lane's columns
+  // allows it, the IEEE division otherwise (the same codes either way)
+  bool fast = true;
+  float rs[S::VE];
+#pragma unroll
+  for (int j = 0; j < S::VE; ++j) {
+    fast = fast && div_rn_ok(sc(j));
+    rs[j] = 1.0f / sc(j);
+  }
+  if (__builtin_expect(fast, 1)) put([&](float a, int j) { return div_rn(a, sc(j), rs[j]); });
+  else put([&](float a, int j) { return a / sc(j); });
 }
 
 // 128 transposed rows of 128 bytes from LDS to dst + c * ld (16 bytes per lane, 8 lanes per row)
@@ -115,20 +128,27 @@ template <typename T>
 __device__ __forceinline__ void codes_to_global(const Tile<T>& t, float s, uint8_t* __restrict__ dst, int64_t ld) {
   using S = TileShape<T>;
   uint8_t* p = dst + t.cl * S::VE;
+  auto put = [&](auto quot) {
 #pragma unroll
-  for (int h = 0; h < S::G4; ++h)
+    for (int h = 0; h < S::G4; ++h)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t r = 4 * (t.rl + S::TR * h) + q;
-      if constexpr (S::VE == 8) {
-        const uint32_t lo = e4m3_pack4(t.at(h, q, 0) / s, t.at(h, q, 1) / s, t.at(h, q, 2) / s, t.at(h, q, 3) / s);
-        const uint32_t hi = e4m3_pack4(t.at(h, q, 4) / s, t.at(h, q, 5) / s, t.at(h, q, 6) / s, t.at(h, q, 7) / s);
-        *(u32x2*)(p + r * ld) = u32x2{lo, hi};
-      } else {
-        *(uint32_t*)(p + r * ld) =
-            e4m3_pack4(t.at(h, q, 0) / s, t.at(h, q, 1) / s, t.at(h, q, 2) / s, t.at(h, q, 3) / s);
+      for (int q = 0; q < 4; ++q) {
+        const int64_t r = 4 * (t.rl + S::TR * h) + q;
+        if constexpr (S::VE == 8) {
+          const uint32_t lo =
+              e4m3_pack4(quot(t.at(h, q, 0)), quot(t.at(h, q, 1)), quot(t.at(h, q, 2)), quot(t.at(h, q, 3)));
+          const uint32_t hi =
+              e4m3_pack4(quot(t.at(h, q, 4)), quot(t.at(h, q, 5)), quot(t.at(h, q, 6)), quot(t.at(h, q, 7)));
+          *(u32x2*)(p + r * ld) = u32x2{lo, hi};
+        } else {
+          *(uint32_t*)(p + r * ld) =
+              e4m3_pack4(quot(t.at(h, q, 0)), quot(t.at(h, q, 1)), quot(t.at(h, q, 2)), quot(t.at(h, q, 3)));
+        }
       }
-    }
+  };
+  const float rs = 1.0f / s;
+  if (__builtin_expect(div_rn_ok(s), 1)) put([&](float a) { return div_rn(a, s, rs); });
+  else put([&](float a) { return a / s; });
 }
 
 }  // namespace q8

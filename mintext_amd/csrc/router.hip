@@ -28,25 +28,6 @@ __device__ __forceinline__ bool cand_better(float av, int ai, float bv, int bi) 
   return av > bv || (av == bv && ai < bi);
 }
 
-// Lane exchange of step S of an all-reduce over aligned groups of 2^(S+1) lanes.  Steps 0 and 1
-// are xor 1 and xor 2 (DPP quad permutes); steps 2 and 3 pair the two halves of each 8- and
-// 16-lane group by mirroring (DPP row_half_mirror, row_mirror), which after steps 0..S-1 hands
-// every lane the same partial as the xor-4 / xor-8 partner would; step 4 is xor 16 (ds_swizzle,
-// bitmask mode) and step 5 xor 32.  So the results equal an xor butterfly's bit for bit (the
-// combines are commutative), without the LDS round trip of ds_bpermute.
-template <int S>
-__device__ __forceinline__ int lane_xchg(int v) {
-  if constexpr (S == 0) return __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false);
-  else if constexpr (S == 1) return __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false);
-  else if constexpr (S == 2) return __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false);
-  else if constexpr (S == 3) return __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false);
-  else if constexpr (S == 4) return __builtin_amdgcn_ds_swizzle(v, 0x401F);
-  else return __shfl_xor(v, 32);
-}
-template <int S>
-__device__ __forceinline__ float lane_xchg(float v) {
-  return __int_as_float(lane_xchg<S>(__float_as_int(v)));
-}
 // Arg-max of (value, id, payload) over the token's L lanes (L a power of two <= 64).
 template <int S = 0>
 __device__ __forceinline__ void group_argmax(float& bv, int& bi, float& bs, int L) {
