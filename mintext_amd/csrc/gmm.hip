@@ -1225,6 +1225,284 @@ __global__ __launch_bounds__(WM* WN * 64, MTX_V3_WPE) void gmm_v3_kernel(Args p)
   }
 }
 
+// ---- v4p: persistent workgroups whose ring runs across tiles (FWD / DLHS, plain store) --------
+// With short reductions (a few dozen 32-k stages per tile) the ring fill at every tile start and
+// the dispatch gap between workgroups cost 10-15 % of a 256x256 tile.  This kernel computes the
+// same tiles with the same waves, ring, fragments and MFMA order as gmm_v3_kernel (the same bits),
+// but each workgroup (at most one per CU) walks its XCD's tile range and keeps issuing ring loads
+// across tile boundaries, so the next tile's first three stages are in flight while the current
+// tile's epilogue stores.  The tile list is read through the scalar cache, so that a tile switch
+// waits on lgkmcnt, never on the ring's vmcnt; the epilogue stages each wave's 32 x 64 blocks in
+// its own 4 KB of the tile's last (consumed) ring slot.  Needs Kred >= 4 stages.
+template <int MODE>
+__global__ __launch_bounds__(512, 2) void gmm_v4p_kernel(Args p) {
+  using v3::BKS;
+  using v3::a_off;
+  using v3::bn_off;
+  using Cf = v3::Cfg<256, 4>;
+  constexpr int BN = Cf::BN, NSTAGE = Cf::NSTAGE, PD = Cf::PD;
+  constexpr int A_BYTES = Cf::A_BYTES, STAGE = Cf::STAGE;
+  constexpr int WN = 4, WTM = 128, WTN = 64, TM = 4, TN = 2;
+  constexpr int A_INSTR = 2, B_INSTR = 2, LPS = A_INSTR + B_INSTR;
+  static_assert(MODE == FWD || MODE == DLHS, "v4p mode");
+  static_assert(Cf::BM == 256 && A_BYTES == 16384 && Cf::B_BYTES == 16384 && NSTAGE == 4, "v4p ring");
+  constexpr bool B_T = (MODE == FWD);  // B tile stored [reduction][col]
+  __shared__ __attribute__((aligned(1024))) char lds[NSTAGE * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+  const int wm = wave / WN, wn = wave % WN;
+  const int nn = p.N / BN;
+  const int cnt = p.count[0];
+  const int total = cnt * nn;
+  // XCD x (= blockIdx % 8) walks tiles [x*per, (x+1)*per) with its gridDim/8 workgroups
+  const int nx = (int)(gridDim.x >> 3), xcd = (int)(blockIdx.x & 7), q = (int)(blockIdx.x >> 3);
+  const int per = (total + 7) >> 3;
+  const int lid_end = min((xcd + 1) * per, total);
+  int lid = xcd * per + q;
+  if (lid >= lid_end) return;
+  const int nk = p.Kred / BKS;
+
+  struct Tile {
+    int e, r0, r1, n_tile, zero;
+  };
+  auto decode = [&](int l) -> Tile {
+    const int GM = p.gm;
+    const int grp = l / (GM * nn);
+    const int first_m = grp * GM;
+    const int gsz = min(GM, cnt - first_m);
+    const int local = l - grp * GM * nn;
+    // read-only tile list through the scalar cache (constant address space, uniform index)
+    typedef const __attribute__((address_space(4))) int cint_t;
+    const int mt = __builtin_amdgcn_readfirstlane(first_m + local % gsz);
+    const cint_t* tp = (const cint_t*)(uintptr_t)(p.tiles + mt);
+    Tile T;
+    const int e = tp[0];
+    T.zero = e < 0;
+    T.e = e < 0 ? 0 : e;  // rows past sum(group_sizes): computed with expert 0, stored as 0
+    T.r0 = tp[1];
+    T.r1 = tp[2];
+    T.n_tile = local / gsz;
+    return T;
+  };
+  // per-lane 32-bit byte offsets of the load instructions at k-stage 0 (the v3 layout), and the
+  // tile's uniform weight base
+  struct Src {
+    uint32_t aoff[A_INSTR], boff[B_INSTR];
+    const char* B;
+  };
+  auto make_src = [&](const Tile& T) -> Src {
+    Src S;
+    const int col0 = T.n_tile * BN;
+#pragma unroll
+    for (int i = 0; i < A_INSTR; ++i) {
+      const int seg = wave * A_INSTR + i;
+      const int r = seg * 16 + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
+      const int gr = min(T.r0 + r, T.r1 - 1);  // rows past the group repeat its last row
+      S.aoff[i] = ((uint32_t)gr * (uint32_t)p.Kred + (uint32_t)(c * 8)) * 2u;
+    }
+#pragma unroll
+    for (int i = 0; i < B_INSTR; ++i) {
+      const int seg = wave * B_INSTR + i;
+      if constexpr (B_T) {
+        const int k = seg * 2 + (lane >> 5), c = (lane & 31) ^ ((k & 3) << 2);
+        S.boff[i] = ((uint32_t)k * (uint32_t)p.N + (uint32_t)(col0 + c * 8)) * 2u;
+      } else {
+        const int r = seg * 16 + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
+        S.boff[i] = ((uint32_t)(col0 + r) * (uint32_t)p.Kred + (uint32_t)(c * 8)) * 2u;
+      }
+    }
+    S.B = (const char*)(p.B + (int64_t)T.e * p.Kred * p.N);
+    return S;
+  };
+
+  Tile cur = decode(lid);
+  int lid_next = lid + nx;
+  Tile nxt = lid_next < lid_end ? decode(lid_next) : cur;
+  // sources of the tile whose stages are being issued: the current tile's until its last stage
+  // is issued, then the next tile's (the last tile's steps past its end re-read its first
+  // stages: in bounds, into slots that are never read)
+  Src src = make_src(cur);
+
+  const uint32_t lds_base = lds_addr(lds);
+  const int64_t b_step = B_T ? (int64_t)BKS * p.N * 2 : (int64_t)BKS * 2;
+  // ring step g: stage k of the tile whose sources are in src
+  auto issue = [&](int g, int k) {
+    const uint32_t st = lds_base + (uint32_t)((g & (NSTAGE - 1)) * STAGE);
+    const char* A = (const char*)p.A + (int64_t)k * (BKS * 2);
+#pragma unroll
+    for (int i = 0; i < A_INSTR; ++i) gload_lds16_s(A, src.aoff[i], st + (wave_u * A_INSTR + i) * 1024u);
+    const char* B = src.B + (int64_t)k * b_step;
+#pragma unroll
+    for (int i = 0; i < B_INSTR; ++i)
+      gload_lds16_s(B, src.boff[i], st + (uint32_t)A_BYTES + (wave_u * B_INSTR + i) * 1024u);
+  };
+
+  // ---- fragments (the v3 reads, by ring step) ---------------------------------------------
+  bf16x8 fa[2][TM], fb[2][TN];
+  const int frow = lane & 31, fhalf = lane >> 5;
+  auto read_tr = [&](const char* region, int c0, int kk) -> bf16x8 {
+    const int n = c0 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const int k = kk * 16 + 8 * fhalf + ((lane & 15) >> 2);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(region + bn_off(k, n >> 3) + (n & 7) * 2));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(region + bn_off(k + 4, n >> 3) + (n & 7) * 2));
+    const s16x4 both[2] = {lo, hi};
+    return __builtin_bit_cast(bf16x8, both);
+  };
+  auto read_frags = [&](int g_, int kk, int buf, int nb) {
+    if (nb == 0) return;  // a wave with no rows of the group in this tile runs no MFMA
+    const char* st = lds + (g_ & (NSTAGE - 1)) * STAGE;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      if (i >= nb) continue;
+      const int r = wm * WTM + i * 32 + frow;
+      fa[buf][i] = *(const bf16x8*)(st + a_off(r, kk * 2 + fhalf));
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      if constexpr (B_T) {
+        fb[buf][j] = read_tr(st + A_BYTES, wn * WTN + j * 32, kk);
+      } else {
+        const int r = wn * WTN + j * 32 + frow;
+        fb[buf][j] = *(const bf16x8*)(st + A_BYTES + a_off(r, kk * 2 + fhalf));
+      }
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  // prologue: ring steps 0..PD-1 in flight; steps 0 and 1 landed and visible
+#pragma unroll
+  for (int s = 0; s < PD; ++s) issue(s, s);
+  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
+  __syncthreads();
+  int g = 0;
+
+  for (;;) {
+    // 32-row blocks of this wave that hold rows of the tile (wave-uniform, so that the ring step
+    // g updated under the branch below stays in a scalar register)
+    const int nbi = __builtin_amdgcn_readfirstlane(min(max((cur.r1 - cur.r0 - wm * WTM + 31) / 32, 0), TM));
+    read_frags(g, 0, 0, nbi);
+    auto tile_loop = [&](auto full_tag) {
+      constexpr bool FULL = decltype(full_tag)::value;
+      const int nb = FULL ? TM : nbi;
+      for (int kt = 0; kt < nk; ++kt, ++g) {
+        if (kt + PD == nk) src = make_src(nxt);  // from here on the ring loads the next tile
+        issue(g + PD, kt + PD < nk ? kt + PD : kt + PD - nk);
+        if constexpr (FULL) {
+          // explicit interleave: one fragment read of the next substep after each MFMA
+          __builtin_amdgcn_sched_barrier(0);
+          read_frags(g, 1, 1, nb);
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[0][j], fa[0][i], acc[i][j], 0, 0, 0);
+#pragma unroll
+          for (int qq = 0; qq < TM * TN; ++qq) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          read_frags(g + 1, 0, 0, nb);
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
+#pragma unroll
+          for (int qq = 0; qq < TM * TN; ++qq) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        } else {
+          read_frags(g, 1, 1, nb);
+#pragma unroll
+          for (int i = 0; i < TM; ++i) {
+            if (i >= nb) continue;
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[0][j], fa[0][i], acc[i][j], 0, 0, 0);
+          }
+          read_frags(g + 1, 0, 0, nb);
+#pragma unroll
+          for (int i = 0; i < TM; ++i) {
+            if (i >= nb) continue;
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
+          }
+        }
+        // step g+2 landed (g+3 may be in flight); bare barrier as in v3: the slot refilled next
+        // was read only by fragments that this step's MFMAs consumed
+        __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
+        __builtin_amdgcn_s_barrier();
+      }
+    };
+    // both loop versions execute the same barriers, so the waves of a workgroup may take either
+    if (nbi == TM) tile_loop(std::integral_constant<bool, true>());
+    else tile_loop(std::integral_constant<bool, false>());
+
+    // ---- epilogue: the tile's last ring slot (step g-1) is consumed and is refilled only by the
+    // next tile's first ring load; every wave's fragment reads of it must complete before the
+    // staging writes (the bare barriers do not order them): LDS-only release fence, barrier.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    // acc[i][j][4q+c] of lane l is C[row i*32 + l%32][col j*32 + 8q + 4(l/32) + c]; each wave
+    // stages 32 rows x 64 columns (4 KB, 16-byte chunk c of row r at chunk c ^ (r & 7)) and writes
+    // them back as whole 128-byte rows
+    char* wst = lds + ((g - 1) & (NSTAGE - 1)) * STAGE + wave * 4096;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const bf16x4 v = cur.zero ? bf16x4{(__bf16)0.0f, (__bf16)0.0f, (__bf16)0.0f, (__bf16)0.0f}
+                                    : bf16x4{(__bf16)acc[i][j][4 * gq], (__bf16)acc[i][j][4 * gq + 1],
+                                             (__bf16)acc[i][j][4 * gq + 2], (__bf16)acc[i][j][4 * gq + 3]};
+          *(bf16x4*)(wst + frow * 128 + (((4 * j + gq) ^ (frow & 7)) << 4) + 8 * fhalf) = v;
+        }
+      __builtin_amdgcn_s_waitcnt(MTX_LGKMCNT0);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int rloc = rr * 8 + (lane >> 3);
+        const u32x4 v = *(const u32x4*)(wst + rloc * 128 + (((lane & 7) ^ (rloc & 7)) << 4));
+        const int row = cur.r0 + wm * WTM + i * 32 + rloc;
+        if (row < cur.r1) *(u32x4*)(p.C + (int64_t)row * p.ldc + cur.n_tile * BN + wn * WTN + (lane & 7) * 8) = v;
+      }
+      __builtin_amdgcn_s_waitcnt(MTX_LGKMCNT0);  // reads done before the next block overwrites
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+    // the staging slot is the next tile's first ring load target: every wave's reads of it done
+    // (LDS-only, so the ring's loads in flight are not waited for)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+
+    // ---- next tile ------------------------------------------------------------------------
+    lid = lid_next;
+    if (lid >= lid_end) break;
+    cur = nxt;
+    lid_next = lid + nx;
+    if (lid_next < lid_end) nxt = decode(lid_next);
+  }
+  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));  // the last steps' re-read loads land before exit
+}
+
 }  // namespace mf
 
 // ---- host-side dispatch ----------------------------------------------------------------------
@@ -1290,6 +1568,23 @@ static int launch_v3(const mf::Args& a, int64_t grid, hipStream_t st) {
 #ifndef MTX_V3S_NST
 #define MTX_V3S_NST 3
 #endif
+// Persistent plain-store kernel for reductions of 4 .. MTX_V4P_MAX_STAGES 32-k stages (0: never):
+// one workgroup per CU, each walking its XCD's share of the tile list.  Measured against
+// gmm_v3_kernel on the same box (E = 8, M = 16384, N = 4096): +36 % at Kred 512, +10 % at 1024,
+// but -8 % at 2048 and -26 % at 4096, and -10 % / -19 % on the C5 dlhs / C3 down shapes (Kred
+// 1536-2048).  vmcnt counts loads and stores in one in-order counter, so the next tile's first
+// ring wait also waits for the previous tile's epilogue stores, which a short-lived v3 workgroup
+// leaves draining behind it; that costs more than the saved ring fill once tiles are long.
+#ifndef MTX_V4P_MAX_STAGES
+#define MTX_V4P_MAX_STAGES 32
+#endif
+template <int MODE>
+static int launch_v4p(const mf::Args& a, int64_t max_tiles, int ncu, hipStream_t st) {
+  const int64_t grid = std::min(round_up(max_tiles, 8), (int64_t)kSplitXcd * ncu);
+  if (grid <= 0) return MTX_OK;
+  hipLaunchKernelGGL((mf::gmm_v4p_kernel<MODE>), dim3((unsigned)grid), dim3(512), 0, st, a);
+  return check_launch();
+}
 template <int MODE, int EPI>
 static int launch_v3_small(const mf::Args& a, int64_t grid, hipStream_t st) {
   if (grid <= 0) return MTX_OK;
@@ -1390,6 +1685,15 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
       return launch_mfma<128, 256, 1, 2, mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 128) * (I / 128), st);
     }
     if (mode != 2 && Nout % 256 == 0) {
+      const int64_t nks = Kred / mf::v3::BKS;
+      const int ncu4 = cus_per_xcd();
+      if (big_m && !gath && nks >= 4 && nks <= MTX_V4P_MAX_STAGES && ncu4 >= 1) {
+        // short reductions: persistent workgroups, the ring running across tiles
+        rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, false, spread);
+        if (rc) return rc;
+        const int64_t tiles = gmm_max_tiles(M, E, 256) * (Nout / 256);
+        return mode == 0 ? launch_v4p<mf::FWD>(a, tiles, ncu4, st) : launch_v4p<mf::DLHS>(a, tiles, ncu4, st);
+      }
       if (big_m) {
         // split tail when the workspace carries the partials region (mtx_gmm_workspace_size)
         const int ncu = cus_per_xcd();

@@ -44,3 +44,10 @@ def rel_err(a, b) -> float:
     b = np.asarray(b, dtype=np.float64)
     den = np.linalg.norm(b.ravel())
     return float(np.linalg.norm((a - b).ravel()) / (den if den > 0 else 1.0))
+
+
+def tile_list_workspace_bytes(M: int, E: int) -> int:
+    """The tile-list part of the grouped-GEMM workspace (mtx_gmm_workspace_size without the split
+    tail): with it every tile runs whole, so any two kernels agree bit for bit."""
+    up = lambda a, b: (a + b - 1) // b * b
+    return up(up((48 + 2 * E + 1) * 4, 256) + (-(-M // 64) + E + 1) * 16, 256)

@@ -11,16 +11,13 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import rel_err
+from conftest import rel_err, tile_list_workspace_bytes
 from oracle import moe_oracle as O
 
 pytestmark = pytest.mark.gpu
 
 
-def _tile_list_bytes(M, E):
-    """The tile-list part of the GEMM workspace (mtx_gmm_workspace_size without the split tail)."""
-    up = lambda a, b: (a + b - 1) // b * b
-    return up(up((48 + 2 * E + 1) * 4, 256) + (-(-M // 64) + E + 1) * 16, 256)
+_tile_list_bytes = tile_list_workspace_bytes
 
 
 def _groups(rng, M, E):
