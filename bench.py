@@ -11,8 +11,9 @@ is not part of the path; the logits are an input.)  For ``qwen3_bwd`` a step is 
 backward (dlhs + tgmm for both expert GEMMs) under Zipf-skewed routing.
 
 Prints ONE JSON line (rank 0).  ``roofline`` is measured live for the dominant kernel with HIP
-events on the stream the kernels run on; ``cpu_baseline`` times the numpy oracle (the CPU
-restatement of the reference algorithm) on a bounded sample of the same workload.
+events on the stream the kernels run on; ``cpu_baseline`` times a torch-CPU restatement of the
+reference layer (oracle/cpu_port.py, the reference's arithmetic) on a bounded sample of the same
+workload.
 """
 from __future__ import annotations
 
@@ -528,6 +529,67 @@ def fp8_vendor_study(steps=10, warmup=3):
     return 0
 
 
+def grouped_vendor_study(steps=10, warmup=3):
+    """The bf16 grouped GEMMs beside the vendor's grouped GEMM on the same ragged problems:
+    torch._grouped_mm (on this ROCm build a loop of one hipBLASLt GEMM per group) with the
+    weights in the reference's [E, K, N] layout and k-contiguous ([E, N, K] storage), on the C2
+    and C3 expert shapes with seeded near-uniform loads.  Not a benchmark of the path: one JSON
+    line of timings (and whether the vendor's output equals this library's bit for bit)."""
+    import numpy as np
+    import torch
+
+    from mintext_amd import _lib
+    from mintext_amd.kernels import grouped_matmul
+    from mintext_amd.kernels.grouped_matmul import grouped_matmul_swiglu
+
+    _lib.lib()
+    dev = torch.device("cuda:0")
+
+    def t_ms(fn):
+        for _ in range(warmup):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            fn()
+        b.record()
+        b.synchronize()
+        return a.elapsed_time(b) / steps
+
+    out = {"study": "grouped-vendor", "steps": steps, "vendor": "torch._grouped_mm (hipBLASLt per group)"}
+    rng = np.random.default_rng(1)
+    shapes = {  # name: (rows, K, N, experts)
+        "c2_gate_up": (16384, 4096, 2 * 14336, 8), "c2_down": (16384, 14336, 4096, 8),
+        "c3_gate_up": (32768, 7168, 2 * 2048, 256), "c3_down": (32768, 2048, 7168, 256)}
+    loads = {}
+    for name, (M, Kin, N, E) in shapes.items():
+        if E not in loads:
+            loads[E] = torch.from_numpy(rng.multinomial(M, [1.0 / E] * E).astype(np.int32)).to(dev)
+        gs = loads[E]
+        offs = torch.cumsum(gs, 0).to(torch.int32)
+        g = torch.Generator(device=dev)
+        g.manual_seed(3)
+        x = torch.randn(M, Kin, device=dev, generator=g).bfloat16()
+        w = (torch.randn(E, Kin, N, device=dev, generator=g) * 0.02).bfloat16()
+        w_kc = w.transpose(1, 2).contiguous().transpose(1, 2)  # same values, k-contiguous storage
+        ours = grouped_matmul(x, w, gs)
+        res = {"ours_ms": t_ms(lambda: grouped_matmul(x, w, gs))}
+        if name.endswith("gate_up"):
+            res["ours_with_swiglu_ms"] = t_ms(lambda: grouped_matmul_swiglu(x, w, gs))
+        for tag, wv in (("kn", w), ("kcontig", w_kc)):
+            v = torch._grouped_mm(x, wv, offs=offs, out_dtype=torch.bfloat16)
+            res[f"vendor_{tag}_ms"] = t_ms(lambda: torch._grouped_mm(x, wv, offs=offs, out_dtype=torch.bfloat16))
+            res[f"vendor_{tag}_bits_equal"] = bool(torch.equal(v, ours))
+        flop = 2.0 * M * Kin * N
+        entry = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()}
+        entry.update({k.replace("_ms", "_tflops"): round(flop / v / 1e9, 1) for k, v in res.items() if k.endswith("_ms")})
+        entry["loads"] = [int(gs.min()), int(gs.max())]
+        out[name] = entry
+        del x, w, w_kc, ours
+    print(json.dumps(out))
+    return 0
+
+
 def copy_study(steps=20, warmup=3):
     """The practical HBM ceiling for read+write streams on this box: device-to-device copies of
     64 MiB to 1 GiB (bytes read + bytes written per second) by torch's copy_ and by the library's
@@ -717,9 +779,11 @@ def main(argv=None):
                          "rows inside the gate_up GEMM")
     ap.add_argument("--graph", action="store_true",
                     help="also time the step captured in a HIP graph and replayed (reported as hip_graph)")
-    ap.add_argument("--study", choices=["gemm-power", "fp8-vendor", "gate", "copy", "kernels"], default=None,
+    ap.add_argument("--study", choices=["gemm-power", "fp8-vendor", "grouped-vendor", "gate", "copy", "kernels"],
+                    default=None,
                     help="gemm-power: GEMM timings on normal vs all-zero data (clock / issue-efficiency study); "
                          "fp8-vendor: C4 blockwise fp8 GEMMs beside hipBLASLt's per-tensor / rowwise fp8 GEMMs; "
+                         "grouped-vendor: C2 / C3 bf16 grouped GEMMs beside torch._grouped_mm (hipBLASLt per group); "
                          "gate: router gate GEMM + top-k, hipBLASLt + route_topk vs the fused kernel; "
                          "copy: device-to-device copy bandwidth (the practical read+write HBM ceiling); "
                          "kernels: the reference's benchmarks/benchmark_moe_kernels.py (gate_up grouped GEMM "
@@ -731,6 +795,8 @@ def main(argv=None):
         return gemm_power_study(a.steps if a.steps != 20 else 10, a.warmup)
     if a.study == "fp8-vendor":
         return fp8_vendor_study(a.steps if a.steps != 20 else 10, a.warmup)
+    if a.study == "grouped-vendor":
+        return grouped_vendor_study(a.steps if a.steps != 20 else 10, a.warmup)
     if a.study == "gate":
         return gate_study(a.steps, a.warmup)
     if a.study == "copy":
