@@ -1,0 +1,81 @@
+"""GPU parity sweep of the bf16 grouped GEMM over seeded random shapes (forward and dlhs): expert
+counts 1-48, uniform / Zipf / ragged-with-empty group sizes, rows past sum(group_sizes), and
+reductions on both sides of the persistent kernel's range (Kred <= 1024 runs the persistent
+plain-store kernel, longer ones the per-tile kernel with its split tail).  Each case checks the
+default schedule against the 128-row tiling (the same f32 sums: bit for bit when no tile is split,
+else within a bf16 ulp plus the f32 cancellation error), both against the float64 oracle at
+2e-2, and that rows past the groups are zero."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_err
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _groups(rng, M, E, kind):
+    if kind == "uniform":
+        gs = np.full(E, M // E)
+        gs[: M - gs.sum()] += 1
+    elif kind == "zipf":
+        p = 1.0 / np.arange(1, E + 1) ** 1.2
+        gs = rng.multinomial(M, p[rng.permutation(E)] / p.sum())
+    else:  # ragged, with an empty group when E > 2
+        cut = np.sort(rng.integers(0, M + 1, E - 1))
+        gs = np.diff(np.concatenate([[0], cut, [M]]))
+        if E > 2:
+            gs[1] += gs[2]
+            gs[2] = 0
+    return gs.astype(np.int32)
+
+
+def _cases(n=20, seed=2024):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        E = int(rng.choice([1, 2, 5, 8, 16, 48]))
+        M = int(rng.integers(1, 3000))
+        kred = int(rng.choice([128, 256, 512, 768, 1024, 1280, 2048]))
+        nout = int(rng.choice([256, 512, 768]))
+        kind = str(rng.choice(["uniform", "zipf", "ragged"]))
+        past = int(rng.choice([0, 0, 5, 300]))
+        op = "dlhs" if i % 3 == 2 else "fwd"
+        out.append((i, E, M, kred, nout, kind, past, op))
+    return out
+
+
+@pytest.mark.parametrize("case", _cases(), ids=lambda c: f"c{c[0]}-E{c[1]}-M{c[2]}-K{c[3]}-N{c[4]}-{c[5]}-p{c[6]}-{c[7]}")
+def test_gmm_sweep(dev, case):
+    from mintext_amd.kernels.grouped_matmul import _gmm_dlhs, _gmm_fwd
+
+    i, E, M, kred, nout, kind, past, op = case
+    rng = np.random.default_rng(100 + i)
+    gs = _groups(rng, M, E, kind)
+    Mt = M + past
+    x = (rng.standard_normal((Mt, kred)) * 0.5).astype(np.float32)
+    # forward: w [E, Kred, Nout]; dlhs: w [E, Nout, Kred] (output Nout = Kin, reduction Kred = Kout)
+    wshape = (E, kred, nout) if op == "fwd" else (E, nout, kred)
+    w = (rng.standard_normal(wshape) * 0.05).astype(np.float32)
+    xt = torch.from_numpy(x).to(dev).bfloat16()
+    wt = torch.from_numpy(w).to(dev).bfloat16()
+    gt = torch.from_numpy(gs).to(dev)
+    f = _gmm_fwd if op == "fwd" else _gmm_dlhs
+    out = f(xt, wt, gt)
+    out128 = f(xt, wt, gt, tiling=(128, 1, 256))
+    assert out.shape == (Mt, nout)
+    assert (out[M:] == 0).all(), "rows past sum(group_sizes) must be zero"
+    xr, wr = xt.float().cpu().numpy(), wt.float().cpu().numpy()
+    ref = O.gmm(xr, wr, gs) if op == "fwd" else O.gmm_dlhs(xr, wr, gs)
+    for o in (out, out128):
+        got = o.float().cpu().numpy()
+        assert rel_err(got, ref) < 2e-2, rel_err(got, ref)
+    if kred <= 1024:  # persistent kernel: whole tiles, the sums of the 128-row tiling bit for bit
+        assert torch.equal(out, out128)
+    else:
+        d = (out.float() - out128.float()).abs()
+        bound = out128.float().abs() * 2.0 ** -7 + 1e-5 * float(np.abs(ref).max() if ref.size else 1.0)
+        assert bool((d <= bound).all()), (d - bound).max().item()
