@@ -357,7 +357,8 @@ def tgmm(x, g, group_sizes) -> np.ndarray:
 
 def silu(x):
     x = np.asarray(x, dtype=np.float64)
-    return x / (1.0 + np.exp(-x))
+    with np.errstate(over="ignore"):  # exp(-x) = inf for x < -709: x / inf is the limit, -0
+        return x / (1.0 + np.exp(-x))
 
 
 def swiglu(h) -> np.ndarray:
