@@ -763,6 +763,89 @@ def kernels_study(steps=20, warmup=5, configs=None):
     return 0
 
 
+DISPATCH_BWD_CONFIGS = {  # layer shapes of the bench configs: tokens N, top-k K, d_model D, d_ff I
+    "mixtral": {"N": 8192, "K": 2, "D": 4096, "I": 14336},
+    "deepseek": {"N": 4096, "K": 8, "D": 7168, "I": 2048},
+    "qwen3": {"N": 16384, "K": 8, "D": 2048, "I": 768},
+}
+
+
+def dispatch_bwd_study(steps=20, warmup=5):
+    """The HBM-bound backward kernels of the layer, as its autograd path calls them: the combine's
+    VJP (mtx_unroute_bwd: f32 dout, bf16 expert outputs, f32 router weights -> bf16 d_sorted and
+    f32 d_weights; moe_dispatch.py:102-111), the route's VJP (mtx_unroute with unit weights, bf16;
+    moe_dispatch.py:33-38,67), and SwiGLU with its VJP (mtx_swiglu / mtx_swiglu_bwd, bf16;
+    moe.py:195-196).  Bytes are algorithmic (every input read once, every output written once);
+    times are HIP-event means over ``steps`` calls on the current stream."""
+    import torch
+    from mintext_amd import _lib as L
+
+    dev = torch.device("cuda:0")
+    st = L.stream(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+
+    def t_ms(fn):
+        for _ in range(warmup):
+            fn()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            fn()
+        b.record()
+        b.synchronize()
+        return a.elapsed_time(b) / steps
+
+    out = {"study": "dispatch-bwd", "steps": steps, "peak_GBs": 8000, "rows": []}
+    for name, c in DISPATCH_BWD_CONFIGS.items():
+        N, K, D, I = c["N"], c["K"], c["D"], c["I"]
+        M = N * K
+        inv = torch.randperm(M, device=dev, generator=g).int()
+        w = torch.rand(N, K, device=dev, generator=g)
+        dout = torch.randn(N, D, device=dev, generator=g)
+        Y = torch.randn(M, D, device=dev, generator=g).bfloat16()
+        dY = torch.empty_like(Y)
+        dw = torch.empty_like(w)
+        dx = torch.empty(N, D, dtype=torch.bfloat16, device=dev)
+        row = {"config": name, "N": N, "K": K, "D": D, "I": I}
+
+        def ub():
+            L.call("mtx_unroute_bwd", L.ptr(dout), L.MTX_F32, L.ptr(Y), L.MTX_BF16, L.ptr(inv), L.ptr(w), L.MTX_F32,
+                   N, K, D, L.ptr(dY), L.ptr(dw), st)
+
+        def rv():
+            L.call("mtx_unroute", L.ptr(Y), L.MTX_BF16, L.ptr(inv), None, L.MTX_F32, N, K, D, L.ptr(dx), L.MTX_BF16,
+                   st)
+
+        kernels = {"unroute_bwd": (ub, N * D * 4 + 2 * M * D * 2 + M * 4 * 3),
+                   "route_vjp": (rv, M * D * 2 + N * D * 2 + M * 4)}
+        del_after = []
+        h = torch.randn(M, 2 * I, device=dev, generator=g).bfloat16()
+        dy = torch.randn(M, I, device=dev, generator=g).bfloat16()
+        y = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+        dh = torch.empty_like(h)
+        del_after += [h, dy, y, dh]
+
+        def sw():
+            L.call("mtx_swiglu", L.ptr(h), L.MTX_BF16, M, I, L.ptr(y), st)
+
+        def swb():
+            L.call("mtx_swiglu_bwd", L.ptr(h), L.ptr(dy), L.MTX_BF16, M, I, L.ptr(dh), st)
+
+        kernels["swiglu"] = (sw, M * I * 2 * 3)
+        kernels["swiglu_bwd"] = (swb, M * I * 2 * 5)
+        for kname, (fn, nbytes) in kernels.items():
+            ms = t_ms(fn)
+            row[kname] = {"us": round(ms * 1e3, 1), "MB": round(nbytes / 1e6, 1),
+                          "GBs": round(nbytes / ms / 1e6, 1), "frac": round(nbytes / ms / 1e6 / 8000, 3)}
+        out["rows"].append(row)
+        del inv, w, dout, Y, dY, dw, dx, del_after
+        torch.cuda.empty_cache()
+    print(json.dumps(out))
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -779,7 +862,8 @@ def main(argv=None):
                          "rows inside the gate_up GEMM")
     ap.add_argument("--graph", action="store_true",
                     help="also time the step captured in a HIP graph and replayed (reported as hip_graph)")
-    ap.add_argument("--study", choices=["gemm-power", "fp8-vendor", "grouped-vendor", "gate", "copy", "kernels"],
+    ap.add_argument("--study", choices=["gemm-power", "fp8-vendor", "grouped-vendor", "gate", "copy", "kernels",
+                                        "dispatch-bwd"],
                     default=None,
                     help="gemm-power: GEMM timings on normal vs all-zero data (clock / issue-efficiency study); "
                          "fp8-vendor: C4 blockwise fp8 GEMMs beside hipBLASLt's per-tensor / rowwise fp8 GEMMs; "
@@ -787,7 +871,9 @@ def main(argv=None):
                          "gate: router gate GEMM + top-k, hipBLASLt + route_topk vs the fused kernel; "
                          "copy: device-to-device copy bandwidth (the practical read+write HBM ceiling); "
                          "kernels: the reference's benchmarks/benchmark_moe_kernels.py (gate_up grouped GEMM "
-                         "forward / backward / fwd+bwd per config)")
+                         "forward / backward / fwd+bwd per config); "
+                         "dispatch-bwd: the layer's HBM-bound backward kernels (combine and route VJPs, SwiGLU "
+                         "and its VJP) at the bench shapes")
     ap.add_argument("--configs", nargs="+", default=None, choices=sorted(KERNEL_STUDY_CONFIGS),
                     help="--study kernels: configs to run (default: all)")
     a = ap.parse_args(argv)
@@ -803,6 +889,8 @@ def main(argv=None):
         return copy_study(a.steps, a.warmup)
     if a.study == "kernels":
         return kernels_study(a.steps, a.warmup, a.configs)
+    if a.study == "dispatch-bwd":
+        return dispatch_bwd_study(a.steps, a.warmup)
     if a.copy_calibration:
         import torch
 

@@ -172,4 +172,40 @@ __device__ __forceinline__ void store_from_f32(void* p, int64_t i, int dt, float
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
 
+// Eight consecutive elements p[i .. i+7] as floats and back (i a multiple of 8, p 16-byte
+// aligned): one or two 16-byte accesses, the same conversions as the scalar helpers above.
+typedef __attribute__((ext_vector_type(4))) unsigned int v4u32;
+__device__ __forceinline__ void ld8(const float* p, int64_t i, float v[8]) {
+  const v4u32 a = *(const v4u32*)(p + i), b = *(const v4u32*)(p + i + 4);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    v[q] = __uint_as_float(a[q]);
+    v[4 + q] = __uint_as_float(b[q]);
+  }
+}
+__device__ __forceinline__ void ld8(const uint16_t* p, int64_t i, float v[8]) {
+  const v4u32 a = *(const v4u32*)(p + i);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    v[2 * q] = __uint_as_float(a[q] << 16);
+    v[2 * q + 1] = __uint_as_float(a[q] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void st8(float* p, int64_t i, const float v[8]) {
+  v4u32 a, b;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    a[q] = __float_as_uint(v[q]);
+    b[q] = __float_as_uint(v[4 + q]);
+  }
+  *(v4u32*)(p + i) = a;
+  *(v4u32*)(p + i + 4) = b;
+}
+__device__ __forceinline__ void st8(uint16_t* p, int64_t i, const float v[8]) {
+  v4u32 a;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) a[q] = pack_bf16x2(v[2 * q], v[2 * q + 1]);
+  *(v4u32*)(p + i) = a;
+}
+
 }  // namespace mtx

@@ -799,6 +799,78 @@ __global__ __launch_bounds__(256) void unroute_bwd_kernel(
   }
 }
 
+// The same VJP for D % 8 == 0, 16-byte aligned rows and K <= KM: each lane moves eight
+// consecutive elements per access (16-byte loads and stores) and reads its slice of dout once
+// for all K copies of the token, so every byte moves once: N*D of dout, M*D of Y, M*D of dY.
+template <typename GT, typename YT, typename WT, int KM>
+__global__ __launch_bounds__(256) void unroute_bwd_vec_kernel(
+    const GT* __restrict__ dout, const YT* __restrict__ Y, const int32_t* __restrict__ inv,
+    const WT* __restrict__ w, int64_t N, int K, int64_t D, YT* __restrict__ dY, WT* __restrict__ dw) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  if (n >= N) return;
+  const int64_t M = N * (int64_t)K;
+  int64_t j[KM];
+  float wk[KM], dot[KM];
+#pragma unroll
+  for (int k = 0; k < KM; ++k) {
+    j[k] = -1;
+    wk[k] = 0.0f;
+    dot[k] = 0.0f;
+    if (k < K) {
+      const int64_t jj = inv[n * K + k];
+      if (jj >= 0 && jj < M) {  // rows outside [0, M) are skipped, as in the scalar kernel
+        j[k] = jj;
+        wk[k] = ldf<WT>(w, n * K + k);
+      }
+    }
+  }
+  const GT* g_row = dout + n * D;
+  for (int64_t c = (int64_t)lane * 8; c < D; c += 64 * 8) {
+    float g[8];
+    ld8(g_row, c, g);
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+      if (j[k] < 0) continue;
+      float y[8], o[8];
+      ld8(Y + j[k] * D, c, y);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        dot[k] = fmaf(g[q], y[q], dot[k]);
+        o[q] = wk[k] * g[q];
+      }
+      st8(dY + j[k] * D, c, o);
+    }
+  }
+  if (dw) {
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+      if (j[k] < 0) continue;
+      float s = dot[k];
+      for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+      if (lane == 0) stf<WT>(dw, n * K + k, s);
+    }
+  }
+}
+
+template <typename GT, typename YT, typename WT>
+static void launch_unroute_bwd(const void* dout, const void* Y, const int32_t* inv, const void* w, int64_t N, int K,
+                               int64_t D, void* dY, void* dw, hipStream_t st) {
+  const int64_t blocks = ceil_div(N, 4);
+  const bool vec = D % 8 == 0 && K <= 8 && (uintptr_t)dout % 16 == 0 && (uintptr_t)Y % 16 == 0 &&
+                   (uintptr_t)dY % 16 == 0;
+#define MTX_UBV(KM)                                                                                          \
+  hipLaunchKernelGGL((unroute_bwd_vec_kernel<GT, YT, WT, KM>), dim3(blocks), dim3(256), 0, st, (const GT*)dout, \
+                     (const YT*)Y, inv, (const WT*)w, N, K, D, (YT*)dY, (WT*)dw)
+  if (vec && K <= 2) MTX_UBV(2);
+  else if (vec && K <= 4) MTX_UBV(4);
+  else if (vec) MTX_UBV(8);
+  else
+    hipLaunchKernelGGL((unroute_bwd_kernel<GT, YT, WT>), dim3(blocks), dim3(256), 0, st, (const GT*)dout,
+                       (const YT*)Y, inv, (const WT*)w, N, K, D, (YT*)dY, (WT*)dw);
+#undef MTX_UBV
+}
+
 }  // namespace mtx
 
 using namespace mtx;
@@ -1077,12 +1149,10 @@ extern "C" int mtx_unroute_bwd(const void* dout, int g_dtype, const void* sorted
     return MTX_ERR_ARG;
   if (N == 0) return MTX_OK;
   if (!dout || !sorted_output || !inverse || !topk_w || !d_sorted) return MTX_ERR_ARG;
+  if (K > INT32_MAX) return MTX_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
-  const int64_t blocks = ceil_div(N, 4);
   const int k = (int)K;
-#define MTX_UB(GT, YT, WT)                                                                                   \
-  hipLaunchKernelGGL((unroute_bwd_kernel<GT, YT, WT>), dim3(blocks), dim3(256), 0, st, (const GT*)dout,     \
-                     (const YT*)sorted_output, inverse, (const WT*)topk_w, N, k, D, (YT*)d_sorted, (WT*)d_w)
+#define MTX_UB(GT, YT, WT) launch_unroute_bwd<GT, YT, WT>(dout, sorted_output, inverse, topk_w, N, k, D, d_sorted, d_w, st)
   if (g_dtype == MTX_F32) {
     if (y_dtype == MTX_F32) { if (w_dtype == MTX_F32) MTX_UB(float, float, float); else MTX_UB(float, float, uint16_t); }
     else { if (w_dtype == MTX_F32) MTX_UB(float, uint16_t, float); else MTX_UB(float, uint16_t, uint16_t); }

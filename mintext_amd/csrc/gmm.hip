@@ -415,6 +415,64 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const T* __restrict__ h
   }
 }
 
+// Vector forms of the two kernels above for I % 8 == 0 and 16-byte aligned rows: a thread
+// takes eight consecutive columns of a row (16-byte accesses), and a workgroup spreads over
+// 256 / (I/8) rows when a row has fewer than 256 such chunks.  Each element is computed by the
+// same expression as in the scalar kernels, so the results are the same bits.
+struct RowChunks {
+  int cpr, rpb, rsub, c0, cstep;  // chunks per row, rows per workgroup pass, this thread's row and chunk
+  __device__ RowChunks(int64_t I) {
+    cpr = (int)(I / 8);
+    const int t = threadIdx.x;
+    if (cpr >= 256) { rpb = 1; rsub = 0; c0 = t; cstep = 256; }
+    else { rpb = 256 / cpr; rsub = t / cpr; c0 = t % cpr; cstep = cpr; }
+  }
+};
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_vec_kernel(const T* __restrict__ h, int64_t M, int64_t I,
+                                                         T* __restrict__ out) {
+  const RowChunks rc(I);
+  if (rc.rsub >= rc.rpb) return;
+  for (int64_t r = (int64_t)blockIdx.x * rc.rpb + rc.rsub; r < M; r += (int64_t)gridDim.x * rc.rpb)
+    for (int c = rc.c0; c < rc.cpr; c += rc.cstep) {
+      float g[8], u[8], o[8];
+      ld8(h + r * 2 * I, 8 * (int64_t)c, g);
+      ld8(h + r * 2 * I + I, 8 * (int64_t)c, u);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) o[q] = silu_f32(g[q]) * u[q];
+      st8(out + r * I, 8 * (int64_t)c, o);
+    }
+}
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_bwd_vec_kernel(const T* __restrict__ h, const T* __restrict__ dy,
+                                                             int64_t M, int64_t I, T* __restrict__ dh) {
+  const RowChunks rc(I);
+  if (rc.rsub >= rc.rpb) return;
+  for (int64_t r = (int64_t)blockIdx.x * rc.rpb + rc.rsub; r < M; r += (int64_t)gridDim.x * rc.rpb)
+    for (int c = rc.c0; c < rc.cpr; c += rc.cstep) {
+      float g[8], u[8], d[8], dg[8], du[8];
+      ld8(h + r * 2 * I, 8 * (int64_t)c, g);
+      ld8(h + r * 2 * I + I, 8 * (int64_t)c, u);
+      ld8(dy + r * I, 8 * (int64_t)c, d);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const float s = 1.0f / (1.0f + expf(-g[q]));
+        dg[q] = d[q] * u[q] * (s * (1.0f + g[q] * (1.0f - s)));
+        du[q] = d[q] * g[q] * s;
+      }
+      st8(dh + r * 2 * I, 8 * (int64_t)c, dg);
+      st8(dh + r * 2 * I + I, 8 * (int64_t)c, du);
+    }
+}
+// Workgroups for the vector kernels: one pass of rows each, at most 65536 (grid-stride beyond).
+static int64_t swiglu_vec_blocks(int64_t M, int64_t I) {
+  const int64_t cpr = I / 8, rpb = cpr >= 256 ? 1 : 256 / cpr;
+  return std::min<int64_t>(ceil_div(M, rpb), 65536);
+}
+static bool swiglu_vec_ok(int64_t I, const void* a, const void* b, const void* c) {
+  return I % 8 == 0 && I > 0 && (uintptr_t)a % 16 == 0 && (uintptr_t)b % 16 == 0 && (uintptr_t)c % 16 == 0;
+}
+
 // ---- bf16 MFMA path -------------------------------------------------------------------------
 namespace mf {
 
@@ -1752,6 +1810,15 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
 }
 
 static int launch_swiglu(const void* h, int dtype, int64_t M, int64_t I, void* out, hipStream_t st) {
+  if (M > 0 && swiglu_vec_ok(I, h, h, out)) {
+    const int64_t vb = swiglu_vec_blocks(M, I);
+    if (dtype == MTX_F32)
+      hipLaunchKernelGGL(swiglu_vec_kernel<float>, dim3(vb), dim3(256), 0, st, (const float*)h, M, I, (float*)out);
+    else
+      hipLaunchKernelGGL(swiglu_vec_kernel<uint16_t>, dim3(vb), dim3(256), 0, st, (const uint16_t*)h, M, I,
+                         (uint16_t*)out);
+    return check_launch();
+  }
   int64_t blocks = ceil_div(M * I, 256);
   if (blocks > 65536) blocks = 65536;
   if (blocks == 0) return MTX_OK;
@@ -1913,9 +1980,19 @@ extern "C" int mtx_swiglu_bwd(const void* h, const void* dy, int dtype, int64_t 
   if (M < 0 || I < 0 || (dtype != MTX_F32 && dtype != MTX_BF16)) return MTX_ERR_ARG;
   if (M == 0 || I == 0) return MTX_OK;
   if (!h || !dy || !dh) return MTX_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  if (swiglu_vec_ok(I, h, dy, dh)) {
+    const int64_t vb = swiglu_vec_blocks(M, I);
+    if (dtype == MTX_F32)
+      hipLaunchKernelGGL(swiglu_bwd_vec_kernel<float>, dim3(vb), dim3(256), 0, st, (const float*)h,
+                         (const float*)dy, M, I, (float*)dh);
+    else
+      hipLaunchKernelGGL(swiglu_bwd_vec_kernel<uint16_t>, dim3(vb), dim3(256), 0, st, (const uint16_t*)h,
+                         (const uint16_t*)dy, M, I, (uint16_t*)dh);
+    return check_launch();
+  }
   int64_t blocks = ceil_div(M * I, 256);
   if (blocks > 65536) blocks = 65536;
-  hipStream_t st = (hipStream_t)stream;
   if (dtype == MTX_F32)
     hipLaunchKernelGGL(swiglu_bwd_kernel<float>, dim3(blocks), dim3(256), 0, st, (const float*)h, (const float*)dy, M,
                        I, (float*)dh);

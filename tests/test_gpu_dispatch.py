@@ -242,3 +242,71 @@ def test_sort_with_vjp(dev):
     expect = torch.empty_like(g)
     expect[p.long()] = g
     assert torch.equal(x.grad, expect)
+
+
+@pytest.mark.parametrize("N,K,D,ydt", [(257, 1, 512, torch.bfloat16), (300, 2, 1024, torch.bfloat16),
+                                       (129, 3, 264, torch.float32), (64, 8, 2048, torch.bfloat16),
+                                       (65, 9, 512, torch.bfloat16), (70, 2, 100, torch.bfloat16)])
+def test_unroute_bwd_vector_and_scalar_forms(dev, N, K, D, ydt):
+    """mtx_unroute_bwd with f32 dout and weights (the layer's combine output and router weights):
+    d_sorted bit-exact against f32 products rounded to the row dtype, d_w against a float64 sum.
+    D % 8 == 0 with K <= 8 runs the 16-byte vector kernel; K = 9 and D = 100 the scalar one."""
+    from mintext_amd import _lib as L
+    from mintext_amd.kernels import route
+
+    rng = np.random.default_rng(N * 31 + K)
+    E = max(K, 8)
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(N)]).astype(np.int32)
+    _, si, _ = route(_t(np.zeros((N, 8), np.float32), dev), _t(idx, dev), E)
+    inv = O.invert_permutation(si.cpu().numpy()).astype(np.int32)
+    Y = _t(rng.standard_normal((N * K, D)).astype(np.float32), dev, ydt)
+    w = rng.random((N, K)).astype(np.float32)
+    g = rng.standard_normal((N, D)).astype(np.float32)
+    dY = torch.full_like(Y, 7.0)
+    dw = torch.full((N, K), 7.0, dtype=torch.float32, device=dev)
+    wt, gt, it = _t(w, dev), _t(g, dev), _t(inv, dev)
+    L.call("mtx_unroute_bwd", L.ptr(gt), L.MTX_F32, L.ptr(Y), L.dtype_code(ydt), L.ptr(it), L.ptr(wt), L.MTX_F32,
+           N, K, D, L.ptr(dY), L.ptr(dw), L.stream(dev))
+    torch.cuda.synchronize()
+    want = torch.empty((N * K, D), dtype=torch.float32)
+    want[torch.from_numpy(inv).long()] = torch.from_numpy(np.repeat(w.reshape(-1, 1), D, 1) * np.repeat(g, K, axis=0))
+    assert torch.equal(dY.cpu(), want.to(ydt))
+    Yn = Y.float().cpu().numpy().astype(np.float64)
+    dw_ref = np.einsum("nkd,nd->nk", Yn[inv].reshape(N, K, D), g.astype(np.float64))
+    np.testing.assert_allclose(dw.cpu().numpy(), dw_ref, rtol=1e-5, atol=1e-4 * np.sqrt(D))
+
+
+@pytest.mark.parametrize("M,I", [(300, 8), (257, 768), (64, 2048), (33, 2056), (40, 12)])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_swiglu_vector_form_same_bits_as_scalar(dev, M, I, dt):
+    """mtx_swiglu / mtx_swiglu_bwd: the 16-byte vector kernels (I % 8 == 0, aligned rows) give the
+    bits of the scalar kernels, which run on a copy of the same data one element past a 16-byte
+    boundary; both within
+    rounding of the float64 oracle.  I = 12 runs the scalar kernels only."""
+    from mintext_amd import _lib as L
+
+    rng = np.random.default_rng(M + I)
+    h_np = (rng.standard_normal((M, 2 * I)) * 4).astype(np.float32)
+    dy_np = rng.standard_normal((M, I)).astype(np.float32)
+
+    def at_offset(a):  # the same values at a data pointer one element past a 16-byte boundary
+        flat = torch.empty(a.numel() + 8, dtype=dt, device=dev)
+        v = flat[1:1 + a.numel()].view(a.shape)
+        v.copy_(a)
+        return v
+
+    h = _t(h_np, dev, dt)
+    dy = _t(dy_np, dev, dt)
+    outs = []
+    for hh, dd in ((h, dy), (at_offset(h), at_offset(dy))):
+        y = torch.empty((M, I), dtype=dt, device=dev)
+        dh = torch.empty((M, 2 * I), dtype=dt, device=dev)
+        L.call("mtx_swiglu", L.ptr(hh), L.dtype_code(dt), M, I, L.ptr(y), L.stream(dev))
+        L.call("mtx_swiglu_bwd", L.ptr(hh), L.ptr(dd), L.dtype_code(dt), M, I, L.ptr(dh), L.stream(dev))
+        outs.append((y, dh))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    tol = 1e-5 if dt == torch.float32 else 2e-2
+    hf, dyf = h.float().cpu().numpy(), dy.float().cpu().numpy()
+    assert rel_err(outs[0][0].float().cpu().numpy(), O.swiglu(hf)) < tol
+    assert rel_err(outs[0][1].float().cpu().numpy(), O.swiglu_bwd(hf, dyf)) < tol
