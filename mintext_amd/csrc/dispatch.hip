@@ -802,13 +802,18 @@ __global__ __launch_bounds__(256) void unroute_bwd_kernel(
 // The same VJP for D % 8 == 0, 16-byte aligned rows and K <= KM: each lane moves eight
 // consecutive elements per access (16-byte loads and stores) and reads its slice of dout once
 // for all K copies of the token, so every byte moves once: N*D of dout, M*D of Y, M*D of dY.
-template <typename GT, typename YT, typename WT, int KM>
+// WPT waves share a token (its 16-byte chunks dealt round-robin), for more loads in flight per
+// token; their partial d_w sums are added in wave order through LDS.
+template <typename GT, typename YT, typename WT, int KM, int WPT>
 __global__ __launch_bounds__(256) void unroute_bwd_vec_kernel(
     const GT* __restrict__ dout, const YT* __restrict__ Y, const int32_t* __restrict__ inv,
     const WT* __restrict__ w, int64_t N, int K, int64_t D, YT* __restrict__ dY, WT* __restrict__ dw) {
-  const int lane = threadIdx.x & 63;
-  const int64_t n = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  if (n >= N) return;
+  static_assert(WPT == 1 || WPT == 2 || WPT == 4, "waves per token");
+  __shared__ float s_dot[4][KM];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int part = wave % WPT;
+  const int64_t n = (int64_t)blockIdx.x * (4 / WPT) + wave / WPT;
+  const bool live = n < N;  // no early return: the waves meet at a barrier below
   const int64_t M = N * (int64_t)K;
   int64_t j[KM];
   float wk[KM], dot[KM];
@@ -817,7 +822,7 @@ __global__ __launch_bounds__(256) void unroute_bwd_vec_kernel(
     j[k] = -1;
     wk[k] = 0.0f;
     dot[k] = 0.0f;
-    if (k < K) {
+    if (live && k < K) {
       const int64_t jj = inv[n * K + k];
       if (jj >= 0 && jj < M) {  // rows outside [0, M) are skipped, as in the scalar kernel
         j[k] = jj;
@@ -825,43 +830,69 @@ __global__ __launch_bounds__(256) void unroute_bwd_vec_kernel(
       }
     }
   }
-  const GT* g_row = dout + n * D;
-  for (int64_t c = (int64_t)lane * 8; c < D; c += 64 * 8) {
-    float g[8];
-    ld8(g_row, c, g);
+  if (live) {
+    const GT* g_row = dout + n * D;
+    for (int64_t c = ((int64_t)part * 64 + lane) * 8; c < D; c += 64 * 8 * WPT) {
+      float g[8];
+      ld8(g_row, c, g);
 #pragma unroll
-    for (int k = 0; k < KM; ++k) {
-      if (j[k] < 0) continue;
-      float y[8], o[8];
-      ld8(Y + j[k] * D, c, y);
+      for (int k = 0; k < KM; ++k) {
+        if (j[k] < 0) continue;
+        float y[8], o[8];
+        ld8(Y + j[k] * D, c, y);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        dot[k] = fmaf(g[q], y[q], dot[k]);
-        o[q] = wk[k] * g[q];
+        for (int q = 0; q < 8; ++q) {
+          dot[k] = fmaf(g[q], y[q], dot[k]);
+          o[q] = wk[k] * g[q];
+        }
+        st8(dY + j[k] * D, c, o);
       }
-      st8(dY + j[k] * D, c, o);
     }
   }
-  if (dw) {
+  if (!dw) return;  // uniform: a kernel argument
 #pragma unroll
-    for (int k = 0; k < KM; ++k) {
-      if (j[k] < 0) continue;
-      float s = dot[k];
-      for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-      if (lane == 0) stf<WT>(dw, n * K + k, s);
+  for (int k = 0; k < KM; ++k) {
+    float s = dot[k];
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    dot[k] = s;
+  }
+  if (WPT > 1) {
+    if (lane == 0) {
+#pragma unroll
+      for (int k = 0; k < KM; ++k) s_dot[wave][k] = dot[k];
     }
+    __syncthreads();
+    if (part == 0) {
+#pragma unroll
+      for (int k = 0; k < KM; ++k) {
+        float s = s_dot[wave][k];
+        for (int p = 1; p < WPT; ++p) s += s_dot[wave + p][k];
+        dot[k] = s;
+      }
+    }
+  }
+  if (live && part == 0 && lane == 0) {
+#pragma unroll
+    for (int k = 0; k < KM; ++k)
+      if (j[k] >= 0) stf<WT>(dw, n * K + k, dot[k]);
   }
 }
 
+// Waves per token of the vector kernel.  Measured on the C2 / C3 / C4 shapes (f32 dout, bf16
+// rows): 1 wave 87 / 218 / 293 us, 2 waves 84 / 220 / 262 us, 4 waves 81 / 229 / 265 us.
+#ifndef MTX_UB_WPT
+#define MTX_UB_WPT 2
+#endif
 template <typename GT, typename YT, typename WT>
 static void launch_unroute_bwd(const void* dout, const void* Y, const int32_t* inv, const void* w, int64_t N, int K,
                                int64_t D, void* dY, void* dw, hipStream_t st) {
   const int64_t blocks = ceil_div(N, 4);
   const bool vec = D % 8 == 0 && K <= 8 && (uintptr_t)dout % 16 == 0 && (uintptr_t)Y % 16 == 0 &&
                    (uintptr_t)dY % 16 == 0;
-#define MTX_UBV(KM)                                                                                          \
-  hipLaunchKernelGGL((unroute_bwd_vec_kernel<GT, YT, WT, KM>), dim3(blocks), dim3(256), 0, st, (const GT*)dout, \
-                     (const YT*)Y, inv, (const WT*)w, N, K, D, (YT*)dY, (WT*)dw)
+  constexpr int WPT = MTX_UB_WPT;
+#define MTX_UBV(KM)                                                                                             \
+  hipLaunchKernelGGL((unroute_bwd_vec_kernel<GT, YT, WT, KM, WPT>), dim3(ceil_div(N, 4 / WPT)), dim3(256), 0, st, \
+                     (const GT*)dout, (const YT*)Y, inv, (const WT*)w, N, K, D, (YT*)dY, (WT*)dw)
   if (vec && K <= 2) MTX_UBV(2);
   else if (vec && K <= 4) MTX_UBV(4);
   else if (vec) MTX_UBV(8);
