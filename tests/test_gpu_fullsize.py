@@ -11,6 +11,8 @@ must agree bit for bit), and checks sampled rows of every stage against the floa
 * C4 (Qwen3, fp8): token-order 1x128 quantiser -> fp8 gate_up + SwiGLU + re-quantisation on the
   gathered rows -> fp8 down at K_in = 768 -> combine;
 * C5 (Qwen3 backward, bf16, Zipf-skewed loads): dlhs of both expert GEMMs and both tgmm.
+* the study of the layer's HBM-bound backward kernels (``bench.py --study dispatch-bwd``, C2 /
+  C3 / C4 shapes): the combine and route VJPs, SwiGLU and its VJP.
 
 Sampled rows cover every expert's first and last rows (partial m-tiles) and random interior
 rows; tolerances are the north-star ones (bf16 2e-2, fp8 6e-2 against the unquantised product
@@ -344,3 +346,76 @@ def test_c5_qwen3_backward_full_size(dev, loads):
         ref_d = _host(st[r0:r1][:, torch.from_numpy(kd).to(dev)]).T @ _host(gh[r0:r1][:, torch.from_numpy(nd).to(dev)])
         assert rel_err(got_c, ref_c) < 2e-2, f"tgmm (down) expert {e}"
         assert rel_err(got_d, ref_d) < 2e-2, f"tgmm (gate_up) expert {e}"
+
+
+@pytest.mark.parametrize("cfg", ["mixtral", "deepseek", "qwen3"])
+def test_dispatch_bwd_study_flows_full_size(dev, cfg):
+    """The calls ``bench.py --study dispatch-bwd`` times, at its shapes: the combine VJP
+    (mtx_unroute_bwd, f32 dout and weights, bf16 rows) with d_sorted bit-exact over the whole
+    array against f32 products rounded to bf16 and d_weights within 1e-5 (plus a sqrt(D)-scaled
+    absolute term) of float64 on sampled tokens; the route VJP (mtx_unroute, unit weights, bf16)
+    within one bf16 rounding (plus the f32 sum's own rounding) of float64 on sampled tokens; SwiGLU and its VJP (bf16) bit-identical
+    between the 16-byte vector kernels and the scalar kernels over the whole array (the scalar
+    ones on a copy one element past a 16-byte boundary) and within 2e-2 of the oracle on sampled
+    rows."""
+    from mintext_amd import _lib as L
+
+    c = _bench().DISPATCH_BWD_CONFIGS[cfg]
+    N, K, D, I = c["N"], c["K"], c["D"], c["I"]
+    M = N * K
+    st = L.stream(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    inv = torch.randperm(M, device=dev, generator=g).int()
+    w = torch.rand(N, K, device=dev, generator=g)
+    dout = torch.randn(N, D, device=dev, generator=g)
+    Y = torch.randn(M, D, device=dev, generator=g).bfloat16()
+    dY = torch.empty_like(Y)
+    dw = torch.empty_like(w)
+    dx = torch.empty(N, D, dtype=torch.bfloat16, device=dev)
+    L.call("mtx_unroute_bwd", L.ptr(dout), L.MTX_F32, L.ptr(Y), L.MTX_BF16, L.ptr(inv), L.ptr(w), L.MTX_F32,
+           N, K, D, L.ptr(dY), L.ptr(dw), st)
+    L.call("mtx_unroute", L.ptr(Y), L.MTX_BF16, L.ptr(inv), None, L.MTX_F32, N, K, D, L.ptr(dx), L.MTX_BF16, st)
+    torch.cuda.synchronize()
+    invc = inv.long().cpu()
+    want = torch.empty(M, D, dtype=torch.float32)
+    want[invc] = (w.cpu().reshape(-1, 1) * dout.cpu().repeat_interleave(K, dim=0))
+    assert torch.equal(dY.cpu(), want.to(torch.bfloat16))
+    del want
+    rng = np.random.default_rng(0)
+    toks = np.unique(np.concatenate([[0, N - 1], rng.integers(0, N, 254)]))
+    rows = invc.reshape(N, K)[toks]                           # [t, K] sorted rows of each sampled token
+    Yt = _host(Y[rows.reshape(-1).to(dev)]).reshape(len(toks), K, D)
+    dw_ref = np.einsum("tkd,td->tk", Yt, _host(dout[torch.from_numpy(toks).to(dev)]))
+    np.testing.assert_allclose(_host(dw[torch.from_numpy(toks).to(dev)]), dw_ref, rtol=1e-5, atol=1e-5 * np.sqrt(D))
+    dx_ref = Yt.sum(axis=1)
+    got = _host(dx[torch.from_numpy(toks).to(dev)])
+    # one bf16 rounding of the f32 sum of K bf16 values (the f32 sum itself exact but for
+    # operands whose exponents differ by more than f32's mantissa allows)
+    bound = 2.0 ** -8 * np.abs(dx_ref) + K * 2.0 ** -22 * np.abs(Yt).max(axis=1)
+    assert np.all(np.abs(got - dx_ref) <= bound)
+    del inv, w, dout, Y, dY, dw, dx
+
+    h = torch.randn(M, 2 * I, device=dev, generator=g).bfloat16()
+    dy = torch.randn(M, I, device=dev, generator=g).bfloat16()
+
+    def at_offset(a):
+        flat = torch.empty(a.numel() + 8, dtype=a.dtype, device=dev)
+        v = flat[1:1 + a.numel()].view(a.shape)
+        v.copy_(a)
+        return v
+
+    outs = []
+    for hh, dd in ((h, dy), (at_offset(h), at_offset(dy))):
+        y = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+        dh = torch.empty(M, 2 * I, dtype=torch.bfloat16, device=dev)
+        L.call("mtx_swiglu", L.ptr(hh), L.MTX_BF16, M, I, L.ptr(y), st)
+        L.call("mtx_swiglu_bwd", L.ptr(hh), L.ptr(dd), L.MTX_BF16, M, I, L.ptr(dh), st)
+        outs.append((y, dh))
+        del hh, dd
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    sr = torch.from_numpy(np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, 126)]))).to(dev)
+    hs, dys = _host(h[sr]), _host(dy[sr])
+    assert rel_err(_host(outs[0][0][sr]), O.swiglu(hs)) < 2e-2
+    assert rel_err(_host(outs[0][1][sr]), O.swiglu_bwd(hs, dys)) < 2e-2
