@@ -244,13 +244,19 @@ def test_sort_with_vjp(dev):
     assert torch.equal(x.grad, expect)
 
 
-@pytest.mark.parametrize("N,K,D,ydt", [(257, 1, 512, torch.bfloat16), (300, 2, 1024, torch.bfloat16),
-                                       (129, 3, 264, torch.float32), (64, 8, 2048, torch.bfloat16),
-                                       (65, 9, 512, torch.bfloat16), (70, 2, 100, torch.bfloat16)])
-def test_unroute_bwd_vector_and_scalar_forms(dev, N, K, D, ydt):
-    """mtx_unroute_bwd with f32 dout and weights (the layer's combine output and router weights):
-    d_sorted bit-exact against f32 products rounded to the row dtype, d_w against a float64 sum.
-    D % 8 == 0 with K <= 8 runs the 16-byte vector kernel; K = 9 and D = 100 the scalar one."""
+_F32, _BF16 = torch.float32, torch.bfloat16
+
+
+@pytest.mark.parametrize("N,K,D,ydt,gdt,wdt", [(257, 1, 512, _BF16, _F32, _F32), (300, 2, 1024, _BF16, _F32, _F32),
+                                               (129, 3, 264, _F32, _F32, _F32), (64, 8, 2048, _BF16, _F32, _F32),
+                                               (65, 9, 512, _BF16, _F32, _F32), (70, 2, 100, _BF16, _F32, _F32),
+                                               (200, 2, 512, _BF16, _BF16, _BF16), (100, 8, 256, _BF16, _BF16, _F32),
+                                               (90, 4, 136, _F32, _BF16, _BF16)])
+def test_unroute_bwd_vector_and_scalar_forms(dev, N, K, D, ydt, gdt, wdt):
+    """mtx_unroute_bwd (the layer's combine output and router weights as dout / w, in f32 or bf16):
+    d_sorted bit-exact against the f32 products of the inputs rounded to the row dtype, d_w against
+    a float64 sum (rounded to bf16 when w is bf16).  D % 8 == 0 with K <= 8 runs the 16-byte vector
+    kernel; K = 9 and D = 100 the scalar one."""
     from mintext_amd import _lib as L
     from mintext_amd.kernels import route
 
@@ -260,20 +266,23 @@ def test_unroute_bwd_vector_and_scalar_forms(dev, N, K, D, ydt):
     _, si, _ = route(_t(np.zeros((N, 8), np.float32), dev), _t(idx, dev), E)
     inv = O.invert_permutation(si.cpu().numpy()).astype(np.int32)
     Y = _t(rng.standard_normal((N * K, D)).astype(np.float32), dev, ydt)
-    w = rng.random((N, K)).astype(np.float32)
-    g = rng.standard_normal((N, D)).astype(np.float32)
+    wt = _t(rng.random((N, K)).astype(np.float32), dev, wdt)
+    gt = _t(rng.standard_normal((N, D)).astype(np.float32), dev, gdt)
+    w = wt.float().cpu().numpy()  # the values the kernel reads, as f32
+    g = gt.float().cpu().numpy()
     dY = torch.full_like(Y, 7.0)
-    dw = torch.full((N, K), 7.0, dtype=torch.float32, device=dev)
-    wt, gt, it = _t(w, dev), _t(g, dev), _t(inv, dev)
-    L.call("mtx_unroute_bwd", L.ptr(gt), L.MTX_F32, L.ptr(Y), L.dtype_code(ydt), L.ptr(it), L.ptr(wt), L.MTX_F32,
-           N, K, D, L.ptr(dY), L.ptr(dw), L.stream(dev))
+    dw = torch.full((N, K), 7.0, dtype=wdt, device=dev)
+    it = _t(inv, dev)
+    L.call("mtx_unroute_bwd", L.ptr(gt), L.dtype_code(gdt), L.ptr(Y), L.dtype_code(ydt), L.ptr(it), L.ptr(wt),
+           L.dtype_code(wdt), N, K, D, L.ptr(dY), L.ptr(dw), L.stream(dev))
     torch.cuda.synchronize()
     want = torch.empty((N * K, D), dtype=torch.float32)
     want[torch.from_numpy(inv).long()] = torch.from_numpy(np.repeat(w.reshape(-1, 1), D, 1) * np.repeat(g, K, axis=0))
     assert torch.equal(dY.cpu(), want.to(ydt))
     Yn = Y.float().cpu().numpy().astype(np.float64)
     dw_ref = np.einsum("nkd,nd->nk", Yn[inv].reshape(N, K, D), g.astype(np.float64))
-    np.testing.assert_allclose(dw.cpu().numpy(), dw_ref, rtol=1e-5, atol=1e-4 * np.sqrt(D))
+    rtol = 1e-5 if wdt == _F32 else 2.0 ** -8  # bf16 d_w: one rounding of the f32 sum
+    np.testing.assert_allclose(dw.float().cpu().numpy(), dw_ref, rtol=rtol, atol=1e-4 * np.sqrt(D))
 
 
 @pytest.mark.parametrize("M,I", [(300, 8), (257, 768), (64, 2048), (33, 2056), (40, 12)])
