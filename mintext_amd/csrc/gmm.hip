@@ -1561,6 +1561,356 @@ __global__ __launch_bounds__(512, 2) void gmm_v4p_kernel(Args p) {
   __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));  // the last steps' re-read loads land before exit
 }
 
+// ---- w4: one wave per SIMD (FWD / SWIGLU / DLHS, 256x256 tiles) ------------------------------------
+// The v3 tile, ring, DMA layouts, fragment reads and MFMA order with 4 waves instead of 8: a wave
+// owns a 128x128 quarter of the tile (16 accumulator blocks, which live in the AGPRs), so each
+// SIMD runs one wave that interleaves its own fragment reads with its MFMAs instead of sharing the
+// MFMA pipe with a second wave behind a per-stage barrier, and the fragment reads per stage drop
+// from 96 KB to 64 KB per CU.  Every output element gets the MFMA sequence of gmm_v3_kernel
+// (operands swapped, k in ring order), hence the same bits.  A tile with at most 128 rows of its
+// group runs the thin form instead: the four waves split the 256 columns (128x64 wave tiles, the
+// v3 wave tile) over the tile's ceil(rows/32) row blocks only, and the ring loads 128 A rows.
+namespace w4 {
+constexpr int NT = 256, BM = 256, BN = 256, NSTAGE = 4, PD = 3;
+constexpr int A_BYTES = BM * v3::BKS * 2, STAGE = A_BYTES + BN * v3::BKS * 2;  // 16 + 16 KB
+
+struct Tile {
+  int e, r0, r1, n_tile;
+  int piece, npieces, split_u;  // k-piece of a split tail tile (1 piece: whole tile)
+};
+
+// One tile with TM x TN 32x32 accumulator blocks per wave.  THIN: wave w owns the 32-column blocks
+// of the tile's columns [64w, 64w + 64) (SwiGLU: gate block and its up block), rows 0 .. 32 TM.
+template <int MODE, int EPI, int TM, int TN, bool THIN>
+__device__ __forceinline__ void tile(const Args& p, char* lds, int* s_last, const Tile& t) {
+  using v3::a_off;
+  using v3::bn_off;
+  using v3::BKS;
+  constexpr int A_ROWS = THIN ? 128 : 256;
+  constexpr int A_INSTR = A_ROWS * BKS * 2 / 1024 / 4;  // 1 KB load instructions per wave per stage
+  constexpr int B_INSTR = 4;
+  constexpr int LPS = A_INSTR + B_INSTR;
+  constexpr bool B_T = (MODE == FWD);  // B stage stored [reduction][col] (transpose reads)
+  static_assert(EPI != EPI_SWIGLU || TN % 2 == 0, "SwiGLU pairs gate/up blocks");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = THIN ? 0 : (wave >> 1);
+  const int wn = THIN ? wave : (wave & 1);
+  const int e = t.e, r0 = t.r0, r1 = t.r1, n_tile = t.n_tile, col0 = n_tile * BN;
+  // tile-local column of the wave's 32-column block j; SwiGLU pairs gate block j with up block
+  // j + TN/2 (64 tile columns further: the B stage holds, per 128 columns, 64 gate then 64 up)
+  auto cbase = [&](int j) -> int {
+    if constexpr (THIN) {
+      if constexpr (EPI == EPI_SWIGLU) return (wn >> 1) * 128 + (wn & 1) * 32 + j * 64;
+      return wn * 64 + j * 32;
+    }
+    return wn * 128 + j * 32;
+  };
+
+  const int nk_all = p.Kred / BKS;
+  const int kb0 = t.piece * nk_all / t.npieces;
+  const int nk = (t.piece + 1) * nk_all / t.npieces - kb0;
+
+  // ---- per-lane global byte offsets of the ring loads at k-stage 0 (the v3 layouts) ---------
+  uint32_t aoff[A_INSTR], boff[B_INSTR];
+#pragma unroll
+  for (int i = 0; i < A_INSTR; ++i) {
+    const int seg = wave * A_INSTR + i;
+    const int r = seg * 16 + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
+    int gr = r0 + r;
+    gr = gr < r1 ? gr : r1 - 1;  // rows past the group repeat its last row: never used, cache hits
+    if (MODE == FWD && p.gather) gr = min(max(p.gather[gr], 0) / p.gather_div, p.gather_rows - 1);
+    aoff[i] = ((uint32_t)gr * (uint32_t)p.Kred + (uint32_t)(c * 8)) * 2u;
+  }
+#pragma unroll
+  for (int i = 0; i < B_INSTR; ++i) {
+    const int seg = wave * B_INSTR + i;
+    if constexpr (B_T) {
+      const int k = seg * 2 + (lane >> 5), c = (lane & 31) ^ ((k & 3) << 2);
+      const int tc = c * 8;
+      int gc;
+      if constexpr (EPI == EPI_SWIGLU) {
+        const int w_ = tc >> 7, within = tc & 127;
+        gc = (within >> 6) * p.I + n_tile * (BN / 2) + w_ * 64 + (within & 63);
+      } else {
+        gc = col0 + tc;
+      }
+      boff[i] = ((uint32_t)k * (uint32_t)p.N + (uint32_t)gc) * 2u;
+    } else {
+      const int r = seg * 16 + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
+      boff[i] = ((uint32_t)(col0 + r) * (uint32_t)p.Kred + (uint32_t)(c * 8)) * 2u;
+    }
+  }
+  const char* Ab = (const char*)p.A;
+  const char* Bb = (const char*)(p.B + (int64_t)e * p.Kred * p.N);
+  const int64_t b_step = B_T ? (int64_t)BKS * p.N * 2 : (int64_t)BKS * 2;
+  const uint32_t lds_base = lds_addr(lds);
+  const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+  // stages past the end re-read the last one into a slot that is no longer read (branch-free)
+  auto issue_stage = [&](int kt_) {
+    const uint32_t st = lds_base + (uint32_t)((kt_ & (NSTAGE - 1)) * STAGE);
+    const int kt = kb0 + min(kt_, nk - 1);
+    const char* a = Ab + (int64_t)kt * (BKS * 2);
+#pragma unroll
+    for (int i = 0; i < A_INSTR; ++i) gload_lds16_s(a, aoff[i], st + (wave_u * A_INSTR + i) * 1024u);
+    const char* b = Bb + (int64_t)kt * b_step;
+#pragma unroll
+    for (int i = 0; i < B_INSTR; ++i) gload_lds16_s(b, boff[i], st + (uint32_t)A_BYTES + (wave_u * B_INSTR + i) * 1024u);
+  };
+
+  // ---- fragments ------------------------------------------------------------------------------
+  bf16x8 fa[2][TM], fb[2][TN];
+  const int frow = lane & 31, fhalf = lane >> 5;
+  auto read_tr = [&](const char* region, int c0, int kk) -> bf16x8 {
+    const int n = c0 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const int k = kk * 16 + 8 * fhalf + ((lane & 15) >> 2);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(region + bn_off(k, n >> 3) + (n & 7) * 2));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(region + bn_off(k + 4, n >> 3) + (n & 7) * 2));
+    const s16x4 both[2] = {lo, hi};
+    return __builtin_bit_cast(bf16x8, both);
+  };
+  auto read_frags = [&](int kt, int kk, int buf) {
+    const char* st = lds + (kt & (NSTAGE - 1)) * STAGE;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[buf][i] = *(const bf16x8*)(st + a_off(wm * 128 + i * 32 + frow, kk * 2 + fhalf));
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      if constexpr (B_T) fb[buf][j] = read_tr(st + A_BYTES, cbase(j), kk);
+      else fb[buf][j] = *(const bf16x8*)(st + A_BYTES + a_off(cbase(j) + frow, kk * 2 + fhalf));
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  // One load instruction of a ring stage: d < A_INSTR loads A, the rest B.
+  auto issue_one = [&](int kt_, int d) {
+    const uint32_t st = lds_base + (uint32_t)((kt_ & (NSTAGE - 1)) * STAGE);
+    const int kt = kb0 + min(kt_, nk - 1);
+    if (d < A_INSTR) {
+      gload_lds16_s(Ab + (int64_t)kt * (BKS * 2), aoff[d], st + (wave_u * A_INSTR + d) * 1024u);
+    } else {
+      const int i = d - A_INSTR;
+      gload_lds16_s(Bb + (int64_t)kt * b_step, boff[i], st + (uint32_t)A_BYTES + (wave_u * B_INSTR + i) * 1024u);
+    }
+  };
+  // fragment slot r of a substep: r < TM reads A block r, else B block r - TM
+  auto read_one = [&](int kt, int kk, int buf, int r) {
+    const char* st = lds + (kt & (NSTAGE - 1)) * STAGE;
+    if (r < TM) {
+      fa[buf][r] = *(const bf16x8*)(st + a_off(wm * 128 + r * 32 + frow, kk * 2 + fhalf));
+    } else {
+      const int j = r - TM;
+      if constexpr (B_T) fb[buf][j] = read_tr(st + A_BYTES, cbase(j), kk);
+      else fb[buf][j] = *(const bf16x8*)(st + A_BYTES + a_off(cbase(j) + frow, kk * 2 + fhalf));
+    }
+  };
+
+  // prologue: stages 0..PD-1 in flight, stages 0 and 1 landed and visible
+#pragma unroll
+  for (int s = 0; s < PD; ++s) issue_stage(s);
+  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
+  __syncthreads();
+  read_frags(0, 0, 0);
+  // Each stage is 2 x S MFMA slots in a fixed order: slot q issues one MFMA, then one fragment read
+  // of the other buffer (substep 1 of this stage during substep 0, substep 0 of the next stage
+  // during substep 1), and the stage's LPS ring loads are spread evenly over the slots, so that the
+  // single wave of the SIMD never stalls its MFMA issue on a burst of loads (+4-5 % on the Mixtral
+  // shapes against issuing them together at the top of the stage).
+  constexpr int S = TM * TN;
+  for (int kt = 0; kt < nk; ++kt) {
+#pragma unroll
+    for (int q = 0; q < 2 * S; ++q) {
+      const int sub = q / S, qq = q % S;
+      const int i = qq / TN, j = qq % TN;
+      __builtin_amdgcn_sched_barrier(0);
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[sub][j], fa[sub][i], acc[i][j], 0, 0, 0);
+      // fragment r goes in slot min(r, S-1): a substep with fewer MFMAs than fragments (TM = 1)
+      // reads the rest in its last slot
+#pragma unroll
+      for (int r = 0; r < TM + TN; ++r) {
+        if (min(r, S - 1) != qq) continue;
+        if (sub == 0) read_one(kt, 1, 1, r);
+        else read_one(kt + 1, 0, 0, r);  // visible since the last barrier (last step: an unused re-read)
+      }
+#pragma unroll
+      for (int d = 0; d < LPS; ++d)
+        if ((d * 2 * S) / LPS == q) issue_one(kt + PD, d);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // stage kt+2 landed before the barrier makes it visible; a bare s_barrier (the slot refilled
+    // next held stage kt, whose fragments this iteration's MFMAs consumed)
+    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
+    __builtin_amdgcn_s_barrier();
+  }
+  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));  // no ring load may land after the ring is reused
+
+  if (t.npieces > 1) {
+    // split tail piece: as in gmm_v3_kernel (partials in piece order, summed by the last arrival)
+    typedef __attribute__((ext_vector_type(4))) float f32x4;
+    constexpr int64_t SLOT4 = kSplitSlotFloats / 4;
+    static_assert(TM * TN * 4 * NT <= SLOT4, "split slot");
+    const int xcd_e = (int)(blockIdx.x & 7);
+    f32x4* part = (f32x4*)(p.split_part + (int64_t)(xcd_e * kSplitItems + t.split_u * t.npieces) * kSplitSlotFloats);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          part[t.piece * SLOT4 + ((i * TN + j) * 4 + g) * NT + tid] =
+              f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (tid == 0)
+      *s_last = __hip_atomic_fetch_add(p.split_cnt + xcd_e * kSplitMaxRem + t.split_u, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == t.npieces - 1;
+    __syncthreads();
+    if (!*s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+#pragma unroll
+    for (int s2 = 0; s2 < kSplitMaxS; ++s2) {
+      if (s2 >= t.npieces) break;
+      const f32x4* src = part + s2 * SLOT4;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const f32x4 v = src[((i * TN + j) * 4 + g) * NT + tid];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[i][j][4 * g + c] = (s2 == 0) ? v[c] : acc[i][j][4 * g + c] + v[c];
+          }
+    }
+  }
+
+  // ---- epilogue: acc[i][j][4g+q] of lane l is C[row i*32 + l%32][col cbase(j) + 8g + 4(l/32) + q];
+  // the tile is staged in the idle ring as bf16 rows (16-byte chunk c of row r at c ^ (r & 15)) and
+  // written back with 16 contiguous bytes per lane, whole 128-byte lines per row.
+  constexpr int OCOLS = (EPI == EPI_SWIGLU) ? BN / 2 : BN;
+  constexpr int OROW = OCOLS * 2, OCH = OROW / 16;
+  static_assert(A_ROWS * OROW <= NSTAGE * STAGE, "staging fits the ring");
+  auto stage4 = [&](int r, int col, bf16x4 v) {
+    const int c = col >> 3;
+    *(bf16x4*)(lds + r * OROW + ((c ^ (r & 15)) << 4) + (col & 7) * 2) = v;
+  };
+  __syncthreads();  // every wave is done with the ring
+  {
+    const int h4 = 4 * fhalf;
+    if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN / 2; ++j) {
+          const int cg = cbase(j), ocol = (cg >> 7) * 64 + (cg & 127);  // gate column -> output column
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const f32x16& gt = acc[i][j];
+            const f32x16& up = acc[i][j + TN / 2];
+            stage4(wm * 128 + i * 32 + frow, ocol + 8 * g + h4,
+                   bf16x4{(__bf16)swiglu_fast(gt[4 * g], up[4 * g]), (__bf16)swiglu_fast(gt[4 * g + 1], up[4 * g + 1]),
+                          (__bf16)swiglu_fast(gt[4 * g + 2], up[4 * g + 2]),
+                          (__bf16)swiglu_fast(gt[4 * g + 3], up[4 * g + 3])});
+          }
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            stage4(wm * 128 + i * 32 + frow, cbase(j) + 8 * g + h4,
+                   bf16x4{(__bf16)acc[i][j][4 * g], (__bf16)acc[i][j][4 * g + 1], (__bf16)acc[i][j][4 * g + 2],
+                          (__bf16)acc[i][j][4 * g + 3]});
+    }
+  }
+  __syncthreads();
+  uint16_t* obase = p.C + ((EPI == EPI_SWIGLU) ? n_tile * (BN / 2) : col0);
+  const int nrows = min(r1 - r0, A_ROWS);
+  constexpr int RPI = 64 / OCH;  // rows per wave instruction
+  for (int rr = wave * RPI + lane / OCH; rr < nrows; rr += NT / OCH) {
+    const int c = lane % OCH;
+    const u32x4 v = *(const u32x4*)(lds + rr * OROW + ((c ^ (rr & 15)) << 4));
+    *(u32x4*)(obase + (int64_t)(r0 + rr) * p.ldc + c * 8) = v;
+  }
+}
+}  // namespace w4
+
+template <int MODE, int EPI>
+__global__ __launch_bounds__(256, 1) void gmm_w4_kernel(Args p) {
+  static_assert(MODE == FWD || MODE == DLHS, "w4 mode");
+  __shared__ __attribute__((aligned(1024))) char lds[w4::NSTAGE * w4::STAGE];
+  __shared__ int s_last;
+  constexpr int BN = w4::BN, NT = w4::NT;
+  const int tid = threadIdx.x;
+  // ---- which output tile (the v3 order: XCD-contiguous ranges, gm m-tiles per group, split tail)
+  w4::Tile t;
+  t.piece = 0;
+  t.npieces = 1;
+  t.split_u = 0;
+  const int nn = (EPI == EPI_SWIGLU) ? (p.I / (BN / 2)) : (p.N / BN);
+  const int cnt = p.count[0];
+  const int total = cnt * nn;
+  const int pid = blockIdx.x;
+  const int total8 = (total + 7) & ~7;
+  const int xcd = pid & 7, q = pid >> 3, per = total8 >> 3;
+  int lid;
+  if (EPI == EPI_STORE && p.split_on) {
+    const int tx = max(0, min(per, total - xcd * per));
+    const int rem = tx % p.ncu_x;
+    int S = (rem > 0 && rem <= kSplitMaxRem && 2 * rem <= p.ncu_x) ? min(kSplitMaxS, p.ncu_x / rem) : 1;
+    S = min(S, max(p.Kred / v3::BKS, 1));
+    const int nwhole = (S > 1) ? tx - rem : tx;
+    if (q >= nwhole + (S > 1 ? rem * S : 0)) return;
+    if (q < nwhole) {
+      lid = xcd * per + q;
+    } else {
+      t.split_u = (q - nwhole) / S;
+      t.piece = (q - nwhole) % S;
+      t.npieces = S;
+      lid = xcd * per + nwhole + t.split_u;
+    }
+  } else {
+    if (pid >= total8) return;
+    lid = xcd * per + q;
+    if (lid >= total) return;
+  }
+  const int GM = p.gm;
+  const int grp = lid / (GM * nn);
+  const int first_m = grp * GM;
+  const int gsz = min(GM, cnt - first_m);
+  const int local = lid - grp * GM * nn;
+  const MTile mt = p.tiles[first_m + local % gsz];
+  t.e = mt.e;
+  t.r0 = mt.r0;
+  t.r1 = mt.r1;
+  t.n_tile = local / gsz;
+  if (t.e < 0) {  // rows past sum(group_sizes): zeros
+    if (t.piece > 0) return;
+    const int ncols = (EPI == EPI_SWIGLU) ? BN / 2 : BN;
+    const int c0 = t.n_tile * ncols;
+    for (int i = tid; i < w4::BM * ncols; i += NT) {
+      const int r = t.r0 + i / ncols;
+      if (r < t.r1) p.C[(int64_t)r * p.ldc + c0 + i % ncols] = 0;
+    }
+    return;
+  }
+  const int rows = t.r1 - t.r0;
+  if (rows > 128) w4::tile<MODE, EPI, 4, 4, false>(p, lds, &s_last, t);
+  else if (rows > 96) w4::tile<MODE, EPI, 4, 2, true>(p, lds, &s_last, t);
+  else if (rows > 64) w4::tile<MODE, EPI, 3, 2, true>(p, lds, &s_last, t);
+  else if (rows > 32) w4::tile<MODE, EPI, 2, 2, true>(p, lds, &s_last, t);
+  else w4::tile<MODE, EPI, 1, 2, true>(p, lds, &s_last, t);
+}
+
 }  // namespace mf
 
 // ---- host-side dispatch ----------------------------------------------------------------------
@@ -1641,6 +1991,25 @@ static int launch_v4p(const mf::Args& a, int64_t max_tiles, int ncu, hipStream_t
   const int64_t grid = std::min(round_up(max_tiles, 8), (int64_t)kSplitXcd * ncu);
   if (grid <= 0) return MTX_OK;
   hipLaunchKernelGGL((mf::gmm_v4p_kernel<MODE>), dim3((unsigned)grid), dim3(512), 0, st, a);
+  return check_launch();
+}
+// One-wave-per-SIMD kernel (gmm_w4_kernel) for the 256-row tile paths: bit 0 SwiGLU, bit 1 plain
+// forward, bit 2 dlhs (0: gmm_v3_kernel everywhere); used when groups hold at least
+// MTX_W4_MIN_MEAN rows on average.  Measured against gmm_v3_kernel (same bits): Mixtral shapes
+// gate_up -3.4 to -5 %, down -2.4 to -3.5 %, Qwen3-shape dlhs -2 to -2.5 % time; DeepSeek-shape
+// groups of ~128 rows +2 to +3 % (a 4-wave tile of 129-255 rows runs all its MFMAs, where v3 skips
+// a wave pair's empty row blocks), hence the threshold.
+#ifndef MTX_W4
+#define MTX_W4 7
+#endif
+#ifndef MTX_W4_MIN_MEAN
+#define MTX_W4_MIN_MEAN 512
+#endif
+template <int MODE, int EPI>
+static int launch_w4(const mf::Args& a, int64_t grid, hipStream_t st) {
+  if (grid <= 0) return MTX_OK;
+  grid = round_up(grid, 8);
+  hipLaunchKernelGGL((mf::gmm_w4_kernel<MODE, EPI>), dim3((unsigned)grid), dim3(256), 0, st, a);
   return check_launch();
 }
 template <int MODE, int EPI>
@@ -1731,10 +2100,12 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
       return MTX_ERR_UNSUPPORTED;
     // one m-tile per scheduling group: spread the m-tiles of experts with several of them
     const int spread = (a.gm == 1) ? MTX_SPREAD_MIN : 0;
+    const bool w4 = big_m && (M / E) >= MTX_W4_MIN_MEAN;
     if (mode == 2 && I % 128 == 0) {
       if (big_m) {
         rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, false, spread);
         if (rc) return rc;
+        if ((MTX_W4 & 1) && w4) return launch_w4<mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 256) * (I / 128), st);
         return launch_v3<mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 256) * (I / 128), st);
       }
       rc = launch_build_tiles(gs, E, M, 128, wsp, st);
@@ -1767,6 +2138,8 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
         if (rc) return rc;
         // split pieces add at most ncu - rem < ncu workgroups per XCD
         const int64_t grid = round_up(gmm_max_tiles(M, E, 256) * (Nout / 256), 8) + (split ? 8 * (int64_t)ncu : 0);
+        if (mode == 0 && (MTX_W4 & 2) && w4) return launch_w4<mf::FWD, mf::EPI_STORE>(a, grid, st);
+        if (mode == 1 && (MTX_W4 & 4) && w4) return launch_w4<mf::DLHS, mf::EPI_STORE>(a, grid, st);
         return mode == 0 ? launch_v3<mf::FWD, mf::EPI_STORE>(a, grid, st) : launch_v3<mf::DLHS, mf::EPI_STORE>(a, grid, st);
       }
       rc = launch_build_tiles(gs, E, M, 128, wsp, st);
