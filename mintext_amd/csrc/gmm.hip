@@ -38,7 +38,8 @@ struct MTile {
 };
 
 // ---- tile scheduler ---------------------------------------------------------------------------
-// Workspace layout (ints): [0] m-tile count, [16 .. 16+E] group offsets (E+1, clamped to M),
+// Workspace layout (ints): [0] m-tile count, [1] m-tiles with an expert, [4 .. 11] tickets of the
+// per-XCD tile queues (zeroed by the tile-list kernel), [16 .. 16+E] group offsets (E+1, clamped to M),
 // [32+E .. ) expert order by descending group size (E), then the MTile array (16B aligned).
 struct GmmWs {
   int* count;
@@ -86,6 +87,7 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
   __shared__ int wsum[16];
   __shared__ long long wsum64[16];
   if (split_cnt && threadIdx.x < kSplitXcd * kSplitMaxRem) split_cnt[threadIdx.x] = 0;
+  if (threadIdx.x >= 4 && threadIdx.x < 4 + kSplitXcd) count[threadIdx.x] = 0;  // tile queue tickets
   __shared__ __attribute__((aligned(16))) int s_gs[1024];
   __shared__ int s_total[2];
   const int e = threadIdx.x, lane = e & 63, w = e >> 6;
@@ -541,6 +543,8 @@ struct Args {
   // TGMM (256-row tiles): xa > 0 gives XCD x = rem % 8 the tiles of one (nrt/xa) x (ntiles/xb)
   // rectangle of each expert's tile grid (few x and g blocks per XCD L2); 0: row-major tiles
   int xa = 0, xb = 0;
+  // gmm_w4_kernel: per-XCD tile queue tickets (8 ints, zero at launch); nullptr: static ranges
+  int* tickets = nullptr;
 };
 
 // ---- tile loaders ------------------------------------------------------------------------------
@@ -1577,6 +1581,7 @@ constexpr int A_BYTES = BM * v3::BKS * 2, STAGE = A_BYTES + BN * v3::BKS * 2;  /
 struct Tile {
   int e, r0, r1, n_tile;
   int piece, npieces, split_u;  // k-piece of a split tail tile (1 piece: whole tile)
+  int queue;                    // tile queue (XCD range) the tile came from
 };
 
 // One tile with TM x TN 32x32 accumulator blocks per wave.  THIN: wave w owns the 32-column blocks
@@ -1756,7 +1761,7 @@ __device__ __forceinline__ void tile(const Args& p, char* lds, int* s_last, cons
     typedef __attribute__((ext_vector_type(4))) float f32x4;
     constexpr int64_t SLOT4 = kSplitSlotFloats / 4;
     static_assert(TM * TN * 4 * NT <= SLOT4, "split slot");
-    const int xcd_e = (int)(blockIdx.x & 7);
+    const int xcd_e = t.queue;
     f32x4* part = (f32x4*)(p.split_part + (int64_t)(xcd_e * kSplitItems + t.split_u * t.npieces) * kSplitSlotFloats);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -1851,7 +1856,13 @@ __global__ __launch_bounds__(256, 1) void gmm_w4_kernel(Args p) {
   __shared__ int s_last;
   constexpr int BN = w4::BN, NT = w4::NT;
   const int tid = threadIdx.x;
-  // ---- which output tile (the v3 order: XCD-contiguous ranges, gm m-tiles per group, split tail)
+  // ---- which output tile.  The v3 order: queue x (the workgroups dispatched to XCD x, pid % 8)
+  // owns the tile range [x*per, x*per + tx) -- gm m-tiles per scheduling group -- followed, when its
+  // last round is sparse, by that round's tiles split into k-pieces (split tail).  Each XCD's first
+  // ncu_x workgroups take their queue's first items in dispatch order; later workgroups take tickets
+  // from their own queue and, once it is exhausted, from the other queues in turn, so that an XCD that
+  // runs ahead finishes the others' tiles instead of idling at the end (the XCDs of one chip run the
+  // same tile list 3-6 % apart).  Which workgroup computes an item does not change its result.
   w4::Tile t;
   t.piece = 0;
   t.npieces = 1;
@@ -1862,26 +1873,60 @@ __global__ __launch_bounds__(256, 1) void gmm_w4_kernel(Args p) {
   const int pid = blockIdx.x;
   const int total8 = (total + 7) & ~7;
   const int xcd = pid & 7, q = pid >> 3, per = total8 >> 3;
-  int lid;
-  if (EPI == EPI_STORE && p.split_on) {
-    const int tx = max(0, min(per, total - xcd * per));
-    const int rem = tx % p.ncu_x;
-    int S = (rem > 0 && rem <= kSplitMaxRem && 2 * rem <= p.ncu_x) ? min(kSplitMaxS, p.ncu_x / rem) : 1;
-    S = min(S, max(p.Kred / v3::BKS, 1));
-    const int nwhole = (S > 1) ? tx - rem : tx;
-    if (q >= nwhole + (S > 1 ? rem * S : 0)) return;
-    if (q < nwhole) {
-      lid = xcd * per + q;
-    } else {
-      t.split_u = (q - nwhole) / S;
-      t.piece = (q - nwhole) % S;
-      t.npieces = S;
-      lid = xcd * per + nwhole + t.split_u;
+  // items of queue x: nwhole whole tiles, then (S > 1) rem tiles in S pieces each
+  auto queue_items = [&](int x, int& nwhole, int& S) -> int {
+    const int tx = max(0, min(per, total - x * per));
+    nwhole = tx;
+    S = 1;
+    if (EPI == EPI_STORE && p.split_on) {
+      const int rem = tx % p.ncu_x;
+      int S_ = (rem > 0 && rem <= kSplitMaxRem && 2 * rem <= p.ncu_x) ? min(kSplitMaxS, p.ncu_x / rem) : 1;
+      S_ = min(S_, max(p.Kred / v3::BKS, 1));
+      if (S_ > 1) {
+        nwhole = tx - rem;
+        S = S_;
+        return nwhole + rem * S_;
+      }
     }
+    return tx;
+  };
+  int qx = xcd, nwhole, S;
+  int nitems = queue_items(xcd, nwhole, S);
+  int item = q;
+  if (p.tickets != nullptr && q >= min(p.ncu_x, nitems)) {
+    __shared__ int s_ticket[2];
+    if (tid == 0) {
+      int got = -1, gq = 0;
+      for (int k = 0; k < 8 && got < 0; ++k) {
+        const int y = (xcd + k) & 7;
+        int nw_, S_;
+        const int ny = queue_items(y, nw_, S_), sy = min(p.ncu_x, ny);
+        if (ny <= sy) continue;  // no items past the statically taken ones
+        const int tk = __hip_atomic_fetch_add(p.tickets + y, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + sy;
+        if (tk < ny) {
+          got = tk;
+          gq = y;
+        }
+      }
+      s_ticket[0] = got;
+      s_ticket[1] = gq;
+    }
+    __syncthreads();
+    item = s_ticket[0];
+    qx = s_ticket[1];
+    if (item < 0) return;
+    nitems = queue_items(qx, nwhole, S);
+  }
+  if (item >= nitems) return;
+  t.queue = qx;
+  int lid;
+  if (item < nwhole) {
+    lid = qx * per + item;
   } else {
-    if (pid >= total8) return;
-    lid = xcd * per + q;
-    if (lid >= total) return;
+    t.split_u = (item - nwhole) / S;
+    t.piece = (item - nwhole) % S;
+    t.npieces = S;
+    lid = qx * per + nwhole + t.split_u;
   }
   const int GM = p.gm;
   const int grp = lid / (GM * nn);
@@ -2005,10 +2050,18 @@ static int launch_v4p(const mf::Args& a, int64_t max_tiles, int ncu, hipStream_t
 #ifndef MTX_W4_MIN_MEAN
 #define MTX_W4_MIN_MEAN 512
 #endif
+#ifndef MTX_W4_QUEUES
+#define MTX_W4_QUEUES 1
+#endif
 template <int MODE, int EPI>
-static int launch_w4(const mf::Args& a, int64_t grid, hipStream_t st) {
+static int launch_w4(mf::Args a, int64_t grid, hipStream_t st) {
   if (grid <= 0) return MTX_OK;
   grid = round_up(grid, 8);
+  const int ncu = cus_per_xcd();
+  if (MTX_W4_QUEUES && ncu >= 1) {
+    a.tickets = const_cast<int*>(a.count) + 4;  // zeroed by the tile-list kernel of this call
+    a.ncu_x = ncu;
+  }
   hipLaunchKernelGGL((mf::gmm_w4_kernel<MODE, EPI>), dim3((unsigned)grid), dim3(256), 0, st, a);
   return check_launch();
 }
