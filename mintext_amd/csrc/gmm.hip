@@ -83,7 +83,8 @@ static inline GmmWs gmm_ws(void* ws, int64_t M, int64_t E) {
 __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __restrict__ gs, int E, int M, int BM,
                                                            int* __restrict__ count, int* __restrict__ offsets,
                                                            int* __restrict__ order, MTile* __restrict__ tiles,
-                                                           int need_order, int* __restrict__ split_cnt, int spread) {
+                                                           int need_order, int* __restrict__ split_cnt, int spread,
+                                                           int align) {
   __shared__ int wsum[16];
   __shared__ long long wsum64[16];
   if (split_cnt && threadIdx.x < kSplitXcd * kSplitMaxRem) split_cnt[threadIdx.x] = 0;
@@ -142,6 +143,44 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
   // big tile b at floor((2b+1) N / 2B) of N -- and the other tiles fill the rest in expert order,
   // so that every XCD's contiguous range holds its share of them.
   __shared__ int s_bstart[1024], s_sstart[1024], s_nbig[1];
+  // Aligned order (align = G > 1, the scheduling group size): expert e's first floor(nt_e / G) * G
+  // m-tiles come first, in expert order, so that every group of G consecutive m-tiles belongs to one
+  // expert (its tiles share each weight strip), and the experts' remaining nt_e % G m-tiles follow at
+  // the end of the list, in expert order.  s_bstart / s_sstart hold the two sections' starts.
+  if (align > 1) {
+    const int na = (e < E) ? (nt / align) * align : 0;
+    const int nr = (e < E) ? nt - na : 0;
+    int ai = na, ri = nr;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int oa = __shfl_up(ai, off), orr = __shfl_up(ri, off);
+      if (lane >= off) {
+        ai += oa;
+        ri += orr;
+      }
+    }
+    __shared__ int wsa[16], wsr[16];
+    if (lane == 63) {
+      wsa[w] = ai;
+      wsr[w] = ri;
+    }
+    __syncthreads();
+    if (e == 0) {
+      int ra = 0, rr = 0;
+      for (int i = 0; i < 16; ++i) {
+        const int xa = wsa[i], xr = wsr[i];
+        wsa[i] = ra;
+        wsr[i] = rr;
+        ra += xa;
+        rr += xr;
+      }
+      s_nbig[0] = ra;
+    }
+    __syncthreads();
+    if (e < E) {
+      s_bstart[e] = ai - na + wsa[w];
+      s_sstart[e] = ri - nr + wsr[w];
+    }
+  }
   if (spread > 0) {
     const int nbig = (e < E && nt >= spread) ? nt : 0;
     int bincl = nbig;
@@ -178,13 +217,20 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
       starts = isbig ? s_bstart : s_sstart;
       idx = isbig ? cnt - 1 : j - cnt;
     }
+    int first = 0;  // index within the expert of the section's first tile
+    if (align > 1) {
+      const int na_total = s_nbig[0];
+      starts = j < na_total ? s_bstart : s_sstart;
+      idx = j < na_total ? j : j - na_total;
+    }
     int lo = 0, hi = E - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
       if (starts[mid] <= idx) lo = mid;
       else hi = mid - 1;
     }
-    const int i = idx - starts[lo];
+    if (align > 1 && j >= s_nbig[0]) first = ((s_r1[lo] - s_r0[lo] + BM - 1) / BM / align) * align;
+    const int i = first + idx - starts[lo];
     MTile t;
     t.e = lo;
     t.r0 = s_r0[lo] + i * BM;
@@ -1574,8 +1620,13 @@ __global__ __launch_bounds__(512, 2) void gmm_v4p_kernel(Args p) {
 // (operands swapped, k in ring order), hence the same bits.  A tile with at most 128 rows of its
 // group runs the thin form instead: the four waves split the 256 columns (128x64 wave tiles, the
 // v3 wave tile) over the tile's ceil(rows/32) row blocks only, and the ring loads 128 A rows.
+#ifndef MTX_W4_NSTAGE
+#define MTX_W4_NSTAGE 4
+#endif
 namespace w4 {
-constexpr int NT = 256, BM = 256, BN = 256, NSTAGE = 4, PD = 3;
+// ring of NSTAGE 32 KB stages, PD = NSTAGE - 1 of them in flight ahead of the one computed
+constexpr int NT = 256, BM = 256, BN = 256, NSTAGE = MTX_W4_NSTAGE, PD = NSTAGE - 1;
+__device__ __forceinline__ int slot(int k) { return (NSTAGE & (NSTAGE - 1)) == 0 ? (k & (NSTAGE - 1)) : (k % NSTAGE); }
 constexpr int A_BYTES = BM * v3::BKS * 2, STAGE = A_BYTES + BN * v3::BKS * 2;  // 16 + 16 KB
 
 struct Tile {
@@ -1652,7 +1703,7 @@ __device__ __forceinline__ void tile(const Args& p, char* lds, int* s_last, cons
   const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
   // stages past the end re-read the last one into a slot that is no longer read (branch-free)
   auto issue_stage = [&](int kt_) {
-    const uint32_t st = lds_base + (uint32_t)((kt_ & (NSTAGE - 1)) * STAGE);
+    const uint32_t st = lds_base + (uint32_t)(slot(kt_) * STAGE);
     const int kt = kb0 + min(kt_, nk - 1);
     const char* a = Ab + (int64_t)kt * (BKS * 2);
 #pragma unroll
@@ -1676,7 +1727,7 @@ __device__ __forceinline__ void tile(const Args& p, char* lds, int* s_last, cons
     return __builtin_bit_cast(bf16x8, both);
   };
   auto read_frags = [&](int kt, int kk, int buf) {
-    const char* st = lds + (kt & (NSTAGE - 1)) * STAGE;
+    const char* st = lds + slot(kt) * STAGE;
 #pragma unroll
     for (int i = 0; i < TM; ++i) fa[buf][i] = *(const bf16x8*)(st + a_off(wm * 128 + i * 32 + frow, kk * 2 + fhalf));
 #pragma unroll
@@ -1696,7 +1747,7 @@ __device__ __forceinline__ void tile(const Args& p, char* lds, int* s_last, cons
 
   // One load instruction of a ring stage: d < A_INSTR loads A, the rest B.
   auto issue_one = [&](int kt_, int d) {
-    const uint32_t st = lds_base + (uint32_t)((kt_ & (NSTAGE - 1)) * STAGE);
+    const uint32_t st = lds_base + (uint32_t)(slot(kt_) * STAGE);
     const int kt = kb0 + min(kt_, nk - 1);
     if (d < A_INSTR) {
       gload_lds16_s(Ab + (int64_t)kt * (BKS * 2), aoff[d], st + (wave_u * A_INSTR + d) * 1024u);
@@ -1707,7 +1758,7 @@ __device__ __forceinline__ void tile(const Args& p, char* lds, int* s_last, cons
   };
   // fragment slot r of a substep: r < TM reads A block r, else B block r - TM
   auto read_one = [&](int kt, int kk, int buf, int r) {
-    const char* st = lds + (kt & (NSTAGE - 1)) * STAGE;
+    const char* st = lds + slot(kt) * STAGE;
     if (r < TM) {
       fa[buf][r] = *(const bf16x8*)(st + a_off(wm * 128 + r * 32 + frow, kk * 2 + fhalf));
     } else {
@@ -1853,7 +1904,9 @@ template <int MODE, int EPI>
 __global__ __launch_bounds__(256, 1) void gmm_w4_kernel(Args p) {
   static_assert(MODE == FWD || MODE == DLHS, "w4 mode");
   __shared__ __attribute__((aligned(1024))) char lds[w4::NSTAGE * w4::STAGE];
-  __shared__ int s_last;
+  // two ints of workgroup state in the ring's last slot: the prologue leaves that slot alone (its
+  // first load is issued after the prologue's barrier) and the split tail uses it after the k-loop
+  int* s_misc = (int*)(lds + (w4::NSTAGE - 1) * w4::STAGE);
   constexpr int BN = w4::BN, NT = w4::NT;
   const int tid = threadIdx.x;
   // ---- which output tile.  The v3 order: queue x (the workgroups dispatched to XCD x, pid % 8)
@@ -1894,7 +1947,7 @@ __global__ __launch_bounds__(256, 1) void gmm_w4_kernel(Args p) {
   int nitems = queue_items(xcd, nwhole, S);
   int item = q;
   if (p.tickets != nullptr && q >= min(p.ncu_x, nitems)) {
-    __shared__ int s_ticket[2];
+    int* s_ticket = s_misc;
     if (tid == 0) {
       int got = -1, gq = 0;
       for (int k = 0; k < 8 && got < 0; ++k) {
@@ -1949,11 +2002,11 @@ __global__ __launch_bounds__(256, 1) void gmm_w4_kernel(Args p) {
     return;
   }
   const int rows = t.r1 - t.r0;
-  if (rows > 128) w4::tile<MODE, EPI, 4, 4, false>(p, lds, &s_last, t);
-  else if (rows > 96) w4::tile<MODE, EPI, 4, 2, true>(p, lds, &s_last, t);
-  else if (rows > 64) w4::tile<MODE, EPI, 3, 2, true>(p, lds, &s_last, t);
-  else if (rows > 32) w4::tile<MODE, EPI, 2, 2, true>(p, lds, &s_last, t);
-  else w4::tile<MODE, EPI, 1, 2, true>(p, lds, &s_last, t);
+  if (rows > 128) w4::tile<MODE, EPI, 4, 4, false>(p, lds, s_misc, t);
+  else if (rows > 96) w4::tile<MODE, EPI, 4, 2, true>(p, lds, s_misc, t);
+  else if (rows > 64) w4::tile<MODE, EPI, 3, 2, true>(p, lds, s_misc, t);
+  else if (rows > 32) w4::tile<MODE, EPI, 2, 2, true>(p, lds, s_misc, t);
+  else w4::tile<MODE, EPI, 1, 2, true>(p, lds, s_misc, t);
 }
 
 }  // namespace mf
@@ -1964,9 +2017,9 @@ struct MfmaCfg {
 };
 
 static int launch_build_tiles(const int32_t* gs, int64_t E, int64_t M, int BM, const GmmWs& w, hipStream_t st,
-                              bool need_order = false, bool reset_split = false, int spread = 0) {
+                              bool need_order = false, bool reset_split = false, int spread = 0, int align = 0) {
   hipLaunchKernelGGL(build_tiles_kernel, dim3(1), dim3(1024), 0, st, gs, (int)E, (int)M, BM, w.count, w.offsets,
-                     w.order, w.tiles, need_order ? 1 : 0, reset_split ? w.split_cnt : (int*)nullptr, spread);
+                     w.order, w.tiles, need_order ? 1 : 0, reset_split ? w.split_cnt : (int*)nullptr, spread, align);
   return check_launch();
 }
 
@@ -2046,6 +2099,10 @@ static int launch_v4p(const mf::Args& a, int64_t max_tiles, int ncu, hipStream_t
 // a wave pair's empty row blocks), hence the threshold.
 #ifndef MTX_W4
 #define MTX_W4 7
+#endif
+// 1: scheduling groups of the 256-row paths hold the m-tiles of one expert (build_tiles_kernel)
+#ifndef MTX_ALIGN_GROUPS
+#define MTX_ALIGN_GROUPS 1
 #endif
 #ifndef MTX_W4_MIN_MEAN
 #define MTX_W4_MIN_MEAN 512
@@ -2154,9 +2211,13 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
     // one m-tile per scheduling group: spread the m-tiles of experts with several of them
     const int spread = (a.gm == 1) ? MTX_SPREAD_MIN : 0;
     const bool w4 = big_m && (M / E) >= MTX_W4_MIN_MEAN;
+    // groups of gm m-tiles that never mix experts (the 256-row paths, when the mean expert fills a
+    // group: C2 -1 %; with Zipf loads, whose remainders then collect at the end of the list from
+    // many experts, C5 dlhs ran 1-3 % slower): see build_tiles_kernel
+    const int align = (MTX_ALIGN_GROUPS && a.gm > 1 && (M / E) >= 256 * a.gm) ? a.gm : 0;
     if (mode == 2 && I % 128 == 0) {
       if (big_m) {
-        rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, false, spread);
+        rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, false, spread, align);
         if (rc) return rc;
         if ((MTX_W4 & 1) && w4) return launch_w4<mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 256) * (I / 128), st);
         return launch_v3<mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 256) * (I / 128), st);
@@ -2171,7 +2232,7 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
       const int ncu4 = cus_per_xcd();
       if (big_m && !gath && nks >= 4 && nks <= MTX_V4P_MAX_STAGES && ncu4 >= 1) {
         // short reductions: persistent workgroups, the ring running across tiles
-        rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, false, spread);
+        rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, false, spread, align);
         if (rc) return rc;
         const int64_t tiles = gmm_max_tiles(M, E, 256) * (Nout / 256);
         return mode == 0 ? launch_v4p<mf::FWD>(a, tiles, ncu4, st) : launch_v4p<mf::DLHS>(a, tiles, ncu4, st);
@@ -2187,7 +2248,7 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
           a.split_part = wsp.split_part;
           a.ncu_x = ncu;
         }
-        rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, split, spread);
+        rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, split, spread, align);
         if (rc) return rc;
         // split pieces add at most ncu - rem < ncu workgroups per XCD
         const int64_t grid = round_up(gmm_max_tiles(M, E, 256) * (Nout / 256), 8) + (split ? 8 * (int64_t)ncu : 0);
