@@ -304,6 +304,34 @@ int mtx_gmm_fp8_swiglu_gathered(const uint8_t* xq, const float* x_scale, int64_t
                                 uint8_t* out_q, float* out_scale, void* out_bf16,
                                 void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---- fp8 e4m3fn blockwise, power-of-two scales ("_p2"; no counterpart in the reference, whose
+ * fp8 convention is per-tensor scaling, mintext/modules/linear.py:37-57) ----------------------
+ * The same layouts and signatures as the entry points above, with every scale the power of two
+ * 2^e, e = ceil(log2(amax/448)) clamped to [-126, 127] (1 when amax == 0): the codes are exact
+ * quotients x * 2^-e.  The GEMMs hand the scales' exponents (the f32 exponent fields) to the
+ * MFMA's E8M0 block-scale operands, so their scales must be powers of two in [2^-126, 2^127]
+ * (quantised by the _p2 quantisers); the SwiGLU epilogue re-quantises in the same mode.  The
+ * GEMMs need Kin >= 256 (MTX_ERR_UNSUPPORTED otherwise).                                    */
+int mtx_quant_fp8_rows_p2(const void* x, int dtype, int64_t M, int64_t D,
+                          uint8_t* xq, float* x_scale, void* stream);
+int mtx_quant_fp8_weights_p2(const void* w, int dtype, int64_t E, int64_t Kin, int64_t Kout,
+                             uint8_t* w_q, float* w_scale, void* stream);
+int mtx_gmm_fp8_p2(const uint8_t* xq, const float* x_scale, const uint8_t* w_q,
+                   const float* w_scale, const int32_t* group_sizes,
+                   int64_t M, int64_t Kin, int64_t Kout, int64_t E, void* out,
+                   void* workspace, int64_t workspace_bytes, void* stream);
+int mtx_gmm_fp8_swiglu_p2(const uint8_t* xq, const float* x_scale, const uint8_t* w_q,
+                          const float* w_scale, const int32_t* group_sizes,
+                          int64_t M, int64_t Kin, int64_t I, int64_t E,
+                          uint8_t* out_q, float* out_scale, void* out_bf16,
+                          void* workspace, int64_t workspace_bytes, void* stream);
+int mtx_gmm_fp8_swiglu_gathered_p2(const uint8_t* xq, const float* x_scale, int64_t x_rows,
+                                   const int32_t* row_index, int64_t index_div, const uint8_t* w_q,
+                                   const float* w_scale, const int32_t* group_sizes,
+                                   int64_t M, int64_t Kin, int64_t I, int64_t E,
+                                   uint8_t* out_q, float* out_scale, void* out_bf16,
+                                   void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---- fp8 e4m3fn blockwise backward (no reference counterpart; the bf16 forms are dlhs and tgmm,
  * mintext/kernels/grouped_matmul.py:151-187 and :197-235, with the forward's fp8 conventions) ----
  * dlhs: dX = dY @ W^T.  W's codes in its own layout, w_qt [E,Kin,Kout] with the same 128x128 block

@@ -70,6 +70,12 @@ SIGNATURES = {
     "mtx_gmm_fp8_swiglu": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "mtx_gmm_fp8_swiglu_gathered": (_I, [_P, _P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P,
                                          _P, _I64, _P]),
+    "mtx_quant_fp8_rows_p2": (_I, [_P, _I, _I64, _I64, _P, _P, _P]),
+    "mtx_quant_fp8_weights_p2": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _P]),
+    "mtx_gmm_fp8_p2": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
+    "mtx_gmm_fp8_swiglu_p2": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
+    "mtx_gmm_fp8_swiglu_gathered_p2": (_I, [_P, _P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P,
+                                            _P, _I64, _P]),
     "mtx_quant_fp8_weights_t": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _P]),
     "mtx_gmm_fp8_dlhs": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "mtx_fp8_grouped_chunks": (_I64, [_I64, _I64]),

@@ -150,6 +150,22 @@ __device__ __forceinline__ float div_rn(float a, float b, float rb) {
   return __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q, b, a), rb, q), a);
 }
 
+// Power-of-two quantisation scale (the MFMA block-scale mode): the smallest 2^e, e in [-126, 127],
+// with amax / 2^e <= 448 -- e = ceil(log2(amax / 448)) for normal amax, written on the bits:
+// amax = 1.f x 2^(E-127) is at most 448 x 2^e = 1.75 x 2^(8+e) iff e >= E - 135 (+1 when f > 0.75).
+// 1 when amax == 0 (as the amax / 448 mode); an infinite or NaN amax gives 2^120 or 2^121.  The
+// quotient x / 2^e is then x * 2^-e exactly, and the MFMA's E8M0 scale operand is e + 127, the
+// f32 exponent field of the scale.
+__device__ __forceinline__ float p2_scale(float amax) {
+  if (amax == 0.0f) return 1.0f;
+  const uint32_t u = __float_as_uint(amax);
+  int e = (int)((u >> 23) & 0xFFu) - 135 + ((u & 0x7FFFFFu) > 0x600000u ? 1 : 0);
+  e = e < -126 ? -126 : (e > 127 ? 127 : e);
+  return __uint_as_float((uint32_t)(e + 127) << 23);
+}
+// E8M0 code (biased exponent) of a power-of-two scale in [2^-126, 2^127]
+__device__ __forceinline__ uint32_t e8m0_of(float s) { return (__float_as_uint(s) >> 23) & 0xFFu; }
+
 __device__ __forceinline__ float e4m3_to_f32(uint8_t v) {
   uint32_t sign = (v & 0x80u) ? 0x80000000u : 0u;
   uint32_t e = (v >> 3) & 0xfu, m = v & 7u;

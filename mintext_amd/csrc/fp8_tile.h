@@ -5,8 +5,9 @@
 // lanes, every load of the tile issued before any math.  Thread (column group cl, row slot rl)
 // holds rows 4 (rl + TR h) + q (q = 0..3), so that it owns four consecutive rows of each of its
 // columns and can pack their four codes into one 32-bit word for the transposed layout.
-// Scales are amax / 448 (1 when the amax is 0) over the whole tile or per column; codes are
-// e4m3 of value / scale (the IEEE quotient's code, through div_rn), by e4m3_pack4.
+// Scales are amax / 448 (1 when the amax is 0) or the power-of-two p2_scale(amax), over the whole
+// tile or per column; codes are e4m3 of value / scale (the IEEE quotient's code, through div_rn;
+// exact for a power-of-two scale), by e4m3_pack4.
 #pragma once
 #include "common.h"
 
@@ -65,19 +66,23 @@ struct Tile {
   }
 };
 
+// amax / 448 (1 when amax == 0), or with P2 the power-of-two scale p2_scale(amax)
+template <bool P2 = false>
 __device__ __forceinline__ float scale_of(float amax) {
+  if constexpr (P2) return p2_scale(amax);
   float s = amax / 448.0f;
   return s == 0.0f ? 1.0f : s;
 }
 
 // one scale for the whole tile (256 threads; red: 4 floats of LDS)
+template <bool P2 = false>
 __device__ __forceinline__ float block_scale(float m, float* red) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
   __syncthreads();
   const float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  return scale_of(r);
+  return scale_of<P2>(r);
 }
 
 // Codes of the tile transposed into LDS: tt[c * TSTRIDE + r] = code of (row r, column c), written as

@@ -18,30 +18,44 @@ def _gs(g):
     return (g if g.dtype == torch.int32 else g.to(torch.int32)).contiguous()
 
 
-def quantize_fp8_rows(x: torch.Tensor):
+# Scale modes.  "amax": scale = amax / 448 (DeepSeek-V3 blockwise).  "pow2": the power-of-two scale
+# 2^ceil(log2(amax / 448)) (exponent in [-126, 127], 1 for an all-zero group): the codes are exact
+# quotients and the GEMMs hand the scales' exponents to the MFMA's E8M0 block-scale operands, so a
+# GEMM in this mode needs operands quantised in it (the "_p2" entry points).
+SCALE_MODES = ("amax", "pow2")
+
+
+def _entry(name: str, scales: str) -> str:
+    if scales not in SCALE_MODES:
+        raise ValueError(f"scales must be one of {SCALE_MODES}, got {scales!r}")
+    return name + ("_p2" if scales == "pow2" else "")
+
+
+def quantize_fp8_rows(x: torch.Tensor, *, scales: str = "amax"):
     """x [M, D] (f32/bf16) -> (xq [M, D] float8_e4m3fn, x_scale [M, D/128] f32)."""
     dev = L.require_device(x)
     x = x.contiguous()
     M, D = x.shape
     xq = torch.empty((M, D), dtype=torch.float8_e4m3fn, device=dev)
     xs = torch.empty((M, D // 128), dtype=torch.float32, device=dev)
-    L.call("mtx_quant_fp8_rows", L.ptr(x), L.dtype_code(x.dtype), M, D, L.ptr(xq), L.ptr(xs), L.stream(dev))
+    L.call(_entry("mtx_quant_fp8_rows", scales), L.ptr(x), L.dtype_code(x.dtype), M, D, L.ptr(xq), L.ptr(xs),
+           L.stream(dev))
     return xq, xs
 
 
-def quantize_fp8_weights(w: torch.Tensor):
+def quantize_fp8_weights(w: torch.Tensor, *, scales: str = "amax"):
     """w [E, Kin, Kout] (reference layout) -> (w_q [E, Kout, Kin] e4m3fn, w_scale [E, Kout/128, Kin/128])."""
     dev = L.require_device(w)
     w = w.contiguous()
     E, Kin, Kout = w.shape
     wq = torch.empty((E, Kout, Kin), dtype=torch.float8_e4m3fn, device=dev)
     ws = torch.empty((E, Kout // 128, Kin // 128), dtype=torch.float32, device=dev)
-    L.call("mtx_quant_fp8_weights", L.ptr(w), L.dtype_code(w.dtype), E, Kin, Kout, L.ptr(wq), L.ptr(ws),
-           L.stream(dev))
+    L.call(_entry("mtx_quant_fp8_weights", scales), L.ptr(w), L.dtype_code(w.dtype), E, Kin, Kout, L.ptr(wq),
+           L.ptr(ws), L.stream(dev))
     return wq, ws
 
 
-def grouped_matmul_fp8(xq, x_scale, w_q, w_scale, group_sizes) -> torch.Tensor:
+def grouped_matmul_fp8(xq, x_scale, w_q, w_scale, group_sizes, *, scales: str = "amax") -> torch.Tensor:
     """out [M, Kout] bf16 = blockwise-dequantised x @ W per group, f32 accumulation."""
     gs = _gs(group_sizes)
     dev = L.require_device(xq, x_scale, w_q, w_scale, gs)
@@ -51,14 +65,16 @@ def grouped_matmul_fp8(xq, x_scale, w_q, w_scale, group_sizes) -> torch.Tensor:
         raise ValueError("fp8 gmm shape mismatch")
     out = torch.empty((M, Kout), dtype=torch.bfloat16, device=dev)
     ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
-    L.call("mtx_gmm_fp8", L.ptr(xq.contiguous()), L.ptr(x_scale.contiguous()), L.ptr(w_q.contiguous()),
+    L.call(_entry("mtx_gmm_fp8", scales), L.ptr(xq.contiguous()), L.ptr(x_scale.contiguous()), L.ptr(w_q.contiguous()),
            L.ptr(w_scale.contiguous()), L.ptr(gs), M, Kin, Kout, E, L.ptr(out), L.ptr(ws), ws.numel(),
            L.stream(dev))
     return out
 
 
-def grouped_matmul_fp8_swiglu(xq, x_scale, w_q, w_scale, group_sizes, *, return_bf16: bool = False):
-    """SwiGLU of the fp8 gate_up GEMM (w_q [E, 2I, Kin]) re-quantised in 1x128 groups.
+def grouped_matmul_fp8_swiglu(xq, x_scale, w_q, w_scale, group_sizes, *, return_bf16: bool = False,
+                              scales: str = "amax"):
+    """SwiGLU of the fp8 gate_up GEMM (w_q [E, 2I, Kin]) re-quantised in 1x128 groups (in the same
+    scale mode as the operands).
 
     Returns (yq [M, I] e4m3fn, y_scale [M, I/128] f32) and, with return_bf16, y [M, I] bf16.
     """
@@ -73,7 +89,8 @@ def grouped_matmul_fp8_swiglu(xq, x_scale, w_q, w_scale, group_sizes, *, return_
     ys = torch.empty((M, I // 128), dtype=torch.float32, device=dev)
     yb = torch.empty((M, I), dtype=torch.bfloat16, device=dev) if return_bf16 else None
     ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
-    L.call("mtx_gmm_fp8_swiglu", L.ptr(xq.contiguous()), L.ptr(x_scale.contiguous()), L.ptr(w_q.contiguous()),
+    L.call(_entry("mtx_gmm_fp8_swiglu", scales), L.ptr(xq.contiguous()), L.ptr(x_scale.contiguous()),
+           L.ptr(w_q.contiguous()),
            L.ptr(w_scale.contiguous()), L.ptr(gs), M, Kin, I, E, L.ptr(yq), L.ptr(ys), L.ptr(yb), L.ptr(ws),
            ws.numel(), L.stream(dev))
     if return_bf16:
@@ -82,7 +99,7 @@ def grouped_matmul_fp8_swiglu(xq, x_scale, w_q, w_scale, group_sizes, *, return_
 
 
 def grouped_matmul_fp8_swiglu_gathered(xq, x_scale, sort_indices, top_k: int, w_q, w_scale, group_sizes, *,
-                                       return_bf16: bool = False):
+                                       return_bf16: bool = False, scales: str = "amax"):
     """``grouped_matmul_fp8_swiglu`` on the routed rows of token-order inputs: xq [T, Kin] and
     x_scale [T, Kin/128] are ``quantize_fp8_rows(tokens)``; sorted row r is token row
     ``sort_indices[r] // top_k``, read by the GEMM's operand loads (the dispatch copy is never
@@ -101,7 +118,8 @@ def grouped_matmul_fp8_swiglu_gathered(xq, x_scale, sort_indices, top_k: int, w_
     ys = torch.empty((M, I // 128), dtype=torch.float32, device=dev)
     yb = torch.empty((M, I), dtype=torch.bfloat16, device=dev) if return_bf16 else None
     ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
-    L.call("mtx_gmm_fp8_swiglu_gathered", L.ptr(xq.contiguous()), L.ptr(x_scale.contiguous()), T, L.ptr(si), top_k,
+    L.call(_entry("mtx_gmm_fp8_swiglu_gathered", scales), L.ptr(xq.contiguous()), L.ptr(x_scale.contiguous()), T,
+           L.ptr(si), top_k,
            L.ptr(w_q.contiguous()), L.ptr(w_scale.contiguous()), L.ptr(gs), M, Kin, I, E, L.ptr(yq), L.ptr(ys),
            L.ptr(yb), L.ptr(ws), ws.numel(), L.stream(dev))
     if return_bf16:

@@ -382,27 +382,54 @@ def swiglu_bwd(h, dy) -> np.ndarray:
 # ---------------------------------------------------------------------------------------------
 
 
-def quant_fp8_rows(x, group: int = 128):
-    """1 x 128 groups: scale = amax/448 (1 if amax == 0), q = RNE(x / scale) in float32."""
+def p2_scale(amax) -> np.ndarray:
+    """Power-of-two quantisation scale: the smallest 2^e, e in [-126, 127], with amax / 2^e <= 448
+    (1 when amax == 0).  No reference counterpart: the scale mode whose exponents the MFMA's E8M0
+    block-scale operands apply (DeepSeek-V3 likewise restricts some fp8 scaling factors to integral
+    powers of 2).  With amax = m 2^E (frexp, m in [0.5, 1)) and 448 = 0.875 2^9, the least e with
+    m 2^E <= 0.875 2^(9+e) is E - 9, plus 1 when m > 0.875.  Non-finite amax (not produced by
+    finite data) follows the kernels' exponent-field rule: 2^120, or 2^121 for a NaN payload
+    above 0x600000."""
+    a = np.asarray(amax, dtype=np.float32)
+    m, E = np.frexp(np.where(np.isfinite(a), a, 1.0).astype(np.float64))
+    e = E.astype(np.int64) - 9 + (m > 0.875)
+    bits = a.view(np.uint32)
+    e = np.where(np.isfinite(a), e, 120 + ((bits & 0x7FFFFF) > 0x600000))
+    e = np.clip(e, -126, 127)
+    s = np.ldexp(np.float64(1.0), e).astype(np.float32)
+    return np.where(a == 0, np.float32(1.0), s).astype(np.float32)
+
+
+def _scale_of(amax, scales: str) -> np.ndarray:
+    if scales == "pow2":
+        return p2_scale(amax)
+    if scales != "amax":
+        raise ValueError(f"unknown scale mode {scales!r}")
+    s = (np.asarray(amax, np.float32) / np.float32(E4M3_MAX)).astype(np.float32)
+    return np.where(s == 0, np.float32(1.0), s).astype(np.float32)
+
+
+def quant_fp8_rows(x, group: int = 128, scales: str = "amax"):
+    """1 x 128 groups: scale = amax/448 (1 if amax == 0), or with scales="pow2" the power-of-two
+    p2_scale(amax); q = RNE(x / scale) in float32 (exact quotients for a power-of-two scale)."""
     x = np.asarray(x, dtype=np.float32)
     M, D = x.shape
     g = x.reshape(M, D // group, group)
     amax = np.abs(g).max(-1)
-    s = (amax / np.float32(E4M3_MAX)).astype(np.float32)
-    s = np.where(s == 0, np.float32(1.0), s).astype(np.float32)
+    s = _scale_of(amax, scales)
     q = e4m3_encode((g / s[..., None]).astype(np.float32)).reshape(M, D)
     return q, s
 
 
-def quant_fp8_weights(w, block: int = 128):
+def quant_fp8_weights(w, block: int = 128, scales: str = "amax"):
     """128 x 128 blocks over (Kin, Kout) of w [E,Kin,Kout]; returns the k-contiguous
-    transposed codes wq [E,Kout,Kin] and scales ws [E,Kout/128,Kin/128]."""
+    transposed codes wq [E,Kout,Kin] and scales ws [E,Kout/128,Kin/128] (amax/448 or, with
+    scales="pow2", p2_scale of the block's amax)."""
     w = np.asarray(w, dtype=np.float32)
     E, Kin, Kout = w.shape
     blk = w.reshape(E, Kin // block, block, Kout // block, block)
     amax = np.abs(blk).max(axis=(2, 4))  # [E, Kin/128, Kout/128]
-    s = (amax / np.float32(E4M3_MAX)).astype(np.float32)
-    s = np.where(s == 0, np.float32(1.0), s).astype(np.float32)
+    s = _scale_of(amax, scales)
     q = e4m3_encode((blk / s[:, :, None, :, None]).astype(np.float32)).reshape(E, Kin, Kout)
     return np.ascontiguousarray(np.swapaxes(q, 1, 2)), np.ascontiguousarray(np.swapaxes(s, 1, 2))
 

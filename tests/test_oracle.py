@@ -326,6 +326,37 @@ def test_quant_weights_layout_and_dequant():
     assert rel_err(O.dequant_weights(wq, ws), w) < 0.04
 
 
+def test_p2_scale_closed_form_and_codes_match_torch():
+    """The power-of-two scale against the float64 closed form 2^ceil(log2(amax/448)) (clamped to
+    [2^-126, 2^127], 1 for amax 0) over many binades and at the binade edges, the invariant that the
+    scaled group maximum lies in (224, 448], and the codes against torch's e4m3 cast of x / scale."""
+    rng = np.random.default_rng(21)
+    amax = (10.0 ** rng.uniform(-35, 37, 20000)).astype(np.float32)
+    edges = np.float32(448.0) * np.ldexp(np.float32(1.0), np.arange(-120, 120)).astype(np.float32)
+    amax = np.concatenate([amax, edges, np.nextafter(edges, np.float32(np.inf)), np.nextafter(edges, np.float32(0)),
+                           np.array([0.0, 1e-40, 1e-45, 3.0e38], np.float32)])
+    s = O.p2_scale(amax)
+    with np.errstate(divide="ignore"):
+        e = np.ceil(np.log2(amax.astype(np.float64) / 448.0))
+    ref = np.where(amax == 0, 1.0, np.ldexp(1.0, np.clip(np.where(amax > 0, e, 0), -126, 127).astype(np.int64)))
+    np.testing.assert_array_equal(s.astype(np.float64), ref)
+    normal = (amax > 448.0 * 2.0 ** -126) & (amax < 448.0 * 2.0 ** 127)
+    q = amax[normal].astype(np.float64) / s[normal]
+    assert (q > 224.0).all() and (q <= 448.0).all()
+    x = (rng.standard_normal((8, 384)) * 10.0 ** rng.uniform(-20, 20, (8, 1))).astype(np.float32)
+    x[3, :128] = 0
+    codes, sc = O.quant_fp8_rows(x, scales="pow2")
+    np.testing.assert_array_equal(sc[3, 0], np.float32(1.0))
+    div = torch.from_numpy(x.reshape(8, 3, 128) / sc[..., None])
+    tq = div.to(torch.float8_e4m3fn).view(torch.uint8).numpy().reshape(8, 384)
+    np.testing.assert_array_equal(codes, tq)
+    w = (rng.standard_normal((2, 256, 384)) * 0.02).astype(np.float32)
+    wq, ws = O.quant_fp8_weights(w, scales="pow2")
+    blk = np.abs(w.reshape(2, 2, 128, 3, 128)).max(axis=(2, 4))  # [E, Kin/128, Kout/128]
+    np.testing.assert_array_equal(ws, np.swapaxes(O.p2_scale(blk), 1, 2))
+    assert rel_err(O.dequant_weights(wq, ws), w) < 0.04
+
+
 def test_gmm_fp8_equals_dequantised_gmm():
     rng = np.random.default_rng(14)
     gs = [40, 0, 88]
