@@ -148,7 +148,8 @@ def router_kwargs(cfg_name):
                 routed_scaling_factor=cfg.get("scale", 1.0))
 
 
-def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_graph=False, gather=True):
+def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_graph=False, gather=True,
+        fp8_scales="amax"):
     import torch
 
     from mintext_amd import _lib
@@ -185,14 +186,17 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
                                              quantize_fp8_weights)
         from mintext_amd.kernels.moe_dispatch import route_quantize_fp8
 
-        guq, gus = quantize_fp8_weights(gate_up)
-        dnq, dns = quantize_fp8_weights(down)
+        f8s = dict(scales=fp8_scales)  # "amax" (scale amax/448) or "pow2" (power-of-two scales, MFMA E8M0)
+        guq, gus = quantize_fp8_weights(gate_up, **f8s)
+        dnq, dns = quantize_fp8_weights(down, **f8s)
     # the route's row gather inside the gate_up GEMM's operand loads (no sorted copy written)
     from mintext_amd.kernels.grouped_matmul import gathered_swiglu_supported, grouped_matmul_swiglu_gathered
     from mintext_amd.kernels.moe_dispatch import route_indices
 
     bwd = cfg_name in ("qwen3_bwd", "qwen3_bwd_fp8")
     gather = gather and not bwd and (D >= 256 if fp8 else gathered_swiglu_supported(x, gate_up))
+    if fp8 and fp8_scales != "amax" and not gather:
+        raise SystemExit("--fp8-scales pow2 needs the gathered layer flow (the fused dispatch quantiser is amax-only)")
 
     def step(timed):
         with torch.no_grad():
@@ -202,7 +206,7 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
             if gather:
                 # permutation only; fp8: the tokens quantised in token order (1x128 groups)
                 if fp8:
-                    xq, xs = quantize_fp8_rows(x)
+                    xq, xs = quantize_fp8_rows(x, **f8s)
                 si, gs, _ = route_indices(idx, Eg)
             elif fp8:
                 # 1x128 quantisation of the tokens fused into their dispatch
@@ -214,7 +218,7 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
                 t_gu.start()
             if gather:
                 if fp8:
-                    yq, ys = grouped_matmul_fp8_swiglu_gathered(xq, xs, si, Kc, guq, gus, gs)
+                    yq, ys = grouped_matmul_fp8_swiglu_gathered(xq, xs, si, Kc, guq, gus, gs, **f8s)
                 else:
                     y = grouped_matmul_swiglu_gathered(x, si, Kc, gate_up, gs)
             elif fp8:
@@ -224,7 +228,7 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
             if timed:
                 t_gu.stop()
                 t_dn.start()
-            o = grouped_matmul_fp8(yq, ys, dnq, dns, gs) if fp8 else grouped_matmul_vjp(y, down, gs)
+            o = grouped_matmul_fp8(yq, ys, dnq, dns, gs, **f8s) if fp8 else grouped_matmul_vjp(y, down, gs)
             if timed:
                 t_dn.stop()
             sh_out = None
@@ -340,9 +344,11 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
     else:
         kern_flops = 2.0 * Mg * D * 2 * I
         achieved = kern_flops / (gu_ms * 1e-3) / 1e12
-        dominant = "gmm_fp8_swiglu (gate_up + SwiGLU + requant)" if fp8 else "gmm_swiglu (gate_up + fused SwiGLU)"
-    traffic = _traffic(cfg_name)
-    tsrc = {"traffic_source": f"profiles/traffic_{cfg_name}.json (rocprofv3 FETCH_SIZE/WRITE_SIZE of this kernel, "
+        dominant = (("gmm_fp8_swiglu_p2 (gate_up + SwiGLU + pow2 requant)" if fp8_scales == "pow2"
+                     else "gmm_fp8_swiglu (gate_up + SwiGLU + requant)") if fp8 else "gmm_swiglu (gate_up + fused SwiGLU)")
+    tname = cfg_name + ("_pow2" if fp8 and fp8_scales == "pow2" and not bwd else "")
+    traffic = _traffic(tname)
+    tsrc = {"traffic_source": f"profiles/traffic_{tname}.json (rocprofv3 FETCH_SIZE/WRITE_SIZE of this kernel, "
                               "scaled by a plain copy's counters)"} if traffic is not None else {}
     if cfg_name == "deepseek":
         # C3 streams its routed weights once per layer at ~128 rows per expert (arithmetic intensity
@@ -389,7 +395,9 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
                    f"qwen3 grouped-GEMM backward (dlhs+tgmm){', fp8 operands' if fp8 else ''}, Zipf(1.2) skew",
                    "T": T, "d_model": D, "experts": E, "top_k": K, "d_ff": I, "routing": cfg["scoring"],
                    "parallelism": "single GPU",
-                   **({"shared_expert": shared_mode if fold else "separate"} if shared is not None else {})},
+                   **({"shared_expert": shared_mode if fold else "separate"} if shared is not None else {}),
+                   **({"fp8_scales": ("amax/448" if fp8_scales == "amax" else "power of two (MFMA E8M0)")}
+                      if fp8 and not bwd else {})},
         "gemm": {"tflops": round(flops_fwd / (gemm_ms * 1e-3) / 1e12, 1),
                  "frac_of_peak": round((flops_fwd / (gemm_ms * 1e-3) / 1e12) / peak, 4),
                  "gate_up_ms": round(gu_ms, 4), "down_ms": round(dn_ms, 4)},
@@ -857,6 +865,8 @@ def main(argv=None):
                     help="deepseek: shared expert run as its own one-group GEMMs (default) or folded into the routed GEMMs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 plain 256 MiB device copies (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--fp8-scales", default="amax", choices=["amax", "pow2"],
+                    help="fp8 configs: block scales amax/448 (default) or powers of two applied by the MFMA")
     ap.add_argument("--no-gather", action="store_true",
                     help="materialise the sorted tokens in the dispatch (route) instead of gathering the token "
                          "rows inside the gate_up GEMM")
@@ -908,7 +918,7 @@ def main(argv=None):
               "collectives); run with --gpus 1", file=sys.stderr)
         return 2
     res = run(a.config, a.steps, a.warmup, cpu_baseline=not a.no_cpu_baseline, shared_mode=a.shared,
-              use_graph=a.graph, gather=not a.no_gather)
+              use_graph=a.graph, gather=not a.no_gather, fp8_scales=a.fp8_scales)
     print(json.dumps(res))
     return 0
 

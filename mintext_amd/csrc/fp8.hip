@@ -1135,9 +1135,11 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
 // leaves the registers for 128x128 wave tiles (16 accumulator blocks, in the AGPRs) with one wave
 // per SIMD, on the schedule of the bf16 gmm_w4_kernel: a stage is 16 MFMA slots, the first eight
 // followed by a fragment read of the next stage and the odd ones by one of the stage's ring loads.
-// One tile per workgroup (a persistent form, whose ring ran across tiles, made the compiler move and
-// spill the 256 accumulators at every tile switch); each block's 256 row scales and two weight-block
-// scales travel with its even stage.  The E8M0 codes are the f32 exponent fields of the scales,
+// One tile per workgroup: two persistent forms (the ring running across tiles) measured 0-13 % slower
+// on the C4 shapes -- the first made the compiler move and spill the 256 accumulators at every tile
+// switch, the second (each tile's first MFMAs from a zero accumulator) still spilled 20-75 VGPRs
+// around the epilogue; each block's 256 row scales and two weight-block scales travel with its even
+// stage.  The E8M0 codes are the f32 exponent fields of the scales,
 // which must be powers of two in [2^-126, 2^127].
 namespace p2 {
 // f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>): indices usable as constants
@@ -1416,7 +1418,7 @@ static inline int64_t f8_ws_bytes(int64_t M, int64_t E, int64_t BM) {
   return 256 + (ceil_div(M, BM) + E + 1) * (int64_t)sizeof(MTileF8);
 }
 
-// Power-of-two scales (p2): the persistent one-wave-per-SIMD kernel with the scales in the MFMA;
+// Power-of-two scales (p2): the one-wave-per-SIMD kernel with the scales in the MFMA;
 // it needs K >= 256 and 32-bit operand offsets (MTX_ERR_UNSUPPORTED otherwise).
 template <int EPI>
 static int launch_fp8_p2(const f8::Args& a, const int32_t* gs, int64_t E, int64_t nn, void* ws, hipStream_t st) {

@@ -199,10 +199,13 @@ def test_c3_deepseek_layer_full_size(dev):
     assert rel_err(_host(f["out"][torch.from_numpy(tokens).to(dev)]), ref) < 2e-2, "layer end to end (bf16)"
 
 
-def test_c4_qwen3_fp8_layer_full_size(dev):
-    """C4 at T=16384, D=2048, E=128, K=8, I=768 in blockwise fp8: quantiser codes bit-exact,
-    gate_up + SwiGLU and the K_in = 768 down GEMM against the dequantised float64 oracle (1e-2)
-    and the unquantised one (6e-2), combine 1e-5, the layer 1e-1 (two quantisations in series)."""
+@pytest.mark.parametrize("scales", ["amax", "pow2"])
+def test_c4_qwen3_fp8_layer_full_size(dev, scales):
+    """C4 at T=16384, D=2048, E=128, K=8, I=768 in blockwise fp8 (amax/448 and power-of-two scales):
+    quantiser codes bit-exact, gate_up + SwiGLU and the K_in = 768 down GEMM against the dequantised
+    float64 oracle (1e-2) and the unquantised one (6e-2; the down GEMM against the product of the
+    GPU's own bf16 SwiGLU output with the unquantised weights), combine 1e-5, the layer 1e-1 (two
+    quantisations in series)."""
     from mintext_amd.kernels import route_topk, unroute
     from mintext_amd.kernels.fp8 import (grouped_matmul_fp8, grouped_matmul_fp8_swiglu_gathered, quantize_fp8_rows,
                                          quantize_fp8_weights)
@@ -215,16 +218,18 @@ def test_c4_qwen3_fp8_layer_full_size(dev):
     with torch.no_grad():
         x, logits, gate_up, down, _, _ = B.layer_inputs("qwen3_fp8", dev)
         idx, w = route_topk(logits, K, **B.router_kwargs("qwen3_fp8"))
-        guq, gus = quantize_fp8_weights(gate_up)
-        dnq, dns = quantize_fp8_weights(down)
+        f8s = dict(scales=scales)
+        guq, gus = quantize_fp8_weights(gate_up, **f8s)
+        dnq, dns = quantize_fp8_weights(down, **f8s)
         # the bench's step
-        xq, xs = quantize_fp8_rows(x)
+        xq, xs = quantize_fp8_rows(x, **f8s)
         si, gs, inv = route_indices(idx, E)
-        yq, ys, yb = grouped_matmul_fp8_swiglu_gathered(xq, xs, si, K, guq, gus, gs, return_bf16=True)
-        o = grouped_matmul_fp8(yq, ys, dnq, dns, gs)
+        yq, ys, yb = grouped_matmul_fp8_swiglu_gathered(xq, xs, si, K, guq, gus, gs, return_bf16=True, **f8s)
+        o = grouped_matmul_fp8(yq, ys, dnq, dns, gs, **f8s)
         out = unroute(o, si, w, K)
-        assert torch.equal(moe_experts_forward_fp8(x, idx, w, guq, gus, dnq, dns), out)
-        yq2, ys2 = grouped_matmul_fp8_swiglu_gathered(xq, xs, si, K, guq, gus, gs)
+        if scales == "amax":
+            assert torch.equal(moe_experts_forward_fp8(x, idx, w, guq, gus, dnq, dns), out)
+        yq2, ys2 = grouped_matmul_fp8_swiglu_gathered(xq, xs, si, K, guq, gus, gs, **f8s)
         assert torch.equal(_u8t(yq2), _u8t(yq)) and torch.equal(ys2, ys)
     oi, _, _ = O.router_softmax(logits.float().cpu().numpy(), K)
     assert np.array_equal(idx.cpu().numpy(), oi)
@@ -240,7 +245,7 @@ def test_c4_qwen3_fp8_layer_full_size(dev):
     tr = torch.from_numpy(rows).to(dev)
     tok = sih[rows] // K
     # quantiser: codes and scales of the sampled tokens bit for bit
-    oq, os_ = O.quant_fp8_rows(x[torch.from_numpy(tok).to(dev)].float().cpu().numpy())
+    oq, os_ = O.quant_fp8_rows(x[torch.from_numpy(tok).to(dev)].float().cpu().numpy(), scales=scales)
     assert np.array_equal(_u8(xq[torch.from_numpy(tok).to(dev)]), oq)
     assert np.array_equal(xs[torch.from_numpy(tok).to(dev)].cpu().numpy(), os_)
     ex = _expert_of(gsh, rows)
@@ -248,8 +253,8 @@ def test_c4_qwen3_fp8_layer_full_size(dev):
     x64 = _host(x[torch.from_numpy(tok).to(dev)])
     yb_g, o_g = _host(yb[tr]), _host(o[tr])
     yq_g, ys_g = _u8(yq[tr]), ys[tr].cpu().numpy()
-    ref_y, ref_y_unq, ref_o, ref_o_unq = (np.empty_like(yb_g), np.empty_like(yb_g), np.empty_like(o_g),
-                                          np.empty_like(o_g))
+    ref_y, ref_y_unq, ref_o, ref_o_unq, ref_o_yb = (np.empty_like(yb_g), np.empty_like(yb_g), np.empty_like(o_g),
+                                                    np.empty_like(o_g), np.empty_like(o_g))
     for e in np.unique(ex):
         sel = np.flatnonzero(ex == e)
         e = int(e)
@@ -259,11 +264,13 @@ def test_c4_qwen3_fp8_layer_full_size(dev):
         ref_y_unq[sel] = O.swiglu(x64[sel] @ _host(gate_up[e]))
         ref_o[sel] = O.dequant_rows(yq_g[sel], ys_g[sel]) @ wdn    # down at K_in = 768 on the GPU's codes
         ref_o_unq[sel] = ref_y_unq[sel] @ _host(down[e])
+        ref_o_yb[sel] = yb_g[sel] @ _host(down[e])                 # the GPU's own SwiGLU output, unquantised W
     assert rel_err(yb_g, ref_y) < 1e-2, "fp8 gate_up + SwiGLU vs dequantised oracle"
     assert rel_err(yb_g, ref_y_unq) < 6e-2, "fp8 gate_up + SwiGLU vs unquantised"
     # the re-quantised intermediate: within e4m3's half-ulp of the SwiGLU output
     assert rel_err(O.dequant_rows(yq_g, ys_g), ref_y) < 4e-2, "SwiGLU re-quantisation"
     assert rel_err(o_g, ref_o) < 1e-2, "fp8 down (K_in=768) vs dequantised oracle"
+    assert rel_err(o_g, ref_o_yb) < 6e-2, "fp8 down (K_in=768) vs bf16 SwiGLU output x unquantised down"
     assert rel_err(o_g, ref_o_unq) < 1e-1, "fp8 down vs unquantised chain"
     wt = w.cpu().numpy().astype(np.float64)
     o_t = _host(o[torch.from_numpy(invh[(tokens[:, None] * K + np.arange(K)).ravel()]).to(dev)])
