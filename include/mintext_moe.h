@@ -266,7 +266,11 @@ int mtx_swiglu_bwd(const void* h, const void* dy, int dtype, int64_t M, int64_t 
  * w_q [E,Kout,Kin] with w_scale [E,Kout/128,Kin/128] (the per-expert nn.Linear layout).
  * Kin, Kout (and I) must be multiples of 128.  The block scales passed to the GEMMs must be
  * finite and nonzero (the quantisers never produce 0).  mtx_quant_fp8_rows needs x and xq
- * 16-byte aligned (MTX_ERR_ARG otherwise).                                                 */
+ * 16-byte aligned (MTX_ERR_ARG otherwise).  Range: the GEMMs (and mtx_tgmm_fp8) carry each
+ * accumulator in the units of the current 128-k block's scale product xs*ws, so a block whose
+ * scale product is more than about 2^96 / (Kin/128) times smaller than an earlier block's of
+ * the same output overflows the accumulator to inf (the true result may be finite).  Real
+ * data stays far inside that; the power-of-two mode below has no such limit.              */
 int mtx_quant_fp8_rows(const void* x, int dtype, int64_t M, int64_t D,
                        uint8_t* xq, float* x_scale, void* stream);
 /* mtx_quant_fp8_rows followed by mtx_route of the codes and scales, in one row pass: tokens

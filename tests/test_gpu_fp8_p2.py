@@ -155,6 +155,36 @@ def test_gmm_fp8_swiglu_gathered_p2_equals_route(dev, T, K, E, D, I):
     assert torch.equal(yq1.view(torch.uint8), yq2.view(torch.uint8))
 
 
+def test_gmm_fp8_p2_extreme_block_scale_ratios(dev):
+    """Neighbouring 128-k blocks of one row whose scales differ by up to 2^100 (a normal block, a
+    block near 1e-33, a normal block; an all-zero block, then tiny ones): the power-of-two mode
+    applies each block's exponents on the MFMA's E8M0 operands and accumulates in true units, so
+    nothing is rescaled between blocks and nothing overflows.  Checked against the dequantised
+    float64 oracle row by row (each row's own scale of magnitude)."""
+    from mintext_amd.kernels.fp8 import grouped_matmul_fp8, quantize_fp8_rows, quantize_fp8_weights
+
+    M, E, Kin, Kout = 512, 2, 512, 256
+    gs = np.array([200, 312], np.int32)
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    x = torch.randn(M, Kin, device=dev, generator=g)
+    blk = torch.ones(M, Kin // 128, device=dev)
+    blk[0::2, 1] = 1e-33                        # normal, tiny, normal, normal
+    blk[1::2, 0] = 0.0                          # zero, then tiny blocks only
+    blk[1::2, 1:] = torch.tensor([1e-30, 3e-28, 1e-31], device=dev)
+    x = (x * blk.repeat_interleave(128, 1)).bfloat16()
+    w = (torch.randn(E, Kin, Kout, device=dev, generator=g) * 0.02).bfloat16()
+    xq, xs = quantize_fp8_rows(x, **P2)
+    wq, ws = quantize_fp8_weights(w, **P2)
+    out = grouped_matmul_fp8(xq, xs, wq, ws, _t(gs, dev), **P2)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    deq = O.gmm_fp8(_u8(xq), xs.cpu().numpy(), _u8(wq), ws.cpu().numpy(), gs)
+    for rows in (slice(0, None, 2), slice(1, None, 2)):
+        assert rel_err(got[rows], deq[rows]) < 1e-2, rel_err(got[rows], deq[rows])
+    assert np.abs(got[1::2]).max() < 1e-25 and np.abs(got[1::2]).max() > 1e-29
+
+
 def test_gmm_fp8_p2_short_k_unsupported(dev):
     from mintext_amd import _lib as L
     from mintext_amd.kernels.fp8 import grouped_matmul_fp8, quantize_fp8_rows, quantize_fp8_weights

@@ -36,8 +36,12 @@ def test_noalloc_gmm_matches_workspace_entry_point(dev, dtype, op):
     lib = L.lib()
     code = {"fwd": L.MTX_GMM_OP_FWD, "swiglu": L.MTX_GMM_OP_SWIGLU, "dlhs": L.MTX_GMM_OP_DLHS}[op]
     stream = L.stream(dev)
-    # 256-row tiles (and, with the full workspace, split tails) first, then 128-row tiles
-    for call, (M, E, Kin, Kout) in enumerate([(8192, 6, 512, 768), (1000, 3, 256, 384)]):
+    # bf16 kernel forms, each call smaller than the one before it on that form: reductions of 2304
+    # (beyond the persistent kernel's 32 stages) with >= 512 rows per expert on average (one-wave-
+    # per-SIMD kernel) and then fewer (8-wave per-tile kernel), both with split tails under the full
+    # workspace; then the persistent short-reduction kernel; then 128-row tiles
+    shapes = [(4096, 4, 2304, 2304), (3000, 8, 2304, 2304), (8192, 6, 512, 768), (1000, 3, 256, 384)]
+    for call, (M, E, Kin, Kout) in enumerate(shapes):
         rng = np.random.default_rng(call * 10 + len(op))
         gs = _groups(rng, M, E)
         a_cols = Kout if op == "dlhs" else Kin
