@@ -46,13 +46,15 @@ CONFIGS = {
 
 
 def _traffic(name: str):
+    """(HBM bytes per launch, kernel description) from profiles/traffic_<name>.json, or (None, None)."""
     p = ROOT / "profiles" / f"traffic_{name}.json"
     if p.exists():
         try:
-            return json.loads(p.read_text()).get("bytes_per_launch")
+            d = json.loads(p.read_text())
+            return d.get("bytes_per_launch"), d.get("kernel")
         except Exception:
-            return None
-    return None
+            return None, None
+    return None, None
 
 
 class EventTimer:
@@ -347,8 +349,8 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
         dominant = (("gmm_fp8_swiglu_p2 (gate_up + SwiGLU + pow2 requant)" if fp8_scales == "pow2"
                      else "gmm_fp8_swiglu (gate_up + SwiGLU + requant)") if fp8 else "gmm_swiglu (gate_up + fused SwiGLU)")
     tname = cfg_name + ("_pow2" if fp8 and fp8_scales == "pow2" and not bwd else "")
-    traffic = _traffic(tname)
-    tsrc = {"traffic_source": f"profiles/traffic_{tname}.json (rocprofv3 FETCH_SIZE/WRITE_SIZE of this kernel, "
+    traffic, tkern = _traffic(tname)
+    tsrc = {"traffic_source": f"profiles/traffic_{tname}.json (rocprofv3 FETCH_SIZE/WRITE_SIZE of {tkern}, "
                               "scaled by a plain copy's counters)"} if traffic is not None else {}
     if cfg_name == "deepseek":
         # C3 streams its routed weights once per layer at ~128 rows per expert (arithmetic intensity
