@@ -223,5 +223,22 @@ __device__ __forceinline__ void st8(uint16_t* p, int64_t i, const float v[8]) {
   for (int q = 0; q < 4; ++q) a[q] = pack_bf16x2(v[2 * q], v[2 * q + 1]);
   *(v4u32*)(p + i) = a;
 }
+// Non-temporal stores (data written once and not read soon: streamed past the caches).
+__device__ __forceinline__ void st8_nt(uint16_t* p, int64_t i, const float v[8]) {
+  v4u32 a;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) a[q] = pack_bf16x2(v[2 * q], v[2 * q + 1]);
+  __builtin_nontemporal_store(a, (v4u32*)(p + i));
+}
+__device__ __forceinline__ void st8_nt(float* p, int64_t i, const float v[8]) {
+  v4u32 a, b;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    a[q] = __float_as_uint(v[q]);
+    b[q] = __float_as_uint(v[4 + q]);
+  }
+  __builtin_nontemporal_store(a, (v4u32*)(p + i));
+  __builtin_nontemporal_store(b, (v4u32*)(p + i + 4));
+}
 
 }  // namespace mtx

@@ -251,7 +251,8 @@ _F32, _BF16 = torch.float32, torch.bfloat16
                                                (129, 3, 264, _F32, _F32, _F32), (64, 8, 2048, _BF16, _F32, _F32),
                                                (65, 9, 512, _BF16, _F32, _F32), (70, 2, 100, _BF16, _F32, _F32),
                                                (200, 2, 512, _BF16, _BF16, _BF16), (100, 8, 256, _BF16, _BF16, _F32),
-                                               (90, 4, 136, _F32, _BF16, _BF16)])
+                                               (90, 4, 136, _F32, _BF16, _BF16),
+                                               (50, 8, 1800, _BF16, _F32, _F32)])  # lanes with 1 or 2 chunks
 def test_unroute_bwd_vector_and_scalar_forms(dev, N, K, D, ydt, gdt, wdt):
     """mtx_unroute_bwd (the layer's combine output and router weights as dout / w, in f32 or bf16):
     d_sorted bit-exact against the f32 products of the inputs rounded to the row dtype, d_w against
