@@ -488,7 +488,7 @@ __global__ __launch_bounds__(256) void swiglu_vec_kernel(const T* __restrict__ h
       ld8(h + r * 2 * I + I, 8 * (int64_t)c, u);
 #pragma unroll
       for (int q = 0; q < 8; ++q) o[q] = silu_f32(g[q]) * u[q];
-      st8(out + r * I, 8 * (int64_t)c, o);
+      st8_nt(out + r * I, 8 * (int64_t)c, o);  // written once (C3 68.8 -> 63.4 us; C2, C4 equal)
     }
 }
 template <typename T>
@@ -508,8 +508,8 @@ __global__ __launch_bounds__(256) void swiglu_bwd_vec_kernel(const T* __restrict
         dg[q] = d[q] * u[q] * (s * (1.0f + g[q] * (1.0f - s)));
         du[q] = d[q] * g[q] * s;
       }
-      st8(dh + r * 2 * I, 8 * (int64_t)c, dg);
-      st8(dh + r * 2 * I + I, 8 * (int64_t)c, du);
+      st8_nt(dh + r * 2 * I, 8 * (int64_t)c, dg);  // written once (C3 -4.5 %, C4 -3.8 %, C2 equal)
+      st8_nt(dh + r * 2 * I + I, 8 * (int64_t)c, du);
     }
 }
 // Workgroups for the vector kernels: one pass of rows each, at most 65536 (grid-stride beyond).
