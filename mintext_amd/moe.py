@@ -201,28 +201,33 @@ def shared_expert_forward(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Te
 
 def moe_experts_forward_fp8(x: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
                             gate_up_q: torch.Tensor, gate_up_scale: torch.Tensor, down_q: torch.Tensor,
-                            down_scale: torch.Tensor) -> torch.Tensor:
+                            down_scale: torch.Tensor, *, scales: str = "amax") -> torch.Tensor:
     """Blockwise-fp8 expert layer; weights from ``quantize_fp8_weights`` ([E, Kout, Kin] e4m3).
-    Forward only: raises under autograd when an input requires grad."""
+    ``scales`` is the mode the weights were quantised in and the activations are quantised in:
+    "amax" (scale amax/448) or "pow2" (power-of-two scales applied by the MFMA; needs D and I of at
+    least 256).  Forward only: raises under autograd when an input requires grad."""
     if torch.is_grad_enabled() and any(t.requires_grad for t in (x, topk_weights, gate_up_q, down_q)):
         raise RuntimeError("moe_experts_forward_fp8 is forward-only; run it under torch.no_grad(), or train "
                            "through moe_experts_forward or moe_experts_forward_fp8_train")
-    from .kernels.fp8 import (grouped_matmul_fp8, grouped_matmul_fp8_swiglu, grouped_matmul_fp8_swiglu_gathered,
-                              quantize_fp8_rows)
-
+    from .kernels.fp8 import (SCALE_MODES, grouped_matmul_fp8, grouped_matmul_fp8_swiglu,
+                              grouped_matmul_fp8_swiglu_gathered, quantize_fp8_rows)
+    if scales not in SCALE_MODES:
+        raise ValueError(f"scales must be one of {SCALE_MODES}, got {scales!r}")
+    f8s = dict(scales=scales)
     E = gate_up_q.shape[0]
     T, D = x.shape
-    if D >= 256 and T * D < 2 ** 32 and gate_up_q.shape[1] * D < 2 ** 32:
-        # tokens quantised in token order; the gate_up GEMM gathers their rows (no sorted copy)
-        xq, xs = quantize_fp8_rows(x)
+    if scales == "pow2" or (D >= 256 and T * D < 2 ** 32 and gate_up_q.shape[1] * D < 2 ** 32):
+        # tokens quantised in token order; the gate_up GEMM gathers their rows (no sorted copy).  The
+        # power-of-two GEMMs have no other form: shapes outside it raise from the kernels.
+        xq, xs = quantize_fp8_rows(x, **f8s)
         sort_indices, group_sizes, _ = route_indices(topk_indices, E)
         yq, ys = grouped_matmul_fp8_swiglu_gathered(xq, xs, sort_indices, topk_indices.shape[1], gate_up_q,
-                                                    gate_up_scale, group_sizes)
+                                                    gate_up_scale, group_sizes, **f8s)
     else:
         # 1x128 quantisation of the tokens fused into their dispatch (each row read once)
         sq, ss, sort_indices, group_sizes, _ = route_quantize_fp8(x, topk_indices, E)
         yq, ys = grouped_matmul_fp8_swiglu(sq, ss, gate_up_q, gate_up_scale, group_sizes)
-    out = grouped_matmul_fp8(yq, ys, down_q, down_scale, group_sizes)
+    out = grouped_matmul_fp8(yq, ys, down_q, down_scale, group_sizes, **f8s)
     return unroute(out, sort_indices, topk_weights, topk_indices.shape[1])
 
 

@@ -195,3 +195,47 @@ def test_gmm_fp8_p2_short_k_unsupported(dev):
     wq, ws = quantize_fp8_weights(w, **P2)
     with pytest.raises(L.MtxError):
         grouped_matmul_fp8(xq, xs, wq, ws, _t(np.array([100, 200], np.int32), dev), **P2)
+
+
+def test_layer_forward_pow2_and_unsupported_width(dev):
+    """moe_experts_forward_fp8(scales="pow2") equals its steps (pow2 quantiser, gathered SwiGLU GEMM,
+    down GEMM, combine) bit for bit and stays within 1e-1 of the unquantised float64 layer; a width
+    below 256 raises (the power-of-two GEMMs need K >= 256); an unknown mode raises ValueError."""
+    from mintext_amd import _lib as L
+    from mintext_amd.kernels import unroute
+    from mintext_amd.kernels.fp8 import (grouped_matmul_fp8, grouped_matmul_fp8_swiglu_gathered, quantize_fp8_rows,
+                                         quantize_fp8_weights)
+    from mintext_amd.kernels.moe_dispatch import route_indices
+    from mintext_amd.moe import moe_experts_forward_fp8
+
+    rng = np.random.default_rng(11)
+    T, K, E, D, I = 700, 4, 8, 512, 256
+    idx = _t(np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32), dev)
+    w = _t(rng.random((T, K)).astype(np.float32), dev)
+    x = torch.randn(T, D, device=dev).bfloat16()
+    gu = (torch.randn(E, D, 2 * I, device=dev) * 0.05).bfloat16()
+    dn = (torch.randn(E, I, D, device=dev) * 0.05).bfloat16()
+    with torch.no_grad():
+        guq, gus = quantize_fp8_weights(gu, **P2)
+        dnq, dns = quantize_fp8_weights(dn, **P2)
+        out = moe_experts_forward_fp8(x, idx, w, guq, gus, dnq, dns, **P2)
+        xq, xs = quantize_fp8_rows(x, **P2)
+        si, gs, _ = route_indices(idx, E)
+        yq, ys = grouped_matmul_fp8_swiglu_gathered(xq, xs, si, K, guq, gus, gs, **P2)
+        ref = unroute(grouped_matmul_fp8(yq, ys, dnq, dns, gs, **P2), si, w, K)
+        assert torch.equal(out, ref)
+        xh, ih, wh = x.double().cpu().numpy(), idx.cpu().numpy(), w.double().cpu().numpy()
+        guh, dnh = gu.double().cpu().numpy(), dn.double().cpu().numpy()
+        want = np.zeros((T, D))
+        for k in range(K):
+            for e in range(E):
+                sel = np.flatnonzero(ih[:, k] == e)
+                want[sel] += wh[sel, k:k + 1] * (O.swiglu(xh[sel] @ guh[e]) @ dnh[e])
+        assert rel_err(out.double().cpu().numpy(), want) < 1e-1
+        xs_ = torch.randn(T, 128, device=dev).bfloat16()
+        g2q, g2s = quantize_fp8_weights((torch.randn(E, 128, 2 * I, device=dev) * 0.05).bfloat16(), **P2)
+        d2q, d2s = quantize_fp8_weights((torch.randn(E, I, 128, device=dev) * 0.05).bfloat16(), **P2)
+        with pytest.raises(L.MtxError):
+            moe_experts_forward_fp8(xs_, idx, w, g2q, g2s, d2q, d2s, **P2)
+        with pytest.raises(ValueError):
+            moe_experts_forward_fp8(x, idx, w, guq, gus, dnq, dns, scales="e8m0")

@@ -227,8 +227,7 @@ def test_c4_qwen3_fp8_layer_full_size(dev, scales):
         yq, ys, yb = grouped_matmul_fp8_swiglu_gathered(xq, xs, si, K, guq, gus, gs, return_bf16=True, **f8s)
         o = grouped_matmul_fp8(yq, ys, dnq, dns, gs, **f8s)
         out = unroute(o, si, w, K)
-        if scales == "amax":
-            assert torch.equal(moe_experts_forward_fp8(x, idx, w, guq, gus, dnq, dns), out)
+        assert torch.equal(moe_experts_forward_fp8(x, idx, w, guq, gus, dnq, dns, **f8s), out)
         yq2, ys2 = grouped_matmul_fp8_swiglu_gathered(xq, xs, si, K, guq, gus, gs, **f8s)
         assert torch.equal(_u8t(yq2), _u8t(yq)) and torch.equal(ys2, ys)
     oi, _, _ = O.router_softmax(logits.float().cpu().numpy(), K)
