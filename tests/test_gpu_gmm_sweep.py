@@ -4,7 +4,9 @@ reductions on both sides of the persistent kernel's range (Kred <= 1024 runs the
 plain-store kernel, longer ones the per-tile kernel with its split tail).  Each case checks the
 default schedule against the 128-row tiling (the same f32 sums: bit for bit when no tile is split,
 else within a bf16 ulp plus the f32 cancellation error), both against the float64 oracle at
-2e-2, and that rows past the groups are zero."""
+2e-2, and that rows past the groups are zero.  A second seeded set holds groups of 512 rows or
+more on average with long reductions (forward, dlhs) and the fused SwiGLU: the shapes of the
+one-wave-per-SIMD kernel, with its thin, partial and split-tail tiles."""
 from __future__ import annotations
 
 import numpy as np
@@ -78,4 +80,64 @@ def test_gmm_sweep(dev, case):
     else:
         d = (out.float() - out128.float()).abs()
         bound = out128.float().abs() * 2.0 ** -7 + 1e-5 * float(np.abs(ref).max() if ref.size else 1.0)
+        assert bool((d <= bound).all()), (d - bound).max().item()
+
+
+def _cases_large(n=12, seed=4242):
+    """Shapes on the one-wave-per-SIMD kernel's side of the dispatch: groups of 512 rows or more
+    on average, reductions past the persistent kernel's 1024 (forward, dlhs) and any reduction
+    for the fused SwiGLU (which always takes that kernel at this mean)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        op = ("fwd", "dlhs", "swiglu")[i % 3]
+        E = int(rng.choice([1, 2, 3, 4, 6, 8]))
+        M = E * int(rng.integers(512, 2400)) + int(rng.integers(0, 256))
+        kred = int(rng.choice([512, 768, 1152, 2304] if op == "swiglu" else [1056, 1152, 1536, 2048, 2304, 3072]))
+        nout = int(rng.choice([256, 512, 768, 1024, 1536]))
+        kind = str(rng.choice(["uniform", "zipf", "ragged"]))
+        past = int(rng.choice([0, 7, 256]))
+        out.append((i, E, M, kred, nout, kind, past, op))
+    return out
+
+
+@pytest.mark.parametrize("case", _cases_large(), ids=lambda c: f"c{c[0]}-E{c[1]}-M{c[2]}-K{c[3]}-N{c[4]}-{c[5]}-p{c[6]}-{c[7]}")
+def test_gmm_sweep_large_groups(dev, case):
+    from mintext_amd.kernels.grouped_matmul import _gmm_dlhs, _gmm_fwd, grouped_matmul_swiglu
+
+    i, E, M, kred, nout, kind, past, op = case
+    rng = np.random.default_rng(500 + i)
+    gs = _groups(rng, M, E, kind)
+    Mt = M + past
+    x = (rng.standard_normal((Mt, kred)) * 0.5).astype(np.float32)
+    wshape = (E, nout, kred) if op == "dlhs" else (E, kred, nout)
+    w = (rng.standard_normal(wshape) * 0.05).astype(np.float32)
+    xt = torch.from_numpy(x).to(dev).bfloat16()
+    wt = torch.from_numpy(w).to(dev).bfloat16()
+    gt = torch.from_numpy(gs).to(dev)
+    f = {"fwd": _gmm_fwd, "dlhs": _gmm_dlhs}.get(op)
+    if f is None:
+        out = grouped_matmul_swiglu(xt, wt, gt)
+        out128 = grouped_matmul_swiglu(xt, wt, gt, tiling=(128, 1, 256))
+    else:
+        out = f(xt, wt, gt)
+        out128 = f(xt, wt, gt, tiling=(128, 1, 256))
+    ncols = nout // 2 if op == "swiglu" else nout
+    assert out.shape == (Mt, ncols)
+    assert (out[M:] == 0).all(), "rows past sum(group_sizes) must be zero"
+    xr, wr = xt.float().cpu().numpy(), wt.float().cpu().numpy()
+    if op == "dlhs":
+        ref = O.gmm_dlhs(xr, wr, gs)
+    else:
+        ref = O.gmm(xr, wr, gs)
+        if op == "swiglu":
+            ref = O.swiglu(ref)
+    for o in (out, out128):
+        got = o.float().cpu().numpy()
+        assert rel_err(got[:M], ref[:M]) < 2e-2, rel_err(got[:M], ref[:M])
+    if op == "swiglu":  # whole tiles (no split tail on this path): the 128-row tiling's bits
+        assert torch.equal(out, out128)
+    else:
+        d = (out.float() - out128.float()).abs()
+        bound = out128.float().abs() * 2.0 ** -7 + 1e-5 * float(np.abs(ref).max())
         assert bool((d <= bound).all()), (d - bound).max().item()
