@@ -786,7 +786,10 @@ def dispatch_bwd_study(steps=20, warmup=5):
     f32 d_weights; moe_dispatch.py:102-111), the route's VJP (mtx_unroute with unit weights, bf16;
     moe_dispatch.py:33-38,67), and SwiGLU with its VJP (mtx_swiglu / mtx_swiglu_bwd, bf16;
     moe.py:195-196).  Bytes are algorithmic (every input read once, every output written once);
-    times are HIP-event means over ``steps`` calls on the current stream."""
+    times are HIP-event means over ``steps`` calls on the current stream, after ``warmup`` calls.
+    Before a shape is timed its kernels run in turn for at least 50 ms: on these boxes the first
+    few milliseconds after a large buffer is first touched run up to 1.5x slower for any kernel
+    that streams it (SwiGLU on the C2 shape: 220 us, then 350, then 280-240 us per call)."""
     import torch
     from mintext_amd import _lib as L
 
@@ -845,6 +848,11 @@ def dispatch_bwd_study(steps=20, warmup=5):
 
         kernels["swiglu"] = (sw, M * I * 2 * 3)
         kernels["swiglu_bwd"] = (swb, M * I * 2 * 5)
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < 0.05:
+            for fn, _ in kernels.values():
+                fn()
+            torch.cuda.synchronize()
         for kname, (fn, nbytes) in kernels.items():
             ms = t_ms(fn)
             row[kname] = {"us": round(ms * 1e3, 1), "MB": round(nbytes / 1e6, 1),

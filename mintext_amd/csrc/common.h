@@ -223,6 +223,24 @@ __device__ __forceinline__ void st8(uint16_t* p, int64_t i, const float v[8]) {
   for (int q = 0; q < 4; ++q) a[q] = pack_bf16x2(v[2 * q], v[2 * q + 1]);
   *(v4u32*)(p + i) = a;
 }
+// Non-temporal loads (data read once: streamed past the caches), same conversions as ld8.
+__device__ __forceinline__ void ld8_nt(const float* p, int64_t i, float v[8]) {
+  const v4u32 a = __builtin_nontemporal_load((const v4u32*)(p + i));
+  const v4u32 b = __builtin_nontemporal_load((const v4u32*)(p + i + 4));
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    v[q] = __uint_as_float(a[q]);
+    v[4 + q] = __uint_as_float(b[q]);
+  }
+}
+__device__ __forceinline__ void ld8_nt(const uint16_t* p, int64_t i, float v[8]) {
+  const v4u32 a = __builtin_nontemporal_load((const v4u32*)(p + i));
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    v[2 * q] = __uint_as_float(a[q] << 16);
+    v[2 * q + 1] = __uint_as_float(a[q] & 0xffff0000u);
+  }
+}
 // Non-temporal stores (data written once and not read soon: streamed past the caches).
 __device__ __forceinline__ void st8_nt(uint16_t* p, int64_t i, const float v[8]) {
   v4u32 a;

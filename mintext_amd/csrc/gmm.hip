@@ -463,59 +463,80 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const T* __restrict__ h
   }
 }
 
-// Vector forms of the two kernels above for I % 8 == 0 and 16-byte aligned rows: a thread
-// takes eight consecutive columns of a row (16-byte accesses), and a workgroup spreads over
-// 256 / (I/8) rows when a row has fewer than 256 such chunks.  Each element is computed by the
-// same expression as in the scalar kernels, so the results are the same bits.
-struct RowChunks {
-  int cpr, rpb, rsub, c0, cstep;  // chunks per row, rows per workgroup pass, this thread's row and chunk
-  __device__ RowChunks(int64_t I) {
-    cpr = (int)(I / 8);
-    const int t = threadIdx.x;
-    if (cpr >= 256) { rpb = 1; rsub = 0; c0 = t; cstep = 256; }
-    else { rpb = 256 / cpr; rsub = t / cpr; c0 = t % cpr; cstep = cpr; }
-  }
-};
-template <typename T>
+// Vector forms of the two kernels above for I % 8 == 0 and 16-byte aligned rows.  The M x I/8
+// chunks of eight columns are numbered row-major; a workgroup takes 512 consecutive chunks, two
+// per thread 256 apart, and issues every load before its stores; loads and stores are
+// non-temporal (each byte is touched once).  Q is the chunk index type: 32-bit when M * I/8 fits.
+// Against one row per workgroup with plain loads (same bits), C2 / C3 / C4 shapes: swiglu 5.25 /
+// 6.21 / 5.46 -> 6.13 / 6.05 / 6.27 TB/s, swiglu_bwd 5.18 / 5.94 / 5.92 -> 6.04 / 6.26 / 6.26; one
+// chunk per thread or four, and persistent grids of 4-16 workgroups per CU, were slower.  Each element is computed by the same
+// expression as in the scalar kernels, so the results are the same bits.
+constexpr int kSwChunks = 2;  // chunks per thread
+template <typename T, typename Q>
 __global__ __launch_bounds__(256) void swiglu_vec_kernel(const T* __restrict__ h, int64_t M, int64_t I,
                                                          T* __restrict__ out) {
-  const RowChunks rc(I);
-  if (rc.rsub >= rc.rpb) return;
-  for (int64_t r = (int64_t)blockIdx.x * rc.rpb + rc.rsub; r < M; r += (int64_t)gridDim.x * rc.rpb)
-    for (int c = rc.c0; c < rc.cpr; c += rc.cstep) {
-      float g[8], u[8], o[8];
-      ld8(h + r * 2 * I, 8 * (int64_t)c, g);
-      ld8(h + r * 2 * I + I, 8 * (int64_t)c, u);
+  const Q cpr = (Q)(I / 8), total = (Q)M * cpr;
+  const Q step = (Q)gridDim.x * 256 * kSwChunks;
+  for (Q b = (Q)blockIdx.x * 256 * kSwChunks + threadIdx.x; b < total; b += step) {
+    float g[kSwChunks][8], u[kSwChunks][8];
+    int64_t r[kSwChunks], c[kSwChunks];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) o[q] = silu_f32(g[q]) * u[q];
-      st8_nt(out + r * I, 8 * (int64_t)c, o);  // written once (C3 68.8 -> 63.4 us; C2, C4 equal)
+    for (int k = 0; k < kSwChunks; ++k) {
+      const Q q = min(b + (Q)(k * 256), total - 1);  // in bounds; the store below is guarded
+      r[k] = (int64_t)(q / cpr);
+      c[k] = 8 * (int64_t)(q - (Q)r[k] * cpr);
+      ld8_nt(h + r[k] * 2 * I, c[k], g[k]);
+      ld8_nt(h + r[k] * 2 * I + I, c[k], u[k]);
     }
+#pragma unroll
+    for (int k = 0; k < kSwChunks; ++k) {
+      if (b + (Q)(k * 256) >= total) break;
+      float o[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) o[q] = silu_f32(g[k][q]) * u[k][q];
+      st8_nt(out + r[k] * I, c[k], o);
+    }
+  }
 }
-template <typename T>
+template <typename T, typename Q>
 __global__ __launch_bounds__(256) void swiglu_bwd_vec_kernel(const T* __restrict__ h, const T* __restrict__ dy,
                                                              int64_t M, int64_t I, T* __restrict__ dh) {
-  const RowChunks rc(I);
-  if (rc.rsub >= rc.rpb) return;
-  for (int64_t r = (int64_t)blockIdx.x * rc.rpb + rc.rsub; r < M; r += (int64_t)gridDim.x * rc.rpb)
-    for (int c = rc.c0; c < rc.cpr; c += rc.cstep) {
-      float g[8], u[8], d[8], dg[8], du[8];
-      ld8(h + r * 2 * I, 8 * (int64_t)c, g);
-      ld8(h + r * 2 * I + I, 8 * (int64_t)c, u);
-      ld8(dy + r * I, 8 * (int64_t)c, d);
+  const Q cpr = (Q)(I / 8), total = (Q)M * cpr;
+  const Q step = (Q)gridDim.x * 256 * kSwChunks;
+  for (Q b = (Q)blockIdx.x * 256 * kSwChunks + threadIdx.x; b < total; b += step) {
+    float g[kSwChunks][8], u[kSwChunks][8], d[kSwChunks][8];
+    int64_t r[kSwChunks], c[kSwChunks];
+#pragma unroll
+    for (int k = 0; k < kSwChunks; ++k) {
+      const Q q = min(b + (Q)(k * 256), total - 1);
+      r[k] = (int64_t)(q / cpr);
+      c[k] = 8 * (int64_t)(q - (Q)r[k] * cpr);
+      ld8_nt(h + r[k] * 2 * I, c[k], g[k]);
+      ld8_nt(h + r[k] * 2 * I + I, c[k], u[k]);
+      ld8_nt(dy + r[k] * I, c[k], d[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < kSwChunks; ++k) {
+      if (b + (Q)(k * 256) >= total) break;
+      float dg[8], du[8];
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const float s = 1.0f / (1.0f + expf(-g[q]));
-        dg[q] = d[q] * u[q] * (s * (1.0f + g[q] * (1.0f - s)));
-        du[q] = d[q] * g[q] * s;
+        const float s = 1.0f / (1.0f + expf(-g[k][q]));
+        dg[q] = d[k][q] * u[k][q] * (s * (1.0f + g[k][q] * (1.0f - s)));
+        du[q] = d[k][q] * g[k][q] * s;
       }
-      st8_nt(dh + r * 2 * I, 8 * (int64_t)c, dg);  // written once (C3 -4.5 %, C4 -3.8 %, C2 equal)
-      st8_nt(dh + r * 2 * I + I, 8 * (int64_t)c, du);
+      st8_nt(dh + r[k] * 2 * I, c[k], dg);
+      st8_nt(dh + r[k] * 2 * I + I, c[k], du);
     }
+  }
 }
-// Workgroups for the vector kernels: one pass of rows each, at most 65536 (grid-stride beyond).
+// Workgroups for the vector kernels: 512 chunks each, at most 2^20 (grid-stride beyond).
 static int64_t swiglu_vec_blocks(int64_t M, int64_t I) {
-  const int64_t cpr = I / 8, rpb = cpr >= 256 ? 1 : 256 / cpr;
-  return std::min<int64_t>(ceil_div(M, rpb), 65536);
+  return std::min<int64_t>(ceil_div(M * (I / 8), 256 * kSwChunks), int64_t(1) << 20);
+}
+// 32-bit chunk indices when every index the kernels form (up to total - 1 + one grid stride) fits.
+static bool swiglu_vec_narrow(int64_t M, int64_t I) {
+  return M * (I / 8) + swiglu_vec_blocks(M, I) * 256 * kSwChunks < (int64_t(1) << 32);
 }
 static bool swiglu_vec_ok(int64_t I, const void* a, const void* b, const void* c) {
   return I % 8 == 0 && I > 0 && (uintptr_t)a % 16 == 0 && (uintptr_t)b % 16 == 0 && (uintptr_t)c % 16 == 0;
@@ -2299,11 +2320,15 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
 static int launch_swiglu(const void* h, int dtype, int64_t M, int64_t I, void* out, hipStream_t st) {
   if (M > 0 && swiglu_vec_ok(I, h, h, out)) {
     const int64_t vb = swiglu_vec_blocks(M, I);
-    if (dtype == MTX_F32)
-      hipLaunchKernelGGL(swiglu_vec_kernel<float>, dim3(vb), dim3(256), 0, st, (const float*)h, M, I, (float*)out);
-    else
-      hipLaunchKernelGGL(swiglu_vec_kernel<uint16_t>, dim3(vb), dim3(256), 0, st, (const uint16_t*)h, M, I,
-                         (uint16_t*)out);
+#define MTX_SW(T, Q) hipLaunchKernelGGL((swiglu_vec_kernel<T, Q>), dim3(vb), dim3(256), 0, st, (const T*)h, M, I, (T*)out)
+    if (dtype == MTX_F32) {
+      if (swiglu_vec_narrow(M, I)) MTX_SW(float, uint32_t);
+      else MTX_SW(float, uint64_t);
+    } else {
+      if (swiglu_vec_narrow(M, I)) MTX_SW(uint16_t, uint32_t);
+      else MTX_SW(uint16_t, uint64_t);
+    }
+#undef MTX_SW
     return check_launch();
   }
   int64_t blocks = ceil_div(M * I, 256);
@@ -2470,12 +2495,17 @@ extern "C" int mtx_swiglu_bwd(const void* h, const void* dy, int dtype, int64_t 
   hipStream_t st = (hipStream_t)stream;
   if (swiglu_vec_ok(I, h, dy, dh)) {
     const int64_t vb = swiglu_vec_blocks(M, I);
-    if (dtype == MTX_F32)
-      hipLaunchKernelGGL(swiglu_bwd_vec_kernel<float>, dim3(vb), dim3(256), 0, st, (const float*)h,
-                         (const float*)dy, M, I, (float*)dh);
-    else
-      hipLaunchKernelGGL(swiglu_bwd_vec_kernel<uint16_t>, dim3(vb), dim3(256), 0, st, (const uint16_t*)h,
-                         (const uint16_t*)dy, M, I, (uint16_t*)dh);
+#define MTX_SW(T, Q)                                                                                          \
+  hipLaunchKernelGGL((swiglu_bwd_vec_kernel<T, Q>), dim3(vb), dim3(256), 0, st, (const T*)h, (const T*)dy, M, I, \
+                     (T*)dh)
+    if (dtype == MTX_F32) {
+      if (swiglu_vec_narrow(M, I)) MTX_SW(float, uint32_t);
+      else MTX_SW(float, uint64_t);
+    } else {
+      if (swiglu_vec_narrow(M, I)) MTX_SW(uint16_t, uint32_t);
+      else MTX_SW(uint16_t, uint64_t);
+    }
+#undef MTX_SW
     return check_launch();
   }
   int64_t blocks = ceil_div(M * I, 256);
