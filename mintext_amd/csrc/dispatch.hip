@@ -836,7 +836,9 @@ __global__ __launch_bounds__(256) void unroute_bwd_vec_kernel(
   }
   if (live) {
     // two of the lane's chunks per pass (more loads in flight per lane: C4 268 -> 248 us); d_sorted
-    // is written once, with non-temporal stores (C2 83 -> 61 us, C4 248 -> 245 us, C3 unchanged)
+    // is written once, with non-temporal stores (C2 83 -> 61 us, C4 248 -> 245 us, C3 unchanged);
+    // the expert rows are read once, with non-temporal loads when K > 2 (C3 217 -> 196 us, C4 245
+    // -> 222 us; C2 +1 %, so plain there; non-temporal dout loads gave nothing)
     const GT* g_row = dout + n * D;
     constexpr int64_t step = 64 * 8 * WPT;
     for (int64_t c = ((int64_t)part * 64 + lane) * 8; c < D; c += 2 * step) {
@@ -848,8 +850,13 @@ __global__ __launch_bounds__(256) void unroute_bwd_vec_kernel(
       for (int k = 0; k < KM; ++k) {
         if (j[k] < 0) continue;
         float y[8], y2[8], o[8];
-        ld8(Y + j[k] * D, c, y);
-        if (two) ld8(Y + j[k] * D, c + step, y2);
+        if constexpr (KM > 2) {
+          ld8_nt(Y + j[k] * D, c, y);
+          if (two) ld8_nt(Y + j[k] * D, c + step, y2);
+        } else {
+          ld8(Y + j[k] * D, c, y);
+          if (two) ld8(Y + j[k] * D, c + step, y2);
+        }
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
           dot[k] = fmaf(g[q], y[q], dot[k]);
