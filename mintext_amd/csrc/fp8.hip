@@ -764,6 +764,12 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v3_kernel(Args p) {
 // even stage of every 128-k block also carries that block's 256 x-row scales (global_load_lds
 // of 4 bytes per lane, waves 0-3) and its two weight-block scales (wave 4), so no tile prologue
 // waits on memory.  Needs K >= 256 (four stages per tile, three in flight).
+// P2 (power-of-two scales, p2_scale): the scales are E8M0 codes (their f32 exponent fields) given
+// to v_mfma_scale_f32_32x32x64_f8f6f4, which multiplies each lane's codes by 2^(code - 127) -- the
+// row's 1x128 activation scale and the weight block's 128x128 scale, constant over the MFMA's 64
+// k -- so the accumulators stay in true units over all of K: no rescale at the block boundaries
+// and no scale multiply in the epilogue.  On the C4 shapes this is 8-9 % faster than the one-wave-
+// per-SIMD per-tile kernel it replaced (the same bits: the same MFMA sequence per output element).
 namespace v4 {
 constexpr int BM = 256, BN = 256, BKB = 64, NSTAGE = 4, PD = 3;
 constexpr int A_BYTES = BM * BKB, B_BYTES = BN * BKB;
@@ -775,7 +781,7 @@ struct Tile {
 };
 }  // namespace v4
 
-template <int EPI>
+template <int EPI, bool P2 = false>
 __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
   using namespace v4;
   using v3::a_off;
@@ -920,6 +926,31 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
     }
   };
   auto half_of = [&](int j) -> int { return (EPI == EPI_SWIGLU_Q) ? j : 0; };
+  // P2 (power-of-two scales): the same block scales as E8M0 codes for the MFMA's scale operands --
+  // the lane's four row-block codes packed one per byte (opsel i), the weight block code(s) per half
+  uint32_t ea_c = 0, ea_n = 0, eb_c[NSB] = {}, eb_n[NSB] = {};
+  auto read_codes = [&](int g, uint32_t& ea, uint32_t (&eb)[NSB]) {
+    const float* sc = (const float*)(lds + (g & (NSTAGE - 1)) * STAGE + S_OFF);
+    uint32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) s |= e8m0_of(sc[wm * WTM + i * 32 + frow]) << (8 * i);
+    ea = s;
+    if (EPI == EPI_SWIGLU_Q) {
+      eb[0] = e8m0_of(sc[256]);
+      eb[NSB - 1] = e8m0_of(sc[257]);
+    } else {
+      eb[0] = e8m0_of(sc[256 + (wn >> 1)]);
+    }
+  };
+  // acc += B_j A_i with the codes of the current block (opsel must be a constant: one case per i)
+  auto mfma_p2 = [&](const i32x8& b, const i32x8& a, const f32x16& c, int i, uint32_t eb) -> f32x16 {
+    switch (i) {
+      case 0: return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, (int)eb, 0, (int)ea_c);
+      case 1: return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, (int)eb, 1, (int)ea_c);
+      case 2: return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, (int)eb, 2, (int)ea_c);
+      default: return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, (int)eb, 3, (int)ea_c);
+    }
+  };
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -935,7 +966,8 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
   issue(2, 2, true);
   __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));
   __syncthreads();
-  read_scales(0, sa_c, sb_c);
+  if constexpr (P2) read_codes(0, ea_c, eb_c);
+  else read_scales(0, sa_c, sb_c);
 #pragma unroll
   for (int i = 0; i < TM; ++i) fr_a[i] = rd_a(0, i);
 #pragma unroll
@@ -961,8 +993,11 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr_b[cb][j], fr_a[i], acc[i][j], 0, 0, 0, 127,
-                                                                    0, 127);
+        if constexpr (P2)
+          acc[i][j] = mfma_p2(fr_b[cb][j], fr_a[i], acc[i][j], i, eb_c[half_of(j)]);
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr_b[cb][j], fr_a[i], acc[i][j], 0, 0, 0, 127,
+                                                                      0, 127);
         if (rescale && i * TN + j + 1 < TM * TN) rescale_acc(i * TN + j + 1);
       }
       fr_a[i] = rd_a(g_ + 1, i);
@@ -975,7 +1010,12 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
       // even stage kt (ring step g): B fragments in set 0
       issue(g + PD, kt + PD, false);
       float f[TM][NSB] = {};
-      if (kb > 0) {
+      if (P2 && kb > 0) {  // true units throughout: only the codes change
+        ea_c = ea_n;
+#pragma unroll
+        for (int h = 0; h < NSB; ++h) eb_c[h] = eb_n[h];
+        rot_stage(g, 0, false, f);
+      } else if (kb > 0) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -997,7 +1037,8 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
       __builtin_amdgcn_s_barrier();
       // odd stage kt+1 (ring step g+1): B fragments in set 1
       issue(g + 1 + PD, kt + 1 + PD, true);
-      read_scales(g + 2, sa_n, sb_n);  // next block's scales (or the next tile's)
+      if constexpr (P2) read_codes(g + 2, ea_n, eb_n);  // next block's codes (or the next tile's)
+      else read_scales(g + 2, sa_n, sb_n);              // next block's scales (or the next tile's)
       rot_stage(g + 1, 1, false, f);
       __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));  // step g+3 landed (g+4 may be in flight)
       __builtin_amdgcn_s_barrier();
@@ -1011,8 +1052,8 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
       for (int j = 0; j < TN; ++j) {
         const float fa = sa_c[i], fb_ = sb_c[half_of(j)];
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-          acc[i][j][v] = cur.zero ? 0.0f : (acc[i][j][v] * fa) * fb_;  // (not 0 * x: x may be NaN)
+        for (int v = 0; v < 16; ++v)  // (not 0 * x: x may be NaN)
+          acc[i][j][v] = cur.zero ? 0.0f : (P2 ? acc[i][j][v] : (acc[i][j][v] * fa) * fb_);
       }
     // Outputs are staged through ring slot g-1 (the tile's last stage, consumed; the next DMA
     // into it is issued after the closing barrier) so that every global store writes 16
@@ -1070,9 +1111,16 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
       for (int i = 0; i < TM; ++i) {
         const int rl = erow + i * 32, row = cur.r0 + rl;
         const f32x4 mx = *(const f32x4*)(red + rl * 4);
-        float sc = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])) / 448.0f;
-        if (sc == 0.0f) sc = 1.0f;
-        const float inv = 1.0f / sc;
+        const float amax = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+        float sc, inv;
+        if constexpr (P2) {
+          sc = p2_scale(amax);
+          inv = __builtin_amdgcn_ldexpf(1.0f, 127 - (int)e8m0_of(sc));  // 2^-e, exact
+        } else {
+          sc = amax / 448.0f;
+          if (sc == 0.0f) sc = 1.0f;
+          inv = 1.0f / sc;
+        }
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq) {
           const uint32_t qv = e4m3_pack4(y[i][4 * gq] * inv, y[i][4 * gq + 1] * inv, y[i][4 * gq + 2] * inv,
@@ -1119,297 +1167,18 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
       nxt = decode(lid_next);
       snxt = make_src(nxt);
     }
+    if constexpr (P2) {
+      ea_c = ea_n;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) sa_c[i] = sa_n[i];
+      for (int h = 0; h < NSB; ++h) eb_c[h] = eb_n[h];
+    } else {
 #pragma unroll
-    for (int h = 0; h < NSB; ++h) sb_c[h] = sb_n[h];
+      for (int i = 0; i < TM; ++i) sa_c[i] = sa_n[i];
+#pragma unroll
+      for (int h = 0; h < NSB; ++h) sb_c[h] = sb_n[h];
+    }
   }
   __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));  // filler loads of the last steps land before exit
-}
-
-// ---- p2: power-of-two block scales applied by the MFMA, one wave per SIMD ----------------------------
-// With power-of-two scales (p2_scale) the block scaling needs no arithmetic of its own:
-// v_mfma_scale_f32_32x32x64_f8f6f4 multiplies the codes of each lane by 2^(E8M0 - 127) -- the row's
-// 1x128 activation scale and the weight block's 128x128 scale, both constant over the MFMA's 64 k --
-// so one accumulator set runs over all of K in true units and the k-loop does no VALU work.  That
-// leaves the registers for 128x128 wave tiles (16 accumulator blocks, in the AGPRs) with one wave
-// per SIMD, on the schedule of the bf16 gmm_w4_kernel: a stage is 16 MFMA slots, the first eight
-// followed by a fragment read of the next stage and the odd ones by one of the stage's ring loads.
-// One tile per workgroup: two persistent forms (the ring running across tiles) measured 0-13 % slower
-// on the C4 shapes -- the first made the compiler move and spill the 256 accumulators at every tile
-// switch, the second (each tile's first MFMAs from a zero accumulator) still spilled 20-75 VGPRs
-// around the epilogue; each block's 256 row scales and two weight-block scales travel with its even
-// stage.  The E8M0 codes are the f32 exponent fields of the scales,
-// which must be powers of two in [2^-126, 2^127].
-namespace p2 {
-// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>): indices usable as constants
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-constexpr int BM = 256, BN = 256, BKB = 64, NSTAGE = 4, PD = 3, NT = 256, GM = 8;
-constexpr int A_BYTES = BM * BKB, B_BYTES = BN * BKB;
-// per slot after the codes: [0, 1K) the 256 x-row scales, [1K, 1K+8) the two weight-block scales
-// (wave 0; its other lanes write copies up to 1K+256), [1K + 256 w, +256) filler of waves 1-3
-constexpr int S_OFF = A_BYTES + B_BYTES, STAGE = S_OFF + 2048;
-}  // namespace p2
-
-template <int EPI>
-__global__ __launch_bounds__(256, 1) void gmm_fp8_p2_kernel(Args p) {
-  using namespace p2;
-  using v3::a_off;
-  constexpr int WTM = 128, TM = 4, TN = 4;
-  constexpr int LPS = 8;  // data loads per wave and stage (A 4, B 4); even stages add two scale loads
-  __shared__ __attribute__((aligned(1024))) char lds[NSTAGE * STAGE];
-  __shared__ float red[BM * 2];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
-  const int wm = wave >> 1, wn = wave & 1;
-  const int nn = (EPI == EPI_SWIGLU_Q) ? (p.I / 128) : (p.N / BN);
-  const int cnt = p.count[0];
-  const int total = cnt * nn;
-  // XCD x (= blockIdx % 8) runs tiles [x*per, (x+1)*per) in dispatch order
-  const int pid = blockIdx.x, total8 = (total + 7) & ~7;
-  if (pid >= total8) return;
-  const int lid = (pid & 7) * (total8 >> 3) + (pid >> 3);
-  if (lid >= total) return;
-  const int nkb = p.K / 128, nk = p.K / BKB;
-
-  // tile (GM m-tiles per scheduling group, consecutive tiles sweep the group's m-tiles first)
-  const int grp = lid / (GM * nn);
-  const int first_m = grp * GM;
-  const int gsz = min(GM, cnt - first_m);
-  const int local = lid - grp * GM * nn;
-  const MTileF8 mt = p.tiles[first_m + local % gsz];
-  const int n_tile = local / gsz;
-  const bool zero = mt.e < 0;                 // rows past sum(group_sizes): computed with expert 0,
-  const int e = zero ? 0 : mt.e, r0 = mt.r0, r1 = mt.r1;  // stored as 0
-
-  // weight row of tile-local column c: a SwiGLU tile holds, per 128 columns, 64 gate rows then the
-  // 64 matching up rows (a wave's gate block j pairs with its up block j + 2)
-  auto b_row = [&](int c) -> int {
-    if (EPI == EPI_SWIGLU_Q) return ((c & 127) >> 6) * p.I + n_tile * 128 + (c >> 7) * 64 + (c & 63);
-    return n_tile * BN + c;
-  };
-  auto x_row = [&](int r) -> int {
-    return p.gather ? min(max(p.gather[r], 0) / p.gather_div, p.gather_rows - 1) : r;
-  };
-  // per-lane 32-bit byte offsets of the loads at k-stage 0
-  uint32_t aoff[4], boff[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = (wave * 4 + i) * 16 + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
-    aoff[i] = (uint32_t)x_row(min(r0 + r, r1 - 1)) * (uint32_t)p.K + (uint32_t)(c * 16);
-    boff[i] = (uint32_t)b_row(r) * (uint32_t)p.K + (uint32_t)(c * 16);
-  }
-  const uint8_t* Bw = p.wq + (int64_t)e * p.N * p.K;
-  // scale loads: the wave's 64 row scales; wave 0 also the two weight-block scales, the other waves
-  // a filler load (same per-wave load count)
-  const uint32_t so = (uint32_t)x_row(min(r0 + 64 * wave + lane, r1 - 1)) * (uint32_t)nkb * 4u;
-  const float* sb2 = p.xs;
-  uint32_t so2 = so;
-  if (wave_u == 0) {
-    const int h = lane & 1;
-    const int nblk = (EPI == EPI_SWIGLU_Q) ? (h * (p.I / 128) + n_tile) : (n_tile * 2 + h);
-    sb2 = p.ws + (int64_t)e * (p.N / 128) * nkb;
-    so2 = (uint32_t)nblk * (uint32_t)nkb * 4u;
-  }
-
-  const uint32_t lds_base = lds_addr(lds);
-  // load d of ring step kt_ (d < 4 A, d < 8 B, 8 and 9 the scales of an even stage); steps past the
-  // end re-read the last stage (in bounds) into a slot that is no longer read
-  auto issue_one = [&](int kt_, int d) {
-    const int k = min(kt_, nk - 1);
-    const uint32_t st = lds_base + (uint32_t)((kt_ & (NSTAGE - 1)) * STAGE);
-    const uint32_t kofs = (uint32_t)k * BKB;
-    if (d < 4) gload_lds16_s(p.xq + kofs, aoff[d], st + (wave_u * 4 + d) * 1024u);
-    else if (d < 8) gload_lds16_s(Bw + kofs, boff[d - 4], st + (uint32_t)A_BYTES + (wave_u * 4 + d - 4) * 1024u);
-    else if (d == 8) gload_lds4_s(p.xs + (k >> 1), so, st + (uint32_t)S_OFF + wave_u * 256u);
-    else gload_lds4_s(sb2 + (k >> 1), so2, st + (uint32_t)S_OFF + 1024u + wave_u * 256u);
-  };
-
-  const int frow = lane & 31, fhalf = lane >> 5;
-  auto ld32 = [&](const char* base, int r) -> i32x8 {
-    const u32x4 lo = *(const u32x4*)(base + a_off(r, 2 * fhalf));
-    const u32x4 hi = *(const u32x4*)(base + a_off(r, 2 * fhalf + 1));
-    return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-  };
-  // Fragments: one rotating A set fa[TM] -- row block i of the next stage is read right after the
-  // last of this stage's four MFMAs that use it -- and two B sets fb[2][TN] (each B block is used
-  // across the whole stage).
-  i32x8 fa[TM], fb[2][TN];
-  auto read_a = [&](int kt, int i) { fa[i] = ld32(lds + (kt & (NSTAGE - 1)) * STAGE, wm * WTM + i * 32 + frow); };
-  auto read_b = [&](int kt, int b, int j) {
-    fb[b][j] = ld32(lds + (kt & (NSTAGE - 1)) * STAGE + A_BYTES, wn * 128 + j * 32 + frow);
-  };
-  // E8M0 scales of the k-block whose even stage is ring step kt: the lane's four row-block scales
-  // packed one per byte (selected by the MFMA's opsel), and the weight block(s) of the wave
-  uint32_t sa_c = 0, sa_n = 0, sw_c[2] = {0, 0}, sw_n[2] = {0, 0};
-  auto read_scales = [&](int kt) {
-    const float* sc = (const float*)(lds + (kt & (NSTAGE - 1)) * STAGE + S_OFF);
-    uint32_t s = 0;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) s |= e8m0_of(sc[wm * WTM + i * 32 + frow]) << (8 * i);
-    sa_n = s;
-    if (EPI == EPI_SWIGLU_Q) {
-      sw_n[0] = e8m0_of(sc[256]);
-      sw_n[1] = e8m0_of(sc[257]);
-    } else {
-      sw_n[0] = sw_n[1] = e8m0_of(sc[256 + wn]);
-    }
-  };
-
-  f32x16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-
-  // prologue: ring steps 0..2 in flight; steps 0 and 1 landed (step 2 = LPS + 2 loads may not)
-#pragma unroll
-  for (int s = 0; s < PD; ++s) {
-#pragma unroll
-    for (int d = 0; d < LPS + 2; ++d)
-      if (d < LPS || (s & 1) == 0) issue_one(s, d);
-  }
-  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 2));
-  __syncthreads();
-  read_scales(0);
-#pragma unroll
-  for (int i = 0; i < TM; ++i) read_a(0, i);
-#pragma unroll
-  for (int j = 0; j < TN; ++j) read_b(0, 0, j);
-
-  // One stage (ring step kt, B fragments in set b): 16 MFMA slots, row block i in slots 4i..4i+3.
-  // Slots 0-3 read the B fragments of step kt+1 into the other set and slot 4i+3 the A fragment i of
-  // step kt+1 (after its last use here); odd slots issue the data loads of step kt+3, slots 0 and 8
-  // its scale loads when it is an even stage; an odd stage reads the next k-block's scales (step
-  // kt+1, visible since the last barrier) in slot 12.
-  auto stage = [&](int kt, auto b_tag, auto even_tag) {
-    constexpr int b = decltype(b_tag)::value;
-    constexpr bool EVEN = decltype(even_tag)::value;  // kt even: the first stage of a k-block
-    if (EVEN) {
-      sa_c = sa_n;
-      sw_c[0] = sw_n[0];
-      sw_c[1] = sw_n[1];
-    }
-    static_for<TM * TN>([&](auto QQ) {
-      constexpr int qq = decltype(QQ)::value, i = qq / TN, j = qq % TN;
-      __builtin_amdgcn_sched_barrier(0);
-      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-          fb[b][j], fa[i], acc[i][j], 0, 0, 0, (int)sw_c[(EPI == EPI_SWIGLU_Q) ? (j >> 1) : 0], i, (int)sa_c);
-      if (qq < TN) read_b(kt + 1, b ^ 1, qq);
-      if (j == TN - 1) read_a(kt + 1, i);
-      if (qq & 1) issue_one(kt + PD, qq >> 1);
-      if (!EVEN && (qq == 0 || qq == 8)) issue_one(kt + PD, 8 + (qq >> 3));  // step kt+3 is even
-      if (!EVEN && qq == 12) read_scales(kt + 1);
-    });
-    __builtin_amdgcn_sched_barrier(0);
-    // step kt+2 landed (kt+3, LPS or LPS + 2 loads, may be in flight), then a bare s_barrier: the
-    // slot refilled next held step kt, whose fragments this stage's MFMAs consumed
-    if (EVEN) __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS));
-    else __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 2));
-    __builtin_amdgcn_s_barrier();
-  };
-  for (int kt = 0; kt < nk; kt += 2) {  // nk is even (K % 128 == 0)
-    stage(kt, std::integral_constant<int, 0>(), std::true_type());
-    stage(kt + 1, std::integral_constant<int, 1>(), std::false_type());
-  }
-  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));  // the re-read loads land before the ring is reused
-  __syncthreads();                           // every wave is done with the ring
-
-  // ---- epilogue: outputs staged through the idle ring, whole 128-byte lines to HBM ----------
-  char* stg = lds;
-  if (EPI == EPI_STORE) {
-    // per wave: 32 rows x 128 bf16 columns (256 bytes) at a time; 16-byte chunk c of row r at
-    // chunk c ^ (r & 15)
-    char* wst = stg + wave * 8192;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          const bf16x4 v = zero ? bf16x4{(__bf16)0.0f, (__bf16)0.0f, (__bf16)0.0f, (__bf16)0.0f}
-                                : bf16x4{(__bf16)acc[i][j][4 * gq], (__bf16)acc[i][j][4 * gq + 1],
-                                         (__bf16)acc[i][j][4 * gq + 2], (__bf16)acc[i][j][4 * gq + 3]};
-          *(bf16x4*)(wst + frow * 256 + (((4 * j + gq) ^ (frow & 15)) << 4) + 8 * fhalf) = v;
-        }
-      __builtin_amdgcn_s_waitcnt(MTX_LGKMCNT0);
-#pragma unroll
-      for (int rr = 0; rr < 8; ++rr) {
-        const int rloc = rr * 4 + (lane >> 4), c = lane & 15;
-        const u32x4 v = *(const u32x4*)(wst + rloc * 256 + ((c ^ (rloc & 15)) << 4));
-        const int row = r0 + wm * WTM + i * 32 + rloc;
-        if (row < r1) *(u32x4*)(p.out + (int64_t)row * p.ldc + n_tile * BN + wn * 128 + c * 8) = v;
-      }
-      __builtin_amdgcn_s_waitcnt(MTX_LGKMCNT0);  // reads done before the next block overwrites
-    }
-  } else {
-    // y = silu(gate) * up for the wave's 64 output columns (gate block jj, up block jj + 2),
-    // written over the gate accumulators: acc[i][jj] holds y from here on
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      float m = 0.0f;
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float gt = acc[i][jj][v], up = acc[i][jj + 2][v];
-          const float yv = zero ? 0.0f : gt * up * __builtin_amdgcn_rcpf(1.0f + __expf(-gt));
-          acc[i][jj][v] = yv;
-          m = fmaxf(m, fabsf(yv));
-        }
-      m = fmaxf(m, __shfl_xor(m, 32));
-      if (fhalf == 0) red[(wm * WTM + i * 32 + frow) * 2 + wn] = m;
-    }
-    __syncthreads();
-    // e4m3 codes of the tile's 128 output columns: [256 rows][128 bytes], 16-byte chunk c of row r
-    // at chunk c ^ (r & 7)
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int rl = wm * WTM + i * 32 + frow, row = r0 + rl;
-      const float sc = p2_scale(fmaxf(red[rl * 2], red[rl * 2 + 1]));
-      const float inv = __builtin_amdgcn_ldexpf(1.0f, 127 - (int)e8m0_of(sc));  // 2^-e, exact
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          const uint32_t qv = e4m3_pack4(acc[i][jj][4 * gq] * inv, acc[i][jj][4 * gq + 1] * inv,
-                                         acc[i][jj][4 * gq + 2] * inv, acc[i][jj][4 * gq + 3] * inv);
-          const int cb = wn * 64 + jj * 32 + 8 * gq + 4 * fhalf;  // output column (byte) in the tile
-          *(uint32_t*)(stg + rl * 128 + (((cb >> 4) ^ (rl & 7)) << 4) + (cb & 15)) = qv;
-        }
-      if (row < r1) {
-        if (p.out) {
-          uint16_t* brow = p.out + (int64_t)row * p.I + n_tile * 128 + wn * 64 + 4 * fhalf;
-#pragma unroll
-          for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-            for (int gq = 0; gq < 4; ++gq)
-              *(bf16x4*)(brow + jj * 32 + 8 * gq) = bf16x4{(__bf16)acc[i][jj][4 * gq], (__bf16)acc[i][jj][4 * gq + 1],
-                                                           (__bf16)acc[i][jj][4 * gq + 2], (__bf16)acc[i][jj][4 * gq + 3]};
-        }
-        if (wn == 0 && fhalf == 0) p.outs[(int64_t)row * (p.I / 128) + n_tile] = sc;
-      }
-    }
-    __syncthreads();
-    // 256 rows x 128 bytes: 8 lanes per row, 8 rows per wave instruction
-#pragma unroll
-    for (int rr = 0; rr < 8; ++rr) {
-      const int rl = wave * 64 + rr * 8 + (lane >> 3);
-      const u32x4 v = *(const u32x4*)(stg + rl * 128 + (((lane & 7) ^ (rl & 7)) << 4));
-      const int row = r0 + rl;
-      if (row < r1) *(u32x4*)(p.outq + (int64_t)row * p.I + n_tile * 128 + (lane & 7) * 16) = v;
-    }
-  }
 }
 
 }  // namespace f8
@@ -1418,10 +1187,10 @@ static inline int64_t f8_ws_bytes(int64_t M, int64_t E, int64_t BM) {
   return 256 + (ceil_div(M, BM) + E + 1) * (int64_t)sizeof(MTileF8);
 }
 
-// Power-of-two scales (p2): the one-wave-per-SIMD kernel with the scales in the MFMA;
-// it needs K >= 256 and 32-bit operand offsets (MTX_ERR_UNSUPPORTED otherwise).
+// Power-of-two scales (p2): the persistent kernel with the block scales as the MFMA's E8M0
+// operands; it needs K >= 256 and 32-bit operand offsets (MTX_ERR_UNSUPPORTED otherwise).
 template <int EPI>
-static int launch_fp8_p2(const f8::Args& a, const int32_t* gs, int64_t E, int64_t nn, void* ws, hipStream_t st) {
+static int launch_fp8_v4_p2(const f8::Args& a, const int32_t* gs, int64_t E, int64_t nn, void* ws, hipStream_t st) {
   const int64_t a_rows = a.gather ? a.gather_rows : a.M;
   const bool off32 = a_rows * a.K < (int64_t(1) << 32) && (int64_t)a.N * a.K < (int64_t(1) << 32);
   if (!(off32 && a.K >= 256)) return MTX_ERR_UNSUPPORTED;
@@ -1431,8 +1200,11 @@ static int launch_fp8_p2(const f8::Args& a, const int32_t* gs, int64_t E, int64_
   f8::Args b = a;
   b.count = count;
   b.tiles = tiles;
-  const int64_t grid = round_up((ceil_div(a.M, 256) + E + 1) * nn, 8);  // one workgroup per tile
-  hipLaunchKernelGGL((f8::gmm_fp8_p2_kernel<EPI>), dim3((unsigned)grid), dim3(256), 0, st, b);
+  int64_t grid = round_up((ceil_div(a.M, 256) + E + 1) * nn, 8);
+  const int ncu = device_cu_count();
+  const int64_t cap = ncu > 0 ? round_up(ncu, 8) : 256;
+  if (grid > cap) grid = cap;  // persistent: one workgroup per CU (a multiple of the 8 XCDs)
+  hipLaunchKernelGGL((f8::gmm_fp8_v4_kernel<EPI, true>), dim3((unsigned)grid), dim3(512), 0, st, b);
   return check_launch();
 }
 
@@ -1571,7 +1343,7 @@ static int gmm_fp8_entry(bool p2, const uint8_t* xq, const float* x_scale, const
   a.N = (int)Kout;
   a.I = 0;
   a.ldc = (int)Kout;
-  if (p2) return launch_fp8_p2<f8::EPI_STORE>(a, group_sizes, E, Kout / 256, workspace, (hipStream_t)stream);
+  if (p2) return launch_fp8_v4_p2<f8::EPI_STORE>(a, group_sizes, E, Kout / 256, workspace, (hipStream_t)stream);
   return launch_fp8<f8::EPI_STORE>(a, group_sizes, E, Kout / 256, workspace, (hipStream_t)stream);
 }
 
@@ -1617,7 +1389,7 @@ static int fp8_swiglu_entry(const uint8_t* xq, const float* x_scale, const uint8
   a.N = (int)(2 * I);
   a.I = (int)I;
   a.ldc = (int)I;
-  if (p2) return launch_fp8_p2<f8::EPI_SWIGLU_Q>(a, group_sizes, E, I / 128, workspace, (hipStream_t)stream);
+  if (p2) return launch_fp8_v4_p2<f8::EPI_SWIGLU_Q>(a, group_sizes, E, I / 128, workspace, (hipStream_t)stream);
   return launch_fp8<f8::EPI_SWIGLU_Q>(a, group_sizes, E, I / 128, workspace, (hipStream_t)stream);
 }
 
