@@ -197,7 +197,7 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
 
     bwd = cfg_name in ("qwen3_bwd", "qwen3_bwd_fp8")
     gather = gather and not bwd and (D >= 256 if fp8 else gathered_swiglu_supported(x, gate_up))
-    if fp8 and fp8_scales != "amax" and not gather:
+    if fp8 and fp8_scales != "amax" and not gather and not bwd:
         raise SystemExit("--fp8-scales pow2 needs the gathered layer flow (the fused dispatch quantiser is amax-only)")
 
     def step(timed):
@@ -279,27 +279,28 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
         from mintext_amd.kernels.fp8 import (grouped_matmul_fp8_dlhs, quantize_fp8_grouped_t, quantize_fp8_rows,
                                              quantize_fp8_weights_t, tgmm_fp8)
 
+        bf8 = dict(scales=fp8_scales)  # "amax" or "pow2" in every quantisation and GEMM
         with torch.no_grad():
-            dnq, dns = quantize_fp8_weights_t(down)
-            guq, gus = quantize_fp8_weights_t(gate_up)
-            gyq, gys = quantize_fp8_rows(gy)
-            ghq, ghs = quantize_fp8_rows(gh)
-            yt = quantize_fp8_grouped_t(y, gs)
-            gyt = quantize_fp8_grouped_t(gy, gs, blocks=True)
-            stt = quantize_fp8_grouped_t(st, gs)
-            ght = quantize_fp8_grouped_t(gh, gs, blocks=True)
+            dnq, dns = quantize_fp8_weights_t(down, **bf8)
+            guq, gus = quantize_fp8_weights_t(gate_up, **bf8)
+            gyq, gys = quantize_fp8_rows(gy, **bf8)
+            ghq, ghs = quantize_fp8_rows(gh, **bf8)
+            yt = quantize_fp8_grouped_t(y, gs, **bf8)
+            gyt = quantize_fp8_grouped_t(gy, gs, blocks=True, **bf8)
+            stt = quantize_fp8_grouped_t(st, gs, **bf8)
+            ght = quantize_fp8_grouped_t(gh, gs, blocks=True, **bf8)
 
         def step(timed):  # noqa: F811
             with torch.no_grad():
                 if timed:
                     t_dl.start()
-                a = grouped_matmul_fp8_dlhs(gyq, gys, dnq, dns, gs)   # d inter [M, I]
-                b = grouped_matmul_fp8_dlhs(ghq, ghs, guq, gus, gs)   # d x     [M, D]
+                a = grouped_matmul_fp8_dlhs(gyq, gys, dnq, dns, gs, **bf8)   # d inter [M, I]
+                b = grouped_matmul_fp8_dlhs(ghq, ghs, guq, gus, gs, **bf8)   # d x     [M, D]
                 if timed:
                     t_dl.stop()
                     t_tg.start()
-                c = tgmm_fp8(*yt, *gyt, gs, M)                        # d down    [E, I, D]
-                d = tgmm_fp8(*stt, *ght, gs, M)                       # d gate_up [E, D, 2I]
+                c = tgmm_fp8(*yt, *gyt, gs, M, **bf8)                        # d down    [E, I, D]
+                d = tgmm_fp8(*stt, *ght, gs, M, **bf8)                       # d gate_up [E, D, 2I]
                 if timed:
                     t_tg.stop()
                 return a, b, c, d
@@ -399,7 +400,7 @@ def run(cfg_name, steps, warmup, cpu_baseline=True, shared_mode="separate", use_
                    "parallelism": "single GPU",
                    **({"shared_expert": shared_mode if fold else "separate"} if shared is not None else {}),
                    **({"fp8_scales": ("amax/448" if fp8_scales == "amax" else "power of two (MFMA E8M0)")}
-                      if fp8 and not bwd else {})},
+                      if fp8 else {})},
         "gemm": {"tflops": round(flops_fwd / (gemm_ms * 1e-3) / 1e12, 1),
                  "frac_of_peak": round((flops_fwd / (gemm_ms * 1e-3) / 1e12) / peak, 4),
                  "gate_up_ms": round(gu_ms, 4), "down_ms": round(dn_ms, 4)},

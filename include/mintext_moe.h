@@ -364,6 +364,22 @@ int mtx_quant_fp8_grouped_t(const void* x, int dtype, const int32_t* group_sizes
 int mtx_tgmm_fp8(const uint8_t* xt, const float* xt_scale, const uint8_t* gt, const float* gt_scale,
                  const int32_t* group_sizes, int64_t M, int64_t F, int64_t N, int64_t E, void* dw,
                  void* workspace, int64_t workspace_bytes, void* stream);
+/* The backward in the power-of-two mode (the _p2 forward's scales, same layouts and signatures):
+ * quantisers with p2_scale instead of amax / 448, GEMMs whose scales go to the MFMA's E8M0
+ * operands (so they must be powers of two in [2^-126, 2^127]: the outputs of these quantisers and
+ * of mtx_quant_fp8_rows_p2).  The accumulators stay in true units over the whole reduction, so
+ * neighbouring chunks of very different magnitude cannot overflow them.                          */
+int mtx_quant_fp8_weights_t_p2(const void* w, int dtype, int64_t E, int64_t Kin, int64_t Kout,
+                               uint8_t* w_qt, float* w_scale_t, void* stream);
+int mtx_gmm_fp8_dlhs_p2(const uint8_t* gq, const float* g_scale, const uint8_t* w_qt, const float* w_scale_t,
+                        const int32_t* group_sizes, int64_t M, int64_t Kin, int64_t Kout, int64_t E, void* dx,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+int mtx_quant_fp8_grouped_t_p2(const void* x, int dtype, const int32_t* group_sizes, int64_t M, int64_t F,
+                               int64_t E, int blocks, uint8_t* xt, float* xt_scale, void* workspace,
+                               int64_t workspace_bytes, void* stream);
+int mtx_tgmm_fp8_p2(const uint8_t* xt, const float* xt_scale, const uint8_t* gt, const float* gt_scale,
+                    const int32_t* group_sizes, int64_t M, int64_t F, int64_t N, int64_t E, void* dw,
+                    void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---- expert weight layouts -------------------------------------------------------------
  * Batched transpose-copy (the per-expert HF <-> fused conversions of

@@ -82,6 +82,10 @@ SIGNATURES = {
     "mtx_fp8_grouped_workspace_size": (_I64, [_I64]),
     "mtx_quant_fp8_grouped_t": (_I, [_P, _I, _P, _I64, _I64, _I64, _I, _P, _P, _P, _I64, _P]),
     "mtx_tgmm_fp8": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
+    "mtx_quant_fp8_weights_t_p2": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _P]),
+    "mtx_gmm_fp8_dlhs_p2": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
+    "mtx_quant_fp8_grouped_t_p2": (_I, [_P, _I, _P, _I64, _I64, _I64, _I, _P, _P, _P, _I64, _P]),
+    "mtx_tgmm_fp8_p2": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "mtx_transpose_batched": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P]),
     "mtx_stream_copy": (_I, [_P, _P, _I64, _I, _I64, _P]),
 }

@@ -17,6 +17,9 @@
 //       128x128 blocks).  Expert-major blocks keep each tile's 256 rows within a few hundred KB
 //       (a row-major [F, 128*C] layout put them 128*C bytes apart, one page per row).  The GEMM is
 //       the forward kernel's tile loop with a per-expert k-range.
+// Both have a power-of-two mode (the "_p2" entry points): every scale is p2_scale(amax) instead of
+// amax / 448, and the GEMMs give the scales' exponents to the MFMA's E8M0 operands, as the forward's
+// power-of-two mode does (accumulators in true units over the whole reduction).
 #include "common.h"
 #include "lds_dma.h"
 #include "fp8_tile.h"
@@ -34,7 +37,7 @@ typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
 // The 128x128 block (Kin block y, Kout block x) of expert z: the scale of quant_weights_kernel
 // (amax / 448 of the same block) and the same codes, written in W's layout [E, Kin, Kout] with the
 // scale at [E, Kin/128, Kout/128].
-template <typename T>
+template <typename T, bool P2 = false>
 __global__ __launch_bounds__(256) void quant_weights_t_kernel(const T* __restrict__ w, int64_t Kin, int64_t Kout,
                                                               uint8_t* __restrict__ wq, float* __restrict__ ws) {
   __shared__ float red[4];
@@ -48,7 +51,7 @@ __global__ __launch_bounds__(256) void quant_weights_t_kernel(const T* __restric
   float a = 0.0f;
 #pragma unroll
   for (int j = 0; j < S::VE; ++j) a = fmaxf(a, m[j]);
-  const float s = q8::block_scale(a, red);
+  const float s = q8::block_scale<P2>(a, red);
   q8::codes_to_global(t, s, wq + base, Kout);
   if (threadIdx.x == 0) ws[(e * (Kin / 128) + blockIdx.y) * (Kout / 128) + blockIdx.x] = s;
 }
@@ -125,7 +128,7 @@ __device__ __forceinline__ int chunk_expert(const int* __restrict__ cb, int E, i
 // xt[128*F*cb[e] + f*128*n_e + 128j + r] (n_e = chunks of expert e).  ROW: scale per feature =
 // amax over the chunk's rows / 448 at xts[F*cb[e] + f*n_e + j]; BLOCK: one scale per 128x128 block
 // at xts[(F/128)*cb[e] + fb*n_e + j].  Codes are e4m3 of v / scale, scale 1 when the amax is 0.
-template <typename T, bool BLOCK>
+template <typename T, bool BLOCK, bool P2 = false>
 __global__ __launch_bounds__(256) void quant_grouped_t_kernel(const T* __restrict__ x, int F, const int* __restrict__ cb,
                                                               const int* __restrict__ off, int E,
                                                               uint8_t* __restrict__ xt, float* __restrict__ xts) {
@@ -148,7 +151,7 @@ __global__ __launch_bounds__(256) void quant_grouped_t_kernel(const T* __restric
     float a = 0.0f;
 #pragma unroll
     for (int i = 0; i < S::VE; ++i) a = fmaxf(a, m[i]);
-    const float s = q8::block_scale(a, &red[0][0]);
+    const float s = q8::block_scale<P2>(a, &red[0][0]);
     q8::codes_to_lds_t(t, [&](int) { return s; }, tt);
     if (tid == 0) xts[(int64_t)(F / 128) * cb[e] + (int64_t)fb * ne + j] = s;
   } else {
@@ -159,7 +162,7 @@ __global__ __launch_bounds__(256) void quant_grouped_t_kernel(const T* __restric
       float a = 0.0f;
 #pragma unroll
       for (int r = 0; r < S::TR; ++r) a = fmaxf(a, red[r][tid]);
-      const float s = q8::scale_of(a);
+      const float s = q8::scale_of<P2>(a);
       scs[tid] = s;
       xts[(int64_t)F * cb[e] + (f0 + tid) * ne + j] = s;
     }
@@ -198,6 +201,7 @@ struct TArgs {
   int xa, xb;         // XCD rectangles: 0 = row-major tiles, else an xa x xb grid of the tile grid
 };
 
+template <bool P2 = false>
 __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
   constexpr int WN = 4, WTM = 128, WTN = 64, TM = 4, TN = 2, LPS = 4;  // data loads per wave and stage
   __shared__ __attribute__((aligned(1024))) char lds[TNST * TSTAGE];
@@ -287,6 +291,26 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
     for (int i = 0; i < TM; ++i) sa[i] = sc[wm * WTM + i * 32 + frow];
     sb = sc[256 + (wn >> 1)];
   };
+  // P2: the same scales as E8M0 codes for the MFMA's scale operands -- the lane's four XT-row codes
+  // packed one per byte (opsel i) and the wave's GT-block code
+  uint32_t ea_c = 0, ea_n = 0, eb_c = 0, eb_n = 0;
+  auto read_codes = [&](int kt, uint32_t& ea, uint32_t& eb) {
+    const float* sc = (const float*)(lds + (kt & (TNST - 1)) * TSTAGE + TS_OFF);
+    uint32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) s |= e8m0_of(sc[wm * WTM + i * 32 + frow]) << (8 * i);
+    ea = s;
+    eb = e8m0_of(sc[256 + (wn >> 1)]);
+  };
+  // acc += GT_j XT_i scaled by the current chunk's codes (opsel is a constant: one case per i)
+  auto mfma_p2 = [&](const i32x8& b, const i32x8& a, const f32x16& c, int i) -> f32x16 {
+    switch (i) {
+      case 0: return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, (int)eb_c, 0, (int)ea_c);
+      case 1: return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, (int)eb_c, 1, (int)ea_c);
+      case 2: return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, (int)eb_c, 2, (int)ea_c);
+      default: return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, (int)eb_c, 3, (int)ea_c);
+    }
+  };
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -312,8 +336,11 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr_b[cb][j], fr_a[i], acc[i][j], 0, 0, 0, 127, 0,
-                                                                    127);
+        if constexpr (P2)
+          acc[i][j] = mfma_p2(fr_b[cb][j], fr_a[i], acc[i][j], i);
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr_b[cb][j], fr_a[i], acc[i][j], 0, 0, 0, 127, 0,
+                                                                      127);
         if (rescale && i * TN + j + 1 < TM * TN) rescale_acc(i * TN + j + 1);
       }
       fr_a[i] = rd_a(kt + 1, i);
@@ -325,7 +352,8 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
   for (int s = 0; s < TPD; ++s) issue_stage(s);  // nk >= 2: stages past the end re-read the last
   __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));
   __syncthreads();
-  read_scales(0, sa_c, sb_c);
+  if constexpr (P2) read_codes(0, ea_c, eb_c);
+  else read_scales(0, sa_c, sb_c);
 #pragma unroll
   for (int i = 0; i < TM; ++i) fr_a[i] = rd_a(0, i);
 #pragma unroll
@@ -334,7 +362,11 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
     const int kt = 2 * kb;
     issue_stage(kt + TPD);  // odd stage: LPS loads
     float f[TM];
-    if (kb > 0) {
+    if (P2 && kb > 0) {  // true units throughout: only the codes change
+      ea_c = ea_n;
+      eb_c = eb_n;
+      rot_stage(kt, 0, false, f);
+    } else if (kb > 0) {
       // (sa_c / sa_n) * (sb_c / sb_n): no product of two small scales is formed
       const float rb = sb_c * __builtin_amdgcn_rcpf(sb_n);
 #pragma unroll
@@ -354,7 +386,8 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
     __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS));
     __builtin_amdgcn_s_barrier();
     issue_stage(kt + 1 + TPD);  // even stage: LPS + 1 loads
-    read_scales(kt + 2, sa_n, sb_n);  // the next chunk's scales (past the last: an unused slot)
+    if constexpr (P2) read_codes(kt + 2, ea_n, eb_n);  // the next chunk's codes (past the last: unused)
+    else read_scales(kt + 2, sa_n, sb_n);  // the next chunk's scales (past the last: an unused slot)
     rot_stage(kt + 1, 1, false, f);  // its fragment reads of stage kt+2 past the end are unused
     __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));  // stage kt+3 landed; kt+4 may still be in flight
     __builtin_amdgcn_s_barrier();
@@ -371,7 +404,7 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = (acc[i][j][v] * sa_c[i]) * sb_c;
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = P2 ? acc[i][j][v] : (acc[i][j][v] * sa_c[i]) * sb_c;
   char* wst = lds + wave * 4096;
   const uint32_t lo = (uint32_t)(wm * WTM + (lane >> 3)) * (uint32_t)p.N + (uint32_t)(wn * WTN + (lane & 7) * 8);
 #pragma unroll
@@ -402,8 +435,9 @@ static inline int64_t fp8_grouped_chunks(int64_t M, int64_t E) { return ceil_div
 
 using namespace mtx;
 
-extern "C" int mtx_quant_fp8_weights_t(const void* w, int dtype, int64_t E, int64_t Kin, int64_t Kout, uint8_t* w_qt,
-                                       float* w_scale_t, void* stream) {
+template <bool P2>
+static int quant_weights_t_entry(const void* w, int dtype, int64_t E, int64_t Kin, int64_t Kout, uint8_t* w_qt,
+                                 float* w_scale_t, void* stream) {
   if (E < 0 || Kin < 0 || Kout < 0 || Kin % 128 || Kout % 128 || (dtype != MTX_F32 && dtype != MTX_BF16))
     return MTX_ERR_ARG;
   if (E == 0 || Kin == 0 || Kout == 0) return MTX_OK;
@@ -413,12 +447,22 @@ extern "C" int mtx_quant_fp8_weights_t(const void* w, int dtype, int64_t E, int6
   dim3 grid((unsigned)(Kout / 128), (unsigned)(Kin / 128), (unsigned)E);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MTX_F32)
-    hipLaunchKernelGGL(f8b::quant_weights_t_kernel<float>, grid, dim3(256), 0, st, (const float*)w, Kin, Kout, w_qt,
-                       w_scale_t);
-  else
-    hipLaunchKernelGGL(f8b::quant_weights_t_kernel<uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)w, Kin, Kout,
+    hipLaunchKernelGGL((f8b::quant_weights_t_kernel<float, P2>), grid, dim3(256), 0, st, (const float*)w, Kin, Kout,
                        w_qt, w_scale_t);
+  else
+    hipLaunchKernelGGL((f8b::quant_weights_t_kernel<uint16_t, P2>), grid, dim3(256), 0, st, (const uint16_t*)w, Kin,
+                       Kout, w_qt, w_scale_t);
   return check_launch();
+}
+
+extern "C" int mtx_quant_fp8_weights_t(const void* w, int dtype, int64_t E, int64_t Kin, int64_t Kout, uint8_t* w_qt,
+                                       float* w_scale_t, void* stream) {
+  return quant_weights_t_entry<false>(w, dtype, E, Kin, Kout, w_qt, w_scale_t, stream);
+}
+
+extern "C" int mtx_quant_fp8_weights_t_p2(const void* w, int dtype, int64_t E, int64_t Kin, int64_t Kout,
+                                          uint8_t* w_qt, float* w_scale_t, void* stream) {
+  return quant_weights_t_entry<true>(w, dtype, E, Kin, Kout, w_qt, w_scale_t, stream);
 }
 
 extern "C" int64_t mtx_fp8_grouped_chunks(int64_t M, int64_t E) {
@@ -442,9 +486,10 @@ static int grouped_prologue(const int32_t* gs, int64_t E, int64_t M, void* ws, h
   return check_launch();
 }
 
-extern "C" int mtx_quant_fp8_grouped_t(const void* x, int dtype, const int32_t* group_sizes, int64_t M, int64_t F,
-                                       int64_t E, int blocks, uint8_t* xt, float* xt_scale, void* workspace,
-                                       int64_t workspace_bytes, void* stream) {
+template <bool P2>
+static int quant_grouped_t_entry(const void* x, int dtype, const int32_t* group_sizes, int64_t M, int64_t F, int64_t E,
+                                 int blocks, uint8_t* xt, float* xt_scale, void* workspace, int64_t workspace_bytes,
+                                 void* stream) {
   if (M < 0 || M > INT32_MAX / 2 || F <= 0 || F % 128 || E < 1 || E > 1024) return MTX_ERR_ARG;
   if (dtype != MTX_F32 && dtype != MTX_BF16) return MTX_ERR_ARG;
   if (!workspace || workspace_bytes < mtx_fp8_grouped_workspace_size(E)) return MTX_ERR_WORKSPACE;
@@ -458,7 +503,7 @@ extern "C" int mtx_quant_fp8_grouped_t(const void* x, int dtype, const int32_t* 
   if (rc) return rc;
   dim3 grid((unsigned)C, (unsigned)(F / 128));
 #define MTX_QG(T, B)                                                                                              \
-  hipLaunchKernelGGL((f8b::quant_grouped_t_kernel<T, B>), grid, dim3(256), 0, st, (const T*)x, (int)F, cb, off, \
+  hipLaunchKernelGGL((f8b::quant_grouped_t_kernel<T, B, P2>), grid, dim3(256), 0, st, (const T*)x, (int)F, cb, off, \
                      (int)E, xt, xt_scale)
   if (dtype == MTX_F32) {
     if (blocks) MTX_QG(float, true); else MTX_QG(float, false);
@@ -469,9 +514,23 @@ extern "C" int mtx_quant_fp8_grouped_t(const void* x, int dtype, const int32_t* 
   return check_launch();
 }
 
-extern "C" int mtx_tgmm_fp8(const uint8_t* xt, const float* xt_scale, const uint8_t* gt, const float* gt_scale,
-                            const int32_t* group_sizes, int64_t M, int64_t F, int64_t N, int64_t E, void* dw,
-                            void* workspace, int64_t workspace_bytes, void* stream) {
+extern "C" int mtx_quant_fp8_grouped_t(const void* x, int dtype, const int32_t* group_sizes, int64_t M, int64_t F,
+                                       int64_t E, int blocks, uint8_t* xt, float* xt_scale, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
+  return quant_grouped_t_entry<false>(x, dtype, group_sizes, M, F, E, blocks, xt, xt_scale, workspace,
+                                      workspace_bytes, stream);
+}
+
+extern "C" int mtx_quant_fp8_grouped_t_p2(const void* x, int dtype, const int32_t* group_sizes, int64_t M, int64_t F,
+                                          int64_t E, int blocks, uint8_t* xt, float* xt_scale, void* workspace,
+                                          int64_t workspace_bytes, void* stream) {
+  return quant_grouped_t_entry<true>(x, dtype, group_sizes, M, F, E, blocks, xt, xt_scale, workspace,
+                                     workspace_bytes, stream);
+}
+
+static int tgmm_fp8_entry(bool p2, const uint8_t* xt, const float* xt_scale, const uint8_t* gt,
+                          const float* gt_scale, const int32_t* group_sizes, int64_t M, int64_t F, int64_t N, int64_t E,
+                          void* dw, void* workspace, int64_t workspace_bytes, void* stream) {
   if (M < 0 || M > INT32_MAX / 2 || F <= 0 || N <= 0 || E < 1 || E > 1024) return MTX_ERR_ARG;
   if (F % 128 || N % 128) return MTX_ERR_ARG;
   if (F % 256 || N % 256) return MTX_ERR_UNSUPPORTED;
@@ -510,8 +569,23 @@ extern "C" int mtx_tgmm_fp8(const uint8_t* xt, const float* xt_scale, const uint
     }
   }
   const int64_t grid = round_up(E * (F / 256) * (N / 256), 8);
-  hipLaunchKernelGGL(f8b::tgmm_fp8_kernel, dim3((unsigned)grid), dim3(512), 0, st, a);
+  if (p2) hipLaunchKernelGGL(f8b::tgmm_fp8_kernel<true>, dim3((unsigned)grid), dim3(512), 0, st, a);
+  else hipLaunchKernelGGL(f8b::tgmm_fp8_kernel<false>, dim3((unsigned)grid), dim3(512), 0, st, a);
   return check_launch();
+}
+
+extern "C" int mtx_tgmm_fp8(const uint8_t* xt, const float* xt_scale, const uint8_t* gt, const float* gt_scale,
+                            const int32_t* group_sizes, int64_t M, int64_t F, int64_t N, int64_t E, void* dw,
+                            void* workspace, int64_t workspace_bytes, void* stream) {
+  return tgmm_fp8_entry(false, xt, xt_scale, gt, gt_scale, group_sizes, M, F, N, E, dw, workspace, workspace_bytes,
+                        stream);
+}
+
+extern "C" int mtx_tgmm_fp8_p2(const uint8_t* xt, const float* xt_scale, const uint8_t* gt, const float* gt_scale,
+                               const int32_t* group_sizes, int64_t M, int64_t F, int64_t N, int64_t E, void* dw,
+                               void* workspace, int64_t workspace_bytes, void* stream) {
+  return tgmm_fp8_entry(true, xt, xt_scale, gt, gt_scale, group_sizes, M, F, N, E, dw, workspace, workspace_bytes,
+                        stream);
 }
 
 extern "C" int mtx_gmm_fp8_dlhs(const uint8_t* gq, const float* g_scale, const uint8_t* w_qt, const float* w_scale_t,
@@ -521,4 +595,12 @@ extern "C" int mtx_gmm_fp8_dlhs(const uint8_t* gq, const float* g_scale, const u
   // layout [E, Kin, Kout] (rows = output columns, k-contiguous over the reduction Kout)
   return mtx_gmm_fp8(gq, g_scale, w_qt, w_scale_t, group_sizes, M, Kout, Kin, E, dx, workspace, workspace_bytes,
                      stream);
+}
+
+extern "C" int mtx_gmm_fp8_dlhs_p2(const uint8_t* gq, const float* g_scale, const uint8_t* w_qt,
+                                   const float* w_scale_t, const int32_t* group_sizes, int64_t M, int64_t Kin,
+                                   int64_t Kout, int64_t E, void* dx, void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
+  return mtx_gmm_fp8_p2(gq, g_scale, w_qt, w_scale_t, group_sizes, M, Kout, Kin, E, dx, workspace, workspace_bytes,
+                        stream);
 }

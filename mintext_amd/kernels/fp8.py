@@ -129,9 +129,10 @@ def grouped_matmul_fp8_swiglu_gathered(xq, x_scale, sort_indices, top_k: int, w_
 
 # ---- backward: dlhs and tgmm with fp8 operands ----------------------------------------------------
 # The bf16 forms are grouped_matmul.py:151-187 (dlhs) and :197-235 (tgmm); the fp8 ones keep the
-# forward's conventions (e4m3fn codes, f32 scale = amax / 448 per group).
+# forward's conventions (e4m3fn codes, f32 scale = amax / 448 per group, or the power-of-two mode,
+# ``scales="pow2"``, whose GEMMs need operands quantised in it).
 
-def quantize_fp8_weights_t(w: torch.Tensor):
+def quantize_fp8_weights_t(w: torch.Tensor, *, scales: str = "amax"):
     """w [E, Kin, Kout] -> (w_qt [E, Kin, Kout] e4m3fn, w_scale_t [E, Kin/128, Kout/128]): the 128x128
     blocks and codes of ``quantize_fp8_weights`` kept in w's own layout, the operand of
     ``grouped_matmul_fp8_dlhs`` (a load-time transform beside the forward one)."""
@@ -140,12 +141,12 @@ def quantize_fp8_weights_t(w: torch.Tensor):
     E, Kin, Kout = w.shape
     wq = torch.empty((E, Kin, Kout), dtype=torch.float8_e4m3fn, device=dev)
     ws = torch.empty((E, Kin // 128, Kout // 128), dtype=torch.float32, device=dev)
-    L.call("mtx_quant_fp8_weights_t", L.ptr(w), L.dtype_code(w.dtype), E, Kin, Kout, L.ptr(wq), L.ptr(ws),
-           L.stream(dev))
+    L.call(_entry("mtx_quant_fp8_weights_t", scales), L.ptr(w), L.dtype_code(w.dtype), E, Kin, Kout, L.ptr(wq),
+           L.ptr(ws), L.stream(dev))
     return wq, ws
 
 
-def grouped_matmul_fp8_dlhs(gq, g_scale, w_qt, w_scale_t, group_sizes) -> torch.Tensor:
+def grouped_matmul_fp8_dlhs(gq, g_scale, w_qt, w_scale_t, group_sizes, *, scales: str = "amax") -> torch.Tensor:
     """dX [M, Kin] bf16 = dequant(gq) @ dequant(W[g])^T per group, f32 accumulation: the fp8 dlhs
     (``mtx_gmm_fp8_dlhs``).  gq [M, Kout] / g_scale [M, Kout/128] from ``quantize_fp8_rows`` of the
     upstream gradient; w_qt / w_scale_t from ``quantize_fp8_weights_t``."""
@@ -157,12 +158,14 @@ def grouped_matmul_fp8_dlhs(gq, g_scale, w_qt, w_scale_t, group_sizes) -> torch.
         raise ValueError("fp8 dlhs shape mismatch")
     dx = torch.empty((M, Kin), dtype=torch.bfloat16, device=dev)
     ws = L.workspace(L.query("mtx_gmm_workspace_size", M, E), dev)
-    L.call("mtx_gmm_fp8_dlhs", L.ptr(gq.contiguous()), L.ptr(g_scale.contiguous()), L.ptr(w_qt.contiguous()),
-           L.ptr(w_scale_t.contiguous()), L.ptr(gs), M, Kin, Kout, E, L.ptr(dx), L.ptr(ws), ws.numel(), L.stream(dev))
+    L.call(_entry("mtx_gmm_fp8_dlhs", scales), L.ptr(gq.contiguous()), L.ptr(g_scale.contiguous()),
+           L.ptr(w_qt.contiguous()), L.ptr(w_scale_t.contiguous()), L.ptr(gs), M, Kin, Kout, E, L.ptr(dx), L.ptr(ws),
+           ws.numel(), L.stream(dev))
     return dx
 
 
-def quantize_fp8_grouped_t(x: torch.Tensor, group_sizes: torch.Tensor, *, blocks: bool = False):
+def quantize_fp8_grouped_t(x: torch.Tensor, group_sizes: torch.Tensor, *, blocks: bool = False,
+                           scales: str = "amax"):
     """Operand of ``tgmm_fp8``: x [M, F] (f32/bf16, rows grouped by expert) quantised in chunks of
     128 consecutive rows of each expert (chunk j of expert e = its rows 128j .. 128j+127,
     zero-padded) and transposed per expert into expert-major blocks: flat codes of F*128*C bytes
@@ -181,13 +184,13 @@ def quantize_fp8_grouped_t(x: torch.Tensor, group_sizes: torch.Tensor, *, blocks
     xt._mtx_features = F
     xs._mtx_features = F
     ws = L.workspace(L.query("mtx_fp8_grouped_workspace_size", E), dev)
-    L.call("mtx_quant_fp8_grouped_t", L.ptr(x), L.dtype_code(x.dtype), L.ptr(gs), M, F, E, int(bool(blocks)),
-           L.ptr(xt), L.ptr(xs), L.ptr(ws), ws.numel(), L.stream(dev))
+    L.call(_entry("mtx_quant_fp8_grouped_t", scales), L.ptr(x), L.dtype_code(x.dtype), L.ptr(gs), M, F, E,
+           int(bool(blocks)), L.ptr(xt), L.ptr(xs), L.ptr(ws), ws.numel(), L.stream(dev))
     return xt, xs
 
 
 def tgmm_fp8(xt, xt_scale, gt, gt_scale, group_sizes, M: int, F: int | None = None,
-             N: int | None = None) -> torch.Tensor:
+             N: int | None = None, *, scales: str = "amax") -> torch.Tensor:
     """dW [E, F, N] bf16 = per group dequant(x)^T @ dequant(g) with f32 accumulation (``mtx_tgmm_fp8``):
     x from ``quantize_fp8_grouped_t(x, gs)`` (per-feature chunk scales), g from
     ``quantize_fp8_grouped_t(g, gs, blocks=True)``; M = rows of x and g, F / N their columns (taken
@@ -205,8 +208,9 @@ def tgmm_fp8(xt, xt_scale, gt, gt_scale, group_sizes, M: int, F: int | None = No
         raise ValueError("tgmm_fp8: operands were not quantised with these M, F, N and group count")
     dw = torch.empty((E, F, N), dtype=torch.bfloat16, device=dev)
     ws = L.workspace(L.query("mtx_fp8_grouped_workspace_size", E), dev)
-    L.call("mtx_tgmm_fp8", L.ptr(xt.contiguous()), L.ptr(xt_scale.contiguous()), L.ptr(gt.contiguous()),
-           L.ptr(gt_scale.contiguous()), L.ptr(gs), M, F, N, E, L.ptr(dw), L.ptr(ws), ws.numel(), L.stream(dev))
+    L.call(_entry("mtx_tgmm_fp8", scales), L.ptr(xt.contiguous()), L.ptr(xt_scale.contiguous()),
+           L.ptr(gt.contiguous()), L.ptr(gt_scale.contiguous()), L.ptr(gs), M, F, N, E, L.ptr(dw), L.ptr(ws),
+           ws.numel(), L.stream(dev))
     return dw
 
 
@@ -216,44 +220,52 @@ class _GMMFP8(torch.autograd.Function):
     """Forward: 1x128 row groups of x and 128x128 blocks of W, fp8 grouped GEMM.  Backward: the fp8
     dlhs (1x128 groups of the gradient rows against W's blocks in its own layout) and the fp8 tgmm
     (x and the gradient quantised in 128-row chunks of each expert).  The quantisations follow
-    the forward's conventions (scale = amax / 448, e4m3fn codes), and the backward treats each
+    the forward's conventions (e4m3fn codes; scale = amax / 448, or power-of-two scales in every
+    quantisation with ``scales="pow2"``), and the backward treats each
     quantise/dequantise pair as the identity (straight-through), as fp8 training recipes do; the
     reference's only fp8 product (the per-tensor matmul of mintext/modules/linear.py:37-57) has no
     grouped form to pin this against."""
 
     @staticmethod
-    def forward(ctx, x, weights, group_sizes):
+    def forward(ctx, x, weights, group_sizes, scales):
         gs = _gs(group_sizes)
-        xq, xs = quantize_fp8_rows(x)
-        wq, wsc = quantize_fp8_weights(weights)
-        out = grouped_matmul_fp8(xq, xs, wq, wsc, gs)
+        f8s = dict(scales=scales)
+        xq, xs = quantize_fp8_rows(x, **f8s)
+        wq, wsc = quantize_fp8_weights(weights, **f8s)
+        out = grouped_matmul_fp8(xq, xs, wq, wsc, gs, **f8s)
         ctx.save_for_backward(x, weights, gs)
+        ctx.scales = scales
         return out
 
     @staticmethod
     def backward(ctx, grad):
         x, w, gs = ctx.saved_tensors
+        f8s = dict(scales=ctx.scales)
         grad = grad.contiguous()
         dx = dw = None
         if ctx.needs_input_grad[0]:
-            gq, g_s = quantize_fp8_rows(grad)
-            wqt, wst = quantize_fp8_weights_t(w)
-            dx = grouped_matmul_fp8_dlhs(gq, g_s, wqt, wst, gs).to(x.dtype)
+            gq, g_s = quantize_fp8_rows(grad, **f8s)
+            wqt, wst = quantize_fp8_weights_t(w, **f8s)
+            dx = grouped_matmul_fp8_dlhs(gq, g_s, wqt, wst, gs, **f8s).to(x.dtype)
         if ctx.needs_input_grad[1]:
             M = x.shape[0]
-            xt, xts = quantize_fp8_grouped_t(x, gs)
-            gt, gts = quantize_fp8_grouped_t(grad, gs, blocks=True)
-            dw = tgmm_fp8(xt, xts, gt, gts, gs, M, x.shape[1], grad.shape[1]).to(w.dtype)
-        return dx, dw, None
+            xt, xts = quantize_fp8_grouped_t(x, gs, **f8s)
+            gt, gts = quantize_fp8_grouped_t(grad, gs, blocks=True, **f8s)
+            dw = tgmm_fp8(xt, xts, gt, gts, gs, M, x.shape[1], grad.shape[1], **f8s).to(w.dtype)
+        return dx, dw, None, None
 
 
-def grouped_matmul_fp8_vjp(x: torch.Tensor, weights: torch.Tensor, group_sizes: torch.Tensor) -> torch.Tensor:
+def grouped_matmul_fp8_vjp(x: torch.Tensor, weights: torch.Tensor, group_sizes: torch.Tensor, *,
+                           scales: str = "amax") -> torch.Tensor:
     """Blockwise-fp8 counterpart of ``grouped_matmul_vjp`` (grouped_matmul.py:83-190): x [M, Kin]
     and weights [E, Kin, Kout] (bf16 / f32 master values, the reference layout) are quantised on
     each call; the output is bf16 [M, Kout] and differentiable in (x, weights), both backward GEMMs
-    on fp8 operands.  Kin and Kout must be multiples of 256 (the tgmm tiles)."""
+    on fp8 operands.  Kin and Kout must be multiples of 256 (the tgmm tiles).  ``scales``: "amax"
+    (amax / 448) or "pow2" (power-of-two scales, applied by the MFMA) in every quantisation."""
     if x.dim() != 2 or weights.dim() != 3 or weights.shape[1] != x.shape[1]:
         raise ValueError(f"grouped_matmul_fp8_vjp: x {tuple(x.shape)} and weights {tuple(weights.shape)} do not match")
     if x.shape[1] % 256 or weights.shape[2] % 256:
         raise ValueError("grouped_matmul_fp8_vjp needs Kin and Kout multiples of 256")
-    return _GMMFP8.apply(x, weights, group_sizes)
+    if scales not in SCALE_MODES:
+        raise ValueError(f"scales must be one of {SCALE_MODES}, got {scales!r}")
+    return _GMMFP8.apply(x, weights, group_sizes, scales)

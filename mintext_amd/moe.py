@@ -232,20 +232,21 @@ def moe_experts_forward_fp8(x: torch.Tensor, topk_indices: torch.Tensor, topk_we
 
 
 def moe_experts_forward_fp8_train(x: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
-                                  gate_up: torch.Tensor, down: torch.Tensor) -> torch.Tensor:
+                                  gate_up: torch.Tensor, down: torch.Tensor, *, scales: str = "amax") -> torch.Tensor:
     """Differentiable blockwise-fp8 expert layer: the composition of ``moe_experts_forward``
     (route, gate_up GEMM, SwiGLU, down GEMM, combine; moe.py:161-221) with both grouped GEMMs as
     ``grouped_matmul_fp8_vjp``, so that all six GEMMs of a training step (the two forward
     products, the two dlhs and the two tgmm) run on fp8 operands.  gate_up [E, D, 2I] and down
     [E, I, D] are the master weights (reference layout), quantised on each call; x [N, D] bf16.
-    Gradients reach x, topk_weights, gate_up and down."""
+    Gradients reach x, topk_weights, gate_up and down.  ``scales``: "amax" (amax / 448) or "pow2"
+    (power-of-two scales applied by the MFMA) in every quantisation."""
     from .kernels.fp8 import grouped_matmul_fp8_vjp
 
     E = gate_up.shape[0]
     sorted_tokens, sort_indices, group_sizes = route(x, topk_indices, E)
-    h = grouped_matmul_fp8_vjp(sorted_tokens, gate_up, group_sizes)
+    h = grouped_matmul_fp8_vjp(sorted_tokens, gate_up, group_sizes, scales=scales)
     inter = swiglu_autograd(h)
-    out = grouped_matmul_fp8_vjp(inter, down, group_sizes)
+    out = grouped_matmul_fp8_vjp(inter, down, group_sizes, scales=scales)
     return unroute(out, sort_indices, topk_weights, topk_indices.shape[1])
 
 

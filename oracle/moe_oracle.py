@@ -453,11 +453,11 @@ def gmm_fp8(xq, xs, wq, ws, group_sizes) -> np.ndarray:
     return gmm(dequant_rows(xq, xs), dequant_weights(wq, ws), group_sizes)
 
 
-def quant_fp8_weights_t(w, block: int = 128):
+def quant_fp8_weights_t(w, block: int = 128, scales: str = "amax"):
     """The 128 x 128 blocks of ``quant_fp8_weights`` with the codes kept in w's own layout:
     (wq [E,Kin,Kout], ws [E,Kin/128,Kout/128]) -- the weight operand of the fp8 dlhs, whose
     reduction is Kout (grouped_matmul.py:162-176 with swapaxes(W,1,2) in fp8)."""
-    q, sc = quant_fp8_weights(w, block)
+    q, sc = quant_fp8_weights(w, block, scales)
     return np.ascontiguousarray(np.swapaxes(q, 1, 2)), np.ascontiguousarray(np.swapaxes(sc, 1, 2))
 
 
@@ -478,13 +478,15 @@ def fp8_group_chunks(group_sizes, M: int, block: int = 128):
     return off, cb
 
 
-def quant_fp8_grouped_t(x, group_sizes, blocks: bool, C: int | None = None, block: int = 128):
+def quant_fp8_grouped_t(x, group_sizes, blocks: bool, C: int | None = None, block: int = 128,
+                        scales: str = "amax"):
     """The tgmm operands: x [M,F] quantised in expert-aligned chunks of 128 rows (chunk j of expert
     e = its rows 128j .. 128j+127, zero past the expert) and transposed per expert, in expert-major
     blocks: returns flat codes (expert e's block [F, 128 n_e] at offset 128*F*cb[e], n_e = its
     chunks) and flat scales -- one per feature and chunk ([F, n_e] at F*cb[e], ``blocks`` False,
     1 x 128 along the transposed row) or one per 128 features and chunk ([F/128, n_e] at
-    (F/128)*cb[e], ``blocks`` True, 128 x 128).  scale = amax/448 (1 if 0), q = RNE(x / scale).
+    (F/128)*cb[e], ``blocks`` True, 128 x 128).  scale = amax/448 (1 if 0) or, with scales="pow2",
+    p2_scale(amax); q = RNE(x / scale).
     C (chunk slots allocated) defaults to ceil(M/128) + E; slots past the groups stay 0."""
     x = np.asarray(x, dtype=np.float32)
     M, F = x.shape
@@ -505,8 +507,7 @@ def quant_fp8_grouped_t(x, group_sizes, blocks: bool, C: int | None = None, bloc
             amax = np.abs(t.reshape(F // block, block, ne, block)).max(axis=(1, 3))  # [F/128, ne]
         else:
             amax = np.abs(t).max(-1)  # [F, ne]
-        sc = (amax / np.float32(E4M3_MAX)).astype(np.float32)
-        sc = np.where(sc == 0, np.float32(1.0), sc).astype(np.float32)
+        sc = _scale_of(amax.astype(np.float32), scales)
         sfull = np.repeat(sc, block, axis=0) if blocks else sc  # [F, ne]
         q = e4m3_encode((t / sfull[:, :, None]).astype(np.float32))
         xt[block * F * int(cb[e]):block * F * int(cb[e + 1])] = q.reshape(-1)

@@ -1,7 +1,7 @@
 """GPU parity of the blockwise-fp8 backward (dlhs and tgmm with e4m3 operands; the bf16 forms are
 grouped_matmul.py:151-187 and :197-235): quantisers bit-exact against the oracle, the GEMMs within
 1e-2 of the dequantised float64 oracle and 6e-2 of the unquantised product, empty and skewed groups,
-the C5 backward shapes at full size."""
+the C5 backward shapes at full size; in both scale modes (amax/448 and power-of-two)."""
 from __future__ import annotations
 
 import numpy as np
@@ -31,30 +31,35 @@ def _zipf_groups(rng, M, E, empty=(1,)):
     return gs
 
 
+SCALES = ["amax", "pow2"]
+
+
+@pytest.mark.parametrize("scales", SCALES)
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
-def test_quant_weights_t_bit_exact(dev, dt):
+def test_quant_weights_t_bit_exact(dev, dt, scales):
     from mintext_amd.kernels.fp8 import quantize_fp8_weights, quantize_fp8_weights_t
 
     w = (torch.randn(3, 256, 384, device=dev) * 0.02).to(dt)
     w[1, :128, :128] = 0  # an all-zero block -> scale 1
-    q, s = quantize_fp8_weights_t(w)
-    oq, os_ = O.quant_fp8_weights_t(w.float().cpu().numpy())
+    q, s = quantize_fp8_weights_t(w, scales=scales)
+    oq, os_ = O.quant_fp8_weights_t(w.float().cpu().numpy(), scales=scales)
     assert np.array_equal(_u8(q), oq) and np.array_equal(s.cpu().numpy(), os_)
     # the same blocks as the forward's prepack
-    qf, sf = quantize_fp8_weights(w)
+    qf, sf = quantize_fp8_weights(w, scales=scales)
     assert torch.equal(q.view(torch.uint8), qf.view(torch.uint8).transpose(1, 2)) and torch.equal(s, sf.transpose(1, 2))
 
 
+@pytest.mark.parametrize("scales", SCALES)
 @pytest.mark.parametrize("blocks", [False, True])
 @pytest.mark.parametrize("M,F,E", [(1000, 256, 6), (4095, 512, 16), (129, 128, 3), (5000, 768, 64)])
-def test_quant_grouped_t_bit_exact(dev, blocks, M, F, E):
+def test_quant_grouped_t_bit_exact(dev, blocks, M, F, E, scales):
     from mintext_amd.kernels.fp8 import quantize_fp8_grouped_t
 
     rng = np.random.default_rng(M + F)
     gs = _zipf_groups(rng, M - 7, E)  # 7 rows past sum(group_sizes): not quantised
     x = (torch.randn(M, F, device=dev) * torch.rand(1, F, device=dev) * 5).bfloat16()
-    xt, xs = quantize_fp8_grouped_t(x, _t(gs, dev), blocks=blocks)
-    oq, os_ = O.quant_fp8_grouped_t(x.float().cpu().numpy(), gs, blocks)
+    xt, xs = quantize_fp8_grouped_t(x, _t(gs, dev), blocks=blocks, scales=scales)
+    oq, os_ = O.quant_fp8_grouped_t(x.float().cpu().numpy(), gs, blocks, scales=scales)
     _, cb = O.fp8_group_chunks(gs, M)
     used = int(cb[-1])
     assert np.array_equal(_u8(xt)[:128 * F * used], oq[:128 * F * used])
@@ -62,17 +67,18 @@ def test_quant_grouped_t_bit_exact(dev, blocks, M, F, E):
     assert np.array_equal(xs.cpu().numpy()[:nf * used], os_[:nf * used])
 
 
+@pytest.mark.parametrize("scales", SCALES)
 @pytest.mark.parametrize("M,Kin,Kout,E", [(2000, 256, 384, 6), (3000, 768, 2048, 16), (700, 2048, 1536, 4)])
-def test_gmm_fp8_dlhs(dev, M, Kin, Kout, E):
+def test_gmm_fp8_dlhs(dev, M, Kin, Kout, E, scales):
     from mintext_amd.kernels.fp8 import grouped_matmul_fp8_dlhs, quantize_fp8_rows, quantize_fp8_weights_t
 
     rng = np.random.default_rng(M)
     gs = _zipf_groups(rng, M, E)
     g = torch.randn(M, Kout, device=dev).bfloat16()
     w = (torch.randn(E, Kin, Kout, device=dev) * 0.02).bfloat16()
-    gq, gsc = quantize_fp8_rows(g)
-    wq, ws = quantize_fp8_weights_t(w)
-    dx = grouped_matmul_fp8_dlhs(gq, gsc, wq, ws, _t(gs, dev))
+    gq, gsc = quantize_fp8_rows(g, scales=scales)
+    wq, ws = quantize_fp8_weights_t(w, scales=scales)
+    dx = grouped_matmul_fp8_dlhs(gq, gsc, wq, ws, _t(gs, dev), scales=scales)
     assert dx.dtype == torch.bfloat16 and dx.shape == (M, Kin)
     got = dx.float().cpu().numpy()
     ref_q = O.gmm_fp8_dlhs(_u8(gq), gsc.cpu().numpy(), _u8(wq), ws.cpu().numpy(), gs)
@@ -81,9 +87,10 @@ def test_gmm_fp8_dlhs(dev, M, Kin, Kout, E):
     assert rel_err(got, ref) < 6e-2
 
 
+@pytest.mark.parametrize("scales", SCALES)
 @pytest.mark.parametrize("M,F,N,E", [(2000, 256, 256, 6), (5000, 768, 2048, 16), (3000, 2048, 1536, 8),
                                      (300, 256, 512, 40)])
-def test_tgmm_fp8(dev, M, F, N, E):
+def test_tgmm_fp8(dev, M, F, N, E, scales):
     from mintext_amd.kernels.fp8 import quantize_fp8_grouped_t, tgmm_fp8
 
     rng = np.random.default_rng(M + E)
@@ -91,9 +98,9 @@ def test_tgmm_fp8(dev, M, F, N, E):
     x = torch.randn(M, F, device=dev).bfloat16()
     g = torch.randn(M, N, device=dev).bfloat16()
     tg = _t(gs, dev)
-    xt, xs = quantize_fp8_grouped_t(x, tg)
-    gt, gsc = quantize_fp8_grouped_t(g, tg, blocks=True)
-    dw = tgmm_fp8(xt, xs, gt, gsc, tg, M)
+    xt, xs = quantize_fp8_grouped_t(x, tg, scales=scales)
+    gt, gsc = quantize_fp8_grouped_t(g, tg, blocks=True, scales=scales)
+    dw = tgmm_fp8(xt, xs, gt, gsc, tg, M, scales=scales)
     assert dw.dtype == torch.bfloat16 and dw.shape == (E, F, N)
     got = dw.float().cpu().numpy()
     for e in np.flatnonzero(gs == 0):
@@ -105,7 +112,8 @@ def test_tgmm_fp8(dev, M, F, N, E):
 
 
 @pytest.mark.timeout(600)
-def test_fp8_backward_c5_full_size(dev):
+@pytest.mark.parametrize("scales", SCALES)
+def test_fp8_backward_c5_full_size(dev, scales):
     """The C5 backward shapes (M=131072, D=2048, I=768, E=128, the bench's Zipf(1.2) routing) with
     fp8 operands: dlhs of both expert GEMMs on sampled rows, tgmm of both on sampled blocks."""
     import bench
@@ -123,12 +131,15 @@ def test_fp8_backward_c5_full_size(dev):
         gy = torch.randn(M, D, device=dev, generator=g).bfloat16()    # d out of the down GEMM
         gh = torch.randn(M, 2 * I, device=dev, generator=g).bfloat16()  # d out of the gate_up GEMM
         y = torch.randn(M, I, device=dev, generator=g).bfloat16()      # the down GEMM's input
-        dnq, dns = quantize_fp8_weights_t(down)
-        guq, gus = quantize_fp8_weights_t(gate_up)
-        a = grouped_matmul_fp8_dlhs(*quantize_fp8_rows(gy), dnq, dns, gs)   # [M, I]
-        b = grouped_matmul_fp8_dlhs(*quantize_fp8_rows(gh), guq, gus, gs)   # [M, D]
-        c = tgmm_fp8(*quantize_fp8_grouped_t(y, gs), *quantize_fp8_grouped_t(gy, gs, blocks=True), gs, M)   # [E, I, D]
-        d = tgmm_fp8(*quantize_fp8_grouped_t(st, gs), *quantize_fp8_grouped_t(gh, gs, blocks=True), gs, M)  # [E, D, 2I]
+        f8s = dict(scales=scales)
+        dnq, dns = quantize_fp8_weights_t(down, **f8s)
+        guq, gus = quantize_fp8_weights_t(gate_up, **f8s)
+        a = grouped_matmul_fp8_dlhs(*quantize_fp8_rows(gy, **f8s), dnq, dns, gs, **f8s)   # [M, I]
+        b = grouped_matmul_fp8_dlhs(*quantize_fp8_rows(gh, **f8s), guq, gus, gs, **f8s)   # [M, D]
+        c = tgmm_fp8(*quantize_fp8_grouped_t(y, gs, **f8s), *quantize_fp8_grouped_t(gy, gs, blocks=True, **f8s), gs, M,
+                     **f8s)  # [E, I, D]
+        d = tgmm_fp8(*quantize_fp8_grouped_t(st, gs, **f8s), *quantize_fp8_grouped_t(gh, gs, blocks=True, **f8s), gs,
+                     M, **f8s)  # [E, D, 2I]
     gsh = gs.cpu().numpy()
     off = np.concatenate([[0], np.cumsum(gsh)])
     rng = np.random.default_rng(61)
@@ -152,7 +163,8 @@ def test_fp8_backward_c5_full_size(dev):
         assert rel_err(got_d, ref_d) < 6e-2, f"tgmm gate_up, expert {e}"
 
 
-def test_gmm_fp8_vjp_matches_kernels_and_oracle(dev):
+@pytest.mark.parametrize("scales", SCALES)
+def test_gmm_fp8_vjp_matches_kernels_and_oracle(dev, scales):
     """grouped_matmul_fp8_vjp: the forward and both gradients are bit for bit the fp8 kernels on the
     quantised operands (rows / 128x128 blocks / 128-row chunks), and within 6e-2 of the float64
     product and VJP of the unquantised operands; an empty group gets a zero weight gradient."""
@@ -167,13 +179,15 @@ def test_gmm_fp8_vjp_matches_kernels_and_oracle(dev):
     x = torch.randn(M, Kin, device=dev).bfloat16().requires_grad_(True)
     w = (torch.randn(E, Kin, Kout, device=dev) * 0.02).bfloat16().requires_grad_(True)
     G = torch.randn(M, Kout, device=dev).bfloat16()
-    out = grouped_matmul_fp8_vjp(x, w, tg)
+    f8s = dict(scales=scales)
+    out = grouped_matmul_fp8_vjp(x, w, tg, **f8s)
     out.backward(G)
     assert out.dtype == torch.bfloat16 and x.grad.dtype == torch.bfloat16 and w.grad.dtype == torch.bfloat16
     with torch.no_grad():
-        ref_out = grouped_matmul_fp8(*quantize_fp8_rows(x), *quantize_fp8_weights(w), tg)
-        ref_dx = grouped_matmul_fp8_dlhs(*quantize_fp8_rows(G), *quantize_fp8_weights_t(w), tg)
-        ref_dw = tgmm_fp8(*quantize_fp8_grouped_t(x, tg), *quantize_fp8_grouped_t(G, tg, blocks=True), tg, M)
+        ref_out = grouped_matmul_fp8(*quantize_fp8_rows(x, **f8s), *quantize_fp8_weights(w, **f8s), tg, **f8s)
+        ref_dx = grouped_matmul_fp8_dlhs(*quantize_fp8_rows(G, **f8s), *quantize_fp8_weights_t(w, **f8s), tg, **f8s)
+        ref_dw = tgmm_fp8(*quantize_fp8_grouped_t(x, tg, **f8s), *quantize_fp8_grouped_t(G, tg, blocks=True, **f8s),
+                          tg, M, **f8s)
     assert torch.equal(out, ref_out) and torch.equal(x.grad, ref_dx) and torch.equal(w.grad, ref_dw)
     f = lambda t: t.detach().float().cpu().numpy()
     assert rel_err(f(out), O.gmm(f(x), f(w), gs)) < 6e-2
@@ -183,8 +197,9 @@ def test_gmm_fp8_vjp_matches_kernels_and_oracle(dev):
         assert not w.grad[e].any()
 
 
+@pytest.mark.parametrize("scales", SCALES)
 @pytest.mark.parametrize("T,D,E,K,I", [(1024, 512, 16, 4, 256), (2048, 256, 8, 2, 512)])
-def test_fp8_layer_training_matches_oracle_vjp(dev, T, D, E, K, I):
+def test_fp8_layer_training_matches_oracle_vjp(dev, T, D, E, K, I, scales):
     """moe_experts_forward_fp8_train (all six GEMMs on fp8 operands) against the float64 forward
     and VJP of the unquantised layer.  Each fp8 GEMM is within 6e-2 of its unquantised product
     (test above); the layer and its gradients pass through two of them in series (the output:
@@ -201,7 +216,7 @@ def test_fp8_layer_training_matches_oracle_vjp(dev, T, D, E, K, I):
     idx, w = route_topk(torch.randn(T, E, device=dev, generator=gen), K)
     w = w.clone().requires_grad_(True)
     G = torch.randn(T, D, device=dev, generator=gen)
-    out = moe_experts_forward_fp8_train(x, idx, w, gu, dn)
+    out = moe_experts_forward_fp8_train(x, idx, w, gu, dn, scales=scales)
     assert out.dtype == torch.float32
     (out * G).sum().backward()
     f = lambda a: a.detach().float().cpu().numpy()
@@ -212,3 +227,40 @@ def test_fp8_layer_training_matches_oracle_vjp(dev, T, D, E, K, I):
         errs[name] = rel_err(f(got), r)
     print("fp8 training layer rel errors", {k: round(v, 4) for k, v in errs.items()})
     assert all(v < 1e-1 for v in errs.values()), errs
+
+
+def test_tgmm_fp8_p2_chunks_of_very_different_magnitude(dev):
+    """Power-of-two mode: neighbouring 128-row chunks of an expert whose scales are 2^100 and more
+    apart (a normal chunk, a chunk of values near 1e-33 with a subnormal-range scale, an all-zero
+    chunk, then normal again) -- the accumulators stay in true units, so dW is finite and within
+    1e-2 of the dequantised float64 product and 6e-2 of the unquantised one.  The dlhs of the same
+    rows goes through the forward kernel's power-of-two mode."""
+    from mintext_amd.kernels.fp8 import (grouped_matmul_fp8_dlhs, quantize_fp8_grouped_t, quantize_fp8_rows,
+                                         quantize_fp8_weights_t, tgmm_fp8)
+
+    gs = np.array([512, 0, 384], np.int32)
+    M, F, N = int(gs.sum()), 256, 512
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+    x = torch.randn(M, F, device=dev, generator=gen)
+    g = torch.randn(M, N, device=dev, generator=gen)
+    x[128:256] *= 1e-33   # chunk 1 of expert 0: scale near 2^-117
+    g[128:256] *= 1e-30
+    x[256:384] = 0        # chunk 2: scale 1
+    x[512 + 128:512 + 256] *= 3e-28
+    tg = _t(gs, dev)
+    xt, xs = quantize_fp8_grouped_t(x, tg, scales="pow2")
+    gt, gsc = quantize_fp8_grouped_t(g, tg, blocks=True, scales="pow2")
+    dw = tgmm_fp8(xt, xs, gt, gsc, tg, M, scales="pow2")
+    got = dw.float().cpu().numpy()
+    assert np.isfinite(got).all() and not got[1].any()
+    ref_q = O.tgmm_fp8(_u8(xt), xs.cpu().numpy(), _u8(gt), gsc.cpu().numpy(), gs, M, F, N)
+    assert rel_err(got, ref_q) < 1e-2
+    assert rel_err(got, O.tgmm(x.cpu().numpy(), g.cpu().numpy(), gs)) < 6e-2
+    w = torch.randn(3, F, N, device=dev, generator=gen) * 0.02
+    gq, gsc2 = quantize_fp8_rows(g, scales="pow2")
+    wq, ws = quantize_fp8_weights_t(w, scales="pow2")
+    dx = grouped_matmul_fp8_dlhs(gq, gsc2, wq, ws, tg, scales="pow2").float().cpu().numpy()
+    assert np.isfinite(dx).all()
+    ref_dx = O.gmm_fp8_dlhs(_u8(gq), gsc2.cpu().numpy(), _u8(wq), ws.cpu().numpy(), gs)
+    assert rel_err(dx, ref_dx) < 1e-2

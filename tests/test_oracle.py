@@ -468,13 +468,14 @@ def test_planted_mistake_is_caught():
 
 
 # ------------------------------------------------------------------------ fp8 backward operands
-def test_quant_weights_t_is_the_forward_blocks_in_w_layout():
+@pytest.mark.parametrize("scales", ["amax", "pow2"])
+def test_quant_weights_t_is_the_forward_blocks_in_w_layout(scales):
     """The dlhs weight operand: the forward's 128x128 blocks (pinned through quant_fp8_weights
-    against torch's e4m3 cast) with codes in w's own layout; dequantised it is within half an e4m3
-    step of w everywhere."""
+    against torch's e4m3 cast, in both scale modes) with codes in w's own layout; dequantised it is
+    within half an e4m3 step of w everywhere."""
     w = (np.random.default_rng(3).standard_normal((2, 256, 384)) * 0.05).astype(np.float32)
-    q, s = O.quant_fp8_weights_t(w)
-    qf, sf = O.quant_fp8_weights(w)
+    q, s = O.quant_fp8_weights_t(w, scales=scales)
+    qf, sf = O.quant_fp8_weights(w, scales=scales)
     assert q.shape == (2, 256, 384) and s.shape == (2, 2, 3)
     assert np.array_equal(q, np.swapaxes(qf, 1, 2)) and np.array_equal(s, np.swapaxes(sf, 1, 2))
     deq = O.e4m3_decode(q).astype(np.float64) * np.repeat(np.repeat(s, 128, 1), 128, 2)
@@ -497,16 +498,17 @@ def test_gmm_fp8_dlhs_equals_dequantised_dlhs():
     assert rel_err(got, O.gmm_dlhs(g, w, gs)) < 6e-2
 
 
+@pytest.mark.parametrize("scales", ["amax", "pow2"])
 @pytest.mark.parametrize("blocks", [False, True])
-def test_quant_grouped_t_chunks_equal_row_and_block_quantisers(blocks):
+def test_quant_grouped_t_chunks_equal_row_and_block_quantisers(blocks, scales):
     """Each expert-aligned chunk of the transposed operand is quant_fp8_rows (1x128 along the
-    transposed row) or, with blocks, quant_fp8_weights (128x128) of that zero-padded chunk, stored
-    in expert-major blocks."""
+    transposed row) or, with blocks, quant_fp8_weights (128x128) of that zero-padded chunk, in the
+    same scale mode, stored in expert-major blocks."""
     rng = np.random.default_rng(5)
     gs = np.array([130, 0, 5, 256, 0, 77], np.int32)
     M, F = int(gs.sum()) + 9, 256
     x = (rng.standard_normal((M, F)) * rng.uniform(0.01, 10, (1, F))).astype(np.float32)
-    xt, xs = O.quant_fp8_grouped_t(x, gs, blocks)
+    xt, xs = O.quant_fp8_grouped_t(x, gs, blocks, scales=scales)
     off, cb = O.fp8_group_chunks(gs, M)
     assert int(cb[-1]) == sum(-(-int(g) // 128) for g in gs)
     nf = F // 128 if blocks else F
@@ -520,10 +522,10 @@ def test_quant_grouped_t_chunks_equal_row_and_block_quantisers(blocks):
             rows = x[r0:min(r0 + 128, int(off[e + 1]))]
             chunk[: len(rows)] = rows
             if blocks:
-                q, s = O.quant_fp8_weights(chunk[None])  # [1, F, 128] codes, [1, F/128, 1] scales
+                q, s = O.quant_fp8_weights(chunk[None], scales=scales)  # [1, F, 128] codes, [1, F/128, 1] scales
                 assert np.array_equal(blk[:, 128 * j:128 * (j + 1)], q[0]) and np.array_equal(sce[:, j], s[0, :, 0])
             else:
-                q, s = O.quant_fp8_rows(np.ascontiguousarray(chunk.T))
+                q, s = O.quant_fp8_rows(np.ascontiguousarray(chunk.T), scales=scales)
                 assert np.array_equal(blk[:, 128 * j:128 * (j + 1)], q) and np.array_equal(sce[:, j], s[:, 0])
     # round trip within the e4m3 bound, padding dropped
     d = O.dequant_grouped_t(xt, xs, gs, M, F, blocks)
