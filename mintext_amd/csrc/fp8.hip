@@ -194,6 +194,7 @@ __global__ __launch_bounds__(1024) void build_tiles_f8_kernel(const int32_t* __r
     tiles[s_total[1] + z] = t;
   }
   if (e == 0) count[0] = s_total[1] + ntail;
+  if (e >= 8 && e < 16) count[e] = 0;  // the persistent kernel's per-XCD tile tickets
 }
 
 // ---- GEMM --------------------------------------------------------------------------------------
@@ -873,7 +874,16 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
   int lid_next = lid + nx;
   Tile nxt = lid_next < lid_end ? decode(lid_next) : cur;
   Src scur = make_src(cur), snxt = make_src(nxt);
-
+  // Tiles past each workgroup's first two come from its XCD's ticket counter (count[8 + xcd],
+  // zeroed by the tile-list kernel): ticket t is tile xcd*per + 2*nx + t, so a workgroup that
+  // finishes early takes more tiles.  Wave 0 takes the ticket of the tile after next at the start
+  // of each epilogue and publishes it through LDS before the epilogue's last barrier (by then the
+  // ring loads issued before the epilogue have landed, so its wait for the atomic costs little);
+  // inside the k-loop the ticket's register would not fit beside the accumulators.
+#ifndef MTX_F8_TICKETS
+#define MTX_F8_TICKETS 1
+#endif
+  __shared__ int s_ticket;
   const uint32_t lds_base = lds_addr(lds);
   // issue ring step g = stage kt of the current tile, or of the next one when kt >= nk
   // (uniform bases in SGPRs, per-lane 32-bit offsets)
@@ -1004,47 +1014,55 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
     }
   };
 
-  for (;;) {
-    for (int kb = 0; kb < nkb; ++kb) {
-      const int kt = 2 * kb;
-      // even stage kt (ring step g): B fragments in set 0
-      issue(g + PD, kt + PD, false);
-      float f[TM][NSB] = {};
-      if (P2 && kb > 0) {  // true units throughout: only the codes change
-        ea_c = ea_n;
+  // One 128-k block (an even and an odd stage); FIRST: the tile's first block (no rescale).
+  auto kblock = [&](int kb, auto first_tag) {
+    constexpr bool FIRST = decltype(first_tag)::value;
+    const int kt = 2 * kb;
+    // even stage kt (ring step g): B fragments in set 0
+    issue(g + PD, kt + PD, false);
+    float f[TM][NSB] = {};
+    if (FIRST) {
+      rot_stage(g, 0, false, f);
+    } else if (P2) {  // true units throughout: only the codes change
+      ea_c = ea_n;
 #pragma unroll
-        for (int h = 0; h < NSB; ++h) eb_c[h] = eb_n[h];
-        rot_stage(g, 0, false, f);
-      } else if (kb > 0) {
+      for (int h = 0; h < NSB; ++h) eb_c[h] = eb_n[h];
+      rot_stage(g, 0, false, f);
+    } else {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int h = 0; h < NSB; ++h)  // (sa_c / sa_n) * (sb_c / sb_n): no product of two small scales
-            f[i][h] = (sa_c[i] * __builtin_amdgcn_rcpf(sa_n[i])) * (sb_c[h] * __builtin_amdgcn_rcpf(sb_n[h]));
+        for (int h = 0; h < NSB; ++h)  // (sa_c / sa_n) * (sb_c / sb_n): no product of two small scales
+          f[i][h] = (sa_c[i] * __builtin_amdgcn_rcpf(sa_n[i])) * (sb_c[h] * __builtin_amdgcn_rcpf(sb_n[h]));
 #pragma unroll
-        for (int i = 0; i < TM; ++i) sa_c[i] = sa_n[i];
+      for (int i = 0; i < TM; ++i) sa_c[i] = sa_n[i];
 #pragma unroll
-        for (int h = 0; h < NSB; ++h) sb_c[h] = sb_n[h];
-        rot_stage(g, 0, true, f);
-      } else {
-        rot_stage(g, 0, false, f);
-      }
-      // Step g+2 landed (g+3 may be in flight), then a bare s_barrier: __syncthreads() would
-      // also wait for this wave's outstanding LDS reads, which are the fragments of the next
-      // step (visible since the previous barrier) and need not complete before it.  Slots are
-      // refilled only after every wave's MFMAs consumed the fragments read from them.
-      __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS));
-      __builtin_amdgcn_s_barrier();
-      // odd stage kt+1 (ring step g+1): B fragments in set 1
-      issue(g + 1 + PD, kt + 1 + PD, true);
-      if constexpr (P2) read_codes(g + 2, ea_n, eb_n);  // next block's codes (or the next tile's)
-      else read_scales(g + 2, sa_n, sb_n);              // next block's scales (or the next tile's)
-      rot_stage(g + 1, 1, false, f);
-      __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));  // step g+3 landed (g+4 may be in flight)
-      __builtin_amdgcn_s_barrier();
-      g += 2;
+      for (int h = 0; h < NSB; ++h) sb_c[h] = sb_n[h];
+      rot_stage(g, 0, true, f);
     }
+    // Step g+2 landed (g+3 may be in flight), then a bare s_barrier: __syncthreads() would
+    // also wait for this wave's outstanding LDS reads, which are the fragments of the next
+    // step (visible since the previous barrier) and need not complete before it.  Slots are
+    // refilled only after every wave's MFMAs consumed the fragments read from them.
+    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS));
+    __builtin_amdgcn_s_barrier();
+    // odd stage kt+1 (ring step g+1): B fragments in set 1
+    issue(g + 1 + PD, kt + 1 + PD, true);
+    if constexpr (P2) read_codes(g + 2, ea_n, eb_n);  // next block's codes (or the next tile's)
+    else read_scales(g + 2, sa_n, sb_n);              // next block's scales (or the next tile's)
+    rot_stage(g + 1, 1, false, f);
+    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));  // step g+3 landed (g+4 may be in flight)
+    __builtin_amdgcn_s_barrier();
+    g += 2;
+  };
 
+  for (;;) {
+    kblock(0, std::true_type());
+    for (int kb = 1; kb < nkb; ++kb) kblock(kb, std::false_type());
+
+    int tk = 0;
+    if (MTX_F8_TICKETS && wave_u == 0 && lane == 0)
+      tk = __hip_atomic_fetch_add(const_cast<int*>(p.count) + 8 + xcd, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // ---- epilogue of the current tile (the next tile's first stages are in flight) ---------
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -1089,6 +1107,7 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
         }
         __builtin_amdgcn_s_waitcnt(MTX_LGKMCNT0);  // reads done before the next block overwrites
       }
+      if (MTX_F8_TICKETS && wave_u == 0 && lane == 0) s_ticket = tk;
       __syncthreads();  // staging slot free before the next tile's first ring load
     } else {
       float y[TM][16];
@@ -1139,6 +1158,7 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
           if (wn == 0 && fhalf == 0) p.outs[(int64_t)row * (p.I / 128) + cur.n_tile] = sc;
         }
       }
+      if (MTX_F8_TICKETS && wave_u == 0 && lane == 0) s_ticket = tk;
       __syncthreads();
       // 256 rows x 128 bytes: 8 lanes per row, 8 rows per wave instruction
 #pragma unroll
@@ -1150,6 +1170,8 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
       }
       __syncthreads();  // red and the staging slot are reused by the next tile
     }
+    // the tile after next (s_ticket is rewritten only in the next tile's epilogue)
+    const int lid_after = MTX_F8_TICKETS ? xcd * per + 2 * nx + s_ticket : lid_next + nx;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -1162,7 +1184,7 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
     if (lid >= lid_end) break;
     cur = nxt;
     scur = snxt;
-    lid_next = lid + nx;
+    lid_next = lid_after;
     if (lid_next < lid_end) {
       nxt = decode(lid_next);
       snxt = make_src(nxt);
