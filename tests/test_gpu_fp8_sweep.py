@@ -1,9 +1,11 @@
 """GPU parity sweep of the blockwise-fp8 grouped GEMM (the persistent kernel) over seeded random
 shapes: expert counts 1-128, uniform / Zipf / ragged-with-empty group sizes, rows past
 sum(group_sizes), reductions of 2-24 blocks, per-128-block magnitudes spread over 1e-3 .. 1e3
-(the block-to-block rescaling), plain store and SwiGLU + re-quantisation.  Each case is checked
-against the dequantise-then-float64 oracle (1e-2) and the unquantised float64 product (6e-2),
-and rows past the groups must be zero."""
+(the block-to-block rescaling), plain store and SwiGLU + re-quantisation, in both scale modes
+(amax/448 and power-of-two); three larger cases give every workgroup more than two tiles, so that
+tiles come from the per-XCD ticket counters.  Each case is checked against the
+dequantise-then-float64 oracle (1e-2) and the unquantised float64 product (6e-2), and rows past
+the groups must be zero."""
 from __future__ import annotations
 
 import numpy as np
@@ -44,6 +46,9 @@ def _cases(n=16, seed=77):
         past = int(rng.choice([0, 0, 7, 300]))
         swiglu = bool(i % 4 == 3)
         out.append((i, E, M, kin, kout, kind, past, swiglu))
+    # many tiles per workgroup (ticketed tiles): 1400-2900 tiles of 256 x 256
+    out += [(n, 16, 60000, 512, 1536, "zipf", 7, False), (n + 1, 8, 40000, 768, 2048, "uniform", 0, True),
+            (n + 2, 128, 50000, 256, 1536, "ragged", 300, False)]
     return out
 
 
@@ -51,8 +56,9 @@ def _u8(t):
     return t.view(torch.uint8).cpu().numpy()
 
 
+@pytest.mark.parametrize("scales", ["amax", "pow2"])
 @pytest.mark.parametrize("case", _cases(), ids=lambda c: f"c{c[0]}-E{c[1]}-M{c[2]}-K{c[3]}-N{c[4]}-{c[5]}-p{c[6]}-{'swiglu' if c[7] else 'store'}")
-def test_gmm_fp8_sweep(dev, case):
+def test_gmm_fp8_sweep(dev, case, scales):
     from mintext_amd.kernels.fp8 import grouped_matmul_fp8, grouped_matmul_fp8_swiglu, quantize_fp8_rows, \
         quantize_fp8_weights
 
@@ -64,19 +70,20 @@ def test_gmm_fp8_sweep(dev, case):
     x = (torch.randn(Mt, kin, device=dev) * blk.repeat_interleave(128, 1)).bfloat16()
     wblk = torch.from_numpy(10.0 ** rng.uniform(-1, 1, (E, kin // 128, 1))).float().to(dev)
     w = (torch.randn(E, kin, kout, device=dev) * 0.02 * wblk.repeat_interleave(128, 1)).bfloat16()
-    xq, xs = quantize_fp8_rows(x)
-    wq, ws = quantize_fp8_weights(w)
+    f8s = dict(scales=scales)
+    xq, xs = quantize_fp8_rows(x, **f8s)
+    wq, ws = quantize_fp8_weights(w, **f8s)
     gt = torch.from_numpy(gs).to(dev)
     deq = O.gmm_fp8(_u8(xq), xs.cpu().numpy(), _u8(wq), ws.cpu().numpy(), gs)
     if not swiglu:
-        out = grouped_matmul_fp8(xq, xs, wq, ws, gt)
+        out = grouped_matmul_fp8(xq, xs, wq, ws, gt, **f8s)
         got = out.float().cpu().numpy()
         assert (out[M:] == 0).all(), "rows past sum(group_sizes) must be zero"
         assert rel_err(got, deq) < 1e-2, rel_err(got, deq)
         full = O.gmm(x.float().cpu().numpy(), w.float().cpu().numpy(), gs)
         assert rel_err(got, full) < 6e-2, rel_err(got, full)
     else:
-        yq, ys, yb = grouped_matmul_fp8_swiglu(xq, xs, wq, ws, gt, return_bf16=True)
+        yq, ys, yb = grouped_matmul_fp8_swiglu(xq, xs, wq, ws, gt, return_bf16=True, **f8s)
         ref = O.swiglu(deq)
         assert rel_err(yb.float().cpu().numpy()[:M], ref[:M]) < 1e-2
         assert (yb[M:] == 0).all() and (_u8(yq)[M:] == 0).all()
