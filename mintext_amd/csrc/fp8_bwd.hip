@@ -60,10 +60,11 @@ __global__ __launch_bounds__(256) void quant_weights_t_kernel(const T* __restric
 // One workgroup, E <= 1024: row offsets off[E+1] of the groups (clamped to M like the forward's
 // tile builder), chunk bases cb[E+1] (cb[e] = sum of ceil(rows/128) over the experts before e)
 // and the experts in descending size order (ties: lower id first), so the longest reductions
-// start first.
+// start first; misc[0] = the experts with rows (a prefix of that order), misc[8..15] = 0 (the
+// persistent tgmm's tile tickets).
 __global__ __launch_bounds__(1024) void chunk_prologue_kernel(const int32_t* __restrict__ gs, int E, int M,
                                                               int* __restrict__ cb, int* __restrict__ off,
-                                                              int* __restrict__ order) {
+                                                              int* __restrict__ order, int* __restrict__ misc) {
   __shared__ long long wsum64[16];
   __shared__ int wsum[16];
   __shared__ int s_rows[1024];
@@ -108,6 +109,9 @@ __global__ __launch_bounds__(1024) void chunk_prologue_kernel(const int32_t* __r
     for (int h = 0; h < E; ++h) rank += (s_rows[h] > rows || (s_rows[h] == rows && h < e)) ? 1 : 0;
     order[rank] = e;
   }
+  const int nrows = __syncthreads_count(e < E && nch >= 1);
+  if (e == 0) misc[0] = nrows;
+  if (e >= 8 && e < 16) misc[e] = 0;
 }
 
 // expert owning chunk c: the last e with cb[e] <= c (experts without chunks share their
@@ -427,6 +431,359 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_kernel(TArgs p) {
   }
 }
 
+// ---- persistent tgmm ---------------------------------------------------------------------------
+// The tiles and arithmetic of tgmm_fp8_kernel (the same MFMA sequence per output element, so the
+// same bits) with one workgroup per CU and the ring of gmm_fp8_v4_kernel running across tiles: the
+// next tile's first three stages are loaded during the current tile's last three, so a tile starts
+// without the ring prologue (5.4 us of a C5 tile's 27 us in the per-tile kernel, with 1-2 us
+// between workgroups).  The tiles of the experts with rows (misc[0] of them, a prefix of `order`)
+// come in tgmm_fp8_kernel's order: XCD x takes tiles 8j + x (the per-tile kernel's XCD of the same
+// tile, so the XCD rectangles stay), its workgroups their first j statically and the rest from the
+// XCD's ticket counter misc[8 + x], drawn by wave 0 at the start of each epilogue.  An expert
+// of one chunk (two stages) is too short for the three-stage lookahead to stay within the next
+// tile: around its tiles the ring restarts.  The zero tiles of the experts without rows are
+// written first.  misc is written by chunk_prologue_kernel.
+template <bool P2 = false>
+__global__ __launch_bounds__(512, 2) void tgmm_fp8_p_kernel(TArgs p, int* misc) {
+  constexpr int WN = 4, WTM = 128, WTN = 64, TM = 4, TN = 2, LPS = 4;  // data loads per wave and stage
+  __shared__ __attribute__((aligned(1024))) char lds[TNST * TSTAGE];
+  __shared__ int s_ticket;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+  const int wm = wave / WN, wn = wave % WN;
+  const int nf = p.F / TBM, nn = p.N / TBN, per_e = nf * nn;
+  typedef const __attribute__((address_space(4))) int cint_t;
+  const int n_rows = __builtin_amdgcn_readfirstlane(*(const cint_t*)(uintptr_t)misc);
+  const int total = n_rows * per_e, all = p.E * per_e;
+  const int nx = (int)(gridDim.x >> 3), xcd = (int)(blockIdx.x & 7), q = (int)(blockIdx.x >> 3);
+
+  struct Tile {
+    int e, fb, nb, c0, nch;
+  };
+  // tile lid of tgmm_fp8_kernel's order (experts by descending size, xa x xb XCD rectangles); the
+  // read-only lists go through the scalar cache
+  auto decode = [&](int lid) -> Tile {
+    Tile T;
+    const int ei = lid / per_e, rem = lid - ei * per_e;
+    T.e = __builtin_amdgcn_readfirstlane(((const cint_t*)(uintptr_t)p.order)[ei]);
+    if (p.xa > 0) {
+      const int x = rem & 7, qq = rem >> 3, rh = nf / p.xa, rw = nn / p.xb;
+      T.fb = (x % p.xa) * rh + qq / rw;
+      T.nb = (x / p.xa) * rw + qq % rw;
+    } else {
+      T.fb = rem / nn;
+      T.nb = rem % nn;
+    }
+    const cint_t* cbp = (const cint_t*)(uintptr_t)p.cb;
+    T.c0 = __builtin_amdgcn_readfirstlane(cbp[T.e]);
+    T.nch = __builtin_amdgcn_readfirstlane(cbp[T.e + 1]) - T.c0;
+    return T;
+  };
+  struct Src {
+    uint32_t aoff[2], boff[2];
+    const uint8_t* A;
+    const uint8_t* B;
+    const float* sb;  // this wave's scale base (uniform) ...
+    uint32_t so;      // ... + this lane's byte offset: its scale for chunk 0 (one float per chunk after it)
+  };
+  // per-lane sources: lane l of segment s fills tile row 16s + l/4, chunk slot l%4; waves 0-3 load
+  // the XT-row scales of rows 64w + l, wave 4 the two GT-block scales, the others a filler
+  auto make_src = [&](const Tile& T) -> Src {
+    Src S;
+    const uint32_t lde = (uint32_t)T.nch * 128u;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int seg = wave * 2 + i;
+      const int r = seg * 16 + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
+      S.aoff[i] = (uint32_t)(T.fb * TBM + r) * lde + (uint32_t)(c * 16);
+      S.boff[i] = (uint32_t)(T.nb * TBN + r) * lde + (uint32_t)(c * 16);
+    }
+    S.A = p.xt + (int64_t)128 * p.F * T.c0;
+    S.B = p.gt + (int64_t)128 * p.N * T.c0;
+    if (wave_u < 4) {
+      S.sb = p.xts + (int64_t)p.F * T.c0;
+      S.so = (uint32_t)(T.fb * TBM + 64 * wave + lane) * (uint32_t)T.nch * 4u;
+    } else if (wave_u == 4) {
+      S.sb = p.gts + (int64_t)(p.N / 128) * T.c0;
+      S.so = (uint32_t)(T.nb * 2 + (lane & 1)) * (uint32_t)T.nch * 4u;
+    } else {
+      S.sb = p.xts + (int64_t)p.F * T.c0;
+      S.so = 0u;
+    }
+    return S;
+  };
+
+  Tile cur{}, nxt{};
+  Src scur{}, snxt{};
+  int nk_cur = 0, nk_nxt = 0;
+  const uint32_t lds_base = lds_addr(lds);
+  // issue ring step g = stage kt of the current tile, or stage kt - nk_cur of the next one
+  // (clamped to its last stage: stages past the end re-read it into a slot that is not read)
+  auto issue = [&](int g, int kt, bool even) {
+    const bool in = kt < nk_cur;
+    const int k = in ? kt : min(kt - nk_cur, nk_nxt - 1);
+    const uint32_t st = lds_base + (uint32_t)((g & (TNST - 1)) * TSTAGE);
+    const uint32_t kofs = (uint32_t)k * TBK;
+    const uint8_t* A = (in ? scur.A : snxt.A) + kofs;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) gload_lds16_s(A, in ? scur.aoff[i] : snxt.aoff[i], st + (wave_u * 2 + i) * 1024u);
+    const uint8_t* B = (in ? scur.B : snxt.B) + kofs;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      gload_lds16_s(B, in ? scur.boff[i] : snxt.boff[i], st + (uint32_t)TA_BYTES + (wave_u * 2 + i) * 1024u);
+    if (even) gload_lds4_s((in ? scur.sb : snxt.sb) + (k >> 1), in ? scur.so : snxt.so, st + (uint32_t)TS_OFF + wave_u * 256u);
+  };
+
+  const int frow = lane & 31, fhalf = lane >> 5;
+  auto ld32 = [&](const char* base, int r) -> i32x8 {
+    const u32x4 lo = *(const u32x4*)(base + t_off(r, 2 * fhalf));
+    const u32x4 hi = *(const u32x4*)(base + t_off(r, 2 * fhalf + 1));
+    return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  };
+  // rotating fragments (tgmm_fp8_kernel's schedule)
+  i32x8 fr_a[TM], fr_b[2][TN];
+  auto rd_a = [&](int g_, int i) -> i32x8 { return ld32(lds + (g_ & (TNST - 1)) * TSTAGE, wm * WTM + i * 32 + frow); };
+  auto rd_b = [&](int g_, int j) -> i32x8 {
+    return ld32(lds + (g_ & (TNST - 1)) * TSTAGE + TA_BYTES, wn * WTN + j * 32 + frow);
+  };
+  // scales of the chunk whose even stage sits in ring step g: the lane's four XT rows, the wave's GT block
+  float sa_c[TM], sa_n[TM], sb_c = 0.0f, sb_n = 0.0f;
+  auto read_scales = [&](int g, float* sa, float& sb) {
+    const float* sc = (const float*)(lds + (g & (TNST - 1)) * TSTAGE + TS_OFF);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) sa[i] = sc[wm * WTM + i * 32 + frow];
+    sb = sc[256 + (wn >> 1)];
+  };
+  // P2: the same scales as E8M0 codes (the lane's four XT-row codes one per byte, opsel i)
+  uint32_t ea_c = 0, ea_n = 0, eb_c = 0, eb_n = 0;
+  auto read_codes = [&](int g, uint32_t& ea, uint32_t& eb) {
+    const float* sc = (const float*)(lds + (g & (TNST - 1)) * TSTAGE + TS_OFF);
+    uint32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) s |= e8m0_of(sc[wm * WTM + i * 32 + frow]) << (8 * i);
+    ea = s;
+    eb = e8m0_of(sc[256 + (wn >> 1)]);
+  };
+  auto mfma_p2 = [&](const i32x8& b, const i32x8& a, const f32x16& c, int i) -> f32x16 {
+    switch (i) {
+      case 0: return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, (int)eb_c, 0, (int)ea_c);
+      case 1: return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, (int)eb_c, 1, (int)ea_c);
+      case 2: return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, (int)eb_c, 2, (int)ea_c);
+      default: return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, (int)eb_c, 3, (int)ea_c);
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  // one stage: MFMAs of ring step g_ on fr_a / fr_b[cb] with step g_+1's fragments read in
+  // between; at a chunk boundary (amax scales) each accumulator moves to the new chunk's units
+  // one slot ahead of its MFMA
+  auto rot_stage = [&](int g_, int cb, bool rescale, const float (&f)[TM]) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fr_b[cb ^ 1][j] = rd_b(g_ + 1, j);
+    auto rescale_acc = [&](int qq) {
+      const int i = qq / TN, j = qq % TN;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] *= f[i];
+    };
+    if (rescale) rescale_acc(0);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        if constexpr (P2)
+          acc[i][j] = mfma_p2(fr_b[cb][j], fr_a[i], acc[i][j], i);
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr_b[cb][j], fr_a[i], acc[i][j], 0, 0, 0, 127,
+                                                                      0, 127);
+        if (rescale && i * TN + j + 1 < TM * TN) rescale_acc(i * TN + j + 1);
+      }
+      fr_a[i] = rd_a(g_ + 1, i);
+    }
+  };
+  int g = 0;
+  // one chunk (an even and an odd stage); FIRST: the tile's first chunk (no rescale)
+  auto kchunk = [&](int kb, auto first_tag) {
+    constexpr bool FIRST = decltype(first_tag)::value;
+    const int kt = 2 * kb;
+    issue(g + TPD, kt + TPD, false);
+    float f[TM] = {};
+    if (FIRST) {
+      rot_stage(g, 0, false, f);
+    } else if (P2) {
+      ea_c = ea_n;
+      eb_c = eb_n;
+      rot_stage(g, 0, false, f);
+    } else {
+      // (sa_c / sa_n) * (sb_c / sb_n): no product of two small scales is formed
+      const float rb = sb_c * __builtin_amdgcn_rcpf(sb_n);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        f[i] = (sa_c[i] * __builtin_amdgcn_rcpf(sa_n[i])) * rb;
+        sa_c[i] = sa_n[i];
+      }
+      sb_c = sb_n;
+      rot_stage(g, 0, true, f);
+    }
+    // step g+2 landed (g+3 may be in flight); bare s_barrier (tgmm_fp8_kernel)
+    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS));
+    __builtin_amdgcn_s_barrier();
+    issue(g + 1 + TPD, kt + 1 + TPD, true);
+    if constexpr (P2) read_codes(g + 2, ea_n, eb_n);  // the next chunk's codes (or the next tile's)
+    else read_scales(g + 2, sa_n, sb_n);              // the next chunk's scales (or the next tile's)
+    rot_stage(g + 1, 1, false, f);
+    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));  // step g+3 landed (g+4 may be in flight)
+    __builtin_amdgcn_s_barrier();
+    g += 2;
+  };
+  // prologue of a ring that starts at tile cur: steps 0..2; 0 and 1 landed
+  auto prologue = [&]() {
+    g = 0;
+    issue(0, 0, true);
+    issue(1, 1, false);
+    issue(2, 2, true);
+    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + 1));
+    __syncthreads();
+    if constexpr (P2) read_codes(0, ea_c, eb_c);
+    else read_scales(0, sa_c, sb_c);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fr_a[i] = rd_a(0, i);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fr_b[0][j] = rd_b(0, j);
+  };
+  // epilogue: scale (amax), stage through ring slot `slot` (32 rows x 64 bf16 columns per wave at
+  // a time, 16-byte chunk c of row r at chunk c ^ (r & 7)) and store whole 128-byte row segments;
+  // before the staging writes, every wave's fragment reads have completed (an LDS-only release
+  // fence, then a barrier)
+  auto epilogue = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          acc[i][j][v] = P2 ? acc[i][j][v] : (acc[i][j][v] * sa_c[i]) * sb_c;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    char* wst = lds + slot * TSTAGE + wave * 4096;
+    uint16_t* out = p.dw + (int64_t)cur.e * p.F * p.N + (int64_t)cur.fb * TBM * p.N + cur.nb * TBN;
+    const uint32_t lo = (uint32_t)(wm * WTM + (lane >> 3)) * (uint32_t)p.N + (uint32_t)(wn * WTN + (lane & 7) * 8);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq)
+          *(bf16x4*)(wst + frow * 128 + (((4 * j + gq) ^ (frow & 7)) << 4) + 8 * fhalf) =
+              bf16x4{(__bf16)acc[i][j][4 * gq], (__bf16)acc[i][j][4 * gq + 1], (__bf16)acc[i][j][4 * gq + 2],
+                     (__bf16)acc[i][j][4 * gq + 3]};
+      __builtin_amdgcn_s_waitcnt(MTX_LGKMCNT0);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int rloc = rr * 8 + (lane >> 3);
+        const u32x4 v = *(const u32x4*)(wst + rloc * 128 + (((lane & 7) ^ (rloc & 7)) << 4));
+        *(u32x4*)(out + lo + (uint32_t)(i * 32 + rr * 8) * (uint32_t)p.N) = v;
+      }
+      __builtin_amdgcn_s_waitcnt(MTX_LGKMCNT0);  // reads done before the next block overwrites
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+  };
+
+  // ---- phase 1: experts of two or more chunks, the ring running across tiles ---------------------
+  // ---- the zero tiles of the experts without rows (no LDS) ---------------------------------------
+  for (int lid = total + (int)blockIdx.x; lid < all; lid += (int)gridDim.x) {
+    const Tile T = decode(lid);
+    uint16_t* out = p.dw + (int64_t)T.e * p.F * p.N + (int64_t)T.fb * TBM * p.N + T.nb * TBN;
+    for (int i = tid; i < TBM * TBN / 8; i += 512) {
+      const int r = i / (TBN / 8), cc = (i % (TBN / 8)) * 8;
+      *(u32x4*)(out + (int64_t)r * p.N + cc) = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  // ---- the tiles of the experts with rows ---------------------------------------------------------
+  // The ring runs on from cur into nxt (chain) when both have two or more chunks: the three-stage
+  // lookahead then stays within nxt.  Otherwise the lookahead re-reads cur's last stage into slots
+  // that are not read, and the ring restarts at nxt with a prologue once those loads have landed.
+  auto valid = [&](int jj) { return 8 * jj + xcd < total; };
+  int j = q;
+  if (valid(j)) {
+    // the first tile is static and runs without lookahead; its epilogue draws two tickets (the
+    // next tile and the one after), every later epilogue one (the tile after the next), so that a
+    // workgroup holds at most one tile beyond the current one
+    int j_next = -1;
+    cur = decode(8 * j + xcd);
+    scur = make_src(cur);
+    nk_cur = 2 * cur.nch;
+    snxt = scur;
+    nk_nxt = nk_cur;
+    bool chain = false;
+    auto set_lookahead = [&]() {
+      chain = valid(j_next) && cur.nch >= 2 && nxt.nch >= 2;
+      if (chain) {
+        snxt = make_src(nxt);
+        nk_nxt = 2 * nxt.nch;
+      } else {
+        snxt = scur;
+        nk_nxt = nk_cur;
+      }
+    };
+    prologue();
+    for (;;) {
+      kchunk(0, std::true_type());
+      for (int kb = 1; kb < cur.nch; ++kb) kchunk(kb, std::false_type());
+      int tk = 0;
+      if (wave_u == 0 && lane == 0)
+        tk = __hip_atomic_fetch_add(misc + 8 + xcd, j_next < 0 ? 2 : 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // steps g .. g+2 (the next tile's first stages, or re-reads) are in flight; slot g-1 is free
+      epilogue((g + TNST - 1) & (TNST - 1));
+      if (wave_u == 0 && lane == 0) s_ticket = tk;
+      __syncthreads();  // staging slot and s_ticket
+      const int t = s_ticket;  // rewritten only in the next epilogue
+      const bool first = j_next < 0;
+      if (first) j_next = nx + t;
+      const int j_after = first ? nx + t + 1 : nx + t;  // tickets rise, so j_next invalid => j_after too
+      j = j_next;
+      if (!valid(j)) break;
+      const bool chained = chain;
+      if (first) nxt = decode(8 * j + xcd);
+      cur = nxt;
+      nk_cur = 2 * cur.nch;
+      scur = chained ? snxt : make_src(cur);
+      j_next = j_after;
+      if (valid(j_next)) nxt = decode(8 * j_next + xcd);
+      set_lookahead();
+      if (chained) {
+        if constexpr (P2) {
+          ea_c = ea_n;
+          eb_c = eb_n;
+        } else {
+#pragma unroll
+          for (int i = 0; i < TM; ++i) sa_c[i] = sa_n[i];
+          sb_c = sb_n;
+        }
+      } else {
+        // every wave's re-reads have landed before the prologue refills the ring
+        __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));
+        __syncthreads();
+        prologue();
+      }
+    }
+    // the loads past the last tile land before the workgroup ends
+    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));
+    __syncthreads();
+  }
+}
+
 }  // namespace f8b
 
 static inline int64_t fp8_grouped_chunks(int64_t M, int64_t E) { return ceil_div(M, 128) + E; }
@@ -472,17 +829,20 @@ extern "C" int64_t mtx_fp8_grouped_chunks(int64_t M, int64_t E) {
 
 extern "C" int64_t mtx_fp8_grouped_workspace_size(int64_t E) {
   if (E < 1) return -1;
-  return round_up((3 * E + 2) * 4, 256);
+  return round_up((3 * E + 2 + 24) * 4, 256);
 }
 
-// workspace: cb [E+1], off [E+1], order [E] (ints)
+// workspace: cb [E+1], off [E+1], order [E], misc [24] (ints)
 static int grouped_prologue(const int32_t* gs, int64_t E, int64_t M, void* ws, hipStream_t st, int** cb, int** off,
-                            int** order) {
+                            int** order, int** misc = nullptr) {
   int* b = (int*)ws;
   *cb = b;
   *off = b + E + 1;
   *order = b + 2 * E + 2;
-  hipLaunchKernelGGL(f8b::chunk_prologue_kernel, dim3(1), dim3(1024), 0, st, gs, (int)E, (int)M, *cb, *off, *order);
+  int* m = b + 3 * E + 2;
+  if (misc) *misc = m;
+  hipLaunchKernelGGL(f8b::chunk_prologue_kernel, dim3(1), dim3(1024), 0, st, gs, (int)E, (int)M, *cb, *off, *order,
+                     m);
   return check_launch();
 }
 
@@ -540,8 +900,8 @@ static int tgmm_fp8_entry(bool p2, const uint8_t* xt, const float* xt_scale, con
   const int64_t C = fp8_grouped_chunks(M, E);
   if ((F > N ? F : N) * C * 128 >= (int64_t(1) << 32)) return MTX_ERR_UNSUPPORTED;  // 32-bit byte offsets
   hipStream_t st = (hipStream_t)stream;
-  int *cb, *off, *order;
-  int rc = grouped_prologue(group_sizes, E, M, workspace, st, &cb, &off, &order);
+  int *cb, *off, *order, *misc;
+  int rc = grouped_prologue(group_sizes, E, M, workspace, st, &cb, &off, &order, &misc);
   if (rc) return rc;
   f8b::TArgs a;
   a.xt = xt;
@@ -568,7 +928,21 @@ static int tgmm_fp8_entry(bool p2, const uint8_t* xt, const float* xt_scale, con
       a.xb = xb;
     }
   }
-  const int64_t grid = round_up(E * (F / 256) * (N / 256), 8);
+  const int64_t tiles = E * (F / 256) * (N / 256);
+#ifndef MTX_TGMM_PERSISTENT
+#define MTX_TGMM_PERSISTENT 1
+#endif
+  // one workgroup per CU (a multiple of the 8 XCDs); with fewer than 8 tiles per workgroup the
+  // tickets drawn a tile ahead leave the last tiles on few workgroups: the per-tile kernel then
+  const int ncu = device_cu_count();
+  const int64_t pgrid = ncu > 0 ? round_up(ncu, 8) : 256;
+  if (MTX_TGMM_PERSISTENT && tiles >= 8 * pgrid) {
+    const int64_t grid = pgrid;
+    if (p2) hipLaunchKernelGGL(f8b::tgmm_fp8_p_kernel<true>, dim3((unsigned)grid), dim3(512), 0, st, a, misc);
+    else hipLaunchKernelGGL(f8b::tgmm_fp8_p_kernel<false>, dim3((unsigned)grid), dim3(512), 0, st, a, misc);
+    return check_launch();
+  }
+  const int64_t grid = round_up(tiles, 8);
   if (p2) hipLaunchKernelGGL(f8b::tgmm_fp8_kernel<true>, dim3((unsigned)grid), dim3(512), 0, st, a);
   else hipLaunchKernelGGL(f8b::tgmm_fp8_kernel<false>, dim3((unsigned)grid), dim3(512), 0, st, a);
   return check_launch();

@@ -111,6 +111,41 @@ def test_tgmm_fp8(dev, M, F, N, E, scales):
     assert rel_err(got, ref) < 6e-2
 
 
+@pytest.mark.parametrize("scales", SCALES)
+def test_tgmm_fp8_persistent_matches_per_tile(dev, scales):
+    """2048 tiles (E=64, 1024 x 2048 per expert) take the persistent kernel, whose ring runs across
+    tiles and restarts around experts of one chunk: empty experts give zeros, the result is within
+    1e-2 of the dequantised oracle, and each checked expert's dW has the bits of the same expert
+    computed alone (a one-expert problem of few tiles, which takes the per-tile kernel)."""
+    from mintext_amd.kernels.fp8 import quantize_fp8_grouped_t, tgmm_fp8
+
+    E, F, N = 64, 1024, 2048
+    rng = np.random.default_rng(2048)
+    gs = _zipf_groups(rng, 9000, E, empty=(0, 5, 40))
+    gs[[7, 9, 11]] = [1, 128, 129]  # one chunk (two), two chunks
+    gs[3] += 3000                   # a long tile early in the order
+    M = int(gs.sum())
+    x = torch.randn(M, F, device=dev).bfloat16()
+    g = torch.randn(M, N, device=dev).bfloat16()
+    f8s = dict(scales=scales)
+    dw = tgmm_fp8(*quantize_fp8_grouped_t(x, _t(gs, dev), **f8s),
+                  *quantize_fp8_grouped_t(g, _t(gs, dev), blocks=True, **f8s), _t(gs, dev), M, **f8s)
+    got = dw.float().cpu().numpy()
+    for e in np.flatnonzero(gs == 0):
+        assert not got[e].any()
+    xt, xs = quantize_fp8_grouped_t(x, _t(gs, dev), **f8s)
+    gt, gsc = quantize_fp8_grouped_t(g, _t(gs, dev), blocks=True, **f8s)
+    ref_q = O.tgmm_fp8(_u8(xt), xs.cpu().numpy(), _u8(gt), gsc.cpu().numpy(), gs, M, F, N)
+    assert rel_err(got, ref_q) < 1e-2
+    off = np.concatenate([[0], np.cumsum(gs)])
+    for e in (3, 7, 9, 11, int(np.argmax(gs)), int(np.flatnonzero(gs)[-1])):
+        r0, r1 = int(off[e]), int(off[e + 1])
+        one = _t(np.array([r1 - r0], np.int32), dev)
+        alone = tgmm_fp8(*quantize_fp8_grouped_t(x[r0:r1], one, **f8s),
+                         *quantize_fp8_grouped_t(g[r0:r1], one, blocks=True, **f8s), one, r1 - r0, **f8s)
+        assert torch.equal(alone[0].view(torch.int16), dw[e].view(torch.int16)), f"expert {e}"
+
+
 @pytest.mark.timeout(600)
 @pytest.mark.parametrize("scales", SCALES)
 def test_fp8_backward_c5_full_size(dev, scales):
