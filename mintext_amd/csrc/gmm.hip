@@ -253,7 +253,12 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
     count[0] = s_total[1] + ntail;
     count[1] = s_total[1];  // tiles with an expert (the rest are zero tiles)
   }
-  // expert order by descending group size (ties: lower id first), used by tgmm
+  // expert order by descending group size (ties: lower id first), used by tgmm; count[2] = the
+  // experts with rows before M is applied (a prefix of that order)
+  if (need_order) {
+    const int nz = __syncthreads_count(e < E && g > 0);
+    if (e == 0) count[2] = nz;
+  }
   if (need_order && e < E) {
     // four sizes per LDS read; entries past E hold 0 and never rank ahead (o > g fails for
     // g >= 0, and o == g needs h < e < E)
@@ -1632,6 +1637,259 @@ __global__ __launch_bounds__(512, 2) void gmm_v4p_kernel(Args p) {
   __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));  // the last steps' re-read loads land before exit
 }
 
+// ---- tgmm_v4p: persistent tgmm (256x256 tiles) ----------------------------------------------------
+// The tiles, waves, ring, transposed DMA layouts, fragment reads, reduction-tail masking and MFMA
+// order of gmm_v3_kernel in TGMM mode (the same bits), with one workgroup per CU and the ring
+// running across tiles: the next tile's first three stages are loaded during the current tile's
+// last three, so a tile starts without the ring prologue.  Tiles come in the v3 order (experts by
+// descending group size, XCD x = tile % 8 with the xa x xb XCD rectangles); the count[2] experts
+// with rows (a prefix of that order) are computed here, XCD x's workgroups taking their first
+// tile statically and the rest from the XCD's ticket counter count[4 + x], drawn by wave 0 at the
+// start of each epilogue: the first epilogue draws two (the next tile and the one after), every
+// later one one, so that a workgroup holds at most one tile beyond the current one.  The ring
+// runs on into the next tile when both have three or more stages (the three-stage lookahead then
+// stays within it); otherwise the lookahead re-reads the current tile's last stage into slots that
+// are not read and the ring restarts.  The zero tiles of the other experts are written first.  A
+// tile's loads need no per-lane state beyond its uniform (r0, row0, col0): lane l of segment s
+// loads reduction row 2s + l/32 (clamped to M-1) at chunk slot l%32.
+__global__ __launch_bounds__(512, 2) void tgmm_v4p_kernel(Args p) {
+  using v3::BKS;
+  using v3::bn_off;
+  using Cf = v3::Cfg<256, 4>;
+  constexpr int BM = Cf::BM, BN = Cf::BN, NSTAGE = Cf::NSTAGE, PD = Cf::PD;
+  constexpr int A_BYTES = Cf::A_BYTES, STAGE = Cf::STAGE;
+  constexpr int WN = 4, WTM = 128, WTN = 64, TM = 4, TN = 2;
+  constexpr int A_INSTR = 2, B_INSTR = 2, LPS = A_INSTR + B_INSTR;
+  static_assert(A_BYTES == 16384 && Cf::B_BYTES == 16384 && NSTAGE == 4 && PD == 3, "tgmm_v4p ring");
+  __shared__ __attribute__((aligned(1024))) char lds[NSTAGE * STAGE];
+  __shared__ int s_ticket;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+  const int wm = wave / WN, wn = wave % WN;
+  const int nr = p.Kd / BM, nc = p.N / BN, per_e = nr * nc;
+  typedef const __attribute__((address_space(4))) int cint_t;
+  const int n_rows = __builtin_amdgcn_readfirstlane(((const cint_t*)(uintptr_t)p.count)[2]);
+  const int total = n_rows * per_e, all = p.E * per_e;
+  const int nx = (int)(gridDim.x >> 3), xcd = (int)(blockIdx.x & 7), q = (int)(blockIdx.x >> 3);
+
+  struct Tile {
+    int e, row0, col0, r0, nk, tail;
+  };
+  // tile lid of the v3 order; the read-only lists go through the scalar cache.  An expert whose
+  // rows were all dropped (past M) still has one stage, wholly masked: its tile stores zeros.
+  auto decode = [&](int lid) -> Tile {
+    Tile T;
+    const int ei = lid / per_e, rem = lid - ei * per_e;
+    T.e = __builtin_amdgcn_readfirstlane(((const cint_t*)(uintptr_t)p.order)[ei]);
+    int n_tile;
+    if (p.xa > 0) {
+      const int x = rem & 7, qq = rem >> 3, rh = nr / p.xa, rw = nc / p.xb;
+      T.row0 = ((x % p.xa) * rh + qq / rw) * BM;
+      n_tile = (x / p.xa) * rw + qq % rw;
+    } else {
+      T.row0 = (rem / nc) * BM;
+      n_tile = rem % nc;
+    }
+    T.col0 = n_tile * BN;
+    const cint_t* ofs = (const cint_t*)(uintptr_t)p.offsets;
+    T.r0 = __builtin_amdgcn_readfirstlane(ofs[T.e]);
+    const int rows = max(__builtin_amdgcn_readfirstlane(ofs[T.e + 1]) - T.r0, 0);
+    T.nk = max((rows + BKS - 1) / BKS, 1);
+    T.tail = rows - (T.nk - 1) * BKS;
+    return T;
+  };
+
+  // ---- the zero tiles of the experts without rows (no LDS) ---------------------------------------
+  for (int lid = total + (int)blockIdx.x; lid < all; lid += (int)gridDim.x) {
+    const Tile T = decode(lid);
+    uint16_t* out = p.C + (int64_t)T.e * p.Kd * p.N + (int64_t)T.row0 * p.N + T.col0;
+    for (int i = tid; i < BM * BN / 8; i += 512) {
+      const int r = i / (BN / 8), c = (i % (BN / 8)) * 8;
+      *(u32x4*)(out + (int64_t)r * p.N + c) = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
+  // per-lane load constants: reduction row kl[i] of segment wave*2+i, column offset cb[i] (bytes)
+  int kl[2];
+  uint32_t cb[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    kl[i] = (wave * 2 + i) * 2 + (lane >> 5);
+    cb[i] = (uint32_t)(((lane & 31) ^ ((kl[i] & 3) << 2)) * 16);
+  }
+  const uint32_t lds_base = lds_addr(lds);
+  const int mlast = p.M - 1;
+  const uint32_t lda = (uint32_t)p.Kd * 2u, ldb = (uint32_t)p.N * 2u;
+  Tile cur{}, nxt{}, la{};  // la: the tile the lookahead loads (nxt when the ring runs on, else cur)
+  // ring step g: stage kt counted from the current tile's start (past its end: the lookahead tile's
+  // stage, clamped to its last)
+  auto issue = [&](int g, int kt) {
+    const bool in = kt < cur.nk;
+    const int k = in ? kt : min(kt - cur.nk, la.nk - 1);
+    const int r0 = in ? cur.r0 : la.r0, row0 = in ? cur.row0 : la.row0, col0 = in ? cur.col0 : la.col0;
+    const uint32_t st = lds_base + (uint32_t)((g & (NSTAGE - 1)) * STAGE);
+    const int rb = r0 + k * BKS;
+#pragma unroll
+    for (int i = 0; i < A_INSTR; ++i) {
+      const uint32_t row = (uint32_t)min(rb + kl[i], mlast);
+      gload_lds16_s(p.A, row * lda + (uint32_t)row0 * 2u + cb[i], st + (wave_u * A_INSTR + i) * 1024u);
+    }
+#pragma unroll
+    for (int i = 0; i < B_INSTR; ++i) {
+      const uint32_t row = (uint32_t)min(rb + kl[i], mlast);
+      gload_lds16_s(p.B, row * ldb + (uint32_t)col0 * 2u + cb[i], st + (uint32_t)A_BYTES + (wave_u * B_INSTR + i) * 1024u);
+    }
+  };
+
+  // ---- fragments (the v3 TGMM reads, by ring step) ------------------------------------------------
+  bf16x8 fa[2][TM], fb[2][TN];
+  const int frow = lane & 31, fhalf = lane >> 5;
+  auto read_tr = [&](const char* region, int c0, int kk) -> bf16x8 {
+    const int n = c0 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const int k = kk * 16 + 8 * fhalf + ((lane & 15) >> 2);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(region + bn_off(k, n >> 3) + (n & 7) * 2));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(region + bn_off(k + 4, n >> 3) + (n & 7) * 2));
+    const s16x4 both[2] = {lo, hi};
+    return __builtin_bit_cast(bf16x8, both);
+  };
+  auto read_frags = [&](int g_, int kk, int buf) {
+    const char* st = lds + (g_ & (NSTAGE - 1)) * STAGE;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[buf][i] = read_tr(st, wm * WTM + i * 32, kk);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[buf][j] = read_tr(st + A_BYTES, wn * WTN + j * 32, kk);
+  };
+  // reduction tail: keep only the first `rem` rows of the tile's last stage (both operands)
+  auto mask_frags = [&](int buf, int kk, int rem) {
+    const int nv = min(max(rem - kk * 16 - 8 * fhalf, 0), 8);
+    u32x4 m;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) m[d] = (2 * d + 1 < nv) ? 0xFFFFFFFFu : ((2 * d < nv) ? 0xFFFFu : 0u);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[buf][i] = __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, fa[buf][i]) & m);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[buf][j] = __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, fb[buf][j]) & m);
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  int g = 0;
+  // ring prologue at the current tile: steps 0..PD-1 in flight, 0 and 1 landed and visible
+  auto prologue = [&]() {
+    g = 0;
+#pragma unroll
+    for (int s2 = 0; s2 < PD; ++s2) issue(s2, s2);
+    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
+    __syncthreads();
+    read_frags(0, 0, 0);
+  };
+
+  auto valid = [&](int jj) { return 8 * jj + xcd < total; };
+  int j = q;
+  if (valid(j)) {
+    int j_next = -1;
+    cur = decode(8 * j + xcd);
+    la = cur;
+    bool chain = false;
+    prologue();
+    for (;;) {
+      const int nk = cur.nk, tail = cur.tail;
+      for (int kt = 0; kt < nk; ++kt, ++g) {
+        issue(g + PD, kt + PD);
+        read_frags(g, 1, 1);
+        if (tail < BKS && kt == nk - 1) mask_frags(0, 0, tail);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int jj = 0; jj < TN; ++jj)
+            acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[0][jj], fa[0][i], acc[i][jj], 0, 0, 0);
+        // the next step's first fragments: the next stage of this tile, or of the next one
+        read_frags(g + 1, 0, 0);
+        if (tail < BKS && kt == nk - 1) mask_frags(1, 1, tail);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int jj = 0; jj < TN; ++jj)
+            acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[1][jj], fa[1][i], acc[i][jj], 0, 0, 0);
+        // step g+2 landed (g+3 may be in flight); bare barrier as in v3
+        __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
+        __builtin_amdgcn_s_barrier();
+      }
+      int tk = 0;
+      if (wave_u == 0 && lane == 0)
+        tk = __hip_atomic_fetch_add(const_cast<int*>(p.count) + 4 + xcd, j_next < 0 ? 2 : 1, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+      // ---- epilogue: the tile's last ring slot (step g-1) is consumed and is refilled only by the
+      // next step's load; every wave's fragment reads of it complete before the staging writes
+      // (LDS-only release fence, barrier).  acc[i][j][4q+c] of lane l is dW[row i*32 + l%32][col
+      // j*32 + 8q + 4(l/32) + c]; each wave stages 32 rows x 64 columns (16-byte chunk c of row r at
+      // chunk c ^ (r & 7)) and writes whole 128-byte row segments.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+      __builtin_amdgcn_s_barrier();
+      char* wst = lds + ((g - 1) & (NSTAGE - 1)) * STAGE + wave * 4096;
+      uint16_t* out = p.C + (int64_t)cur.e * p.Kd * p.N + (int64_t)cur.row0 * p.N + cur.col0;
+      const uint32_t lo = (uint32_t)(wm * WTM + (lane >> 3)) * (uint32_t)p.N + (uint32_t)(wn * WTN + (lane & 7) * 8);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int jj = 0; jj < TN; ++jj)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq)
+            *(bf16x4*)(wst + frow * 128 + (((4 * jj + gq) ^ (frow & 7)) << 4) + 8 * fhalf) =
+                bf16x4{(__bf16)acc[i][jj][4 * gq], (__bf16)acc[i][jj][4 * gq + 1], (__bf16)acc[i][jj][4 * gq + 2],
+                       (__bf16)acc[i][jj][4 * gq + 3]};
+        __builtin_amdgcn_s_waitcnt(MTX_LGKMCNT0);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int rloc = rr * 8 + (lane >> 3);
+          const u32x4 v = *(const u32x4*)(wst + rloc * 128 + (((lane & 7) ^ (rloc & 7)) << 4));
+          *(u32x4*)(out + lo + (uint32_t)(i * 32 + rr * 8) * (uint32_t)p.N) = v;
+        }
+        __builtin_amdgcn_s_waitcnt(MTX_LGKMCNT0);  // reads done before the next block overwrites
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int jj = 0; jj < TN; ++jj)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[i][jj][v] = 0.0f;
+      if (wave_u == 0 && lane == 0) s_ticket = tk;
+      __syncthreads();  // the staging slot and s_ticket
+      const int t = s_ticket;  // rewritten only in the next epilogue
+      const bool first = j_next < 0;
+      if (first) j_next = nx + t;
+      const int j_after = first ? nx + t + 1 : nx + t;  // tickets rise, so j_next invalid => j_after too
+      j = j_next;
+      if (!valid(j)) break;
+      const bool chained = chain;
+      if (first) nxt = decode(8 * j + xcd);
+      cur = nxt;
+      j_next = j_after;
+      if (valid(j_next)) nxt = decode(8 * j_next + xcd);
+      chain = valid(j_next) && cur.nk >= PD && nxt.nk >= PD;
+      la = chain ? nxt : cur;
+      if (!chained) {
+        // every wave's re-reads have landed before the prologue refills the ring
+        __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));
+        __syncthreads();
+        prologue();
+      }
+    }
+    // the loads past the last tile land before the workgroup ends
+    __builtin_amdgcn_s_waitcnt(MTX_VMCNT(0));
+    __syncthreads();
+  }
+}
+
 // ---- w4: one wave per SIMD (FWD / SWIGLU / DLHS, 256x256 tiles) ------------------------------------
 // The v3 tile, ring, DMA layouts, fragment reads and MFMA order with 4 waves instead of 8: a wave
 // owns a 128x128 quarter of the tile (16 accumulator blocks, which live in the AGPRs), so each
@@ -2427,6 +2685,9 @@ extern "C" int mtx_swiglu(const void* h, int dtype, int64_t M, int64_t I, void* 
   return launch_swiglu(h, dtype, M, I, out, (hipStream_t)stream);
 }
 
+#ifndef MTX_TGMM_V4P
+#define MTX_TGMM_V4P 1
+#endif
 extern "C" int mtx_tgmm(const void* x, const void* g, const int32_t* group_sizes, int dtype, int64_t M, int64_t K,
                         int64_t N, int64_t E, void* dw, void* workspace, int64_t workspace_bytes, void* stream) {
   if (dtype != MTX_F32 && dtype != MTX_BF16) return MTX_ERR_ARG;
@@ -2469,7 +2730,14 @@ extern "C" int mtx_tgmm(const void* x, const void* g, const int32_t* group_sizes
         a.xa = xa;
         a.xb = xb;
       }
-      return launch_v3<mf::TGMM, mf::EPI_STORE>(a, E * (K / 256) * (N / 256), st);
+      // with 8 or more tiles per CU: persistent workgroups, the ring running across tiles
+      const int64_t tiles = E * (K / 256) * (N / 256);
+      const int ncu4 = cus_per_xcd();
+      if (MTX_TGMM_V4P && ncu4 >= 1 && tiles >= (int64_t)8 * kSplitXcd * ncu4) {
+        hipLaunchKernelGGL(mf::tgmm_v4p_kernel, dim3((unsigned)(kSplitXcd * ncu4)), dim3(512), 0, st, a);
+        return check_launch();
+      }
+      return launch_v3<mf::TGMM, mf::EPI_STORE>(a, tiles, st);
     }
     if (K % 256 == 0 && N % 256 == 0) {
       const int64_t grid = round_up(E * (K / 256) * (N / 256), 8);
