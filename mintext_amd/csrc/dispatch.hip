@@ -838,38 +838,51 @@ __global__ __launch_bounds__(256) void unroute_bwd_vec_kernel(
     // two of the lane's chunks per pass (more loads in flight per lane: C4 268 -> 248 us); d_sorted
     // is written once, with non-temporal stores (C2 83 -> 61 us, C4 248 -> 245 us, C3 unchanged);
     // the expert rows are read once, with non-temporal loads when K > 2 (C3 217 -> 196 us, C4 245
-    // -> 222 us; C2 +1 %, so plain there; non-temporal dout loads gave nothing)
+    // -> 222 us; C2 +1 %, so plain there; non-temporal dout loads gave nothing).  Every row's loads
+    // of a pass are issued before its first store, from rows that are always in bounds (a skipped
+    // row reads the token's first kept row, unused), so that 2 KM loads per lane are in flight
+    // instead of two per row in turn.
+    int64_t jl[KM];
+    int64_t j0 = 0;
+#pragma unroll
+    for (int k = KM - 1; k >= 0; --k) j0 = j[k] >= 0 ? j[k] : j0;
+#pragma unroll
+    for (int k = 0; k < KM; ++k) jl[k] = j[k] >= 0 ? j[k] : j0;
     const GT* g_row = dout + n * D;
     constexpr int64_t step = 64 * 8 * WPT;
     for (int64_t c = ((int64_t)part * 64 + lane) * 8; c < D; c += 2 * step) {
       const bool two = c + step < D;  // the lane's last pass may hold one chunk
+      const int64_t c2 = two ? c + step : c;  // (one chunk: the second loads re-read the first)
       float g[8], g2[8];
       ld8(g_row, c, g);
-      if (two) ld8(g_row, c + step, g2);
+      ld8(g_row, c2, g2);
+      float y[KM][8], y2[KM][8];
 #pragma unroll
       for (int k = 0; k < KM; ++k) {
-        if (j[k] < 0) continue;
-        float y[8], y2[8], o[8];
         if constexpr (KM > 2) {
-          ld8_nt(Y + j[k] * D, c, y);
-          if (two) ld8_nt(Y + j[k] * D, c + step, y2);
+          ld8_nt(Y + jl[k] * D, c, y[k]);
+          ld8_nt(Y + jl[k] * D, c2, y2[k]);
         } else {
-          ld8(Y + j[k] * D, c, y);
-          if (two) ld8(Y + j[k] * D, c + step, y2);
+          ld8(Y + jl[k] * D, c, y[k]);
+          ld8(Y + jl[k] * D, c2, y2[k]);
         }
+      }
+#pragma unroll
+      for (int k = 0; k < KM; ++k) {
+        float o[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-          dot[k] = fmaf(g[q], y[q], dot[k]);
+          dot[k] = fmaf(g[q], y[k][q], dot[k]);
           o[q] = wk[k] * g[q];
         }
-        st8_nt(dY + j[k] * D, c, o);
+        if (j[k] >= 0) st8_nt(dY + j[k] * D, c, o);
         if (two) {
 #pragma unroll
           for (int q = 0; q < 8; ++q) {
-            dot[k] = fmaf(g2[q], y2[q], dot[k]);
+            dot[k] = fmaf(g2[q], y2[k][q], dot[k]);
             o[q] = wk[k] * g2[q];
           }
-          st8_nt(dY + j[k] * D, c + step, o);
+          if (j[k] >= 0) st8_nt(dY + j[k] * D, c2, o);
         }
       }
     }
