@@ -89,3 +89,52 @@ def test_gmm_fp8_sweep(dev, case, scales):
         assert (yb[M:] == 0).all() and (_u8(yq)[M:] == 0).all()
         d = O.dequant_rows(_u8(yq), ys.cpu().numpy())
         assert rel_err(d[:M], ref[:M]) < 6e-2
+
+
+def _cases_tgmm(n=4, seed=8080):
+    """fp8 tgmm shapes of 2048 or more 256x256 tiles (the persistent kernel's range on a 256-CU
+    part): experts of 0, 1-128 and thousands of rows, and group sizes summing past M."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        E = int(rng.choice([64, 128]))
+        F = int(rng.choice([768, 1024, 2048]))
+        N = int(rng.choice([1024, 1536, 2048]))
+        while E * (F // 256) * (N // 256) < 2048:
+            N += 512
+        out.append((i, E, F, N, i % 2 == 1))
+    return out
+
+
+@pytest.mark.parametrize("scales", ["amax", "pow2"])
+@pytest.mark.parametrize("case", _cases_tgmm(), ids=lambda c: f"t{c[0]}-E{c[1]}-F{c[2]}-N{c[3]}-past{int(c[4])}")
+def test_tgmm_fp8_sweep_persistent_every_expert_bits(dev, case, scales):
+    """Every expert's dW from the persistent fp8 tgmm has the bits of the same expert quantised and
+    computed alone (a one-expert problem of few tiles, on the per-tile kernel); empty experts,
+    and experts whose rows all lie past M, are zero."""
+    from mintext_amd.kernels.fp8 import quantize_fp8_grouped_t, tgmm_fp8
+
+    i, E, F, N, past = case
+    rng = np.random.default_rng(600 + i)
+    gs = rng.integers(0, 700, E).astype(np.int32)
+    gs[rng.choice(E, E // 8, replace=False)] = 0
+    small = rng.choice(np.flatnonzero(gs), 6, replace=False)
+    gs[small] = rng.integers(1, 129, 6)
+    gs[int(rng.integers(0, E))] = int(rng.integers(3000, 9000))
+    M = int(gs.sum()) - (int(gs.sum()) // 10 if past else 0)
+    x = torch.randn(M, F, device=dev).bfloat16()
+    g = torch.randn(M, N, device=dev).bfloat16()
+    tg = torch.from_numpy(gs).to(dev)
+    f8s = dict(scales=scales)
+    dw = tgmm_fp8(*quantize_fp8_grouped_t(x, tg, **f8s), *quantize_fp8_grouped_t(g, tg, blocks=True, **f8s), tg, M,
+                  **f8s)
+    off = np.minimum(np.concatenate([[0], np.cumsum(gs)]), M)
+    for e in range(E):
+        r0, r1 = int(off[e]), int(off[e + 1])
+        if r1 == r0:
+            assert not dw[e].any(), f"expert {e}"
+            continue
+        one = torch.tensor([r1 - r0], dtype=torch.int32, device=dev)
+        alone = tgmm_fp8(*quantize_fp8_grouped_t(x[r0:r1], one, **f8s),
+                         *quantize_fp8_grouped_t(g[r0:r1], one, blocks=True, **f8s), one, r1 - r0, **f8s)
+        assert torch.equal(alone[0].view(torch.int16), dw[e].view(torch.int16)), f"expert {e}"

@@ -141,3 +141,46 @@ def test_gmm_sweep_large_groups(dev, case):
         d = (out.float() - out128.float()).abs()
         bound = out128.float().abs() * 2.0 ** -7 + 1e-5 * float(np.abs(ref).max())
         assert bool((d <= bound).all()), (d - bound).max().item()
+
+
+def _cases_tgmm(n=6, seed=9090):
+    """tgmm shapes of 2048 or more 256x256 tiles (the persistent kernel's range on a 256-CU part):
+    experts of 0, 1-95 and thousands of rows, and group sizes summing past M."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        E = int(rng.choice([64, 96, 128]))
+        K = int(rng.choice([768, 1024, 2048]))
+        N = int(rng.choice([1024, 1536, 2048]))
+        while E * (K // 256) * (N // 256) < 2048:
+            N += 512
+        past = i % 3 == 2
+        out.append((i, E, K, N, past))
+    return out
+
+
+@pytest.mark.parametrize("case", _cases_tgmm(), ids=lambda c: f"t{c[0]}-E{c[1]}-K{c[2]}-N{c[3]}-past{int(c[4])}")
+def test_tgmm_sweep_persistent_every_expert_bits(dev, case):
+    """Every expert's dW from the persistent tgmm has the bits of the same expert computed alone
+    (a one-expert problem of few tiles, on the per-tile kernel); empty experts are zero."""
+    from mintext_amd.kernels import tgmm
+
+    i, E, K, N, past = case
+    rng = np.random.default_rng(500 + i)
+    gs = rng.integers(0, 600, E).astype(np.int32)
+    gs[rng.choice(E, E // 8, replace=False)] = 0
+    small = rng.choice(np.flatnonzero(gs), 6, replace=False)
+    gs[small] = rng.integers(1, 96, 6)
+    gs[int(rng.integers(0, E))] = int(rng.integers(3000, 9000))
+    M = int(gs.sum()) - (int(gs.sum()) // 10 if past else 0)
+    x = torch.randn(M, K, device=dev).bfloat16()
+    g = torch.randn(M, N, device=dev).bfloat16()
+    out = tgmm(x, g, torch.from_numpy(gs).to(dev))
+    off = np.minimum(np.concatenate([[0], np.cumsum(gs)]), M)
+    for e in range(E):
+        r0, r1 = int(off[e]), int(off[e + 1])
+        if r1 == r0:
+            assert not out[e].any(), f"expert {e}"
+            continue
+        alone = tgmm(x[r0:r1], g[r0:r1], torch.tensor([r1 - r0], dtype=torch.int32, device=dev))
+        assert torch.equal(alone[0].view(torch.int16), out[e].view(torch.int16)), f"expert {e}"
