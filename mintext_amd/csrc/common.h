@@ -223,6 +223,16 @@ __device__ __forceinline__ void st8(uint16_t* p, int64_t i, const float v[8]) {
   for (int q = 0; q < 4; ++q) a[q] = pack_bf16x2(v[2 * q], v[2 * q + 1]);
   *(v4u32*)(p + i) = a;
 }
+// A relaxed agent-scope fetch-add issued by one lane whose result is first needed much later (a
+// persistent kernel's tile ticket, read at the end of the epilogue).  The address goes through a
+// VGPR so that the compiler does not rewrite it into a wave-level atomic, whose result it reads
+// back at once behind a full vmcnt wait -- that wait would also drain the next tile's ring loads.
+__device__ __forceinline__ int lane_fetch_add(int* p, int v) {
+  typedef __attribute__((address_space(1))) int gint;  // a global atomic, not a flat one
+  uintptr_t a = (uintptr_t)p;
+  asm volatile("" : "+v"(a));
+  return __hip_atomic_fetch_add((gint*)a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 // Non-temporal loads (data read once: streamed past the caches), same conversions as ld8.
 __device__ __forceinline__ void ld8_nt(const float* p, int64_t i, float v[8]) {
   const v4u32 a = __builtin_nontemporal_load((const v4u32*)(p + i));

@@ -743,7 +743,7 @@ __global__ __launch_bounds__(512, 2) void tgmm_fp8_p_kernel(TArgs p, int* misc) 
       for (int kb = 1; kb < cur.nch; ++kb) kchunk(kb, std::false_type());
       int tk = 0;
       if (wave_u == 0 && lane == 0)
-        tk = __hip_atomic_fetch_add(misc + 8 + xcd, j_next < 0 ? 2 : 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        tk = lane_fetch_add(misc + 8 + xcd, j_next < 0 ? 2 : 1);
       // steps g .. g+2 (the next tile's first stages, or re-reads) are in flight; slot g-1 is free
       epilogue((g + TNST - 1) & (TNST - 1));
       if (wave_u == 0 && lane == 0) s_ticket = tk;

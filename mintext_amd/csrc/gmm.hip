@@ -1826,8 +1826,7 @@ __global__ __launch_bounds__(512, 2) void tgmm_v4p_kernel(Args p) {
       }
       int tk = 0;
       if (wave_u == 0 && lane == 0)
-        tk = __hip_atomic_fetch_add(const_cast<int*>(p.count) + 4 + xcd, j_next < 0 ? 2 : 1, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
+        tk = lane_fetch_add(const_cast<int*>(p.count) + 4 + xcd, j_next < 0 ? 2 : 1);
       // ---- epilogue: the tile's last ring slot (step g-1) is consumed and is refilled only by the
       // next step's load; every wave's fragment reads of it complete before the staging writes
       // (LDS-only release fence, barrier).  acc[i][j][4q+c] of lane l is dW[row i*32 + l%32][col
