@@ -776,7 +776,12 @@ constexpr int BM = 256, BN = 256, BKB = 64, NSTAGE = 4, PD = 3;
 constexpr int A_BYTES = BM * BKB, B_BYTES = BN * BKB;
 constexpr int S_OFF = A_BYTES + B_BYTES;  // per slot: [0,1K) x-row scales, [1K,1K+8) weight scales
 constexpr int STAGE = S_OFF + 2048;
-constexpr int GM = 8;
+// m-tiles per scheduling group (consecutive tiles sweep GM m-tiles, then n): 2 for the SwiGLU
+// tiles, 8 for the plain-store ones (C4 gate_up with 2 against 8: pow2 -1.5 to -3.3 %, amax -1 to
+// +0.2 % over four runs on two boxes; the store tiles -- C4 down, the C5 dlhs -- lose 1.5-3 % with
+// 2 or 4)
+template <int EPI>
+constexpr int gm_of() { return EPI == EPI_SWIGLU_Q ? 2 : 8; }
 struct Tile {
   int e, r0, r1, n_tile, zero;
 };
@@ -806,6 +811,7 @@ __global__ __launch_bounds__(512, 2) void gmm_fp8_v4_kernel(Args p) {
   const int nkb = p.K / 128, nk = p.K / BKB;
 
   auto decode = [&](int l) -> Tile {
+    constexpr int GM = gm_of<EPI>();
     const int grp = l / (GM * nn);
     const int first_m = grp * GM;
     const int gsz = min(GM, cnt - first_m);
