@@ -2046,10 +2046,11 @@ __device__ __forceinline__ void tile(const Args& p, char* lds, int* s_last, cons
     }
   };
 
-  // prologue: stages 0..PD-1 in flight, stages 0 and 1 landed and visible
+  // prologue: stages 0..PD-1 in flight, stage 0 landed and visible (stage 1, first read halfway
+  // through stage 0, is waited for there)
 #pragma unroll
   for (int s = 0; s < PD; ++s) issue_stage(s);
-  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 2)));
+  __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS * (PD - 1)));
   __syncthreads();
   read_frags(0, 0, 0);
   // Each stage is 2 x S MFMA slots in a fixed order: slot q issues one MFMA, then one fragment read
@@ -2063,6 +2064,13 @@ __device__ __forceinline__ void tile(const Args& p, char* lds, int* s_last, cons
     for (int q = 0; q < 2 * S; ++q) {
       const int sub = q / S, qq = q % S;
       const int i = qq / TN, j = qq % TN;
+      if (q == S && kt == 0) {
+        // stage 1 landed (stage 2 and the first LPS/2 loads of stage 3 may be in flight) and
+        // visible before its first fragment reads below
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(MTX_VMCNT(LPS + LPS / 2));
+        __builtin_amdgcn_s_barrier();
+      }
       __builtin_amdgcn_sched_barrier(0);
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[sub][j], fa[sub][i], acc[i][j], 0, 0, 0);
       // fragment r goes in slot min(r, S-1): a substep with fewer MFMAs than fragments (TM = 1)
