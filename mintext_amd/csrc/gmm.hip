@@ -84,7 +84,7 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
                                                            int* __restrict__ count, int* __restrict__ offsets,
                                                            int* __restrict__ order, MTile* __restrict__ tiles,
                                                            int need_order, int* __restrict__ split_cnt, int spread,
-                                                           int align) {
+                                                           int align, int merge) {
   __shared__ int wsum[16];
   __shared__ long long wsum64[16];
   if (split_cnt && threadIdx.x < kSplitXcd * kSplitMaxRem) split_cnt[threadIdx.x] = 0;
@@ -147,8 +147,16 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
   // m-tiles come first, in expert order, so that every group of G consecutive m-tiles belongs to one
   // expert (its tiles share each weight strip), and the experts' remaining nt_e % G m-tiles follow at
   // the end of the list, in expert order.  s_bstart / s_sstart hold the two sections' starts.
+  // merge > 0: an expert with at least one full group and at most `merge` m-tiles past its last
+  // group keeps them in that group (a group of G + r), so that they read the expert's weight
+  // strips from L2 beside their siblings instead of streaming them again from HBM at the end of
+  // the list; every tile then records its group (MTile::pad = first m-tile << 8 | size).
+  auto aligned_count = [&](int n) -> int {
+    const int a = (n / align) * align;
+    return (merge > 0 && a > 0 && n - a <= merge) ? n : a;
+  };
   if (align > 1) {
-    const int na = (e < E) ? (nt / align) * align : 0;
+    const int na = (e < E) ? aligned_count(nt) : 0;
     const int nr = (e < E) ? nt - na : 0;
     int ai = na, ri = nr;
     for (int off = 1; off < 64; off <<= 1) {
@@ -205,6 +213,14 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
   __syncthreads();
   const int ntiles = s_total[1];
   const int nbig_total = (spread > 0) ? s_nbig[0] : 0;
+  const int used = min(s_total[0], M);
+  const int ntail = (M - used + BM - 1) / BM;
+  // group record of list position j past the aligned section: fixed groups of `align` from its end
+  auto tail_group = [&](int j) -> int {
+    const int na_total = s_nbig[0];
+    const int first = na_total + ((j - na_total) / align) * align;
+    return (first << 8) | min(align, ntiles + ntail - first);
+  };
   for (int j = e; j < ntiles; j += blockDim.x) {
     // position j -> list (start array) and index in it
     const int* starts = s_tstart;
@@ -229,24 +245,31 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
       if (starts[mid] <= idx) lo = mid;
       else hi = mid - 1;
     }
-    if (align > 1 && j >= s_nbig[0]) first = ((s_r1[lo] - s_r0[lo] + BM - 1) / BM / align) * align;
+    const int na_lo = (align > 1) ? aligned_count((s_r1[lo] - s_r0[lo] + BM - 1) / BM) : 0;
+    if (align > 1 && j >= s_nbig[0]) first = na_lo;
     const int i = first + idx - starts[lo];
     MTile t;
     t.e = lo;
     t.r0 = s_r0[lo] + i * BM;
     t.r1 = min(s_r0[lo] + (i + 1) * BM, s_r1[lo]);
     t.pad = 0;
+    if (align > 1 && merge > 0) {
+      if (j < s_nbig[0]) {  // aligned section: the expert's last group takes its merged tiles
+        const int ng = na_lo / align, gi = min(i / align, ng - 1);
+        t.pad = ((s_bstart[lo] + gi * align) << 8) | (gi == ng - 1 ? na_lo - gi * align : align);
+      } else {
+        t.pad = tail_group(j);
+      }
+    }
     tiles[j] = t;
   }
   // zero tiles for rows past sum(group_sizes)
-  const int used = min(s_total[0], M);
-  const int ntail = (M - used + BM - 1) / BM;
   for (int z = e; z < ntail; z += blockDim.x) {  // may exceed the block when many rows are unused
     MTile t;
     t.e = -1;
     t.r0 = used + z * BM;
     t.r1 = min(used + (z + 1) * BM, M);
-    t.pad = 0;
+    t.pad = (align > 1 && merge > 0) ? tail_group(ntiles + z) : 0;
     tiles[s_total[1] + z] = t;
   }
   if (e == 0) {
@@ -617,6 +640,9 @@ struct Args {
   int xa = 0, xb = 0;
   // gmm_w4_kernel: per-XCD tile queue tickets (8 ints, zero at launch); nullptr: static ranges
   int* tickets = nullptr;
+  // gmm_w4_kernel: 1 = scheduling groups of varying size, each tile's group read from the tile
+  // list (MTile::pad = first m-tile << 8 | m-tiles in the group); 0 = fixed groups of gm
+  int vgroup = 0;
 };
 
 // ---- tile loaders ------------------------------------------------------------------------------
@@ -2267,11 +2293,16 @@ __global__ __launch_bounds__(256, 1) void gmm_w4_kernel(Args p) {
     t.npieces = S;
     lid = qx * per + nwhole + t.split_u;
   }
-  const int GM = p.gm;
-  const int grp = lid / (GM * nn);
-  const int first_m = grp * GM;
-  const int gsz = min(GM, cnt - first_m);
-  const int local = lid - grp * GM * nn;
+  int first_m, gsz;
+  if (p.vgroup) {  // position lid / nn lies inside lid's group
+    const int g = p.tiles[lid / nn].pad;
+    first_m = g >> 8;
+    gsz = g & 255;
+  } else {
+    first_m = (lid / (p.gm * nn)) * p.gm;
+    gsz = min(p.gm, cnt - first_m);
+  }
+  const int local = lid - first_m * nn;
   const MTile mt = p.tiles[first_m + local % gsz];
   t.e = mt.e;
   t.r0 = mt.r0;
@@ -2303,9 +2334,10 @@ struct MfmaCfg {
 };
 
 static int launch_build_tiles(const int32_t* gs, int64_t E, int64_t M, int BM, const GmmWs& w, hipStream_t st,
-                              bool need_order = false, bool reset_split = false, int spread = 0, int align = 0) {
+                              bool need_order = false, bool reset_split = false, int spread = 0, int align = 0,
+                              int merge = 0) {
   hipLaunchKernelGGL(build_tiles_kernel, dim3(1), dim3(1024), 0, st, gs, (int)E, (int)M, BM, w.count, w.offsets,
-                     w.order, w.tiles, need_order ? 1 : 0, reset_split ? w.split_cnt : (int*)nullptr, spread, align);
+                     w.order, w.tiles, need_order ? 1 : 0, reset_split ? w.split_cnt : (int*)nullptr, spread, align, merge);
   return check_launch();
 }
 
@@ -2385,6 +2417,10 @@ static int launch_v4p(const mf::Args& a, int64_t max_tiles, int ncu, hipStream_t
 // a wave pair's empty row blocks), hence the threshold.
 #ifndef MTX_W4
 #define MTX_W4 7
+#endif
+// m-tiles past an expert's last full scheduling group that stay in that group (gmm_w4_kernel)
+#ifndef MTX_MERGE_REM
+#define MTX_MERGE_REM 2
 #endif
 // 1: scheduling groups of the 256-row paths hold the m-tiles of one expert (build_tiles_kernel)
 #ifndef MTX_ALIGN_GROUPS
@@ -2501,11 +2537,18 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
     // group: C2 -1 %; with Zipf loads, whose remainders then collect at the end of the list from
     // many experts, C5 dlhs ran 1-3 % slower): see build_tiles_kernel
     const int align = (MTX_ALIGN_GROUPS && a.gm > 1 && (M / E) >= 256 * a.gm) ? a.gm : 0;
+    // gmm_w4_kernel SwiGLU: an expert's few m-tiles past its last full group join that group, so
+    // that they read its weight strips from L2 beside their siblings (C2 gate_up -0.6 %, three
+    // runs each; the plain-store tiles measured +0.5 % on C2 down: there the thin remainders at
+    // the end of the list fill the last round's gaps)
+    const int merge = (align > 0 && align + MTX_MERGE_REM <= 255 && M / 256 + E < (1 << 22)) ? MTX_MERGE_REM : 0;
     if (mode == 2 && I % 128 == 0) {
       if (big_m) {
-        rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, false, spread, align);
+        const bool use_w4 = (MTX_W4 & 1) && w4;
+        a.vgroup = (use_w4 && merge > 0) ? 1 : 0;
+        rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, false, spread, align, a.vgroup ? merge : 0);
         if (rc) return rc;
-        if ((MTX_W4 & 1) && w4) return launch_w4<mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 256) * (I / 128), st);
+        if (use_w4) return launch_w4<mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 256) * (I / 128), st);
         return launch_v3<mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 256) * (I / 128), st);
       }
       rc = launch_build_tiles(gs, E, M, 128, wsp, st);
@@ -2534,12 +2577,13 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
           a.split_part = wsp.split_part;
           a.ncu_x = ncu;
         }
+        const bool use_w4 = ((mode == 0 && (MTX_W4 & 2)) || (mode == 1 && (MTX_W4 & 4))) && w4;
         rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, split, spread, align);
         if (rc) return rc;
         // split pieces add at most ncu - rem < ncu workgroups per XCD
         const int64_t grid = round_up(gmm_max_tiles(M, E, 256) * (Nout / 256), 8) + (split ? 8 * (int64_t)ncu : 0);
-        if (mode == 0 && (MTX_W4 & 2) && w4) return launch_w4<mf::FWD, mf::EPI_STORE>(a, grid, st);
-        if (mode == 1 && (MTX_W4 & 4) && w4) return launch_w4<mf::DLHS, mf::EPI_STORE>(a, grid, st);
+        if (use_w4) return mode == 0 ? launch_w4<mf::FWD, mf::EPI_STORE>(a, grid, st)
+                                     : launch_w4<mf::DLHS, mf::EPI_STORE>(a, grid, st);
         return mode == 0 ? launch_v3<mf::FWD, mf::EPI_STORE>(a, grid, st) : launch_v3<mf::DLHS, mf::EPI_STORE>(a, grid, st);
       }
       rc = launch_build_tiles(gs, E, M, 128, wsp, st);

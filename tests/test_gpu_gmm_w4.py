@@ -1,10 +1,10 @@
 """GPU parity of the one-wave-per-SIMD grouped GEMM (the 256-row tile path for groups that average
 at least 512 rows): every tile form it has -- whole 256-row tiles, partial tiles of 129-255 rows
 (full form, rows past the group masked), thin tiles of 1-128 rows (1-4 row blocks), split-tail
-pieces and zero tiles for rows past the groups -- for the plain forward, the fused SwiGLU, dlhs
-and the gathered gate_up.  With whole tiles each element is the MFMA sequence of the other bf16
-kernels, so the results equal the 128-row tiling bit for bit; all are checked against the
-float64 oracle at the bf16 bound (2e-2)."""
+pieces, zero tiles for rows past the groups and (SwiGLU) scheduling groups of 8-10 m-tiles -- for
+the plain forward, the fused SwiGLU, dlhs and the gathered gate_up.  With whole tiles each
+element is the MFMA sequence of the other bf16 kernels, so the results equal the 128-row tiling
+bit for bit; all are checked against the float64 oracle at the bf16 bound (2e-2)."""
 from __future__ import annotations
 
 import numpy as np
@@ -24,6 +24,9 @@ GROUPS = [
     [769, 808, 838, 868, 896],
     [897, 1024, 1000, 1279, 0, 1025, 768 + 255],
     [2048 + 14, 2048 + 77, 1984, 2125, 2019, 2058, 2063, 2048],
+    # mean >= 8 x 256 (scheduling groups aligned to experts): one or two m-tiles past a group of
+    # 8 stay in it (groups of 9 and 10), three go to the end of the list
+    [2048 + 300, 2048 + 600, 2048 + 513, 1800, 2500, 2048, 2048 + 256],
 ]
 
 
