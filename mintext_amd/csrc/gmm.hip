@@ -643,6 +643,9 @@ struct Args {
   // gmm_w4_kernel: 1 = scheduling groups of varying size, each tile's group read from the tile
   // list (MTile::pad = first m-tile << 8 | m-tiles in the group); 0 = fixed groups of gm
   int vgroup = 0;
+  // gmm_w4_kernel: 1 = XCD x owns n-tiles [x*nn/8, (x+1)*nn/8) of every m-tile (nn % 8 == 0), so
+  // that the eight XCDs sweep the experts together and read each A tile from HBM about once
+  int nsplit = 0;
 };
 
 // ---- tile loaders ------------------------------------------------------------------------------
@@ -2293,21 +2296,27 @@ __global__ __launch_bounds__(256, 1) void gmm_w4_kernel(Args p) {
     t.npieces = S;
     lid = qx * per + nwhole + t.split_u;
   }
-  int first_m, gsz;
-  if (p.vgroup) {  // position lid / nn lies inside lid's group
-    const int g = p.tiles[lid / nn].pad;
+  int first_m, gsz, n_first = 0, nspan = nn, l = lid;
+  if (p.nsplit) {  // queue x: n-tiles [x*nb, (x+1)*nb) of every m-tile, per = cnt * nb
+    const int nb = nn >> 3, x = lid / per;
+    l = lid - x * per;
+    n_first = x * nb;
+    nspan = nb;
+  }
+  if (p.vgroup) {  // position l / nspan lies inside l's group
+    const int g = p.tiles[l / nspan].pad;
     first_m = g >> 8;
     gsz = g & 255;
   } else {
-    first_m = (lid / (p.gm * nn)) * p.gm;
+    first_m = (l / (p.gm * nspan)) * p.gm;
     gsz = min(p.gm, cnt - first_m);
   }
-  const int local = lid - first_m * nn;
+  const int local = l - first_m * nspan;
   const MTile mt = p.tiles[first_m + local % gsz];
   t.e = mt.e;
   t.r0 = mt.r0;
   t.r1 = mt.r1;
-  t.n_tile = local / gsz;
+  t.n_tile = n_first + local / gsz;
   if (t.e < 0) {  // rows past sum(group_sizes): zeros
     if (t.piece > 0) return;
     const int ncols = (EPI == EPI_SWIGLU) ? BN / 2 : BN;
@@ -2417,6 +2426,15 @@ static int launch_v4p(const mf::Args& a, int64_t max_tiles, int ncu, hipStream_t
 // a wave pair's empty row blocks), hence the threshold.
 #ifndef MTX_W4
 #define MTX_W4 7
+#endif
+// gmm_w4_kernel: n-tiles split over the XCDs (bit 0 plain-store forward, bit 1 SwiGLU).  The eight
+// XCDs then sweep the experts together, each over its eighth of the n-tiles, so an expert's A rows
+// are fetched from HBM about once and re-read from the MALL, instead of once per group of n-tiles
+// that an XCD sweeps: C2 down 1.73 -> 1.64 ms (three runs each).  The SwiGLU tiles (whose A, the
+// token rows, fits the MALL anyway) measured equal, the C5 dlhs +2 % (Zipf loads), so those keep
+// the contiguous XCD ranges.
+#ifndef MTX_NSPLIT
+#define MTX_NSPLIT 1
 #endif
 // m-tiles past an expert's last full scheduling group that stay in that group (gmm_w4_kernel)
 #ifndef MTX_MERGE_REM
@@ -2546,6 +2564,7 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
       if (big_m) {
         const bool use_w4 = (MTX_W4 & 1) && w4;
         a.vgroup = (use_w4 && merge > 0) ? 1 : 0;
+        a.nsplit = ((MTX_NSPLIT & 2) && use_w4 && (I / 128) % 8 == 0) ? 1 : 0;
         rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, false, spread, align, a.vgroup ? merge : 0);
         if (rc) return rc;
         if (use_w4) return launch_w4<mf::FWD, mf::EPI_SWIGLU>(a, gmm_max_tiles(M, E, 256) * (I / 128), st);
@@ -2578,6 +2597,7 @@ static int gmm_driver(int mode, const void* x, const void* w, const int32_t* gs,
           a.ncu_x = ncu;
         }
         const bool use_w4 = ((mode == 0 && (MTX_W4 & 2)) || (mode == 1 && (MTX_W4 & 4))) && w4;
+        a.nsplit = ((MTX_NSPLIT & 1) && use_w4 && mode == 0 && (Nout / 256) % 8 == 0) ? 1 : 0;
         rc = launch_build_tiles(gs, E, M, 256, wsp, st, false, split, spread, align);
         if (rc) return rc;
         // split pieces add at most ncu - rem < ncu workgroups per XCD

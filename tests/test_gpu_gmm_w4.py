@@ -112,3 +112,43 @@ def test_w4_gathered_swiglu_equals_route_then_gmm(dev, T, K, E):
     assert torch.equal(out, ref)
     refo = O.swiglu(O.gmm(st.float().cpu().numpy(), w.float().cpu().numpy(), gs.cpu().numpy()))
     assert rel_err(out.float().cpu().numpy(), refo) < 2e-2
+
+
+@pytest.mark.parametrize("op", ["fwd", "swiglu", "dlhs"])
+@pytest.mark.parametrize("gi", [0, 3])
+def test_w4_n_tiles_split_over_xcds_match_128_row_tiling(dev, op, gi):
+    """A number of n-tiles that is a multiple of 8 (the plain forward's XCD split of the n-tiles;
+    for the SwiGLU, with GROUPS[3], its merged scheduling groups): the bits of the 128-row tiling
+    and the float64 oracle at the bf16 bound."""
+    from mintext_amd import _lib as L
+
+    gs = np.asarray(GROUPS[gi], np.int32)
+    E = len(gs)
+    M = int(gs.sum()) + 300
+    N = 2048  # eight 256-column n-tiles (fwd, dlhs) / eight 128-column SwiGLU tiles
+    rng = np.random.default_rng(11 + gi)
+    if op == "dlhs":  # dx [M, Kin] = g [M, Kout] @ w[e]^T: Kin = N output columns
+        Kin, Kout = N, 512
+        x = rng.standard_normal((M, Kout)).astype(np.float32)
+        w = (rng.standard_normal((E, Kin, Kout)) * 0.05).astype(np.float32)
+    else:
+        Kin, Kout = 512, (N // 2 if op == "swiglu" else N)
+        x = rng.standard_normal((M, Kin)).astype(np.float32)
+        w = (rng.standard_normal((E, Kin, N)) * 0.05).astype(np.float32)
+    x = torch.from_numpy(x).to(dev).bfloat16()
+    w = torch.from_numpy(w).to(dev).bfloat16()
+    g = torch.from_numpy(gs).to(dev)
+    whole_ws = tile_list_workspace_bytes(M, E)
+    full_ws = L.query("mtx_gmm_workspace_size", M, E)
+    whole = _run_tiled(dev, op, x, w, g, M, Kin, Kout, E, 256, whole_ws)
+    t128 = _run_tiled(dev, op, x, w, g, M, Kin, Kout, E, 128, whole_ws)
+    split = _run_tiled(dev, op, x, w, g, M, Kin, Kout, E, 256, full_ws)
+    assert torch.equal(whole, t128), "256-row whole tiles must give the 128-row tiling's bits"
+    used = int(gs.sum())
+    assert (whole[used:] == 0).all() and (split[used:] == 0).all()
+    xf, wf = x.float().cpu().numpy(), w.float().cpu().numpy()
+    ref = O.gmm_dlhs(xf, wf, gs) if op == "dlhs" else O.gmm(xf, wf, gs)
+    if op == "swiglu":
+        ref = O.swiglu(ref)
+    for out in (whole, split):
+        assert rel_err(out.float().cpu().numpy()[:used], ref[:used]) < 2e-2
