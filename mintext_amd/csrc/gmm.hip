@@ -33,6 +33,9 @@
 
 namespace mtx {
 
+// One m-tile of the tile list: expert e (-1: rows past sum(group_sizes), stored as zeros) and rows
+// [r0, r1).  pad is 0, or, when the tile builder merges remainder m-tiles into scheduling groups,
+// the tile's group: first m-tile of the group << 8 | m-tiles in the group.
 struct MTile {
   int e, r0, r1, pad;
 };
